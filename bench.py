@@ -1,0 +1,309 @@
+#!/usr/bin/env python3
+"""Decode-step benchmark of the KV-cache hot path on one MI355X.
+
+Workload (default): Qwen3-0.6B attention shape, 28 layers, batch 64
+sequences of 16384 tokens, FP16 KV in a paged HBM pool (32-token pages,
+block tables randomly permuted per sequence), budget 64 blocks per KV group
+(4 init + 8 local + 52 dynamic), 8 planted high-score blocks per (sequence,
+KV head).  A step = for each layer: append one K/V token per sequence (+seal
+and representative update when a page fills), score + select per KV group,
+sparse GQA decode attention over the selected blocks plus the tail.
+
+Prints one JSON line: µs/layer (value), tokens/s, achieved HBM GB/s of the
+attention kernel against MI355X peak, and the CPU baseline (the oracle's C
+restatement of the reference CPU path timed on a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "solidattention-repro_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+PAGE = 32
+D = 128
+
+CONFIGS = {
+    # name: (layers, batch, query_heads, kv_heads, context, budget, init, local, planted, model)
+    "qwen3-0.6b-b64-16k": (28, 64, 16, 8, 16384, 64, 4, 8, 8, "Qwen3-0.6B"),
+    "qwen3-8b-b32-32k": (36, 32, 32, 8, 32768, 64, 4, 8, 8, "Qwen3-8B"),
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="qwen3-0.6b-b64-16k", choices=sorted(CONFIGS))
+    ap.add_argument("--layers", type=int, default=None, help="override the layer count")
+    ap.add_argument("--splits", type=int, default=0, help="attention splits per (seq, KV head); 0 = library default")
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-seqs", type=int, default=0, help="sequences in the CPU sample (0 = auto)")
+    ap.add_argument("--check-seqs", type=int, default=2, help="sequences parity-checked against the oracle")
+    return ap.parse_args()
+
+
+class Layer:
+    """One layer's device state: paged pool, tables, representatives, and the
+    per-step inputs (q, new K/V) already resident in HBM."""
+
+    def __init__(self, sa, torch, cfg, layer, args, total_steps):
+        layers, batch, hq, hkv, ctx, budget, init, local, planted, _ = cfg
+        self.batch, self.hq, self.hkv = batch, hq, hkv
+        table_stride = (ctx + total_steps + PAGE - 1) // PAGE + 1
+        num_pages = batch * table_stride
+        seed = args.seed + 7919 * layer
+        kv = sa.PagedKV(batch, hq, hkv, table_stride, num_pages=num_pages)
+        g = torch.Generator(device="cpu")
+        g.manual_seed(seed)
+        perm = torch.randperm(num_pages, generator=g, dtype=torch.int64).to(torch.int32)
+        kv.block_table.copy_(perm.view(batch, table_stride))
+        sa.fill_synthetic_f16(kv.pool.view(-1), seed, 0)
+        q = torch.empty((total_steps, batch, hq, D), dtype=torch.float32, device="cuda")
+        sa.fill_synthetic_f32(q.view(-1), seed + 1, 0)
+        knew = torch.empty((total_steps, batch, hkv, D), dtype=torch.float32, device="cuda")
+        vnew = torch.empty_like(knew)
+        sa.fill_synthetic_f32(knew.view(-1), seed + 2, 0)
+        sa.fill_synthetic_f32(vnew.view(-1), seed + 3, 0)
+        # planted high-score blocks: keys = 0.5 * mean(q of the group) + 0.5 * noise
+        if planted:
+            full = ctx // PAGE
+            blocks = torch.randint(0, full, (batch, hkv, planted), generator=g).cuda()
+            grp = hq // hkv
+            qmean = q[0].view(batch, hkv, grp, D).mean(dim=2)  # [B, Hkv, D]
+            pool16 = kv.pool.view(torch.float16)  # [pages, 32, 2, Hkv, D]
+            noise = torch.empty((batch, hkv, planted, PAGE, D), dtype=torch.float32, device="cuda")
+            sa.fill_synthetic_f32(noise.view(-1), seed + 4, 0)
+            pages = torch.gather(kv.block_table.to(torch.int64), 1, blocks.view(batch, -1)).view(batch, hkv, planted)
+            heads = torch.arange(hkv, device="cuda").view(1, hkv, 1).expand(batch, hkv, planted)
+            vals = (0.5 * qmean[:, :, None, None, :] + 0.5 * noise).to(torch.float16)
+            pool16[pages.reshape(-1), :, 0, heads.reshape(-1), :] = vals.reshape(-1, PAGE, D)
+        kv.seq_len.fill_(ctx)
+        sa.seal(kv, 0)
+        self.kv, self.q, self.knew, self.vnew = kv, q, knew, vnew
+        self.budget, self.init, self.local = budget, init, local
+        self.selected = torch.full((batch, hkv, budget), -1, dtype=torch.int32, device="cuda")
+        self.counts = torch.zeros((batch, hkv), dtype=torch.int32, device="cuda")
+        self.out = torch.empty((batch, hq, D), dtype=torch.float32, device="cuda")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the KV-cache hot path is measured at its "
+                                   "real per-GPU shape; --gpus must be 1"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import solidattention_amd as sa
+
+    cfg = list(CONFIGS[args.config])
+    if args.layers:
+        cfg[0] = args.layers
+    layers, batch, hq, hkv, ctx, budget, init, local, planted, model = cfg
+    total_steps = args.warmup + args.steps
+    torch.cuda.set_device(0)
+    log(f"setup {args.config}: layers={layers} batch={batch} ctx={ctx} budget={budget}")
+    t0 = time.time()
+    L = [Layer(sa, torch, cfg, l, args, total_steps) for l in range(layers)]
+    torch.cuda.synchronize()
+    log(f"setup done in {time.time() - t0:.1f}s; pool {L[0].kv.pool.numel() * 2 * layers / 2**30:.1f} GiB")
+
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pages_hint = budget + 2
+    splits = args.splits or sa.default_splits(batch, hkv, pages_hint)
+    ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(batch, hq, hkv, D, splits)
+    workspace = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    stream = torch.cuda.current_stream()
+
+    n_ev = total_steps * layers
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_ev)]
+
+    def step(s, record):
+        for l, ly in enumerate(L):
+            e = ev[s * layers + l] if record else None
+            if e: e[0].record(stream)
+            sa.append_seal(ly.kv, ly.knew[s], ly.vnew[s], 0, status=status)
+            if e: e[1].record(stream)
+            sa.score_select(ly.kv, ly.q[s], hkv, budget, init, local, selected=ly.selected, counts=ly.counts,
+                            status=status)
+            if e: e[2].record(stream)
+            sa.sparse_decode_attention(ly.kv, ly.q[s], ly.selected, ly.counts, scale, out=ly.out, splits=splits,
+                                       workspace=workspace, status=status)
+            if e: e[3].record(stream)
+
+    for s in range(args.warmup):
+        step(s, record=False)
+    torch.cuda.synchronize()
+    log("warmup done")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for s in range(args.warmup, total_steps):
+        step(s, record=True)
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    if int(status.item()) != 0:
+        raise SystemExit(f"device status flagged {int(status.item())}")
+    ms_per_step = total_ms / args.steps
+    us_per_layer = ms_per_step * 1000.0 / layers
+    app, sel, att = [], [], []
+    for s in range(args.warmup, total_steps):
+        for l in range(layers):
+            e = ev[s * layers + l]
+            app.append(e[0].elapsed_time(e[1]))
+            sel.append(e[1].elapsed_time(e[2]))
+            att.append(e[2].elapsed_time(e[3]))
+    att_us = 1000.0 * sum(att) / len(att)
+    sel_us = 1000.0 * sum(sel) / len(sel)
+    app_us = 1000.0 * sum(app) / len(app)
+
+    # algorithmic bytes of one attention launch: selected KV + tail KV + q + out + ids/table entries
+    seq_len = L[-1].kv.seq_len.cpu().numpy().astype(np.int64)
+    sealed = L[-1].kv.sealed.cpu().numpy().astype(np.int64)
+    counts = L[-1].counts.cpu().numpy().astype(np.int64)
+    tail = seq_len - sealed * PAGE
+    kv_tok_bytes = 2 * D * 2  # K+V of one KV head, FP16
+    att_bytes = int(counts.sum() * PAGE * kv_tok_bytes + (tail.sum() * hkv) * kv_tok_bytes +
+                    batch * hq * D * 4 * 2 + counts.sum() * 8)
+    rep_bytes = int(sealed.sum() * hkv * D * 4)
+    layer_bytes = att_bytes + rep_bytes
+    achieved = att_bytes / (att_us * 1e-6) / 1e9
+    layer_gbps = layer_bytes / (us_per_layer * 1e-6) / 1e9
+    log(f"attention {att_us:.2f} us ({achieved:.0f} GB/s), select {sel_us:.2f} us, append {app_us:.2f} us, "
+        f"layer {us_per_layer:.2f} us")
+
+    parity = check_parity(sa, np, torch, L[-1], args, scale, hkv, budget, init, local)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(np, torch, L[0], args, budget, init, local, scale)
+
+    line = {
+        "metric": "sparse decode-attn µs/layer + achieved HBM GB/s (Qwen3-0.6B shape, B=64, 16K)",
+        "value": round(us_per_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 KV, fp32 math",
+        "data": "synthetic (seeded N(0,1) FP16 KV, 8 planted blocks per head, random permuted page tables)",
+        "config": {"workload": f"{model} attention shape decode step: append+seal, score+select, sparse GQA "
+                               f"attention", "layers": layers, "batch": batch, "query_heads": hq,
+                   "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
+                   "init_blocks": init, "local_blocks": local, "page_tokens": PAGE, "splits": splits},
+        "tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
+        "achieved_layer_hbm_gbps": round(layer_gbps, 1),
+        "kernels_us": {"attention": round(att_us, 3), "score_select": round(sel_us, 3),
+                       "append_seal": round(app_us, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "sparse_decode_attention_kernel", "algorithmic_bytes": att_bytes},
+        "parity": parity,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local):
+    """Full-size spot check: for a few sequences of the last layer, the selection
+    (bit-exact) and attention (2e-3) against the oracle on the device bytes."""
+    import oracle as O
+    n = min(args.check_seqs, ly.batch)
+    if n <= 0:
+        return None
+    kv = ly.kv
+    s = args.warmup + args.steps - 1
+    seqs = list(range(n))
+    table = kv.block_table[seqs].cpu().numpy()
+    seq_len = kv.seq_len[seqs].cpu().numpy()
+    sealed = kv.sealed[seqs].cpu().numpy()
+    used = np.unique(table[:, : int(((seq_len.max() + PAGE - 1) // PAGE))])
+    pool = kv.pool[torch.from_numpy(used).cuda().long()].view(torch.int16).cpu().numpy().view(np.uint16)
+    remap = {int(p): i for i, p in enumerate(used)}
+    table_l = np.vectorize(lambda p: remap.get(int(p), 0))(table).astype(np.int32)
+    reps = kv.reps[seqs].cpu().numpy()
+    q = ly.q[s][seqs].cpu().numpy()
+    esel, ecnt = O.paged_score_select(q, reps, sealed, n, ly.hq, hkv, D, kv.rep_heads, kv.rep_stride, hkv, budget,
+                                      init, local)
+    got_sel = ly.selected[seqs].cpu().numpy()
+    got_cnt = ly.counts[seqs].cpu().numpy()
+    sel_ok = bool(np.array_equal(got_cnt, ecnt)) and all(
+        np.array_equal(got_sel[b, g, : ecnt[b, g]], esel[b, g, : ecnt[b, g]]) for b in range(n) for g in range(hkv))
+    expect = O.paged_sparse_attention(pool, PAGE, table_l, seq_len, sealed, esel, ecnt, hkv, q, n, ly.hq, hkv, D,
+                                      scale)
+    got = ly.out[seqs].cpu().numpy()
+    err = np.abs(got.astype(np.float64) - expect)
+    att_ok = bool(((err <= 2e-3) | (err <= 2e-3 * np.abs(expect))).all())
+    return {"sequences": n, "selection_bit_exact": sel_ok, "attention_within_2e-3": att_ok,
+            "attention_max_abs_err": float(err.max())}
+
+
+def cpu_baseline(np, torch, ly, args, budget, init, local, scale):
+    """The oracle's restatement of the reference CPU path (score + select +
+    pack + attention per (sequence, KV group)), single thread, timed on a
+    bounded sample of sequences of the same workload; reported per layer of
+    the full batch by scaling with batch / sample."""
+    import ctypes
+    import oracle as O
+    kv = ly.kv
+    batch, hq, hkv = ly.batch, ly.hq, ly.hkv
+    n = args.cpu_sample_seqs or 2
+    seqs = list(range(n))
+    table = kv.block_table[seqs].cpu().numpy()
+    seq_len = kv.seq_len[seqs].cpu().numpy()
+    sealed = kv.sealed[seqs].cpu().numpy()
+    used = np.unique(table[:, : int(((seq_len.max() + PAGE - 1) // PAGE))])
+    pool = kv.pool[torch.from_numpy(used).cuda().long()].view(torch.int16).cpu().numpy().view(np.uint16)
+    remap = {int(p): i for i, p in enumerate(used)}
+    table_l = np.vectorize(lambda p: remap.get(int(p), 0))(table).astype(np.int32)
+    reps = kv.reps[seqs].cpu().numpy()
+    q = ly.q[0][seqs].cpu().numpy()
+    reps_c = np.ascontiguousarray(reps)
+    t0 = time.perf_counter()
+    reps_loops = 0
+    while True:
+        sel, cnt = O.paged_score_select(q, reps_c, sealed, n, hq, hkv, D, kv.rep_heads, kv.rep_stride, hkv, budget,
+                                        init, local)
+        O.paged_sparse_attention(pool, PAGE, table_l, seq_len, sealed, sel, cnt, hkv, q, n, hq, hkv, D, scale)
+        reps_loops += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps_loops >= 1000:
+            break
+    per_seq_s = el / reps_loops / n
+    per_layer_us = per_seq_s * batch * 1e6
+    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
+            "sample": f"{n} of {batch} sequences of one layer x {reps_loops} repeats (score+select+gather+"
+                      f"attention per KV group, oracle C restatement, 1 thread), scaled to {batch} sequences",
+            "host_cpu": _cpu_model(), "nproc": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,224 @@
+/*
+ * sa_hip.h — C-ABI of the MI355X (gfx950) KV-cache decode hot path.
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device memory;
+ * `stream` arguments are hipStream_t passed as void* (NULL = the null
+ * stream).  Every entry point returns 0 on success or a negative SA_HIP_E*
+ * code; sa_hip_last_error() returns the message of the last failure on the
+ * calling thread.  Hot entry points allocate nothing: scratch memory comes
+ * in through explicit workspace arguments sized by the *_workspace_bytes
+ * queries.  Launches are asynchronous on `stream`.
+ *
+ * Each entry point names the reference interface it replaces (paths are
+ * relative to the reference checkout).  The C++ contract above this layer
+ * is include/solidattention/backend.hpp (AcceleratorBackend, kept with the
+ * reference's names and meaning) plus include/solidattention/hip_kv.hpp.
+ */
+#ifndef SA_HIP_H
+#define SA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_HIP_OK 0
+#define SA_HIP_EINVAL (-1)   /* invalid argument / unsupported shape */
+#define SA_HIP_ERUNTIME (-2) /* HIP runtime error */
+
+/* Tokens per page (and per selectable block).  Fixed: the reference's
+ * 32-token blocks (selection_main.cpp:97, kv_lifecycle_main.cpp:21). */
+#define SA_HIP_PAGE_TOKENS 32
+
+/* Paged KV view.  All arrays are device memory.
+ *   pool        [num_pages][32][2][kv_heads][head_dim] FP16 bits: a page is
+ *               32 tokens in the reference token format
+ *               [K: kv_heads x head_dim][V: kv_heads x head_dim]
+ *               (backend.hpp:18-31, attention_reference.cpp:67-69,84-87).
+ *   block_table [batch][table_stride] page id of each logical block.
+ *   seq_len     [batch] tokens held by each sequence.
+ *   sealed      [batch] sealed (selectable) blocks; tokens
+ *               [sealed*32, seq_len) form the unsealed tail.
+ *   generation  [batch] seal counter (may be NULL).
+ *   reps        [batch][rep_heads][head_dim][rep_stride] fp32 block
+ *               representatives, head_dim-major so that lanes reading
+ *               consecutive blocks are coalesced.  rep_heads is kv_heads
+ *               (one representative per KV head, shared by its query heads)
+ *               or query_heads (one per query head). */
+typedef struct sa_paged_kv {
+  uint16_t* pool;
+  int32_t* block_table;
+  int32_t* seq_len;
+  int32_t* sealed;
+  int32_t* generation;
+  float* reps;
+  int64_t num_pages;
+  int32_t batch;
+  int32_t table_stride;
+  int32_t rep_heads;
+  int32_t rep_stride;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t reserved;
+} sa_paged_kv;
+
+/* Budgeted selection parameters.
+ *   select_groups  kv_heads: each KV group (its G query heads) selects its own
+ *                  blocks; 1: one block set shared by all query heads (the
+ *                  reference's C2 call, selection_main.cpp:178-181).
+ *   budget_blocks  blocks per selection (init + local + dynamic); when a
+ *                  sequence has no more sealed blocks than this, all are
+ *                  selected (the clamp of selection.py:120).
+ *   init_blocks    always-selected leading blocks [0, init).
+ *   local_blocks   always-selected trailing sealed blocks [n-local, n).
+ *   sel_stride     row stride of the selected[] output (>= budget_blocks). */
+typedef struct sa_select_params {
+  int32_t select_groups;
+  int32_t budget_blocks;
+  int32_t init_blocks;
+  int32_t local_blocks;
+  int32_t sel_stride;
+} sa_select_params;
+
+/* ---- library ------------------------------------------------------------ */
+
+const char* sa_hip_last_error(void);
+int sa_hip_abi_version(void);
+/* Number of visible devices (0 when none); does not create a context. */
+int sa_hip_device_count(void);
+
+/* ---- R6: sparse GQA decode attention ------------------------------------ */
+
+/* Workspace for sa_hip_sparse_decode_attention with `splits` partial
+ * results per (sequence, KV head). */
+size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads,
+                                        int32_t kv_heads, int32_t head_dim,
+                                        int32_t splits);
+
+/* Split count the library would pick for a launch (>= 1). */
+int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads,
+                                        int32_t pages_per_group_hint);
+
+/* out[b][h][:] = softmax(scale * q[b][h] . K) V over the tokens of the
+ * selected sealed blocks of h's KV group followed by every tail token of
+ * sequence b; fp32 stable softmax (online, split over `splits` partial
+ * results merged with log-sum-exp).  selected: [batch][select_groups]
+ * [sel_stride] logical block ids; counts: [batch][select_groups].
+ * query, out: [batch][query_heads][head_dim] fp32.  status (optional,
+ * device int32) receives SA status bits for invalid pages/blocks.
+ * Replaces the device side of AcceleratorBackend::attention*
+ * (backend.hpp:50-57; cuda_backend.cpp:109-158, 323-415) and the
+ * tail-inclusive sparse_fp16_attention (qwen_layer_main.cpp:224-268);
+ * semantics of attention_reference (attention_reference.cpp:55-96). */
+int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query,
+                                   const int32_t* selected,
+                                   const int32_t* counts,
+                                   int32_t select_groups, int32_t sel_stride,
+                                   float scale, float* out, void* workspace,
+                                   size_t workspace_bytes, int32_t splits,
+                                   int32_t* status, void* stream);
+
+/* Attention over a contiguous token-major K/V-interleaved buffer of
+ * `tokens` tokens (the AttentionProblem layout, backend.hpp:18-31); the
+ * device kernel of AcceleratorBackend::attention (cuda_backend.cpp:70-158)
+ * without its 128/256-token limits. */
+size_t sa_hip_contiguous_workspace_bytes(int64_t tokens, int32_t query_heads,
+                                         int32_t kv_heads, int32_t head_dim);
+int sa_hip_attention_contiguous(const uint16_t* kv, const float* query,
+                                int64_t tokens, int32_t query_heads,
+                                int32_t kv_heads, int32_t head_dim,
+                                float scale, float* out, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/* Weighted checksum of an output vector, out[0] = sum_i x[i] * (1 + (i%17) *
+ * 0.001); the C1.4 device consumer (cuda_backend.cpp:160-168). */
+int sa_hip_consume_checksum(const float* input, int32_t elements,
+                            float* checksum, void* stream);
+
+/* ---- R3: scoring + budgeted top-k selection ----------------------------- */
+
+/* Per (sequence, selection group): score[b] = sum over the group's query
+ * heads h, in head order, of (sequential fp32 dot(q_h, rep_b) / heads) with
+ * no fused multiply-add, then init/local/dynamic selection with ties broken
+ * towards the lower block id; ids ascending.  Bit-exact with
+ * select_shared_blocks (selection.hpp:24-29, selection.cpp:96-147) applied
+ * to the group.  scores (optional): [batch][select_groups][rep_stride].
+ * Limit: sealed[b] <= 8192 blocks. */
+int sa_hip_score_select(const sa_paged_kv* kv, const float* query,
+                        const sa_select_params* params, int32_t* selected,
+                        int32_t* counts, float* scores, int32_t* status,
+                        void* stream);
+
+/* ---- R8/R9/R4: decode append, seal, representative ---------------------- */
+
+/* Append one token per sequence at position seq_len[b] (fp32 K/V converted
+ * round-to-nearest-even, or raw FP16 bits for the _f16 variant), advance
+ * seq_len, then seal while the tail holds >= local_tokens + 32 tokens: the
+ * oldest tail block becomes selectable, its mean-key representative
+ * (sum of its 32 keys in token order / 32, per KV head) is written to reps
+ * and sealed/generation advance.  k, v: [batch][kv_heads][head_dim].
+ * Replaces append_fp16_kv (qwen_layer_main.cpp:270-281) and the tail seal
+ * of kv_lifecycle_main.cpp:31-45, 92-113 (bit-exact bytes and
+ * representatives). */
+int sa_hip_append_seal(const sa_paged_kv* kv, const float* k, const float* v,
+                       int32_t local_tokens, int32_t* status, void* stream);
+int sa_hip_append_seal_f16(const sa_paged_kv* kv, const uint16_t* k,
+                           const uint16_t* v, int32_t local_tokens,
+                           int32_t* status, void* stream);
+/* Seal only (e.g. after a prefill wrote whole pages and set seq_len). */
+int sa_hip_seal(const sa_paged_kv* kv, int32_t local_tokens, int32_t* status,
+                void* stream);
+
+/* ---- R5: gather / pack --------------------------------------------------- */
+
+/* out + i * page_bytes <- pool + pages[i] * page_bytes for i < count (device
+ * arrays), the placement of UringReader::read_blocks_fixed
+ * (uring_reader.cpp:87-95) for pool-resident blocks.  page_bytes must be a
+ * multiple of 16; pages outside [0, num_pages) are skipped and flagged in
+ * status (optional). */
+int sa_hip_gather_pages(const uint16_t* pool, int64_t page_bytes,
+                        int64_t num_pages, const int32_t* pages,
+                        int32_t count, uint16_t* out, int32_t* status,
+                        void* stream);
+
+/* ---- R10: history prediction and miss correction ------------------------ */
+
+/* Host-only set logic of compare_prediction (pipeline_main.cpp:686-717):
+ * hits, misses (oracle blocks absent from the prediction, oracle order) and
+ * replacement slots (prediction slots whose block left, slot order).
+ * Returns SA_HIP_EINVAL on a cardinality mismatch. */
+int sa_hip_compare_prediction(const int32_t* predicted, const int32_t* oracle,
+                              int32_t n, int32_t* hits, int32_t* misses,
+                              int32_t* replacement_slots, int32_t* miss_count);
+
+/* Copy-stream slot fills: for i < count, hipMemcpyAsync of page_bytes from
+ * pinned host memory src_base + src_blocks[i] * page_bytes into pool page
+ * dst_pages[i] on copy_stream, then record done_event (hipEvent_t) on it.
+ * dst_pages and src_blocks are host arrays.  The compute stream orders
+ * itself after the fills with sa_hip_stream_wait_event instead of a host
+ * barrier.  Replaces CudaPipeline::correct_and_wait
+ * (pipeline_main.cpp:305-331). */
+int sa_hip_fill_pages_async(uint16_t* pool, int64_t page_bytes,
+                            const int32_t* dst_pages,
+                            const void* src_base, const int64_t* src_blocks,
+                            int32_t count, void* copy_stream,
+                            void* done_event);
+int sa_hip_stream_wait_event(void* stream, void* event);
+
+/* ---- synthetic data ------------------------------------------------------ */
+
+/* dst[i] = fp16_rne(normal(seed, first_index + i)), the generator of the
+ * CPU oracle (bit-identical). */
+int sa_hip_fill_synthetic_f16(uint16_t* dst, int64_t count, uint64_t seed,
+                              uint64_t first_index, void* stream);
+int sa_hip_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed,
+                              uint64_t first_index, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SA_HIP_H */

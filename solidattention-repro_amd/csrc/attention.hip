@@ -1,0 +1,387 @@
+// attention.hip — GQA sparse decode attention over paged FP16 KV (gfx950).
+//
+// Semantics: attention_reference (reference cpp/src/attention_reference.cpp
+// :55-96) applied, per (sequence, KV head g), to the tokens of the selected
+// sealed blocks followed by the unsealed tail, for each of the G query heads
+// of g.  Softmax is computed online in the log2 domain and split over
+// `splits` workgroups per (sequence, KV head); partial results are merged
+// with log-sum-exp.  fp32 arithmetic on exact FP16 decodes; the reference's
+// two-pass order is not reproduced (tolerance-checked, not bit-exact).
+//
+// Mapping (head_dim 128): one wave64 walks whole 32-token pages.  A 16-byte
+// load per lane covers 4 rows of 256 B (16 lanes per K or V row of one KV
+// head), so a page's K and V tiles for head g are 8 + 8 dwordx4 loads per
+// lane.  Lane (row r, column c) owns dims [8c, 8c+8) of tokens {r, r+4, ...}.
+// q·k partial dots are reduced across the 16 lanes of a row with DPP; the
+// G query heads of the group reuse every K/V register, so KV bytes are read
+// from HBM once per group.  No MFMA: decode attention is a matrix-vector
+// product (about 2 flop per KV byte at G=2).
+#include "sa_device.hpp"
+#include "sa_internal.hpp"
+
+namespace sa {
+namespace {
+
+constexpr int D = kHeadDim;
+constexpr int kWavesPerGroup = 4;                 // waves per workgroup
+constexpr int kThreads = kWavesPerGroup * kWave;  // 256
+constexpr int kLanesPerRow = D / 8;               // 16 lanes x 8 halves = one 256 B row
+constexpr int kRows = kWave / kLanesPerRow;       // 4 rows per wave-wide load
+constexpr int kIters = kPageTokens / kRows;       // 8 tokens per lane per page
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct Params {
+  const uint16_t* pool;
+  const int32_t* table;
+  const int32_t* seq_len;
+  const int32_t* sealed;
+  const int32_t* selected;
+  const int32_t* counts;
+  const float* query;
+  float* out;
+  float* part;
+  int32_t* status;
+  int64_t num_pages;
+  int64_t contig_tokens;
+  int64_t page_elems;
+  int32_t token_elems;
+  int32_t table_stride;
+  int32_t sel_stride;
+  int32_t select_groups;
+  int32_t kv_per_sel;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t splits;
+  float qscale;  // softmax scale * log2(e)
+};
+
+__device__ inline void unpack8(const uint4& w, float (&f)[8]) {
+  f[0] = lo_h2f(w.x);
+  f[1] = hi_h2f(w.x);
+  f[2] = lo_h2f(w.y);
+  f[3] = hi_h2f(w.y);
+  f[4] = lo_h2f(w.z);
+  f[5] = hi_h2f(w.z);
+  f[6] = lo_h2f(w.w);
+  f[7] = hi_h2f(w.w);
+}
+
+// Page `i` of the (sequence, KV head) list: selected sealed blocks first,
+// then the tail pages.  Returns the page index (or -1 to skip) and the
+// number of valid tokens in it.
+struct PageRef {
+  int64_t page;
+  int valid;
+};
+
+__device__ inline PageRef resolve_page(const Params& p, int b, int i, int n_sel,
+                                       const int32_t* sel, int sealed_b, int64_t len) {
+  PageRef r{-1, 0};
+  int64_t logical;
+  if (i < n_sel) {
+    logical = sel[i];
+    if (logical < 0 || logical >= sealed_b) {
+      flag_status(p.status, kStatusBadBlock);
+      return r;
+    }
+    r.valid = kPageTokens;
+  } else {
+    logical = static_cast<int64_t>(sealed_b) + (i - n_sel);
+    const int64_t left = len - logical * kPageTokens;
+    r.valid = left < kPageTokens ? static_cast<int>(left) : kPageTokens;
+  }
+  if (p.contig_tokens > 0) {
+    r.page = logical;
+    return r;
+  }
+  if (logical >= p.table_stride) {
+    flag_status(p.status, kStatusBadBlock);
+    r.valid = 0;
+    return r;
+  }
+  const int64_t page = p.table[static_cast<int64_t>(b) * p.table_stride + logical];
+  if (page < 0 || page >= p.num_pages) {
+    flag_status(p.status, kStatusBadPage);
+    r.valid = 0;
+    return r;
+  }
+  r.page = page;
+  return r;
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const Params p) {
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const int z = blockIdx.z;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int row = lane / kLanesPerRow;
+  const int col = lane % kLanesPerRow;
+
+  // ---- page list of this (sequence, KV head) -------------------------------
+  int64_t len;
+  int sealed_b, n_sel;
+  const int32_t* sel = nullptr;
+  if (p.contig_tokens > 0) {
+    len = p.contig_tokens;
+    sealed_b = 0;
+    n_sel = 0;
+  } else {
+    len = p.seq_len[b];
+    sealed_b = p.sealed[b];
+    const int sg = g / p.kv_per_sel;
+    n_sel = p.counts[b * p.select_groups + sg];
+    sel = p.selected + static_cast<int64_t>(b * p.select_groups + sg) * p.sel_stride;
+    if (sealed_b < 0 || len < static_cast<int64_t>(sealed_b) * kPageTokens || n_sel < 0 ||
+        n_sel > p.sel_stride) {
+      flag_status(p.status, kStatusBadLength);
+      len = static_cast<int64_t>(sealed_b > 0 ? sealed_b : 0) * kPageTokens;
+      if (n_sel < 0 || n_sel > p.sel_stride) n_sel = 0;
+    }
+  }
+  const int64_t tail_tokens = len - static_cast<int64_t>(sealed_b) * kPageTokens;
+  const int n_tail = static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
+  const int total = n_sel + n_tail;
+
+  // ---- query: dims [8c, 8c+8) of each head of the group, pre-scaled -------
+  float qf[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float4* q4 = reinterpret_cast<const float4*>(
+        p.query + (static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + col * 8);
+    const float4 a = q4[0], c = q4[1];
+    qf[h][0] = a.x * p.qscale;
+    qf[h][1] = a.y * p.qscale;
+    qf[h][2] = a.z * p.qscale;
+    qf[h][3] = a.w * p.qscale;
+    qf[h][4] = c.x * p.qscale;
+    qf[h][5] = c.y * p.qscale;
+    qf[h][6] = c.z * p.qscale;
+    qf[h][7] = c.w * p.qscale;
+  }
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = kNegInf;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
+  }
+
+  const int64_t head_off = static_cast<int64_t>(row) * p.token_elems + g * D + col * 8;
+  const int64_t v_off = static_cast<int64_t>(p.kv_heads) * D;
+  const int64_t step4 = static_cast<int64_t>(kRows) * p.token_elems;
+  const int waves_total = p.splits * kWavesPerGroup;
+
+  for (int i = z * kWavesPerGroup + wave; i < total; i += waves_total) {
+    const PageRef pr = resolve_page(p, b, i, n_sel, sel, sealed_b, len);
+    if (pr.valid <= 0) continue;
+    const uint16_t* kbase = p.pool + pr.page * p.page_elems + head_off;
+    uint4 kr[kIters], vr[kIters];
+    if (pr.valid == kPageTokens) {
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
+        vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        if (it * kRows + row < pr.valid) {
+          kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
+          vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
+        } else {
+          kr[it] = make_uint4(0, 0, 0, 0);
+          vr[it] = make_uint4(0, 0, 0, 0);
+        }
+      }
+    }
+
+    // logits (log2 domain) of this lane's 8 tokens for every head
+    float s[G][kIters];
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      float kf[8];
+      unpack8(kr[it], kf);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a = __builtin_fmaf(qf[h][j], kf[j], a);
+        s[h][it] = row16_sum(a);
+      }
+    }
+
+    float vf[kIters][8];
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) unpack8(vr[it], vf[it]);
+
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float pmax = kNegInf;
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        if (it * kRows + row >= pr.valid) s[h][it] = kNegInf;
+        pmax = fmaxf(pmax, s[h][it]);
+      }
+      pmax = fmaxf(pmax, shfl_xor_f(pmax, 16));
+      pmax = fmaxf(pmax, shfl_xor_f(pmax, 32));
+      const float mn = fmaxf(m[h], pmax);
+      if (mn == kNegInf) continue;  // nothing finite seen yet
+      const float corr = (m[h] == mn) ? 1.0f : __builtin_amdgcn_exp2f(m[h] - mn);
+      m[h] = mn;
+      float lsum = l[h] * corr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[h][j] *= corr;
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        const float pe = __builtin_amdgcn_exp2f(s[h][it] - mn);
+        lsum += pe;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(pe, vf[it][j], acc[h][j]);
+      }
+      l[h] = lsum;
+    }
+  }
+
+  // ---- combine the 4 rows of the wave (same running max in every row) ----
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    l[h] += shfl_xor_f(l[h], 16);
+    l[h] += shfl_xor_f(l[h], 32);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[h][j] += shfl_xor_f(acc[h][j], 16);
+      acc[h][j] += shfl_xor_f(acc[h][j], 32);
+    }
+  }
+
+  // ---- combine the waves of the workgroup through LDS ----------------------
+  __shared__ float sm_m[kWavesPerGroup][G];
+  __shared__ float sm_l[kWavesPerGroup][G];
+  __shared__ float sm_acc[kWavesPerGroup][G][D];
+  if (row == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sm_acc[wave][h][col * 8 + j] = acc[h][j];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      sm_m[wave][h] = m[h];
+      sm_l[wave][h] = l[h];
+    }
+  }
+  __syncthreads();
+
+  for (int o = threadIdx.x; o < G * D; o += kThreads) {
+    const int h = o / D;
+    const int d = o % D;
+    float mx = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWavesPerGroup; ++w) mx = fmaxf(mx, sm_m[w][h]);
+    float lw = 0.0f, aw = 0.0f;
+    if (mx != kNegInf) {
+#pragma unroll
+      for (int w = 0; w < kWavesPerGroup; ++w) {
+        const float mw = sm_m[w][h];
+        if (mw == kNegInf) continue;
+        const float f = __builtin_amdgcn_exp2f(mw - mx);
+        lw = __builtin_fmaf(sm_l[w][h], f, lw);
+        aw = __builtin_fmaf(sm_acc[w][h][d], f, aw);
+      }
+    }
+    const int qh = g * G + h;
+    if (p.splits == 1) {
+      p.out[(static_cast<int64_t>(b) * p.query_heads + qh) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
+    } else {
+      float* rec = p.part + (((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits + z) * G + h) *
+                                part_stride(D);
+      if (d == 0) {
+        rec[0] = mx;
+        rec[1] = lw;
+      }
+      rec[kPartPad + d] = aw;
+    }
+  }
+}
+
+// Log-sum-exp merge of the split partial results of one (sequence, KV head).
+template <int G>
+__global__ __launch_bounds__(kThreads) void merge_partials_kernel(const Params p) {
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const float* base =
+      p.part + ((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits) * G * part_stride(D);
+  for (int o = threadIdx.x; o < G * D; o += kThreads) {
+    const int h = o / D;
+    const int d = o % D;
+    float mx = kNegInf;
+    for (int z = 0; z < p.splits; ++z) mx = fmaxf(mx, base[(z * G + h) * part_stride(D)]);
+    float lw = 0.0f, aw = 0.0f;
+    if (mx != kNegInf) {
+      for (int z = 0; z < p.splits; ++z) {
+        const float* rec = base + (z * G + h) * part_stride(D);
+        if (rec[0] == kNegInf) continue;
+        const float f = __builtin_amdgcn_exp2f(rec[0] - mx);
+        lw = __builtin_fmaf(rec[1], f, lw);
+        aw = __builtin_fmaf(rec[kPartPad + d], f, aw);
+      }
+    }
+    p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] =
+        lw > 0.0f ? aw / lw : 0.0f;
+  }
+}
+
+template <int G>
+hipError_t launch_g(const Params& p, int batch, hipStream_t stream) {
+  const dim3 grid(p.kv_heads, batch, p.splits);
+  hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(kThreads), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  hipLaunchKernelGGL(merge_partials_kernel<G>, dim3(p.kv_heads, batch), dim3(kThreads), 0, stream,
+                     p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t stream) {
+  Params p{};
+  p.pool = a.pool;
+  p.table = a.table;
+  p.seq_len = a.seq_len;
+  p.sealed = a.sealed;
+  p.selected = a.selected;
+  p.counts = a.counts;
+  p.query = a.query;
+  p.out = a.out;
+  p.part = a.part;
+  p.status = a.status;
+  p.num_pages = a.num_pages;
+  p.contig_tokens = a.contig_tokens;
+  p.token_elems = 2 * a.kv_heads * D;
+  p.page_elems = static_cast<int64_t>(kPageTokens) * p.token_elems;
+  p.table_stride = a.table_stride;
+  p.sel_stride = a.sel_stride;
+  p.select_groups = a.select_groups > 0 ? a.select_groups : 1;
+  p.kv_per_sel = a.kv_heads / p.select_groups;
+  p.query_heads = a.query_heads;
+  p.kv_heads = a.kv_heads;
+  p.splits = a.splits;
+  p.qscale = a.scale * 1.4426950408889634f;
+  const int group = a.query_heads / a.kv_heads;
+  switch (group) {
+    case 1: return launch_g<1>(p, a.batch, stream);
+    case 2: return launch_g<2>(p, a.batch, stream);
+    case 4: return launch_g<4>(p, a.batch, stream);
+    case 8: return launch_g<8>(p, a.batch, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace sa

@@ -1,0 +1,359 @@
+// capi.hip — the extern "C" boundary (include/sa_hip.h): argument
+// validation, error strings, launch dispatch.  Hot entry points allocate
+// nothing; scratch comes in through workspace arguments.
+#include "sa_hip.h"
+#include "sa_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return SA_HIP_OK;
+  return fail(SA_HIP_ERUNTIME, "%s: %s", what, hipGetErrorString(e));
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_geometry(const sa_paged_kv* kv, const char* op) {
+  if (!kv) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv", op);
+  if (kv->head_dim != sa::kHeadDim)
+    return fail(SA_HIP_EINVAL, "%s: head_dim %d unsupported (built for %d)", op, kv->head_dim,
+                sa::kHeadDim);
+  if (kv->kv_heads <= 0 || kv->query_heads <= 0 || kv->query_heads % kv->kv_heads != 0)
+    return fail(SA_HIP_EINVAL, "%s: invalid GQA dimensions %d/%d", op, kv->query_heads, kv->kv_heads);
+  const int group = kv->query_heads / kv->kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return fail(SA_HIP_EINVAL, "%s: query heads per KV head must be 1, 2, 4 or 8 (got %d)", op, group);
+  if (kv->batch <= 0 || kv->batch > 65535) return fail(SA_HIP_EINVAL, "%s: batch %d out of range", op, kv->batch);
+  if (kv->table_stride <= 0) return fail(SA_HIP_EINVAL, "%s: table_stride must be positive", op);
+  if (kv->num_pages <= 0) return fail(SA_HIP_EINVAL, "%s: num_pages must be positive", op);
+  if (!kv->pool || !kv->block_table || !kv->seq_len || !kv->sealed)
+    return fail(SA_HIP_EINVAL, "%s: null pool/table/seq_len/sealed", op);
+  if (!aligned16(kv->pool)) return fail(SA_HIP_EINVAL, "%s: pool must be 16-byte aligned", op);
+  return SA_HIP_OK;
+}
+
+int check_reps(const sa_paged_kv* kv, const char* op) {
+  if (!kv->reps) return fail(SA_HIP_EINVAL, "%s: null reps", op);
+  if (kv->rep_heads != kv->kv_heads && kv->rep_heads != kv->query_heads)
+    return fail(SA_HIP_EINVAL, "%s: rep_heads must equal kv_heads or query_heads", op);
+  if (kv->rep_stride <= 0) return fail(SA_HIP_EINVAL, "%s: rep_stride must be positive", op);
+  return SA_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sa_hip_last_error(void) { return g_last_error.c_str(); }
+
+int sa_hip_abi_version(void) { return 1; }
+
+int sa_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+// ---- attention ---------------------------------------------------------------
+
+size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads, int32_t kv_heads,
+                                        int32_t head_dim, int32_t splits) {
+  if (batch <= 0 || kv_heads <= 0 || query_heads <= 0 || splits <= 1) return 0;
+  const size_t group = static_cast<size_t>(query_heads / kv_heads);
+  return static_cast<size_t>(batch) * kv_heads * splits * group * sa::part_stride(head_dim) *
+         sizeof(float);
+}
+
+int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads, int32_t pages_per_group_hint) {
+  // Aim at ~4 pages per wave (4 waves per workgroup) and at least ~1024
+  // workgroups so that all 256 CUs hold several waves.
+  const int64_t pages = std::max<int32_t>(pages_per_group_hint, 1);
+  int64_t splits = std::max<int64_t>(1, (pages + 15) / 16);
+  const int64_t groups = static_cast<int64_t>(std::max(batch, 1)) * std::max(kv_heads, 1);
+  while (groups * splits < 1024 && splits * 4 < pages) splits *= 2;
+  return static_cast<int32_t>(std::min<int64_t>(splits, 64));
+}
+
+static int attention_common(const sa_paged_kv* kv, const float* query, const int32_t* selected,
+                            const int32_t* counts, int32_t select_groups, int32_t sel_stride, float scale,
+                            float* out, void* workspace, size_t workspace_bytes, int32_t splits,
+                            int32_t* status, void* stream, int64_t contig_tokens) {
+  sa::AttnLaunch a{};
+  a.pool = kv->pool;
+  a.table = kv->block_table;
+  a.seq_len = kv->seq_len;
+  a.sealed = kv->sealed;
+  a.selected = selected;
+  a.counts = counts;
+  a.query = query;
+  a.out = out;
+  a.part = static_cast<float*>(workspace);
+  a.status = status;
+  a.num_pages = kv->num_pages;
+  a.contig_tokens = contig_tokens;
+  a.batch = kv->batch;
+  a.table_stride = kv->table_stride;
+  a.sel_stride = sel_stride;
+  a.select_groups = select_groups;
+  a.query_heads = kv->query_heads;
+  a.kv_heads = kv->kv_heads;
+  a.splits = splits;
+  a.scale = scale;
+  const size_t need =
+      sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(SA_HIP_EINVAL, "attention: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  return check_hip(sa::launch_sparse_decode_attention(a, as_stream(stream)), "attention launch");
+}
+
+int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query, const int32_t* selected,
+                                   const int32_t* counts, int32_t select_groups, int32_t sel_stride,
+                                   float scale, float* out, void* workspace, size_t workspace_bytes,
+                                   int32_t splits, int32_t* status, void* stream) {
+  if (int e = check_geometry(kv, "sparse_decode_attention")) return e;
+  if (!query || !out || !selected || !counts)
+    return fail(SA_HIP_EINVAL, "sparse_decode_attention: null query/out/selected/counts");
+  if (!aligned16(query)) return fail(SA_HIP_EINVAL, "sparse_decode_attention: query must be 16-byte aligned");
+  if (select_groups <= 0 || kv->kv_heads % select_groups != 0)
+    return fail(SA_HIP_EINVAL, "sparse_decode_attention: select_groups must divide kv_heads");
+  if (sel_stride <= 0) return fail(SA_HIP_EINVAL, "sparse_decode_attention: sel_stride must be positive");
+  if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "sparse_decode_attention: splits out of range");
+  return attention_common(kv, query, selected, counts, select_groups, sel_stride, scale, out, workspace,
+                          workspace_bytes, splits, status, stream, 0);
+}
+
+static int32_t contiguous_splits(int64_t tokens, int32_t kv_heads) {
+  const int64_t pages = (tokens + SA_HIP_PAGE_TOKENS - 1) / SA_HIP_PAGE_TOKENS;
+  return sa_hip_attention_default_splits(1, kv_heads, static_cast<int32_t>(std::min<int64_t>(pages, 1 << 30)));
+}
+
+size_t sa_hip_contiguous_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t kv_heads,
+                                         int32_t head_dim) {
+  if (tokens <= 0 || kv_heads <= 0) return 0;
+  return sa_hip_attention_workspace_bytes(1, query_heads, kv_heads, head_dim,
+                                          contiguous_splits(tokens, kv_heads));
+}
+
+int sa_hip_attention_contiguous(const uint16_t* kv, const float* query, int64_t tokens, int32_t query_heads,
+                                int32_t kv_heads, int32_t head_dim, float scale, float* out, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  if (!kv || !query || !out) return fail(SA_HIP_EINVAL, "attention_contiguous: null pointer");
+  if (tokens <= 0) return fail(SA_HIP_EINVAL, "attention_contiguous: tokens must be positive");
+  if (!aligned16(kv) || !aligned16(query))
+    return fail(SA_HIP_EINVAL, "attention_contiguous: kv and query must be 16-byte aligned");
+  sa_paged_kv view{};
+  view.pool = const_cast<uint16_t*>(kv);
+  view.block_table = reinterpret_cast<int32_t*>(1);  // unused in contiguous mode
+  view.seq_len = reinterpret_cast<int32_t*>(1);
+  view.sealed = reinterpret_cast<int32_t*>(1);
+  view.num_pages = (tokens + SA_HIP_PAGE_TOKENS - 1) / SA_HIP_PAGE_TOKENS;
+  view.batch = 1;
+  view.table_stride = 1;
+  view.query_heads = query_heads;
+  view.kv_heads = kv_heads;
+  view.head_dim = head_dim;
+  if (int e = check_geometry(&view, "attention_contiguous")) return e;
+  return attention_common(&view, query, nullptr, nullptr, 1, 1, scale, out, workspace, workspace_bytes,
+                          contiguous_splits(tokens, kv_heads), nullptr, stream, tokens);
+}
+
+int sa_hip_consume_checksum(const float* input, int32_t elements, float* checksum, void* stream) {
+  if (!input || !checksum || elements < 0) return fail(SA_HIP_EINVAL, "consume_checksum: bad arguments");
+  return check_hip(sa::launch_consume_checksum(input, elements, checksum, as_stream(stream)), "consume launch");
+}
+
+// ---- selection ---------------------------------------------------------------
+
+int sa_hip_score_select(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
+                        int32_t* selected, int32_t* counts, float* scores, int32_t* status, void* stream) {
+  if (int e = check_geometry(kv, "score_select")) return e;
+  if (int e = check_reps(kv, "score_select")) return e;
+  if (!params || !query || !selected || !counts)
+    return fail(SA_HIP_EINVAL, "score_select: null params/query/selected/counts");
+  const sa_select_params& s = *params;
+  if (s.select_groups <= 0 || kv->kv_heads % s.select_groups != 0)
+    return fail(SA_HIP_EINVAL, "score_select: select_groups must divide kv_heads");
+  const int heads_per_sel = kv->query_heads / s.select_groups;
+  if (heads_per_sel > sa::kMaxSelectHeads)
+    return fail(SA_HIP_EINVAL, "score_select: %d query heads per selection group exceeds %d", heads_per_sel,
+                sa::kMaxSelectHeads);
+  if (s.budget_blocks <= 0 || s.init_blocks < 0 || s.local_blocks < 0 ||
+      s.init_blocks + s.local_blocks > s.budget_blocks)
+    return fail(SA_HIP_EINVAL, "score_select: invalid representative selection dimensions "
+                               "(budget %d, init %d, local %d)", s.budget_blocks, s.init_blocks, s.local_blocks);
+  if (s.sel_stride < s.budget_blocks)
+    return fail(SA_HIP_EINVAL, "score_select: sel_stride %d < budget %d", s.sel_stride, s.budget_blocks);
+  sa::SelectLaunch l{};
+  l.query = query;
+  l.reps = kv->reps;
+  l.sealed = kv->sealed;
+  l.selected = selected;
+  l.counts = counts;
+  l.scores = scores;
+  l.status = status;
+  l.batch = kv->batch;
+  l.query_heads = kv->query_heads;
+  l.kv_heads = kv->kv_heads;
+  l.rep_heads = kv->rep_heads;
+  l.rep_stride = kv->rep_stride;
+  l.select_groups = s.select_groups;
+  l.budget = s.budget_blocks;
+  l.init_blocks = s.init_blocks;
+  l.local_blocks = s.local_blocks;
+  l.sel_stride = s.sel_stride;
+  return check_hip(sa::launch_score_select(l, as_stream(stream)), "score_select launch");
+}
+
+// ---- append / seal -------------------------------------------------------------
+
+static int lifecycle_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
+                            const uint16_t* v16, int32_t local_tokens, int append, int32_t* status,
+                            void* stream, const char* op) {
+  if (int e = check_geometry(kv, op)) return e;
+  if (int e = check_reps(kv, op)) return e;
+  if (local_tokens < 0) return fail(SA_HIP_EINVAL, "%s: local_tokens must be >= 0", op);
+  if (append) {
+    const void* a = k16 ? static_cast<const void*>(k16) : static_cast<const void*>(k);
+    const void* b = v16 ? static_cast<const void*>(v16) : static_cast<const void*>(v);
+    if (!a || !b) return fail(SA_HIP_EINVAL, "%s: null k/v", op);
+    if (!aligned16(a) || !aligned16(b)) return fail(SA_HIP_EINVAL, "%s: k/v must be 16-byte aligned", op);
+  }
+  sa::LifecycleLaunch l{};
+  l.pool = kv->pool;
+  l.table = kv->block_table;
+  l.seq_len = kv->seq_len;
+  l.sealed = kv->sealed;
+  l.generation = kv->generation;
+  l.reps = kv->reps;
+  l.status = status;
+  l.k = k;
+  l.v = v;
+  l.k16 = k16;
+  l.v16 = v16;
+  l.num_pages = kv->num_pages;
+  l.batch = kv->batch;
+  l.table_stride = kv->table_stride;
+  l.rep_heads = kv->rep_heads;
+  l.rep_stride = kv->rep_stride;
+  l.query_heads = kv->query_heads;
+  l.kv_heads = kv->kv_heads;
+  l.local_tokens = local_tokens;
+  l.append = append;
+  return check_hip(sa::launch_append_seal(l, as_stream(stream)), op);
+}
+
+int sa_hip_append_seal(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
+                       int32_t* status, void* stream) {
+  return lifecycle_common(kv, k, v, nullptr, nullptr, local_tokens, 1, status, stream, "append_seal");
+}
+
+int sa_hip_append_seal_f16(const sa_paged_kv* kv, const uint16_t* k, const uint16_t* v, int32_t local_tokens,
+                           int32_t* status, void* stream) {
+  if (!k || !v) return fail(SA_HIP_EINVAL, "append_seal_f16: null k/v");
+  return lifecycle_common(kv, nullptr, nullptr, k, v, local_tokens, 1, status, stream, "append_seal_f16");
+}
+
+int sa_hip_seal(const sa_paged_kv* kv, int32_t local_tokens, int32_t* status, void* stream) {
+  return lifecycle_common(kv, nullptr, nullptr, nullptr, nullptr, local_tokens, 0, status, stream, "seal");
+}
+
+// ---- gather --------------------------------------------------------------------
+
+int sa_hip_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* pages,
+                        int32_t count, uint16_t* out, int32_t* status, void* stream) {
+  if (!pool || !pages || !out) return fail(SA_HIP_EINVAL, "gather_pages: null pointer");
+  if (page_bytes <= 0 || page_bytes % 16 != 0)
+    return fail(SA_HIP_EINVAL, "gather_pages: page_bytes must be a positive multiple of 16");
+  if (!aligned16(pool) || !aligned16(out)) return fail(SA_HIP_EINVAL, "gather_pages: pool/out must be 16-byte aligned");
+  if (count < 0 || count > 65535) return fail(SA_HIP_EINVAL, "gather_pages: count out of range");
+  return check_hip(sa::launch_gather_pages(pool, page_bytes, num_pages, pages, count, out, status,
+                                           as_stream(stream)),
+                   "gather launch");
+}
+
+// ---- history prediction and correction -------------------------------------
+
+int sa_hip_compare_prediction(const int32_t* predicted, const int32_t* oracle, int32_t n, int32_t* hits,
+                              int32_t* misses, int32_t* replacement_slots, int32_t* miss_count) {
+  if (n < 0 || (n > 0 && (!predicted || !oracle || !misses || !replacement_slots)) || !hits || !miss_count)
+    return fail(SA_HIP_EINVAL, "compare_prediction: bad arguments");
+  int32_t evicted = 0, missing = 0, h = 0;
+  const int32_t* oe = oracle + n;
+  const int32_t* pe = predicted + n;
+  for (int32_t slot = 0; slot < n; ++slot) {
+    if (std::find(oracle, oe, predicted[slot]) != oe) ++h;
+    else replacement_slots[evicted++] = slot;
+  }
+  for (int32_t i = 0; i < n; ++i)
+    if (std::find(predicted, pe, oracle[i]) == pe) misses[missing++] = oracle[i];
+  *hits = h;
+  *miss_count = missing;
+  if (missing != evicted) return fail(SA_HIP_EINVAL, "prediction correction cardinality mismatch");
+  return SA_HIP_OK;
+}
+
+int sa_hip_fill_pages_async(uint16_t* pool, int64_t page_bytes, const int32_t* dst_pages, const void* src_base,
+                            const int64_t* src_blocks, int32_t count, void* copy_stream, void* done_event) {
+  if (count < 0 || (count > 0 && (!pool || !dst_pages || !src_base || !src_blocks)) || page_bytes <= 0)
+    return fail(SA_HIP_EINVAL, "fill_pages_async: bad arguments");
+  auto* dst = reinterpret_cast<uint8_t*>(pool);
+  const auto* src = static_cast<const uint8_t*>(src_base);
+  for (int32_t i = 0; i < count; ++i) {
+    if (dst_pages[i] < 0 || src_blocks[i] < 0)
+      return fail(SA_HIP_EINVAL, "fill_pages_async: negative page/block index at %d", i);
+    if (int e = check_hip(hipMemcpyAsync(dst + static_cast<int64_t>(dst_pages[i]) * page_bytes,
+                                         src + src_blocks[i] * page_bytes, static_cast<size_t>(page_bytes),
+                                         hipMemcpyHostToDevice, as_stream(copy_stream)),
+                          "fill_pages_async: hipMemcpyAsync"))
+      return e;
+  }
+  if (done_event)
+    return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(done_event), as_stream(copy_stream)),
+                     "fill_pages_async: hipEventRecord");
+  return SA_HIP_OK;
+}
+
+int sa_hip_stream_wait_event(void* stream, void* event) {
+  if (!event) return fail(SA_HIP_EINVAL, "stream_wait_event: null event");
+  return check_hip(hipStreamWaitEvent(as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0),
+                   "hipStreamWaitEvent");
+}
+
+// ---- synthetic data --------------------------------------------------------------
+
+int sa_hip_fill_synthetic_f16(uint16_t* dst, int64_t count, uint64_t seed, uint64_t first_index, void* stream) {
+  if (!dst || count < 0) return fail(SA_HIP_EINVAL, "fill_synthetic_f16: bad arguments");
+  return check_hip(sa::launch_fill_synthetic_f16(dst, count, seed, first_index, as_stream(stream)),
+                   "fill_synthetic_f16 launch");
+}
+
+int sa_hip_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed, uint64_t first_index, void* stream) {
+  if (!dst || count < 0) return fail(SA_HIP_EINVAL, "fill_synthetic_f32: bad arguments");
+  return check_hip(sa::launch_fill_synthetic_f32(dst, count, seed, first_index, as_stream(stream)),
+                   "fill_synthetic_f32 launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,229 @@
+// lifecycle.hip — decode-token append, 32-token seal with mean-key
+// representative, page gather, synthetic data and the output consumer
+// (gfx950).
+//
+// Append follows the reference's append_fp16_kv (cpp/src/qwen_layer_main.cpp
+// :270-281): one token's K and V, converted fp32 -> FP16 round-to-nearest-
+// even, written at the token's slot of the token-major page.  The seal
+// follows the tail lifecycle of cpp/src/kv_lifecycle_main.cpp:92-113: while
+// the tail holds at least local_tokens + 32 tokens the oldest tail block is
+// sealed and the generation advances.  With paging, "erase" is only the
+// sealed-count advance: the block stays in its page.  The representative is
+// the mean key of the block (sum of its 32 keys in token order, divided by
+// 32), i.e. the reference's build_local_causal_representatives with window 1
+// and top-k 32 (cpp/src/selection.cpp:12-94), bit-exact.
+#include "sa_device.hpp"
+#include "sa_internal.hpp"
+
+namespace sa {
+namespace {
+
+constexpr int D = kHeadDim;
+constexpr int kThreads = 256;
+
+struct Params {
+  uint16_t* pool;
+  const int32_t* table;
+  int32_t* seq_len;
+  int32_t* sealed;
+  int32_t* generation;
+  float* reps;
+  int32_t* status;
+  const float* k;
+  const float* v;
+  const uint16_t* k16;
+  const uint16_t* v16;
+  int64_t num_pages;
+  int64_t page_elems;
+  int32_t token_elems;
+  int32_t width;          // kv_heads * head_dim
+  int32_t table_stride;
+  int32_t rep_heads;
+  int32_t rep_stride;
+  int32_t group;
+  int32_t local_tokens;
+  int32_t append;
+};
+
+__device__ inline int64_t table_page(const Params& p, int b, int64_t logical) {
+  if (logical < 0 || logical >= p.table_stride) return -1;
+  const int64_t page = p.table[static_cast<int64_t>(b) * p.table_stride + logical];
+  return (page >= 0 && page < p.num_pages) ? page : -1;
+}
+
+__global__ __launch_bounds__(kThreads) void append_seal_kernel(const Params p) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  int64_t len = p.seq_len[b];
+
+  if (p.append) {
+    const int64_t page = table_page(p, b, len / kPageTokens);
+    if (page < 0) {
+      if (tid == 0) flag_status(p.status, kStatusCapacity);
+      return;
+    }
+    uint16_t* dst = p.pool + page * p.page_elems + (len % kPageTokens) * p.token_elems;
+    const int64_t src = static_cast<int64_t>(b) * p.width;
+    // 4 consecutive values per thread and half: 8-byte stores, coalesced.
+    for (int e = tid * 4; e < p.width; e += kThreads * 4) {
+      ushort4 kk, vv;
+      if (p.k16) {
+        kk = *reinterpret_cast<const ushort4*>(p.k16 + src + e);
+        vv = *reinterpret_cast<const ushort4*>(p.v16 + src + e);
+      } else {
+        const float4 kf = *reinterpret_cast<const float4*>(p.k + src + e);
+        const float4 vf = *reinterpret_cast<const float4*>(p.v + src + e);
+        kk = make_ushort4(f2h_rne(kf.x), f2h_rne(kf.y), f2h_rne(kf.z), f2h_rne(kf.w));
+        vv = make_ushort4(f2h_rne(vf.x), f2h_rne(vf.y), f2h_rne(vf.z), f2h_rne(vf.w));
+      }
+      *reinterpret_cast<ushort4*>(dst + e) = kk;
+      *reinterpret_cast<ushort4*>(dst + p.width + e) = vv;
+    }
+    len += 1;
+    // The seal below may read the token just written by other threads.
+    __syncthreads();
+    if (tid == 0) p.seq_len[b] = static_cast<int32_t>(len);
+  }
+
+  int64_t s = p.sealed[b];
+  int added = 0;
+  while (len >= (s + 1) * kPageTokens + p.local_tokens) {
+    const int64_t page = s < p.rep_stride ? table_page(p, b, s) : -1;
+    if (page < 0) {
+      if (tid == 0) flag_status(p.status, kStatusCapacity);
+      break;
+    }
+    const uint16_t* src = p.pool + page * p.page_elems;
+    for (int o = tid; o < p.width; o += kThreads) {  // o = kv_head * D + d
+      float sum = 0.0f;
+#pragma unroll 8
+      for (int t = 0; t < kPageTokens; ++t) sum = sum + h2f(src[t * p.token_elems + o]);
+      const float rep = sum / static_cast<float>(kPageTokens);
+      const int g = o / D;
+      const int d = o % D;
+      // group == 1 for per-KV-head representatives; otherwise every query
+      // head of the group receives the (identical) mean key.
+      for (int j = 0; j < p.group; ++j)
+        p.reps[((static_cast<int64_t>(b) * p.rep_heads + g * p.group + j) * D + d) * p.rep_stride + s] =
+            rep;
+    }
+    ++s;
+    ++added;
+  }
+  if (tid == 0) {
+    p.sealed[b] = static_cast<int32_t>(s);
+    if (p.generation) p.generation[b] += added;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void gather_pages_kernel(const uint4* pool, int64_t page_vecs,
+                                                                int64_t num_pages, const int32_t* pages,
+                                                                uint4* out, int32_t* status) {
+  const int i = blockIdx.y;
+  const int64_t page = pages[i];
+  if (page < 0 || page >= num_pages) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) flag_status(status, kStatusBadPage);
+    return;
+  }
+  const uint4* src = pool + page * page_vecs;
+  uint4* dst = out + static_cast<int64_t>(i) * page_vecs;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; e < page_vecs;
+       e += static_cast<int64_t>(gridDim.x) * kThreads)
+    dst[e] = src[e];
+}
+
+__global__ __launch_bounds__(kThreads) void fill_synthetic_f16_kernel(uint16_t* dst, int64_t count,
+                                                                      uint64_t seed_mixed,
+                                                                      uint64_t first) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    dst[i] = f2h_rne(synth_normal(seed_mixed, first + static_cast<uint64_t>(i)));
+}
+
+__global__ __launch_bounds__(kThreads) void fill_synthetic_f32_kernel(float* dst, int64_t count,
+                                                                      uint64_t seed_mixed,
+                                                                      uint64_t first) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    dst[i] = synth_normal(seed_mixed, first + static_cast<uint64_t>(i));
+}
+
+// C1.4 consumer: a serial weighted checksum, the reference's consume_attention
+// (cpp/src/cuda_backend.cpp:160-168).  One lane, sequential order.
+__global__ void consume_checksum_kernel(const float* input, int32_t elements, float* checksum) {
+  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+  float value = 0.0f;
+  for (int i = 0; i < elements; ++i)
+    value = value + input[i] * (1.0f + static_cast<float>(i % 17) * 0.001f);
+  checksum[0] = value;
+}
+
+int grid_for(int64_t items, int per_block) {
+  const int64_t g = (items + per_block - 1) / per_block;
+  return static_cast<int>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
+}
+
+}  // namespace
+
+hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream) {
+  Params p{};
+  p.pool = l.pool;
+  p.table = l.table;
+  p.seq_len = l.seq_len;
+  p.sealed = l.sealed;
+  p.generation = l.generation;
+  p.reps = l.reps;
+  p.status = l.status;
+  p.k = l.k;
+  p.v = l.v;
+  p.k16 = l.k16;
+  p.v16 = l.v16;
+  p.num_pages = l.num_pages;
+  p.token_elems = 2 * l.kv_heads * D;
+  p.page_elems = static_cast<int64_t>(kPageTokens) * p.token_elems;
+  p.width = l.kv_heads * D;
+  p.table_stride = l.table_stride;
+  p.rep_heads = l.rep_heads;
+  p.rep_stride = l.rep_stride;
+  p.group = l.rep_heads == l.kv_heads ? 1 : l.query_heads / l.kv_heads;
+  p.local_tokens = l.local_tokens;
+  p.append = l.append;
+  hipLaunchKernelGGL(append_seal_kernel, dim3(l.batch), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t num_pages,
+                               const int32_t* pages, int32_t count, uint16_t* out,
+                               int32_t* status, hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  const int64_t vecs = page_bytes / 16;
+  const dim3 grid(grid_for(vecs, kThreads * 4), count);
+  hipLaunchKernelGGL(gather_pages_kernel, grid, dim3(kThreads), 0, stream,
+                     reinterpret_cast<const uint4*>(pool), vecs, num_pages, pages,
+                     reinterpret_cast<uint4*>(out), status);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_synthetic_f16(uint16_t* dst, int64_t count, uint64_t seed,
+                                     uint64_t first_index, hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_synthetic_f16_kernel, dim3(grid_for(count, kThreads * 8)), dim3(kThreads), 0,
+                     stream, dst, count, mix64(seed), first_index);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed, uint64_t first_index,
+                                     hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_synthetic_f32_kernel, dim3(grid_for(count, kThreads * 8)), dim3(kThreads), 0,
+                     stream, dst, count, mix64(seed), first_index);
+  return hipGetLastError();
+}
+
+hipError_t launch_consume_checksum(const float* input, int32_t elements, float* checksum,
+                                   hipStream_t stream) {
+  hipLaunchKernelGGL(consume_checksum_kernel, dim3(1), dim3(64), 0, stream, input, elements, checksum);
+  return hipGetLastError();
+}
+
+}  // namespace sa

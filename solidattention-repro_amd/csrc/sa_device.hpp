@@ -1,0 +1,94 @@
+// sa_device.hpp — device-side helpers shared by the gfx950 kernels of the
+// KV-cache decode hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sa {
+
+// ---- geometry ------------------------------------------------------------
+// A page holds kPageTokens tokens.  A token is [K: Hkv x D][V: Hkv x D] FP16,
+// the reference's token-major K/V-interleaved format (backend.hpp:18-31 of
+// the reference), so a 32-token page at Hkv=8, D=128 is 128 KiB and a block
+// read from the host store lands in a page with one copy.
+constexpr int kPageTokens = 32;
+constexpr int kWave = 64;
+
+// Status bits a kernel ORs into an optional device status word.
+enum StatusBits : int32_t {
+  kStatusBadPage = 1,       // page id outside [0, num_pages)
+  kStatusBadBlock = 2,      // logical block outside the table / sealed range
+  kStatusBadLength = 4,     // seq_len / sealed inconsistent
+  kStatusCapacity = 8,      // representative or table capacity exceeded
+};
+
+__device__ inline void flag_status(int32_t* status, int32_t bits) {
+  if (status) atomicOr(status, bits);
+}
+
+// ---- FP16 ------------------------------------------------------------------
+// v_cvt_f32_f16 is exact for every FP16 input (subnormals included), so it
+// equals the reference's bit-level decode (attention_reference.cpp:30-53).
+__device__ inline float h2f(uint16_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+// v_cvt_f16_f32 under the default MODE (round to nearest even): the
+// reference's device append conversion (cvt.rn.f16.f32,
+// qwen_layer_main.cpp:277-278).
+__device__ inline uint16_t f2h_rne(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// Low / high half of a packed pair as fp32.
+__device__ inline float lo_h2f(uint32_t w) { return h2f(static_cast<uint16_t>(w & 0xffffu)); }
+__device__ inline float hi_h2f(uint32_t w) { return h2f(static_cast<uint16_t>(w >> 16)); }
+
+// ---- cross-lane reductions (DPP, 16-lane rows) --------------------------
+// DPP controls (gfx9): quad_perm, row_half_mirror, row_mirror.
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int Ctrl>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), Ctrl, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
+// After the two quad steps all lanes of a quad hold the same value, so the
+// half-row and row mirrors act as exchanges with the other quad / half.
+__device__ inline float row16_sum(float v) {
+  v += dpp_f<kDppQuadXor1>(v);
+  v += dpp_f<kDppQuadXor2>(v);
+  v += dpp_f<kDppRowHalfMirror>(v);
+  v += dpp_f<kDppRowMirror>(v);
+  return v;
+}
+
+__device__ inline float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+// ---- synthetic data (bit-identical to the host generator) ----------------
+// splitmix64 output function.
+__device__ __host__ inline uint64_t mix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+// Irwin-Hall(4) normal: exact integer sum of four 16-bit uniforms, centred,
+// times 1/sigma in one fp32 multiply.
+__device__ inline float synth_normal(uint64_t seed_mixed, uint64_t index) {
+  const uint64_t h = mix64(seed_mixed ^ index);
+  const int32_t sum = static_cast<int32_t>(h & 0xffffu) + static_cast<int32_t>((h >> 16) & 0xffffu) +
+                      static_cast<int32_t>((h >> 32) & 0xffffu) + static_cast<int32_t>(h >> 48) - 131070;
+  return __fmul_rn(static_cast<float>(sum), 2.6428937e-05f);
+}
+
+}  // namespace sa

@@ -1,0 +1,104 @@
+// sa_internal.hpp — host-side launch interface between the C-ABI layer
+// (capi.hip) and the kernel files.  Not installed; not part of the ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace sa {
+
+constexpr int kHeadDim = 128;      // head_dim the tuned kernels are built for
+constexpr int kPartPad = 4;        // floats before the accumulator in a partial record
+constexpr int kMaxSelectBlocks = 8192;
+constexpr int kMaxSelectHeads = 32;
+
+// Partial-result record of one (sequence, KV head, split, query head):
+// [0] running max (log2 domain), [1] denominator, [kPartPad, kPartPad + D)
+// accumulator.
+constexpr int part_stride(int head_dim) { return head_dim + kPartPad; }
+
+struct AttnLaunch {
+  const uint16_t* pool;
+  const int32_t* table;
+  const int32_t* seq_len;
+  const int32_t* sealed;
+  const int32_t* selected;
+  const int32_t* counts;
+  const float* query;
+  float* out;
+  float* part;
+  int32_t* status;
+  int64_t num_pages;
+  int64_t contig_tokens;   // > 0: contiguous token buffer mode (batch 1, no table)
+  int32_t batch;
+  int32_t table_stride;
+  int32_t sel_stride;
+  int32_t select_groups;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t splits;
+  float scale;
+};
+
+hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t stream);
+
+struct SelectLaunch {
+  const float* query;
+  const float* reps;
+  const int32_t* sealed;
+  int32_t* selected;
+  int32_t* counts;
+  float* scores;
+  int32_t* status;
+  int32_t batch;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t rep_heads;
+  int32_t rep_stride;
+  int32_t select_groups;
+  int32_t budget;
+  int32_t init_blocks;
+  int32_t local_blocks;
+  int32_t sel_stride;
+};
+
+hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream);
+
+struct LifecycleLaunch {
+  uint16_t* pool;
+  const int32_t* table;
+  int32_t* seq_len;
+  int32_t* sealed;
+  int32_t* generation;
+  float* reps;
+  int32_t* status;
+  const float* k;
+  const float* v;
+  const uint16_t* k16;
+  const uint16_t* v16;
+  int64_t num_pages;
+  int32_t batch;
+  int32_t table_stride;
+  int32_t rep_heads;
+  int32_t rep_stride;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t local_tokens;
+  int32_t append;   // 0: seal only
+};
+
+hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream);
+
+hipError_t launch_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t num_pages,
+                               const int32_t* pages, int32_t count, uint16_t* out,
+                               int32_t* status, hipStream_t stream);
+
+hipError_t launch_fill_synthetic_f16(uint16_t* dst, int64_t count, uint64_t seed,
+                                     uint64_t first_index, hipStream_t stream);
+hipError_t launch_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed,
+                                     uint64_t first_index, hipStream_t stream);
+hipError_t launch_consume_checksum(const float* input, int32_t elements, float* checksum,
+                                   hipStream_t stream);
+
+}  // namespace sa

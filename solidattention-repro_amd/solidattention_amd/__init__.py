@@ -1,0 +1,285 @@
+"""Python binding of the MI355X KV-cache decode hot path (libsa_hip.so).
+
+ctypes over the C-ABI of include/sa_hip.h.  Device memory and streams come
+from PyTorch (plumbing only); every computation runs in the HIP library.
+There is no CPU fallback: loading fails loudly when libsa_hip.so is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(LIB_DIR, "libsa_hip.so")
+
+PAGE_TOKENS = 32
+HEAD_DIM = 128
+
+STATUS_BAD_PAGE = 1
+STATUS_BAD_BLOCK = 2
+STATUS_BAD_LENGTH = 4
+STATUS_CAPACITY = 8
+
+
+class SaHipError(RuntimeError):
+    pass
+
+
+class PagedKVStruct(C.Structure):
+    """Mirror of sa_paged_kv (include/sa_hip.h)."""
+    _fields_ = [
+        ("pool", C.c_void_p), ("block_table", C.c_void_p), ("seq_len", C.c_void_p),
+        ("sealed", C.c_void_p), ("generation", C.c_void_p), ("reps", C.c_void_p),
+        ("num_pages", C.c_int64), ("batch", C.c_int32), ("table_stride", C.c_int32),
+        ("rep_heads", C.c_int32), ("rep_stride", C.c_int32), ("query_heads", C.c_int32),
+        ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("reserved", C.c_int32),
+    ]
+
+
+class SelectParamsStruct(C.Structure):
+    """Mirror of sa_select_params (include/sa_hip.h)."""
+    _fields_ = [("select_groups", C.c_int32), ("budget_blocks", C.c_int32),
+                ("init_blocks", C.c_int32), ("local_blocks", C.c_int32),
+                ("sel_stride", C.c_int32)]
+
+
+# name -> (restype, argtypes)
+_P, _I32, _I64, _SZ, _F = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t, C.c_float
+_KV = C.POINTER(PagedKVStruct)
+EXPORTS = {
+    "sa_hip_last_error": (C.c_char_p, []),
+    "sa_hip_abi_version": (C.c_int, []),
+    "sa_hip_device_count": (C.c_int, []),
+    "sa_hip_attention_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
+    "sa_hip_attention_default_splits": (_I32, [_I32, _I32, _I32]),
+    "sa_hip_sparse_decode_attention": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _P, _P]),
+    "sa_hip_contiguous_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
+    "sa_hip_attention_contiguous": (C.c_int, [_P, _P, _I64, _I32, _I32, _I32, _F, _P, _P, _SZ, _P]),
+    "sa_hip_consume_checksum": (C.c_int, [_P, _I32, _P, _P]),
+    "sa_hip_score_select": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _P, _P]),
+    "sa_hip_append_seal": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
+    "sa_hip_append_seal_f16": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
+    "sa_hip_seal": (C.c_int, [_KV, _I32, _P, _P]),
+    "sa_hip_gather_pages": (C.c_int, [_P, _I64, _I64, _P, _I32, _P, _P, _P]),
+    "sa_hip_compare_prediction": (C.c_int, [_P, _P, _I32, _P, _P, _P, _P]),
+    "sa_hip_fill_pages_async": (C.c_int, [_P, _I64, _P, _P, _P, _I32, _P, _P]),
+    "sa_hip_stream_wait_event": (C.c_int, [_P, _P]),
+    "sa_hip_fill_synthetic_f16": (C.c_int, [_P, _I64, C.c_uint64, C.c_uint64, _P]),
+    "sa_hip_fill_synthetic_f32": (C.c_int, [_P, _I64, C.c_uint64, C.c_uint64, _P]),
+}
+
+_lib: C.CDLL | None = None
+
+
+def build() -> None:
+    """Compile libsa_hip.so for gfx950 (hipcc cross-compiles without a GPU)."""
+    subprocess.run(["make", "-s", "-B", "-j8", "-C", LIB_DIR], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise SaHipError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                             "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in EXPORTS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "sa_hip") -> None:
+    if rc != 0:
+        msg = lib().sa_hip_last_error().decode(errors="replace")
+        raise SaHipError(f"{what} failed ({rc}): {msg}")
+
+
+# --------------------------------------------------------------------------
+# torch plumbing helpers (imported lazily so the CPU tests need no GPU)
+# --------------------------------------------------------------------------
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+class PagedKV:
+    """Device-resident paged FP16 KV slot pool of one layer.
+
+    pool         uint16 [num_pages, 32, 2, kv_heads, head_dim]
+    block_table  int32  [batch, table_stride]
+    seq_len      int32  [batch]
+    sealed       int32  [batch]
+    generation   int32  [batch]
+    reps         fp32   [batch, rep_heads, head_dim, rep_stride]
+    """
+
+    def __init__(self, batch, query_heads, kv_heads, table_stride, num_pages=None,
+                 rep_heads=None, rep_stride=None, head_dim=HEAD_DIM, device="cuda", pool=None):
+        import torch
+        self.batch, self.query_heads, self.kv_heads = batch, query_heads, kv_heads
+        self.head_dim = head_dim
+        self.table_stride = table_stride
+        self.num_pages = num_pages if num_pages is not None else batch * table_stride
+        self.rep_heads = rep_heads if rep_heads is not None else kv_heads
+        self.rep_stride = rep_stride if rep_stride is not None else table_stride
+        dev = torch.device(device)
+        if pool is None:
+            pool = torch.zeros((self.num_pages, PAGE_TOKENS, 2, kv_heads, head_dim),
+                               dtype=torch.uint16, device=dev)
+        self.pool = pool
+        self.block_table = torch.zeros((batch, table_stride), dtype=torch.int32, device=dev)
+        self.seq_len = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.sealed = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.generation = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.reps = torch.zeros((batch, self.rep_heads, head_dim, self.rep_stride),
+                                dtype=torch.float32, device=dev)
+
+    def struct(self) -> PagedKVStruct:
+        return PagedKVStruct(
+            self.pool.data_ptr(), self.block_table.data_ptr(), self.seq_len.data_ptr(),
+            self.sealed.data_ptr(), self.generation.data_ptr(), self.reps.data_ptr(),
+            self.num_pages, self.batch, self.table_stride, self.rep_heads, self.rep_stride,
+            self.query_heads, self.kv_heads, self.head_dim, 0)
+
+    @property
+    def page_bytes(self) -> int:
+        return PAGE_TOKENS * 2 * self.kv_heads * self.head_dim * 2
+
+
+def score_select(kv: PagedKV, query, select_groups, budget, init, local, selected=None, counts=None,
+                 scores=None, status=None, sel_stride=None, stream=None):
+    import torch
+    sel_stride = sel_stride or budget
+    dev = query.device
+    if selected is None:
+        selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride)
+    s = kv.struct()
+    check(lib().sa_hip_score_select(C.byref(s), _ptr(query), C.byref(params), _ptr(selected), _ptr(counts),
+                                    _ptr(scores), _ptr(status), _stream(stream)), "score_select")
+    return selected, counts
+
+
+def attention_workspace(kv: PagedKV, splits, device="cuda"):
+    import torch
+    n = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, splits)
+    return torch.empty(max(n // 4, 1), dtype=torch.float32, device=device), n
+
+
+def default_splits(batch, kv_heads, pages_hint):
+    return int(lib().sa_hip_attention_default_splits(batch, kv_heads, pages_hint))
+
+
+def sparse_decode_attention(kv: PagedKV, query, selected, counts, scale, out=None, splits=None,
+                            workspace=None, status=None, stream=None):
+    import torch
+    select_groups, sel_stride = selected.shape[1], selected.shape[2]
+    if splits is None:
+        splits = default_splits(kv.batch, kv.kv_heads, sel_stride + 2)
+    if out is None:
+        out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=query.device)
+    nbytes = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, splits)
+    if workspace is None and nbytes:
+        workspace = torch.empty(nbytes // 4, dtype=torch.float32, device=query.device)
+    s = kv.struct()
+    check(lib().sa_hip_sparse_decode_attention(
+        C.byref(s), _ptr(query), _ptr(selected), _ptr(counts), select_groups, sel_stride, C.c_float(scale),
+        _ptr(out), _ptr(workspace) if nbytes else None, nbytes, splits, _ptr(status), _stream(stream)),
+        "sparse_decode_attention")
+    return out
+
+
+def attention_contiguous(kv16, query, tokens, query_heads, kv_heads, scale, out=None, head_dim=HEAD_DIM,
+                         stream=None):
+    import torch
+    if out is None:
+        out = torch.empty((query_heads, head_dim), dtype=torch.float32, device=query.device)
+    nbytes = lib().sa_hip_contiguous_workspace_bytes(tokens, query_heads, kv_heads, head_dim)
+    ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=query.device)
+    check(lib().sa_hip_attention_contiguous(_ptr(kv16), _ptr(query), tokens, query_heads, kv_heads, head_dim,
+                                            C.c_float(scale), _ptr(out), _ptr(ws), nbytes, _stream(stream)),
+          "attention_contiguous")
+    return out
+
+
+def append_seal(kv: PagedKV, k, v, local_tokens, status=None, stream=None):
+    import torch
+    s = kv.struct()
+    if k.dtype == torch.uint16:
+        check(lib().sa_hip_append_seal_f16(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(status),
+                                           _stream(stream)), "append_seal_f16")
+    else:
+        check(lib().sa_hip_append_seal(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(status),
+                                       _stream(stream)), "append_seal")
+
+
+def seal(kv: PagedKV, local_tokens, status=None, stream=None):
+    s = kv.struct()
+    check(lib().sa_hip_seal(C.byref(s), local_tokens, _ptr(status), _stream(stream)), "seal")
+
+
+def gather_pages(pool, page_bytes, num_pages, pages, out, status=None, stream=None):
+    check(lib().sa_hip_gather_pages(_ptr(pool), page_bytes, num_pages, _ptr(pages), pages.numel(), _ptr(out),
+                                    _ptr(status), _stream(stream)), "gather_pages")
+    return out
+
+
+def consume_checksum(x, out, stream=None):
+    check(lib().sa_hip_consume_checksum(_ptr(x), x.numel(), _ptr(out), _stream(stream)), "consume_checksum")
+    return out
+
+
+def fill_synthetic_f16(t, seed, first_index=0, stream=None):
+    check(lib().sa_hip_fill_synthetic_f16(_ptr(t), t.numel(), seed, first_index, _stream(stream)),
+          "fill_synthetic_f16")
+    return t
+
+
+def fill_synthetic_f32(t, seed, first_index=0, stream=None):
+    check(lib().sa_hip_fill_synthetic_f32(_ptr(t), t.numel(), seed, first_index, _stream(stream)),
+          "fill_synthetic_f32")
+    return t
+
+
+def compare_prediction(predicted, oracle_set):
+    """Host set logic of the reference's compare_prediction."""
+    import numpy as np
+    n = len(predicted)
+    p = np.ascontiguousarray(predicted, np.int32)
+    o = np.ascontiguousarray(oracle_set, np.int32)
+    misses = np.zeros(max(n, 1), np.int32)
+    slots = np.zeros(max(n, 1), np.int32)
+    hits = C.c_int32(0)
+    mc = C.c_int32(0)
+    rc = lib().sa_hip_compare_prediction(p.ctypes.data_as(_P), o.ctypes.data_as(_P), n, C.byref(hits),
+                                         misses.ctypes.data_as(_P), slots.ctypes.data_as(_P), C.byref(mc))
+    check(rc, "compare_prediction")
+    return hits.value, misses[: mc.value].tolist(), slots[: mc.value].tolist()
+
+
+def fill_pages_async(pool, page_bytes, dst_pages, src_base_ptr, src_blocks, copy_stream, done_event=None):
+    import numpy as np
+    d = np.ascontiguousarray(dst_pages, np.int32)
+    s = np.ascontiguousarray(src_blocks, np.int64)
+    ev = None if done_event is None else C.c_void_p(done_event.cuda_event)
+    check(lib().sa_hip_fill_pages_async(_ptr(pool), page_bytes, d.ctypes.data_as(_P), C.c_void_p(src_base_ptr),
+                                        s.ctypes.data_as(_P), len(d), C.c_void_p(copy_stream.cuda_stream), ev),
+          "fill_pages_async")
+
+
+def stream_wait_event(stream, event):
+    check(lib().sa_hip_stream_wait_event(C.c_void_p(stream.cuda_stream), C.c_void_p(event.cuda_event)),
+          "stream_wait_event")

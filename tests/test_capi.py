@@ -1,0 +1,90 @@
+"""The C-ABI library loads without a GPU, exports every entry point that
+include/*.h declares, and its host-only logic works (no compute calls)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def declared_symbols():
+    names = set()
+    for name in os.listdir(INCLUDE):
+        if name.endswith(".h"):
+            text = open(os.path.join(INCLUDE, name)).read()
+            names.update(re.findall(r"\b(sa_hip_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "sa_hip_sparse_decode_attention" in syms and len(syms) >= 15
+
+
+def test_library_exports_every_declared_symbol():
+    import solidattention_amd as sa
+    L = C.CDLL(sa.LIB_PATH)
+    missing = [s for s in declared_symbols() if not hasattr(L, s)]
+    assert not missing, missing
+    # and the binding table covers them
+    assert set(declared_symbols()) <= set(sa.EXPORTS)
+
+
+def test_host_only_queries():
+    import solidattention_amd as sa
+    L = sa.lib()
+    assert L.sa_hip_abi_version() == 1
+    # workspace: batch * kv_heads * splits * group * (head_dim + 4) floats
+    assert L.sa_hip_attention_workspace_bytes(64, 16, 8, 128, 4) == 64 * 8 * 4 * 2 * 132 * 4
+    assert L.sa_hip_attention_workspace_bytes(64, 16, 8, 128, 1) == 0
+    s = L.sa_hip_attention_default_splits(64, 8, 66)
+    assert 1 <= s <= 64
+
+
+def test_compare_prediction_matches_oracle_on_p10(oracle_lib):
+    import solidattention_amd as sa
+    O = oracle_lib
+    history = [O.oracle_blocks(0, layer) for layer in range(28)]
+    misses_total = 0
+    for step in range(16):
+        for layer in range(28):
+            oracle_set = O.oracle_blocks(step, layer)
+            hits, misses, slots = sa.compare_prediction(history[layer], oracle_set)
+            st, ohits, omisses, oslots = O.compare_prediction(history[layer], oracle_set)
+            assert (hits, misses, slots) == (ohits, omisses, oslots)
+            misses_total += len(misses)
+            history[layer] = oracle_set
+    assert misses_total == 346
+
+
+def test_compare_prediction_cardinality_error():
+    import solidattention_amd as sa
+    with pytest.raises(sa.SaHipError, match="cardinality"):
+        sa.compare_prediction([0, 0, 2, 15], [0, 1, 2, 15])
+
+
+def test_invalid_arguments_fail_before_any_launch():
+    """Argument validation returns SA_HIP_EINVAL with a message and launches
+    nothing (safe without a GPU)."""
+    import solidattention_amd as sa
+    L = sa.lib()
+    kv = sa.PagedKVStruct()
+    kv.head_dim = 64
+    rc = L.sa_hip_sparse_decode_attention(C.byref(kv), None, None, None, 1, 1, C.c_float(1.0), None, None, 0, 1,
+                                          None, None)
+    assert rc == -1 and b"head_dim" in L.sa_hip_last_error()
+    kv.head_dim, kv.query_heads, kv.kv_heads = 128, 12, 8
+    rc = L.sa_hip_score_select(C.byref(kv), None, None, None, None, None, None, None)
+    assert rc == -1 and b"GQA" in L.sa_hip_last_error()
+    p = sa.SelectParamsStruct(8, 4, 3, 2, 4)
+    kv.query_heads = 16
+    kv.batch, kv.table_stride, kv.num_pages = 1, 4, 4
+    kv.pool = kv.block_table = kv.seq_len = kv.sealed = kv.reps = 16
+    kv.rep_heads, kv.rep_stride = 8, 4
+    rc = L.sa_hip_score_select(C.byref(kv), C.c_void_p(16), C.byref(p), C.c_void_p(16), C.c_void_p(16), None,
+                               None, None)
+    assert rc == -1 and b"budget" in L.sa_hip_last_error()

@@ -1,0 +1,142 @@
+"""GPU parity: sparse GQA decode attention (libsa_hip.so) against the oracle.
+
+Bar: within 2e-3 absolute or relative of the oracle's fp32 two-pass
+attention (attention_reference, reference cpp/src/attention_reference.cpp
+:55-96) on the same tokens.  Selection ids come from the oracle here so the
+attention kernel is checked on its own."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import assert_close_2e3, device_kv, status_tensor, to_dev
+from paged_case import D, PAGE, make_case
+
+pytestmark = pytest.mark.gpu
+
+SCALE = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+
+
+def run_case(hip, case, select_groups, budget, init, local, splits=None):
+    sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, case.batch, case.hq, case.hkv, D,
+                                    case.rep_heads, case.rep_stride, select_groups, budget, init, local)
+    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, sel, cnt,
+                                      select_groups, case.query, case.batch, case.hq, case.hkv, D, SCALE)
+    kv = device_kv(case)
+    st = status_tensor()
+    out = hip.sparse_decode_attention(kv, to_dev(case.query), to_dev(sel), to_dev(cnt), SCALE, splits=splits,
+                                      status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    return out.cpu().numpy(), expect
+
+
+@pytest.mark.parametrize("group,hkv", [(2, 8), (4, 8), (1, 4), (8, 2)])
+def test_paged_group_shapes(hip, group, hkv):
+    print(f"case: group={group} hkv={hkv}", flush=True)
+    case = make_case(10 + group, 3, group * hkv, hkv, [32 * 40 + 5, 32 * 17, 32 * 64 + 31], planted=3)
+    got, expect = run_case(hip, case, hkv, 12, 1, 2)
+    assert_close_2e3(got, expect)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8, 33])
+def test_split_counts(hip, splits):
+    print(f"case: splits={splits}", flush=True)
+    case = make_case(20, 2, 16, 8, [32 * 70 + 9, 32 * 33 + 1])
+    got, expect = run_case(hip, case, 8, 20, 2, 4, splits=splits)
+    assert_close_2e3(got, expect)
+
+
+@pytest.mark.parametrize("tail", [0, 1, 15, 31])
+def test_tail_lengths(hip, tail):
+    print(f"case: tail={tail}", flush=True)
+    case = make_case(30 + tail, 2, 16, 8, [32 * 12 + tail, 32 * 3 + tail])
+    got, expect = run_case(hip, case, 8, 6, 1, 1)
+    assert_close_2e3(got, expect)
+
+
+def test_local_window_tail_up_to_63(hip):
+    """Seal with local_tokens=32 keeps 32..63 tail tokens (two tail pages)."""
+    case = make_case(40, 3, 16, 8, [32 * 9 + 31, 32 * 9 + 2, 32 * 2], local_tokens=32)
+    got, expect = run_case(hip, case, 8, 4, 1, 1)
+    assert_close_2e3(got, expect)
+
+
+def test_shared_selection_mode(hip):
+    case = make_case(41, 2, 16, 8, [32 * 30, 32 * 18 + 3], rep_heads=16)
+    got, expect = run_case(hip, case, 1, 5, 1, 1)
+    assert_close_2e3(got, expect)
+
+
+def test_tail_only_and_empty(hip):
+    """A sequence with no sealed block attends its tail only; an empty
+    sequence yields zeros."""
+    case = make_case(42, 2, 16, 8, [20, 0])
+    got, expect = run_case(hip, case, 8, 4, 0, 0)
+    assert_close_2e3(got, expect)
+    assert np.all(got[1] == 0)
+
+
+def test_full_budget_equals_dense(hip):
+    case = make_case(43, 2, 16, 8, [32 * 20 + 7, 32 * 11])
+    got, expect = run_case(hip, case, 8, 64, 1, 1)
+    for b in range(2):
+        n = int(case.seq_len[b])
+        pages = [case.pool[case.table[b, i]].reshape(PAGE, -1) for i in range((n + PAGE - 1) // PAGE)]
+        dense = O.attention_reference(np.concatenate(pages)[:n].ravel(), case.query[b], n, 16, 8, D, SCALE)
+        assert_close_2e3(got[b], dense)
+
+
+def test_stress_outliers(hip):
+    """1% of tokens at +-60000 exercise the stable softmax."""
+    case = make_case(44, 2, 16, 8, [32 * 50 + 3, 32 * 40 + 31], outliers=0.01)
+    got, expect = run_case(hip, case, 8, 16, 1, 2)
+    assert np.isfinite(got).all()
+    assert_close_2e3(got, expect)
+
+
+def test_key_channel_outliers(hip):
+    """Qwen3-8B-like post-RoPE key outliers: 4 of 128 channels x8."""
+    case = make_case(45, 2, 32, 8, [32 * 64 + 5, 32 * 70], channel_scale=(4, 8.0))
+    got, expect = run_case(hip, case, 8, 16, 2, 3)
+    assert_close_2e3(got, expect)
+
+
+def test_contiguous_c1_fixture(hip):
+    """C1 fixture (reference attention_main.cpp:131-156): 128 tokens, 16/8/128."""
+    kv, q = O.fixture_c1(128, 16, 8, 128)
+    scale = 0.08838834764831845
+    expect = O.attention_reference(kv, q, 128, 16, 8, 128, scale)
+    out = hip.attention_contiguous(to_dev(kv.view(np.int16)).view(torch.uint16), to_dev(q), 128, 16, 8, scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert_close_2e3(got, expect)
+    # the reference's own C1 acceptance bar (attention_main.cpp:265-270)
+    assert np.abs(got - expect).max() <= 2e-5
+    cos = float((got.ravel().astype(np.float64) @ expect.ravel()) /
+                np.sqrt((got.ravel().astype(np.float64) ** 2).sum() * (expect.ravel().astype(np.float64) ** 2).sum()))
+    assert cos >= 0.999999
+
+
+@pytest.mark.parametrize("tokens", [1, 31, 33, 257, 1000, 4096])
+def test_contiguous_lengths(hip, tokens):
+    rng = np.random.default_rng(tokens)
+    kv = rng.standard_normal(tokens * 2 * 8 * 128).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(16 * 128).astype(np.float32)
+    expect = O.attention_reference(kv, q, tokens, 16, 8, 128, SCALE)
+    out = hip.attention_contiguous(to_dev(kv.view(np.int16)).view(torch.uint16), to_dev(q), tokens, 16, 8, SCALE)
+    torch.cuda.synchronize()
+    assert_close_2e3(out.cpu().numpy(), expect)
+
+
+def test_bad_page_is_flagged_not_read(hip):
+    case = make_case(46, 1, 16, 8, [32 * 8])
+    sel = np.zeros((1, 8, 4), np.int32)
+    sel[0, :, :] = [0, 1, 2, 3]
+    cnt = np.full((1, 8), 4, np.int32)
+    kv = device_kv(case)
+    kv.block_table[0, 2] = case.num_pages + 1000  # out of range: must be skipped
+    st = status_tensor()
+    hip.sparse_decode_attention(kv, to_dev(case.query), to_dev(sel), to_dev(cnt), SCALE, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_BAD_PAGE

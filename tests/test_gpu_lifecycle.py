@@ -1,0 +1,153 @@
+"""GPU parity: decode-token append, seal and mean-key representative
+(bit-exact bytes and fp32 bits against the oracle), page gather, the
+synthetic generator and the copy-stream miss correction."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import device_kv, pool_numpy, status_tensor, to_dev
+from paged_case import D, PAGE, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("local_tokens", [0, 32])
+def test_append_seal_sequence_bit_exact(hip, local_tokens):
+    """70 decode steps over 3 sequences with different starting tails."""
+    case = make_case(200 + local_tokens, 3, 16, 8, [32 * 5 + 30, 32 * 2, 32 * 7 + 13], table_stride=16,
+                     local_tokens=local_tokens)
+    kv = device_kv(case)
+    st = status_tensor()
+    rng = np.random.default_rng(9)
+    for step in range(70):
+        k = (rng.standard_normal((3, 8, D)) * 2).astype(np.float32)
+        v = (rng.standard_normal((3, 8, D)) * 2).astype(np.float32)
+        if step == 3:
+            k[0, 0, :4] = [65519.0, 65520.0, 1e-8, -3e-5]  # overflow / subnormal edges
+        hip.append_seal(kv, to_dev(k), to_dev(v), local_tokens, status=st)
+        O.paged_append(case.pool, PAGE, case.table, case.seq_len, k=k, v=v, batch=3, hkv=8, d=D)
+        O.paged_seal(case.pool, PAGE, case.table, case.seq_len, case.sealed, case.generation, case.reps, 8,
+                     case.rep_stride, 3, 16, 8, D, local_tokens)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    assert np.array_equal(kv.seq_len.cpu().numpy(), case.seq_len)
+    assert np.array_equal(kv.sealed.cpu().numpy(), case.sealed)
+    assert np.array_equal(kv.generation.cpu().numpy(), case.generation)
+    assert np.array_equal(pool_numpy(kv), case.pool)
+    assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
+
+
+def test_append_f16_raw_bits(hip):
+    case = make_case(210, 2, 16, 8, [31, 64 + 5], table_stride=8)
+    kv = device_kv(case)
+    rng = np.random.default_rng(3)
+    k16 = rng.integers(0, 65536, size=(2, 8, D)).astype(np.uint16)
+    k16[(k16 & 0x7C00) == 0x7C00] = 0x3C00  # keep values finite
+    v16 = rng.integers(0, 0x7BFF, size=(2, 8, D)).astype(np.uint16)
+    hip.append_seal(kv, to_dev(k16.view(np.int16)).view(torch.uint16),
+                    to_dev(v16.view(np.int16)).view(torch.uint16), 0)
+    O.paged_append(case.pool, PAGE, case.table, case.seq_len, k16=k16, v16=v16, batch=2, hkv=8, d=D)
+    O.paged_seal(case.pool, PAGE, case.table, case.seq_len, case.sealed, case.generation, case.reps, 8,
+                 case.rep_stride, 2, 16, 8, D, 0)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool_numpy(kv), case.pool)
+    assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
+
+
+def test_seal_after_prefill_per_query_head_reps(hip):
+    """Prefill wrote whole pages; one seal call seals every block and writes
+    the same mean key to each query head of the group."""
+    case = make_case(211, 2, 32, 8, [32 * 40 + 3, 32 * 9], rep_heads=32)
+    kv = device_kv(case)
+    kv.sealed.zero_()
+    kv.generation.zero_()
+    kv.reps.zero_()
+    hip.seal(kv, 0)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv.sealed.cpu().numpy(), case.sealed)
+    assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
+
+
+def test_capacity_is_flagged(hip):
+    case = make_case(212, 1, 16, 8, [32 * 4 - 1], table_stride=4)
+    kv = device_kv(case)
+    st = status_tensor()
+    z = torch.zeros((1, 8, D), dtype=torch.float32, device="cuda")
+    hip.append_seal(kv, z, z, 0, status=st)   # fills the last page
+    hip.append_seal(kv, z, z, 0, status=st)   # no page left: flagged, nothing written
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    assert int(kv.seq_len.item()) == 32 * 4
+
+
+def test_gather_pages_bit_exact(hip):
+    case = make_case(213, 2, 16, 8, [32 * 20, 32 * 10])
+    kv = device_kv(case)
+    pages = case.table[[0, 0, 1, 0], [3, 7, 2, 19]].astype(np.int32)
+    out = torch.zeros((4, case.page_elems), dtype=torch.int16, device="cuda").view(torch.uint16)
+    hip.gather_pages(kv.pool, kv.page_bytes, kv.num_pages, to_dev(pages), out)
+    torch.cuda.synchronize()
+    expect = np.zeros(4 * case.page_elems, np.uint16)
+    O.lib().sao_pack_blocks(case.pool.ctypes.data, case.page_elems, pages.ctypes.data, 4, expect.ctypes.data)
+    assert np.array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16).ravel(), expect)
+
+
+@pytest.mark.parametrize("seed", [0, 77])
+def test_synthetic_generator_matches_oracle(hip, seed):
+    n = 1 << 20
+    t16 = torch.empty(n, dtype=torch.int16, device="cuda").view(torch.uint16)
+    t32 = torch.empty(4096, dtype=torch.float32, device="cuda")
+    hip.fill_synthetic_f16(t16, seed, 12345)
+    hip.fill_synthetic_f32(t32, seed, 999)
+    torch.cuda.synchronize()
+    assert np.array_equal(t16.view(torch.int16).cpu().numpy().view(np.uint16), O.synth_half(seed, 12345, n))
+    assert np.array_equal(t32.cpu().numpy().view(np.uint32), O.synth_float(seed, 999, 4096).view(np.uint32))
+
+
+def test_consume_checksum(hip):
+    x = np.random.default_rng(1).standard_normal(2048).astype(np.float32)
+    out = torch.zeros(1, dtype=torch.float32, device="cuda")
+    hip.consume_checksum(to_dev(x), out)
+    torch.cuda.synchronize()
+    expect = np.float32(0)
+    for i, xi in enumerate(x):
+        expect = np.float32(expect + np.float32(xi * np.float32(np.float32(1.0) + np.float32(i % 17) * np.float32(0.001))))
+    assert out.item() == float(expect)
+
+
+def test_miss_correction_copy_stream(hip):
+    """History prediction + correction (reference pipeline_main.cpp:686-717,
+    305-331): missing blocks are copied from pinned host memory into the
+    evicted slots on a copy stream; the compute stream waits on an event;
+    the resident set equals the selection and the slot bytes equal the store."""
+    rng = np.random.default_rng(4)
+    n_blocks, slots = 64, 16
+    page_elems = 32 * 2 * 8 * 128
+    store = torch.from_numpy(rng.integers(0, 65536, size=(n_blocks, page_elems)).astype(np.uint16).view(np.int16))
+    store = store.pin_memory()
+    pool = torch.zeros((slots, page_elems), dtype=torch.int16, device="cuda")
+    predicted = sorted(rng.choice(n_blocks, size=slots, replace=False).tolist())
+    resident = list(predicted)  # slot i holds block resident[i]
+    pool.copy_(store[predicted].cuda())
+    copy_stream = torch.cuda.Stream()
+    compute = torch.cuda.current_stream()
+    done = torch.cuda.Event()
+    done.record(copy_stream)  # materialise the event
+    misses_total = 0
+    for step in range(6):
+        keep = rng.choice(resident, size=12, replace=False).tolist()
+        fresh = rng.choice([b for b in range(n_blocks) if b not in resident], size=4, replace=False).tolist()
+        oracle_set = sorted(keep + fresh)
+        hits, misses, repl = hip.compare_prediction(resident, oracle_set)
+        st, ohits, omisses, orepl = O.compare_prediction(resident, oracle_set)
+        assert (hits, misses, repl) == (ohits, omisses, orepl)
+        hip.fill_pages_async(pool, page_elems * 2, repl, store.data_ptr(), misses, copy_stream, done)
+        hip.stream_wait_event(compute, done)
+        for slot, blk in zip(repl, misses):
+            resident[slot] = blk
+        misses_total += len(misses)
+        assert sorted(resident) == oracle_set
+        compute.synchronize()
+        assert torch.equal(pool.cpu(), store[resident])
+    assert misses_total == 24

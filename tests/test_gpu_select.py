@@ -1,0 +1,101 @@
+"""GPU parity: scoring + budgeted top-k selection, bit-exact against the
+oracle (which is bit-exact against the reference's select_shared_blocks,
+cpp/src/selection.cpp:96-147): same ids, same fp32 score bits."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import device_kv, status_tensor, to_dev
+from paged_case import D, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_select(hip, case, select_groups, budget, init, local, sel_stride=None):
+    kv = device_kv(case)
+    sel_stride = sel_stride or budget
+    scores = torch.zeros((case.batch, select_groups, case.rep_stride), dtype=torch.float32, device="cuda")
+    st = status_tensor()
+    sel, cnt = hip.score_select(kv, to_dev(case.query), select_groups, budget, init, local, scores=scores,
+                                status=st, sel_stride=sel_stride)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    return sel.cpu().numpy(), cnt.cpu().numpy(), scores.cpu().numpy()
+
+
+def check(hip, case, select_groups, budget, init, local):
+    sel, cnt, sc = gpu_select(hip, case, select_groups, budget, init, local)
+    esel, ecnt, esc = O.paged_score_select(case.query, case.reps, case.sealed, case.batch, case.hq, case.hkv, D,
+                                           case.rep_heads, case.rep_stride, select_groups, budget, init, local,
+                                           want_scores=True)
+    assert np.array_equal(cnt, ecnt)
+    for b in range(case.batch):
+        n = int(case.sealed[b])
+        for g in range(select_groups):
+            assert sel[b, g, : cnt[b, g]].tolist() == esel[b, g, : ecnt[b, g]].tolist(), (b, g)
+            assert np.array_equal(sc[b, g, :n].view(np.uint32), esc[b, g, :n].view(np.uint32)), (b, g)
+
+
+@pytest.mark.parametrize("group,hkv", [(2, 8), (4, 8), (1, 8), (8, 2)])
+def test_group_selection_bit_exact(hip, group, hkv):
+    case = make_case(100 + group, 4, group * hkv, hkv, [32 * 512, 32 * 300 + 17, 32 * 64, 32 * 13], planted=8)
+    check(hip, case, hkv, 64, 4, 8)
+
+
+def test_shared_selection_per_query_head_reps(hip):
+    case = make_case(110, 2, 16, 8, [32 * 200, 32 * 77 + 3], rep_heads=16)
+    check(hip, case, 1, 16, 1, 2)
+
+
+def test_shared_selection_kv_reps(hip):
+    case = make_case(111, 2, 32, 8, [32 * 300, 32 * 1000])
+    check(hip, case, 1, 64, 4, 8)
+
+
+@pytest.mark.parametrize("budget,init,local", [(1, 0, 0), (1, 1, 0), (1, 0, 1), (7, 3, 4), (13, 0, 0), (64, 4, 8)])
+def test_budget_shapes(hip, budget, init, local):
+    case = make_case(120 + budget, 3, 16, 8, [32 * 40, 32 * 9, 32 * 5 + 1])
+    check(hip, case, 8, budget, init, local)
+
+
+def test_init_local_overlap_and_clamp(hip):
+    """init + local overlapping on short sequences; budget >= blocks selects all."""
+    case = make_case(130, 4, 16, 8, [32 * 6, 32 * 3, 32 * 1, 32 * 100])
+    check(hip, case, 8, 5, 2, 3)
+
+
+def test_many_ties(hip):
+    """Quantized representatives make many equal scores: ties must go to the
+    lower block id exactly as the reference's stable sort does."""
+    case = make_case(131, 2, 16, 8, [32 * 400, 32 * 257])
+    rng = np.random.default_rng(5)
+    case.reps[:] = (rng.integers(-1, 2, size=case.reps.shape) * 0.5).astype(np.float32)
+    case.query[:] = (rng.integers(-1, 2, size=case.query.shape) * 0.25).astype(np.float32)
+    check(hip, case, 8, 40, 1, 2)
+    check(hip, case, 1, 40, 1, 2)
+
+
+def test_zero_scores(hip):
+    case = make_case(132, 1, 16, 8, [32 * 50])
+    case.reps[:] = 0.0
+    check(hip, case, 8, 10, 2, 2)
+
+
+def test_long_context_4096_blocks(hip):
+    """Long-context shape: 4096 blocks per sequence, budget 128."""
+    case = make_case(133, 2, 32, 8, [32 * 4096, 32 * 3000 + 5], planted=16)
+    check(hip, case, 8, 128, 4, 8)
+
+
+def test_c21_golden_on_gpu(hip):
+    """C2.1: the GPU selection over the reference's InfLLM representatives
+    (per query head, shared selection, budget 4 = init 1 + local 1 + 2)
+    returns the published ids [0, 8, 13, 15]."""
+    kv16, pq = O.fixture_c2(512, 16, 8, 128)
+    reps, _ = O.local_causal_representatives(pq, kv16, 512, 16, 8, 128, 32, 32, 4)  # [16][16][128]
+    case = make_case(134, 1, 16, 8, [512], rep_heads=16, table_stride=16)
+    case.reps[0, :, :, :16] = reps.transpose(0, 2, 1)
+    case.query[0] = pq.reshape(16, 512, 128)[:, 511, :]
+    sel, cnt, _ = gpu_select(hip, case, 1, 4, 1, 1)
+    assert sel[0, 0, : cnt[0, 0]].tolist() == [0, 8, 13, 15]
