@@ -236,7 +236,7 @@ def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local):
     seq_len = kv.seq_len[seqs].cpu().numpy()
     sealed = kv.sealed[seqs].cpu().numpy()
     used = np.unique(table[:, : int(((seq_len.max() + PAGE - 1) // PAGE))])
-    pool = kv.pool[torch.from_numpy(used).cuda().long()].view(torch.int16).cpu().numpy().view(np.uint16)
+    pool = kv.pool.view(torch.int16)[torch.from_numpy(used).cuda().long()].cpu().numpy().view(np.uint16)
     remap = {int(p): i for i, p in enumerate(used)}
     table_l = np.vectorize(lambda p: remap.get(int(p), 0))(table).astype(np.int32)
     reps = kv.reps[seqs].cpu().numpy()
@@ -271,7 +271,7 @@ def cpu_baseline(np, torch, ly, args, budget, init, local, scale):
     seq_len = kv.seq_len[seqs].cpu().numpy()
     sealed = kv.sealed[seqs].cpu().numpy()
     used = np.unique(table[:, : int(((seq_len.max() + PAGE - 1) // PAGE))])
-    pool = kv.pool[torch.from_numpy(used).cuda().long()].view(torch.int16).cpu().numpy().view(np.uint16)
+    pool = kv.pool.view(torch.int16)[torch.from_numpy(used).cuda().long()].cpu().numpy().view(np.uint16)
     remap = {int(p): i for i, p in enumerate(used)}
     table_l = np.vectorize(lambda p: remap.get(int(p), 0))(table).astype(np.int32)
     reps = kv.reps[seqs].cpu().numpy()

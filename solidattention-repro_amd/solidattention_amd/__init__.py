@@ -136,7 +136,7 @@ class PagedKV:
         dev = torch.device(device)
         if pool is None:
             pool = torch.zeros((self.num_pages, PAGE_TOKENS, 2, kv_heads, head_dim),
-                               dtype=torch.uint16, device=dev)
+                               dtype=torch.int16, device=dev).view(torch.uint16)
         self.pool = pool
         self.block_table = torch.zeros((batch, table_stride), dtype=torch.int32, device=dev)
         self.seq_len = torch.zeros(batch, dtype=torch.int32, device=dev)
