@@ -40,6 +40,7 @@ struct Params {
   const float* query;
   float* out;
   float* part;
+  int32_t* counters;
   int32_t* status;
   int64_t num_pages;
   int64_t contig_tokens;
@@ -214,10 +215,7 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
       }
     }
 
-    float vf[kIters][8];
-#pragma unroll
-    for (int it = 0; it < kIters; ++it) unpack8(vr[it], vf[it]);
-
+    // online softmax update: s becomes the page's probabilities
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float pmax = kNegInf;
@@ -229,20 +227,31 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
       pmax = fmaxf(pmax, shfl_xor_f(pmax, 16));
       pmax = fmaxf(pmax, shfl_xor_f(pmax, 32));
       const float mn = fmaxf(m[h], pmax);
-      if (mn == kNegInf) continue;  // nothing finite seen yet
+      // mn == -inf only if nothing finite was seen: keep the state as is
       const float corr = (m[h] == mn) ? 1.0f : __builtin_amdgcn_exp2f(m[h] - mn);
+      const float base = (mn == kNegInf) ? 0.0f : mn;
       m[h] = mn;
       float lsum = l[h] * corr;
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[h][j] *= corr;
 #pragma unroll
       for (int it = 0; it < kIters; ++it) {
-        const float pe = __builtin_amdgcn_exp2f(s[h][it] - mn);
-        lsum += pe;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(pe, vf[it][j], acc[h][j]);
+        s[h][it] = __builtin_amdgcn_exp2f(s[h][it] - base);
+        lsum += s[h][it];
       }
       l[h] = lsum;
+    }
+
+    // P.V, converting each V half at its use
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float vj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc[h][j] = __builtin_fmaf(s[h][it], vj, acc[h][j]);
+      }
     }
   }
 
@@ -308,43 +317,45 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
       rec[kPartPad + d] = aw;
     }
   }
-}
+  if (p.splits == 1) return;
 
-// Log-sum-exp merge of the split partial results of one (sequence, KV head).
-template <int G>
-__global__ __launch_bounds__(kThreads) void merge_partials_kernel(const Params p) {
-  const int g = blockIdx.x;
-  const int b = blockIdx.y;
-  const float* base =
-      p.part + ((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits) * G * part_stride(D);
+  // ---- the last workgroup of this (sequence, KV head) merges the splits ----
+  // Every thread publishes its partial-record stores at device scope before
+  // the arrival count is taken; the last arriving workgroup acquires them.
+  __threadfence();
+  __syncthreads();
+  __shared__ int s_last;
+  int32_t* counter = p.counters + static_cast<int64_t>(b) * p.kv_heads + g;
+  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1) == p.splits - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const float* base = p.part + ((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits) * G * part_stride(D);
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
     const int h = o / D;
     const int d = o % D;
     float mx = kNegInf;
-    for (int z = 0; z < p.splits; ++z) mx = fmaxf(mx, base[(z * G + h) * part_stride(D)]);
+    for (int zz = 0; zz < p.splits; ++zz) mx = fmaxf(mx, base[(zz * G + h) * part_stride(D)]);
     float lw = 0.0f, aw = 0.0f;
     if (mx != kNegInf) {
-      for (int z = 0; z < p.splits; ++z) {
-        const float* rec = base + (z * G + h) * part_stride(D);
+      for (int zz = 0; zz < p.splits; ++zz) {
+        const float* rec = base + (zz * G + h) * part_stride(D);
         if (rec[0] == kNegInf) continue;
         const float f = __builtin_amdgcn_exp2f(rec[0] - mx);
         lw = __builtin_fmaf(rec[1], f, lw);
         aw = __builtin_fmaf(rec[kPartPad + d], f, aw);
       }
     }
-    p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] =
-        lw > 0.0f ? aw / lw : 0.0f;
+    p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
   }
+  // leave the arrival count at zero for the next launch
+  if (threadIdx.x == 0) atomicExch(counter, 0);
 }
 
 template <int G>
 hipError_t launch_g(const Params& p, int batch, hipStream_t stream) {
   const dim3 grid(p.kv_heads, batch, p.splits);
   hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(kThreads), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.splits == 1) return e;
-  hipLaunchKernelGGL(merge_partials_kernel<G>, dim3(p.kv_heads, batch), dim3(kThreads), 0, stream,
-                     p);
   return hipGetLastError();
 }
 
@@ -361,6 +372,7 @@ hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t strea
   p.query = a.query;
   p.out = a.out;
   p.part = a.part;
+  p.counters = a.counters;
   p.status = a.status;
   p.num_pages = a.num_pages;
   p.contig_tokens = a.contig_tokens;

@@ -18,6 +18,12 @@ constexpr int kMaxSelectHeads = 32;
 // accumulator.
 constexpr int part_stride(int head_dim) { return head_dim + kPartPad; }
 
+// Split workspace: arrival counters (one int32 per (sequence, KV head),
+// padded to 256 B) followed by the partial records.
+inline size_t counter_bytes(int batch, int kv_heads) {
+  return (static_cast<size_t>(batch) * kv_heads * sizeof(int32_t) + 255) / 256 * 256;
+}
+
 struct AttnLaunch {
   const uint16_t* pool;
   const int32_t* table;
@@ -27,7 +33,8 @@ struct AttnLaunch {
   const int32_t* counts;
   const float* query;
   float* out;
-  float* part;
+  float* part;             // split partial records
+  int32_t* counters;       // per (sequence, KV head) arrival counts, zero between launches
   int32_t* status;
   int64_t num_pages;
   int64_t contig_tokens;   // > 0: contiguous token buffer mode (batch 1, no table)

@@ -73,8 +73,9 @@ __device__ inline int block_prefix(bool pred, int* scratch, int* total) {
 }
 
 // GR = query heads of the selection group that share one representative row
-// (the group size when representatives are per KV head, else 1).
-template <int GR>
+// (the group size when representatives are per KV head, else 1).  VEC4: the
+// representative rows are 16-byte aligned with rep_stride % 4 == 0.
+template <int GR, bool VEC4>
 __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) {
   const int sg = blockIdx.x;
   const int b = blockIdx.y;
@@ -107,26 +108,67 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
 
   // ---- scores (sequential fp32, no contraction) ----------------------------
   const float heads_f = static_cast<float>(p.heads_per_sel);
-  for (int blk = tid; blk < n; blk += kThreads) {
-    float score = 0.0f;
-    for (int h0 = 0; h0 < p.heads_per_sel; h0 += GR) {
-      const int h = h_first + h0;
-      const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
-      const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * D * p.rep_stride + blk;
-      float dot[GR];
+  if constexpr (VEC4) {
+    // 4 consecutive blocks per lane: one 16-byte load per d feeds 4 x GR
+    // independent sequential chains.  Lanes past n read padding columns of
+    // the representative rows (rep_stride is a multiple of 4) and discard them.
+    for (int blk0 = tid * 4; blk0 < n; blk0 += kThreads * 4) {
+      float score[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int h0 = 0; h0 < p.heads_per_sel; h0 += GR) {
+        const int h = h_first + h0;
+        const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
+        const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * D * p.rep_stride + blk0;
+        float dot[GR][4];
 #pragma unroll
-      for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
-#pragma unroll 8
-      for (int d = 0; d < D; ++d) {
-        const float rv = r[static_cast<int64_t>(d) * p.rep_stride];
+        for (int j = 0; j < GR; ++j) dot[j][0] = dot[j][1] = dot[j][2] = dot[j][3] = 0.0f;
+#pragma unroll 16
+        for (int d = 0; d < D; ++d) {
+          const float4 rv = *reinterpret_cast<const float4*>(r + static_cast<int64_t>(d) * p.rep_stride);
 #pragma unroll
-        for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[(h0 + j) * D + d] * rv;
+          for (int j = 0; j < GR; ++j) {
+            const float qv = q_s[(h0 + j) * D + d];
+            dot[j][0] = dot[j][0] + qv * rv.x;
+            dot[j][1] = dot[j][1] + qv * rv.y;
+            dot[j][2] = dot[j][2] + qv * rv.z;
+            dot[j][3] = dot[j][3] + qv * rv.w;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < GR; ++j) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) score[c] = score[c] + dot[j][c] / heads_f;
+        }
       }
 #pragma unroll
-      for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
+      for (int c = 0; c < 4; ++c) {
+        if (blk0 + c < n) {
+          keys[blk0 + c] = order_key(score[c]);
+          if (p.scores) p.scores[out_row * p.rep_stride + blk0 + c] = score[c];
+        }
+      }
     }
-    keys[blk] = order_key(score);
-    if (p.scores) p.scores[out_row * p.rep_stride + blk] = score;
+  } else {
+    for (int blk = tid; blk < n; blk += kThreads) {
+      float score = 0.0f;
+      for (int h0 = 0; h0 < p.heads_per_sel; h0 += GR) {
+        const int h = h_first + h0;
+        const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
+        const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * D * p.rep_stride + blk;
+        float dot[GR];
+#pragma unroll
+        for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
+#pragma unroll 8
+        for (int d = 0; d < D; ++d) {
+          const float rv = r[static_cast<int64_t>(d) * p.rep_stride];
+#pragma unroll
+          for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[(h0 + j) * D + d] * rv;
+        }
+#pragma unroll
+        for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
+      }
+      keys[blk] = order_key(score);
+      if (p.scores) p.scores[out_row * p.rep_stride + blk] = score;
+    }
   }
   __syncthreads();
 
@@ -207,6 +249,14 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   (void)lane;
 }
 
+template <int GR>
+void launch_gr(const Params& p, dim3 grid, bool vec4, hipStream_t stream) {
+  if (vec4)
+    hipLaunchKernelGGL((score_select_kernel<GR, true>), grid, dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((score_select_kernel<GR, false>), grid, dim3(kThreads), 0, stream, p);
+}
+
 }  // namespace
 
 hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
@@ -230,11 +280,12 @@ hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
   p.sel_stride = s.sel_stride;
   const dim3 grid(s.select_groups, s.batch);
   const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
+  const bool vec4 = (s.rep_stride % 4 == 0) && ((reinterpret_cast<uintptr_t>(s.reps) & 15u) == 0);
   switch (gr) {
-    case 1: hipLaunchKernelGGL(score_select_kernel<1>, grid, dim3(kThreads), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL(score_select_kernel<2>, grid, dim3(kThreads), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL(score_select_kernel<4>, grid, dim3(kThreads), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL(score_select_kernel<8>, grid, dim3(kThreads), 0, stream, p); break;
+    case 1: launch_gr<1>(p, grid, vec4, stream); break;
+    case 2: launch_gr<2>(p, grid, vec4, stream); break;
+    case 4: launch_gr<4>(p, grid, vec4, stream); break;
+    case 8: launch_gr<8>(p, grid, vec4, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -132,7 +132,8 @@ class PagedKV:
         self.table_stride = table_stride
         self.num_pages = num_pages if num_pages is not None else batch * table_stride
         self.rep_heads = rep_heads if rep_heads is not None else kv_heads
-        self.rep_stride = rep_stride if rep_stride is not None else table_stride
+        # a multiple of 4 lets the scoring kernel load 4 blocks per lane
+        self.rep_stride = rep_stride if rep_stride is not None else (table_stride + 3) // 4 * 4
         dev = torch.device(device)
         if pool is None:
             pool = torch.zeros((self.num_pages, PAGE_TOKENS, 2, kv_heads, head_dim),
@@ -176,7 +177,7 @@ def score_select(kv: PagedKV, query, select_groups, budget, init, local, selecte
 def attention_workspace(kv: PagedKV, splits, device="cuda"):
     import torch
     n = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, splits)
-    return torch.empty(max(n // 4, 1), dtype=torch.float32, device=device), n
+    return torch.zeros(max(n // 4, 1), dtype=torch.float32, device=device), n
 
 
 def default_splits(batch, kv_heads, pages_hint):
@@ -193,7 +194,7 @@ def sparse_decode_attention(kv: PagedKV, query, selected, counts, scale, out=Non
         out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=query.device)
     nbytes = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, splits)
     if workspace is None and nbytes:
-        workspace = torch.empty(nbytes // 4, dtype=torch.float32, device=query.device)
+        workspace = torch.zeros(nbytes // 4, dtype=torch.float32, device=query.device)
     s = kv.struct()
     check(lib().sa_hip_sparse_decode_attention(
         C.byref(s), _ptr(query), _ptr(selected), _ptr(counts), select_groups, sel_stride, C.c_float(scale),
@@ -208,7 +209,7 @@ def attention_contiguous(kv16, query, tokens, query_heads, kv_heads, scale, out=
     if out is None:
         out = torch.empty((query_heads, head_dim), dtype=torch.float32, device=query.device)
     nbytes = lib().sa_hip_contiguous_workspace_bytes(tokens, query_heads, kv_heads, head_dim)
-    ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=query.device)
+    ws = torch.zeros(max(nbytes // 4, 1), dtype=torch.float32, device=query.device)
     check(lib().sa_hip_attention_contiguous(_ptr(kv16), _ptr(query), tokens, query_heads, kv_heads, head_dim,
                                             C.c_float(scale), _ptr(out), _ptr(ws), nbytes, _stream(stream)),
           "attention_contiguous")

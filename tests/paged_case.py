@@ -37,7 +37,7 @@ class PagedCase:
 
 
 def make_case(seed, batch, hq, hkv, lengths, table_stride=None, rep_heads=None, local_tokens=0,
-              spare_pages=3, outliers=0.0, planted=0, channel_scale=None, shared_pool=False):
+              spare_pages=3, outliers=0.0, planted=0, channel_scale=None, rep_stride=None):
     """Random FP16 KV in a randomly permuted page pool; sequences hold
     `lengths` tokens; every block past the local tail is sealed with the
     mean-key representative (computed by the oracle's seal)."""
@@ -73,7 +73,7 @@ def make_case(seed, batch, hq, hkv, lengths, table_stride=None, rep_heads=None, 
                     noise = rng.standard_normal((PAGE, D)).astype(np.float32) * 0.5
                     pool.view(np.float16)[page, :, 0, kvh, :] = (0.5 * qmean[None, :] + noise).astype(np.float16)
     rep_heads = rep_heads or hkv
-    rep_stride = table_stride
+    rep_stride = rep_stride or (table_stride + 3) // 4 * 4
     reps = np.zeros((batch, rep_heads, D, rep_stride), np.float32)
     seq_len = lengths.astype(np.int32).copy()
     sealed = np.zeros(batch, np.int32)

@@ -47,6 +47,28 @@ def test_split_counts(hip, splits):
     assert_close_2e3(got, expect)
 
 
+def test_workspace_reuse_across_launches(hip):
+    """The split arrival counters return to zero: repeated launches on one
+    workspace, with different inputs, all match the oracle."""
+    case = make_case(21, 3, 16, 8, [32 * 30 + 3, 32 * 45, 32 * 9 + 30])
+    sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, 3, 16, 8, D, 8, case.rep_stride, 8, 10,
+                                    1, 2)
+    kv = device_kv(case)
+    splits = 4
+    ws, nbytes = hip.attention_workspace(kv, splits)
+    rng = np.random.default_rng(0)
+    for rep in range(5):
+        q = rng.standard_normal(case.query.shape).astype(np.float32)
+        expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, sel, cnt, 8, q,
+                                          3, 16, 8, D, SCALE)
+        out = hip.sparse_decode_attention(kv, to_dev(q), to_dev(sel), to_dev(cnt), SCALE, splits=splits,
+                                          workspace=ws)
+        torch.cuda.synchronize()
+        assert_close_2e3(out.cpu().numpy(), expect)
+    counters = ws.view(torch.int32)[: 3 * 8].cpu().numpy()
+    assert (counters == 0).all()
+
+
 @pytest.mark.parametrize("tail", [0, 1, 15, 31])
 def test_tail_lengths(hip, tail):
     print(f"case: tail={tail}", flush=True)

@@ -43,6 +43,14 @@ def test_group_selection_bit_exact(hip, group, hkv):
     check(hip, case, hkv, 64, 4, 8)
 
 
+def test_unpadded_rep_stride_scalar_path(hip):
+    """rep_stride not a multiple of 4: the one-block-per-lane scoring path."""
+    case = make_case(109, 3, 16, 8, [32 * 129, 32 * 77 + 3, 32 * 7], table_stride=131, rep_stride=131)
+    assert case.rep_stride % 4 != 0
+    check(hip, case, 8, 32, 2, 4)
+    check(hip, case, 1, 32, 2, 4)
+
+
 def test_shared_selection_per_query_head_reps(hip):
     case = make_case(110, 2, 16, 8, [32 * 200, 32 * 77 + 3], rep_heads=16)
     check(hip, case, 1, 16, 1, 2)
