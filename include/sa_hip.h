@@ -93,10 +93,8 @@ int sa_hip_device_count(void);
 /* ---- R6: sparse GQA decode attention ------------------------------------ */
 
 /* Workspace for sa_hip_sparse_decode_attention with `splits` partial
- * results per (sequence, KV head): arrival counters followed by the partial
- * records.  Zero-fill it once when it is allocated; every launch leaves the
- * counters at zero again.  Launches that share a workspace must not run
- * concurrently. */
+ * results per (sequence, KV head) (0 when splits == 1).  Launches that share
+ * a workspace must not run concurrently. */
 size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads,
                                         int32_t kv_heads, int32_t head_dim,
                                         int32_t splits);

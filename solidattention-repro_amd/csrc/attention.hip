@@ -5,17 +5,20 @@
 // sealed blocks followed by the unsealed tail, for each of the G query heads
 // of g.  Softmax is computed online in the log2 domain and split over
 // `splits` workgroups per (sequence, KV head); partial results are merged
-// with log-sum-exp.  fp32 arithmetic on exact FP16 decodes; the reference's
-// two-pass order is not reproduced (tolerance-checked, not bit-exact).
+// with log-sum-exp by a second, small kernel.  fp32 arithmetic on exact FP16
+// decodes; the reference's two-pass order is not reproduced
+// (tolerance-checked, not bit-exact).
 //
 // Mapping (head_dim 128): one wave64 walks whole 32-token pages.  A 16-byte
 // load per lane covers 4 rows of 256 B (16 lanes per K or V row of one KV
 // head), so a page's K and V tiles for head g are 8 + 8 dwordx4 loads per
 // lane.  Lane (row r, column c) owns dims [8c, 8c+8) of tokens {r, r+4, ...}.
-// q·k partial dots are reduced across the 16 lanes of a row with DPP; the
-// G query heads of the group reuse every K/V register, so KV bytes are read
-// from HBM once per group.  No MFMA: decode attention is a matrix-vector
-// product (about 2 flop per KV byte at G=2).
+// q.k partial dots are reduced across the 16 lanes of a row with DPP; the G
+// query heads of the group reuse every K/V register (v_fma_mix_f32 consumes
+// the FP16 halves directly), so KV bytes are read from HBM once per group.
+// No MFMA: decode attention is a matrix-vector product (about 2 flop per KV
+// byte at G=2).  With PF the next page of a wave is loaded into a second
+// register set while the current one is computed.
 #include "sa_device.hpp"
 #include "sa_internal.hpp"
 
@@ -40,7 +43,6 @@ struct Params {
   const float* query;
   float* out;
   float* part;
-  int32_t* counters;
   int32_t* status;
   int64_t num_pages;
   int64_t contig_tokens;
@@ -68,27 +70,34 @@ __device__ inline void unpack8(const uint4& w, float (&f)[8]) {
 }
 
 // Page `i` of the (sequence, KV head) list: selected sealed blocks first,
-// then the tail pages.  Returns the page index (or -1 to skip) and the
-// number of valid tokens in it.
+// then the tail pages.  valid = number of tokens to read (0 = skip).
 struct PageRef {
   int64_t page;
   int valid;
 };
 
-__device__ inline PageRef resolve_page(const Params& p, int b, int i, int n_sel,
-                                       const int32_t* sel, int sealed_b, int64_t len) {
-  PageRef r{-1, 0};
+struct PageList {
+  const int32_t* sel;
+  int64_t len;
+  int sealed;
+  int n_sel;
+  int total;
+};
+
+__device__ inline PageRef resolve_page(const Params& p, int b, int i, const PageList& L) {
+  PageRef r{0, 0};
+  if (i >= L.total) return r;
   int64_t logical;
-  if (i < n_sel) {
-    logical = sel[i];
-    if (logical < 0 || logical >= sealed_b) {
+  if (i < L.n_sel) {
+    logical = L.sel[i];
+    if (logical < 0 || logical >= L.sealed) {
       flag_status(p.status, kStatusBadBlock);
       return r;
     }
     r.valid = kPageTokens;
   } else {
-    logical = static_cast<int64_t>(sealed_b) + (i - n_sel);
-    const int64_t left = len - logical * kPageTokens;
+    logical = static_cast<int64_t>(L.sealed) + (i - L.n_sel);
+    const int64_t left = L.len - logical * kPageTokens;
     r.valid = left < kPageTokens ? static_cast<int>(left) : kPageTokens;
   }
   if (p.contig_tokens > 0) {
@@ -110,7 +119,90 @@ __device__ inline PageRef resolve_page(const Params& p, int b, int i, int n_sel,
   return r;
 }
 
+// Issue the 16 dwordx4 loads of one page's K and V tiles (head g).  Rows past
+// `valid` are not read (a contiguous buffer may end inside the last page).
+__device__ inline void load_page(const Params& p, const PageRef& pr, int64_t head_off, int64_t v_off,
+                                 int64_t step4, int row, uint4 (&kr)[kIters], uint4 (&vr)[kIters]) {
+  const uint16_t* kbase = p.pool + pr.page * p.page_elems + head_off;
+  if (pr.valid == kPageTokens) {
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
+      vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      if (it * kRows + row < pr.valid) {
+        kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
+        vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
+      } else {
+        kr[it] = make_uint4(0, 0, 0, 0);
+        vr[it] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Online-softmax update of the wave state with one page.
 template <int G>
+__device__ inline void process_page(const uint4 (&kr)[kIters], const uint4 (&vr)[kIters], int valid, int row,
+                                    const float (&qf)[G][8], float (&m)[G], float (&l)[G],
+                                    float (&acc)[G][8]) {
+  // logits (log2 domain) of this lane's 8 tokens for every head
+  float s[G][kIters];
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    float kf[8];
+    unpack8(kr[it], kf);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float a = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a = __builtin_fmaf(qf[h][j], kf[j], a);
+      s[h][it] = row16_sum(a);
+    }
+  }
+  // s becomes the page's probabilities relative to the new running max
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float pmax = kNegInf;
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      if (it * kRows + row >= valid) s[h][it] = kNegInf;
+      pmax = fmaxf(pmax, s[h][it]);
+    }
+    pmax = fmaxf(pmax, shfl_xor_f(pmax, 16));
+    pmax = fmaxf(pmax, shfl_xor_f(pmax, 32));
+    const float mn = fmaxf(m[h], pmax);
+    // mn == -inf only if nothing finite was seen: the state stays empty
+    const float corr = (m[h] == mn) ? 1.0f : __builtin_amdgcn_exp2f(m[h] - mn);
+    const float base = (mn == kNegInf) ? 0.0f : mn;
+    m[h] = mn;
+    float lsum = l[h] * corr;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] *= corr;
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      s[h][it] = __builtin_amdgcn_exp2f(s[h][it] - base);
+      lsum += s[h][it];
+    }
+    l[h] = lsum;
+  }
+  // P.V, each V half converted at its use (v_fma_mix_f32)
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float vj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
+#pragma unroll
+      for (int h = 0; h < G; ++h) acc[h][j] = __builtin_fmaf(s[h][it], vj, acc[h][j]);
+    }
+  }
+}
+
+template <int G, bool PF>
 __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const Params p) {
   const int g = blockIdx.x;
   const int b = blockIdx.y;
@@ -121,29 +213,25 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
   const int col = lane % kLanesPerRow;
 
   // ---- page list of this (sequence, KV head) -------------------------------
-  int64_t len;
-  int sealed_b, n_sel;
-  const int32_t* sel = nullptr;
+  PageList L{nullptr, 0, 0, 0, 0};
   if (p.contig_tokens > 0) {
-    len = p.contig_tokens;
-    sealed_b = 0;
-    n_sel = 0;
+    L.len = p.contig_tokens;
   } else {
-    len = p.seq_len[b];
-    sealed_b = p.sealed[b];
+    L.len = p.seq_len[b];
+    L.sealed = p.sealed[b];
     const int sg = g / p.kv_per_sel;
-    n_sel = p.counts[b * p.select_groups + sg];
-    sel = p.selected + static_cast<int64_t>(b * p.select_groups + sg) * p.sel_stride;
-    if (sealed_b < 0 || len < static_cast<int64_t>(sealed_b) * kPageTokens || n_sel < 0 ||
-        n_sel > p.sel_stride) {
+    L.n_sel = p.counts[b * p.select_groups + sg];
+    L.sel = p.selected + static_cast<int64_t>(b * p.select_groups + sg) * p.sel_stride;
+    if (L.sealed < 0 || L.len < static_cast<int64_t>(L.sealed) * kPageTokens || L.n_sel < 0 ||
+        L.n_sel > p.sel_stride) {
       flag_status(p.status, kStatusBadLength);
-      len = static_cast<int64_t>(sealed_b > 0 ? sealed_b : 0) * kPageTokens;
-      if (n_sel < 0 || n_sel > p.sel_stride) n_sel = 0;
+      if (L.sealed < 0) L.sealed = 0;
+      L.len = static_cast<int64_t>(L.sealed) * kPageTokens;
+      if (L.n_sel < 0 || L.n_sel > p.sel_stride) L.n_sel = 0;
     }
   }
-  const int64_t tail_tokens = len - static_cast<int64_t>(sealed_b) * kPageTokens;
-  const int n_tail = static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
-  const int total = n_sel + n_tail;
+  const int64_t tail_tokens = L.len - static_cast<int64_t>(L.sealed) * kPageTokens;
+  L.total = L.n_sel + static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
 
   // ---- query: dims [8c, 8c+8) of each head of the group, pre-scaled -------
   float qf[G][8];
@@ -174,84 +262,33 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
   const int64_t head_off = static_cast<int64_t>(row) * p.token_elems + g * D + col * 8;
   const int64_t v_off = static_cast<int64_t>(p.kv_heads) * D;
   const int64_t step4 = static_cast<int64_t>(kRows) * p.token_elems;
-  const int waves_total = p.splits * kWavesPerGroup;
+  const int stride = p.splits * kWavesPerGroup;
+  int i = z * kWavesPerGroup + wave;
 
-  for (int i = z * kWavesPerGroup + wave; i < total; i += waves_total) {
-    const PageRef pr = resolve_page(p, b, i, n_sel, sel, sealed_b, len);
-    if (pr.valid <= 0) continue;
-    const uint16_t* kbase = p.pool + pr.page * p.page_elems + head_off;
-    uint4 kr[kIters], vr[kIters];
-    if (pr.valid == kPageTokens) {
-#pragma unroll
-      for (int it = 0; it < kIters; ++it) {
-        kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
-        vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
-      }
-    } else {
-#pragma unroll
-      for (int it = 0; it < kIters; ++it) {
-        if (it * kRows + row < pr.valid) {
-          kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
-          vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
-        } else {
-          kr[it] = make_uint4(0, 0, 0, 0);
-          vr[it] = make_uint4(0, 0, 0, 0);
-        }
-      }
+  if constexpr (PF) {
+    // two register sets, ping-pong: the next page is in flight while the
+    // current one is computed
+    uint4 ka[kIters], va[kIters], kb[kIters], vb[kIters];
+    PageRef pa = resolve_page(p, b, i, L);
+    if (pa.valid > 0) load_page(p, pa, head_off, v_off, step4, row, ka, va);
+    while (i < L.total) {
+      const PageRef pb = resolve_page(p, b, i + stride, L);
+      if (pb.valid > 0) load_page(p, pb, head_off, v_off, step4, row, kb, vb);
+      if (pa.valid > 0) process_page<G>(ka, va, pa.valid, row, qf, m, l, acc);
+      i += stride;
+      if (i >= L.total) break;
+      pa = resolve_page(p, b, i + stride, L);
+      if (pa.valid > 0) load_page(p, pa, head_off, v_off, step4, row, ka, va);
+      if (pb.valid > 0) process_page<G>(kb, vb, pb.valid, row, qf, m, l, acc);
+      i += stride;
     }
-
-    // logits (log2 domain) of this lane's 8 tokens for every head
-    float s[G][kIters];
-#pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      float kf[8];
-      unpack8(kr[it], kf);
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float a = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a = __builtin_fmaf(qf[h][j], kf[j], a);
-        s[h][it] = row16_sum(a);
-      }
-    }
-
-    // online softmax update: s becomes the page's probabilities
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float pmax = kNegInf;
-#pragma unroll
-      for (int it = 0; it < kIters; ++it) {
-        if (it * kRows + row >= pr.valid) s[h][it] = kNegInf;
-        pmax = fmaxf(pmax, s[h][it]);
-      }
-      pmax = fmaxf(pmax, shfl_xor_f(pmax, 16));
-      pmax = fmaxf(pmax, shfl_xor_f(pmax, 32));
-      const float mn = fmaxf(m[h], pmax);
-      // mn == -inf only if nothing finite was seen: keep the state as is
-      const float corr = (m[h] == mn) ? 1.0f : __builtin_amdgcn_exp2f(m[h] - mn);
-      const float base = (mn == kNegInf) ? 0.0f : mn;
-      m[h] = mn;
-      float lsum = l[h] * corr;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[h][j] *= corr;
-#pragma unroll
-      for (int it = 0; it < kIters; ++it) {
-        s[h][it] = __builtin_amdgcn_exp2f(s[h][it] - base);
-        lsum += s[h][it];
-      }
-      l[h] = lsum;
-    }
-
-    // P.V, converting each V half at its use
-#pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float vj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
-#pragma unroll
-        for (int h = 0; h < G; ++h) acc[h][j] = __builtin_fmaf(s[h][it], vj, acc[h][j]);
-      }
+  } else {
+    for (; i < L.total; i += stride) {
+      const PageRef pr = resolve_page(p, b, i, L);
+      if (pr.valid <= 0) continue;
+      uint4 kr[kIters], vr[kIters];
+      load_page(p, pr, head_off, v_off, step4, row, kr, vr);
+      process_page<G>(kr, vr, pr.valid, row, qf, m, l, acc);
     }
   }
 
@@ -317,20 +354,15 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
       rec[kPartPad + d] = aw;
     }
   }
-  if (p.splits == 1) return;
+}
 
-  // ---- the last workgroup of this (sequence, KV head) merges the splits ----
-  // Every thread publishes its partial-record stores at device scope before
-  // the arrival count is taken; the last arriving workgroup acquires them.
-  __threadfence();
-  __syncthreads();
-  __shared__ int s_last;
-  int32_t* counter = p.counters + static_cast<int64_t>(b) * p.kv_heads + g;
-  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1) == p.splits - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float* base = p.part + ((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits) * G * part_stride(D);
+// Log-sum-exp merge of the split partial results of one (sequence, KV head).
+template <int G>
+__global__ __launch_bounds__(kThreads) void merge_partials_kernel(const Params p) {
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const float* base =
+      p.part + ((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits) * G * part_stride(D);
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
     const int h = o / D;
     const int d = o % D;
@@ -348,14 +380,18 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
     }
     p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
   }
-  // leave the arrival count at zero for the next launch
-  if (threadIdx.x == 0) atomicExch(counter, 0);
 }
 
 template <int G>
-hipError_t launch_g(const Params& p, int batch, hipStream_t stream) {
+hipError_t launch_g(const Params& p, int batch, bool prefetch, hipStream_t stream) {
   const dim3 grid(p.kv_heads, batch, p.splits);
-  hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(kThreads), 0, stream, p);
+  if (prefetch)
+    hipLaunchKernelGGL((sparse_decode_attention_kernel<G, true>), grid, dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((sparse_decode_attention_kernel<G, false>), grid, dim3(kThreads), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  hipLaunchKernelGGL(merge_partials_kernel<G>, dim3(p.kv_heads, batch), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -372,7 +408,6 @@ hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t strea
   p.query = a.query;
   p.out = a.out;
   p.part = a.part;
-  p.counters = a.counters;
   p.status = a.status;
   p.num_pages = a.num_pages;
   p.contig_tokens = a.contig_tokens;
@@ -387,11 +422,12 @@ hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t strea
   p.splits = a.splits;
   p.qscale = a.scale * 1.4426950408889634f;
   const int group = a.query_heads / a.kv_heads;
+  const bool prefetch = a.variant == 1;
   switch (group) {
-    case 1: return launch_g<1>(p, a.batch, stream);
-    case 2: return launch_g<2>(p, a.batch, stream);
-    case 4: return launch_g<4>(p, a.batch, stream);
-    case 8: return launch_g<8>(p, a.batch, stream);
+    case 1: return launch_g<1>(p, a.batch, prefetch, stream);
+    case 2: return launch_g<2>(p, a.batch, prefetch, stream);
+    case 4: return launch_g<4>(p, a.batch, prefetch, stream);
+    case 8: return launch_g<8>(p, a.batch, prefetch, stream);
     default: return hipErrorInvalidValue;
   }
 }

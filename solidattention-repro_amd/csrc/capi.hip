@@ -83,8 +83,7 @@ size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads, int3
                                         int32_t head_dim, int32_t splits) {
   if (batch <= 0 || kv_heads <= 0 || query_heads <= 0 || splits <= 1) return 0;
   const size_t group = static_cast<size_t>(query_heads / kv_heads);
-  return sa::counter_bytes(batch, kv_heads) +
-         static_cast<size_t>(batch) * kv_heads * splits * group * sa::part_stride(head_dim) * sizeof(float);
+  return static_cast<size_t>(batch) * kv_heads * splits * group * sa::part_stride(head_dim) * sizeof(float);
 }
 
 int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads, int32_t pages_per_group_hint) {
@@ -110,10 +109,7 @@ static int attention_common(const sa_paged_kv* kv, const float* query, const int
   a.counts = counts;
   a.query = query;
   a.out = out;
-  a.counters = static_cast<int32_t*>(workspace);
-  a.part = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                sa::counter_bytes(kv->batch, kv->kv_heads))
-                     : nullptr;
+  a.part = static_cast<float*>(workspace);
   a.status = status;
   a.num_pages = kv->num_pages;
   a.contig_tokens = contig_tokens;

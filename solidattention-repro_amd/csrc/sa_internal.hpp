@@ -18,11 +18,6 @@ constexpr int kMaxSelectHeads = 32;
 // accumulator.
 constexpr int part_stride(int head_dim) { return head_dim + kPartPad; }
 
-// Split workspace: arrival counters (one int32 per (sequence, KV head),
-// padded to 256 B) followed by the partial records.
-inline size_t counter_bytes(int batch, int kv_heads) {
-  return (static_cast<size_t>(batch) * kv_heads * sizeof(int32_t) + 255) / 256 * 256;
-}
 
 struct AttnLaunch {
   const uint16_t* pool;
@@ -34,7 +29,6 @@ struct AttnLaunch {
   const float* query;
   float* out;
   float* part;             // split partial records
-  int32_t* counters;       // per (sequence, KV head) arrival counts, zero between launches
   int32_t* status;
   int64_t num_pages;
   int64_t contig_tokens;   // > 0: contiguous token buffer mode (batch 1, no table)
@@ -45,6 +39,7 @@ struct AttnLaunch {
   int32_t query_heads;
   int32_t kv_heads;
   int32_t splits;
+  int32_t variant;         // 0: one page in flight per wave, 1: next page prefetched
   float scale;
 };
 

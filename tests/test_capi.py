@@ -38,8 +38,8 @@ def test_host_only_queries():
     import solidattention_amd as sa
     L = sa.lib()
     assert L.sa_hip_abi_version() == 1
-    # workspace: arrival counters (256 B aligned) + batch * kv_heads * splits * group * (head_dim + 4) floats
-    assert L.sa_hip_attention_workspace_bytes(64, 16, 8, 128, 4) == 2048 + 64 * 8 * 4 * 2 * 132 * 4
+    # workspace: batch * kv_heads * splits * group * (head_dim + 4) floats
+    assert L.sa_hip_attention_workspace_bytes(64, 16, 8, 128, 4) == 64 * 8 * 4 * 2 * 132 * 4
     assert L.sa_hip_attention_workspace_bytes(64, 16, 8, 128, 1) == 0
     s = L.sa_hip_attention_default_splits(64, 8, 66)
     assert 1 <= s <= 64

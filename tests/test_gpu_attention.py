@@ -48,8 +48,8 @@ def test_split_counts(hip, splits):
 
 
 def test_workspace_reuse_across_launches(hip):
-    """The split arrival counters return to zero: repeated launches on one
-    workspace, with different inputs, all match the oracle."""
+    """Repeated launches on one workspace, with different inputs, all match
+    the oracle."""
     case = make_case(21, 3, 16, 8, [32 * 30 + 3, 32 * 45, 32 * 9 + 30])
     sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, 3, 16, 8, D, 8, case.rep_stride, 8, 10,
                                     1, 2)
@@ -65,8 +65,6 @@ def test_workspace_reuse_across_launches(hip):
                                           workspace=ws)
         torch.cuda.synchronize()
         assert_close_2e3(out.cpu().numpy(), expect)
-    counters = ws.view(torch.int32)[: 3 * 8].cpu().numpy()
-    assert (counters == 0).all()
 
 
 @pytest.mark.parametrize("tail", [0, 1, 15, 31])
