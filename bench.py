@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=0, help="sequences in the CPU sample (0 = auto)")
     ap.add_argument("--check-seqs", type=int, default=2, help="sequences parity-checked against the oracle")
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches only (no HIP graph replay)")
     return ap.parse_args()
 
 
@@ -115,7 +116,10 @@ def main():
     if args.layers:
         cfg[0] = args.layers
     layers, batch, hq, hkv, ctx, budget, init, local, planted, model = cfg
-    total_steps = args.warmup + args.steps
+    graph = not args.no_graph
+    # eager timed steps, then (graph mode) one capture-warmup step and the
+    # graph-replayed timed steps; every step appends one token per layer
+    total_steps = args.warmup + args.steps + ((args.steps + 1) if graph else 0)
     torch.cuda.set_device(0)
     log(f"setup {args.config}: layers={layers} batch={batch} ctx={ctx} budget={budget}")
     t0 = time.time()
@@ -152,19 +156,42 @@ def main():
     torch.cuda.synchronize()
     log("warmup done")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    eager_first = args.warmup
     start.record(stream)
-    for s in range(args.warmup, total_steps):
+    for s in range(eager_first, eager_first + args.steps):
         step(s, record=True)
     end.record(stream)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
+    eager_ms = start.elapsed_time(end)
+    last_step = eager_first + args.steps - 1
+    graph_ms = None
+    if graph:
+        # one HIP graph per decode step (28 layers x append/select/attention
+        # launches); capture records, it does not execute
+        first = eager_first + args.steps
+        graphs = []
+        for s in range(first, first + args.steps + 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step(s, record=False)
+            graphs.append(g)
+        graphs[0].replay()  # warm replay (step `first`)
+        torch.cuda.synchronize()
+        gstream = torch.cuda.current_stream()
+        start.record(gstream)
+        for g in graphs[1:]:
+            g.replay()
+        end.record(gstream)
+        torch.cuda.synchronize()
+        graph_ms = start.elapsed_time(end)
+        last_step = first + args.steps
     if int(status.item()) != 0:
         raise SystemExit(f"device status flagged {int(status.item())}")
+    total_ms = graph_ms if graph else eager_ms
     ms_per_step = total_ms / args.steps
     us_per_layer = ms_per_step * 1000.0 / layers
     app, sel, att = [], [], []
-    for s in range(args.warmup, total_steps):
+    for s in range(eager_first, eager_first + args.steps):
         for l in range(layers):
             e = ev[s * layers + l]
             app.append(e[0].elapsed_time(e[1]))
@@ -189,7 +216,7 @@ def main():
     log(f"attention {att_us:.2f} us ({achieved:.0f} GB/s), select {sel_us:.2f} us, append {app_us:.2f} us, "
         f"layer {us_per_layer:.2f} us")
 
-    parity = check_parity(sa, np, torch, L[-1], args, scale, hkv, budget, init, local)
+    parity = check_parity(sa, np, torch, L[-1], args, scale, hkv, budget, init, local, last_step)
     cpu = None if args.no_cpu_baseline else cpu_baseline(np, torch, L[0], args, budget, init, local, scale)
 
     line = {
@@ -210,6 +237,8 @@ def main():
                    "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
                    "init_blocks": init, "local_blocks": local, "page_tokens": PAGE, "splits": splits},
         "tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
+        "launch": "hip graph per decode step" if graph else "eager",
+        "eager_us_per_layer": round(eager_ms * 1000.0 / args.steps / layers, 3),
         "achieved_layer_hbm_gbps": round(layer_gbps, 1),
         "kernels_us": {"attention": round(att_us, 3), "score_select": round(sel_us, 3),
                        "append_seal": round(app_us, 3)},
@@ -222,7 +251,7 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local):
+def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local, s):
     """Full-size spot check: for a few sequences of the last layer, the selection
     (bit-exact) and attention (2e-3) against the oracle on the device bytes."""
     import oracle as O
@@ -230,7 +259,6 @@ def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local):
     if n <= 0:
         return None
     kv = ly.kv
-    s = args.warmup + args.steps - 1
     seqs = list(range(n))
     table = kv.block_table[seqs].cpu().numpy()
     seq_len = kv.seq_len[seqs].cpu().numpy()

@@ -17,8 +17,11 @@
 // query heads of the group reuse every K/V register (v_fma_mix_f32 consumes
 // the FP16 halves directly), so KV bytes are read from HBM once per group.
 // No MFMA: decode attention is a matrix-vector product (about 2 flop per KV
-// byte at G=2).  With PF the next page of a wave is loaded into a second
-// register set while the current one is computed.
+// byte at G=2).  Measured on MI355X at B=64/16K, one workgroup per
+// (sequence, KV head) with 4 waves of ~16 pages each streams the selected
+// pages at ~5.3 TB/s; the same access pattern with no arithmetic reads at
+// ~5.8 TB/s and a plain contiguous read at ~6.3 TB/s, so latency is hidden
+// by the 8-10 waves per CU and a register-prefetch variant did not help.
 #include "sa_device.hpp"
 #include "sa_internal.hpp"
 
@@ -202,7 +205,7 @@ __device__ inline void process_page(const uint4 (&kr)[kIters], const uint4 (&vr)
   }
 }
 
-template <int G, bool PF>
+template <int G>
 __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const Params p) {
   const int g = blockIdx.x;
   const int b = blockIdx.y;
@@ -265,24 +268,7 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
   const int stride = p.splits * kWavesPerGroup;
   int i = z * kWavesPerGroup + wave;
 
-  if constexpr (PF) {
-    // two register sets, ping-pong: the next page is in flight while the
-    // current one is computed
-    uint4 ka[kIters], va[kIters], kb[kIters], vb[kIters];
-    PageRef pa = resolve_page(p, b, i, L);
-    if (pa.valid > 0) load_page(p, pa, head_off, v_off, step4, row, ka, va);
-    while (i < L.total) {
-      const PageRef pb = resolve_page(p, b, i + stride, L);
-      if (pb.valid > 0) load_page(p, pb, head_off, v_off, step4, row, kb, vb);
-      if (pa.valid > 0) process_page<G>(ka, va, pa.valid, row, qf, m, l, acc);
-      i += stride;
-      if (i >= L.total) break;
-      pa = resolve_page(p, b, i + stride, L);
-      if (pa.valid > 0) load_page(p, pa, head_off, v_off, step4, row, ka, va);
-      if (pb.valid > 0) process_page<G>(kb, vb, pb.valid, row, qf, m, l, acc);
-      i += stride;
-    }
-  } else {
+  {
     for (; i < L.total; i += stride) {
       const PageRef pr = resolve_page(p, b, i, L);
       if (pr.valid <= 0) continue;
@@ -383,12 +369,9 @@ __global__ __launch_bounds__(kThreads) void merge_partials_kernel(const Params p
 }
 
 template <int G>
-hipError_t launch_g(const Params& p, int batch, bool prefetch, hipStream_t stream) {
+hipError_t launch_g(const Params& p, int batch, hipStream_t stream) {
   const dim3 grid(p.kv_heads, batch, p.splits);
-  if (prefetch)
-    hipLaunchKernelGGL((sparse_decode_attention_kernel<G, true>), grid, dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL((sparse_decode_attention_kernel<G, false>), grid, dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(kThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   hipLaunchKernelGGL(merge_partials_kernel<G>, dim3(p.kv_heads, batch), dim3(kThreads), 0, stream, p);
@@ -422,12 +405,11 @@ hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t strea
   p.splits = a.splits;
   p.qscale = a.scale * 1.4426950408889634f;
   const int group = a.query_heads / a.kv_heads;
-  const bool prefetch = a.variant == 1;
   switch (group) {
-    case 1: return launch_g<1>(p, a.batch, prefetch, stream);
-    case 2: return launch_g<2>(p, a.batch, prefetch, stream);
-    case 4: return launch_g<4>(p, a.batch, prefetch, stream);
-    case 8: return launch_g<8>(p, a.batch, prefetch, stream);
+    case 1: return launch_g<1>(p, a.batch, stream);
+    case 2: return launch_g<2>(p, a.batch, stream);
+    case 4: return launch_g<4>(p, a.batch, stream);
+    case 8: return launch_g<8>(p, a.batch, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -39,7 +39,6 @@ struct AttnLaunch {
   int32_t query_heads;
   int32_t kv_heads;
   int32_t splits;
-  int32_t variant;         // 0: one page in flight per wave, 1: next page prefetched
   float scale;
 };
 

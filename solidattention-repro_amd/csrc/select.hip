@@ -5,7 +5,8 @@
 // Scoring: one lane per block.  Representatives are stored head_dim-major
 // ([rep head][d][block]), so for a fixed d the lanes of a wave read 64
 // consecutive floats (coalesced) while each lane keeps the reference's
-// sequential per-(head, block) dot order.  This file is compiled with
+// sequential per-(head, block) dot order.  The workgroup is 8 waves, so
+// 512 blocks (a 16K-token sequence) are scored in one pass.  This file is compiled with
 // -ffp-contract=off: every product and sum is rounded separately, as in the
 // g++-built reference (which contains no FMA).
 //
@@ -22,7 +23,7 @@ namespace sa {
 namespace {
 
 constexpr int D = kHeadDim;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 
 struct Params {
@@ -73,9 +74,8 @@ __device__ inline int block_prefix(bool pred, int* scratch, int* total) {
 }
 
 // GR = query heads of the selection group that share one representative row
-// (the group size when representatives are per KV head, else 1).  VEC4: the
-// representative rows are 16-byte aligned with rep_stride % 4 == 0.
-template <int GR, bool VEC4>
+// (the group size when representatives are per KV head, else 1).
+template <int GR>
 __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) {
   const int sg = blockIdx.x;
   const int b = blockIdx.y;
@@ -107,68 +107,36 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   __syncthreads();
 
   // ---- scores (sequential fp32, no contraction) ----------------------------
+  // One block per lane.  The 128 representative values of a block are loaded
+  // in two batches of 64 independent loads before the sequential chains run,
+  // so the latency of the HBM reads is paid twice per block, not per d.
   const float heads_f = static_cast<float>(p.heads_per_sel);
-  if constexpr (VEC4) {
-    // 4 consecutive blocks per lane: one 16-byte load per d feeds 4 x GR
-    // independent sequential chains.  Lanes past n read padding columns of
-    // the representative rows (rep_stride is a multiple of 4) and discard them.
-    for (int blk0 = tid * 4; blk0 < n; blk0 += kThreads * 4) {
-      float score[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int h0 = 0; h0 < p.heads_per_sel; h0 += GR) {
-        const int h = h_first + h0;
-        const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
-        const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * D * p.rep_stride + blk0;
-        float dot[GR][4];
+  constexpr int kBatch = 64;
+  for (int blk = tid; blk < n; blk += kThreads) {
+    float score = 0.0f;
+    for (int h0 = 0; h0 < p.heads_per_sel; h0 += GR) {
+      const int h = h_first + h0;
+      const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
+      const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * D * p.rep_stride + blk;
+      float dot[GR];
 #pragma unroll
-        for (int j = 0; j < GR; ++j) dot[j][0] = dot[j][1] = dot[j][2] = dot[j][3] = 0.0f;
-#pragma unroll 16
-        for (int d = 0; d < D; ++d) {
-          const float4 rv = *reinterpret_cast<const float4*>(r + static_cast<int64_t>(d) * p.rep_stride);
+      for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
 #pragma unroll
-          for (int j = 0; j < GR; ++j) {
-            const float qv = q_s[(h0 + j) * D + d];
-            dot[j][0] = dot[j][0] + qv * rv.x;
-            dot[j][1] = dot[j][1] + qv * rv.y;
-            dot[j][2] = dot[j][2] + qv * rv.z;
-            dot[j][3] = dot[j][3] + qv * rv.w;
-          }
-        }
+      for (int d0 = 0; d0 < D; d0 += kBatch) {
+        float rv[kBatch];
 #pragma unroll
-        for (int j = 0; j < GR; ++j) {
+        for (int k = 0; k < kBatch; ++k) rv[k] = r[static_cast<int64_t>(d0 + k) * p.rep_stride];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) score[c] = score[c] + dot[j][c] / heads_f;
+        for (int k = 0; k < kBatch; ++k) {
+#pragma unroll
+          for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[(h0 + j) * D + d0 + k] * rv[k];
         }
       }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (blk0 + c < n) {
-          keys[blk0 + c] = order_key(score[c]);
-          if (p.scores) p.scores[out_row * p.rep_stride + blk0 + c] = score[c];
-        }
-      }
+      for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
     }
-  } else {
-    for (int blk = tid; blk < n; blk += kThreads) {
-      float score = 0.0f;
-      for (int h0 = 0; h0 < p.heads_per_sel; h0 += GR) {
-        const int h = h_first + h0;
-        const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
-        const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * D * p.rep_stride + blk;
-        float dot[GR];
-#pragma unroll
-        for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
-#pragma unroll 8
-        for (int d = 0; d < D; ++d) {
-          const float rv = r[static_cast<int64_t>(d) * p.rep_stride];
-#pragma unroll
-          for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[(h0 + j) * D + d] * rv;
-        }
-#pragma unroll
-        for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
-      }
-      keys[blk] = order_key(score);
-      if (p.scores) p.scores[out_row * p.rep_stride + blk] = score;
-    }
+    keys[blk] = order_key(score);
+    if (p.scores) p.scores[out_row * p.rep_stride + blk] = score;
   }
   __syncthreads();
 
@@ -250,11 +218,8 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
 }
 
 template <int GR>
-void launch_gr(const Params& p, dim3 grid, bool vec4, hipStream_t stream) {
-  if (vec4)
-    hipLaunchKernelGGL((score_select_kernel<GR, true>), grid, dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL((score_select_kernel<GR, false>), grid, dim3(kThreads), 0, stream, p);
+void launch_gr(const Params& p, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL(score_select_kernel<GR>, grid, dim3(kThreads), 0, stream, p);
 }
 
 }  // namespace
@@ -280,12 +245,11 @@ hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
   p.sel_stride = s.sel_stride;
   const dim3 grid(s.select_groups, s.batch);
   const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
-  const bool vec4 = (s.rep_stride % 4 == 0) && ((reinterpret_cast<uintptr_t>(s.reps) & 15u) == 0);
   switch (gr) {
-    case 1: launch_gr<1>(p, grid, vec4, stream); break;
-    case 2: launch_gr<2>(p, grid, vec4, stream); break;
-    case 4: launch_gr<4>(p, grid, vec4, stream); break;
-    case 8: launch_gr<8>(p, grid, vec4, stream); break;
+    case 1: launch_gr<1>(p, grid, stream); break;
+    case 2: launch_gr<2>(p, grid, stream); break;
+    case 4: launch_gr<4>(p, grid, stream); break;
+    case 8: launch_gr<8>(p, grid, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
