@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--cpu-sample-seqs", type=int, default=0, help="sequences in the CPU sample (0 = auto)")
     ap.add_argument("--check-seqs", type=int, default=2, help="sequences parity-checked against the oracle")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (no HIP graph replay)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
+                    help="also run one plain page copy of PAGES pages (HBM counter calibration)")
     return ap.parse_args()
 
 
@@ -151,6 +153,15 @@ def main():
                                        workspace=workspace, status=status)
             if e: e[3].record(stream)
 
+    if args.calibrate_copy:
+        # a plain copy of known size: PAGES x 128 KiB read and written once
+        n = args.calibrate_copy
+        src_pages = torch.arange(n, dtype=torch.int32, device="cuda")
+        dst = torch.empty((n, L[0].kv.page_bytes // 2), dtype=torch.int16, device="cuda").view(torch.uint16)
+        sa.gather_pages(L[0].kv.pool, L[0].kv.page_bytes, L[0].kv.num_pages, src_pages, dst)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {n * L[0].kv.page_bytes} bytes read and written by gather_pages_kernel")
+        del dst
     for s in range(args.warmup):
         step(s, record=False)
     torch.cuda.synchronize()
