@@ -1,0 +1,256 @@
+// hip_kv.hpp — C++ API of the MI355X KV-cache decode hot path, over the
+// C-ABI of sa_hip.h (header-only; link libsa_hip.so).
+//
+// New next to the reference's contract (the reference has no paged pool, no
+// GPU selection, no GPU seal and no device gather; README.md:68-70 of the
+// reference).  The semantics it carries are the reference's:
+//   PagedKvPool::append_seal   decode append + seal (qwen_layer_main.cpp
+//                              :270-281, kv_lifecycle_main.cpp:31-45,92-113)
+//   SparseDecoder::select      select_shared_blocks per selection group
+//                              (selection.hpp:24-29, selection.cpp:96-147)
+//   SparseDecoder::attend      attention_reference over the selected blocks
+//                              and the tail (attention_reference.cpp:55-96)
+//   MissCorrector              CudaPipeline::correct_and_wait without the
+//                              host barrier (pipeline_main.cpp:305-331)
+//   compare_prediction         pipeline_main.cpp:686-717
+// Errors are std::runtime_error("operation: message"), as the reference's
+// cuda_check does (cuda_backend.cpp:16-21).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "sa_hip.h"
+
+namespace solidattention::hip {
+
+inline void check(int rc, const char* operation) {
+  if (rc != SA_HIP_OK) throw std::runtime_error(std::string(operation) + ": " + sa_hip_last_error());
+}
+
+inline void hip_check(hipError_t e, const char* operation) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(operation) + ": " + hipGetErrorString(e));
+}
+
+// Owning device allocation (zero-filled).
+template <class T>
+class DeviceArray {
+ public:
+  DeviceArray() = default;
+  explicit DeviceArray(std::size_t n) : n_(n) {
+    if (n_) {
+      hip_check(hipMalloc(reinterpret_cast<void**>(&p_), n_ * sizeof(T)), "hipMalloc");
+      hip_check(hipMemset(p_, 0, n_ * sizeof(T)), "hipMemset");
+    }
+  }
+  ~DeviceArray() {
+    if (p_) (void)hipFree(p_);
+  }
+  DeviceArray(const DeviceArray&) = delete;
+  DeviceArray& operator=(const DeviceArray&) = delete;
+  DeviceArray(DeviceArray&& o) noexcept : p_(std::exchange(o.p_, nullptr)), n_(std::exchange(o.n_, 0)) {}
+  DeviceArray& operator=(DeviceArray&& o) noexcept {
+    if (this != &o) {
+      if (p_) (void)hipFree(p_);
+      p_ = std::exchange(o.p_, nullptr);
+      n_ = std::exchange(o.n_, 0);
+    }
+    return *this;
+  }
+  T* get() const { return p_; }
+  std::size_t size() const { return n_; }
+  void upload(const std::vector<T>& v) {
+    if (v.size() > n_) throw std::runtime_error("upload: host vector larger than device array");
+    hip_check(hipMemcpy(p_, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D");
+  }
+  std::vector<T> download() const {
+    std::vector<T> v(n_);
+    if (n_) hip_check(hipMemcpy(v.data(), p_, n_ * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return v;
+  }
+
+ private:
+  T* p_{};
+  std::size_t n_{};
+};
+
+// One layer's paged FP16 KV slot pool in HBM with its block tables,
+// lengths and block representatives.
+class PagedKvPool {
+ public:
+  PagedKvPool(std::size_t batch, std::size_t query_heads, std::size_t kv_heads, std::size_t table_stride,
+              std::size_t num_pages, std::size_t rep_heads = 0, std::size_t rep_stride = 0,
+              std::size_t head_dim = 128)
+      : batch_(batch), query_heads_(query_heads), kv_heads_(kv_heads), head_dim_(head_dim),
+        table_stride_(table_stride), num_pages_(num_pages), rep_heads_(rep_heads ? rep_heads : kv_heads),
+        rep_stride_(rep_stride ? rep_stride : (table_stride + 3) / 4 * 4),
+        pool_(num_pages * page_elems()), table_(batch * table_stride), seq_len_(batch), sealed_(batch),
+        generation_(batch), reps_(batch * rep_heads_ * head_dim * rep_stride_) {}
+
+  std::size_t page_elems() const { return SA_HIP_PAGE_TOKENS * 2 * kv_heads_ * head_dim_; }
+  std::size_t page_bytes() const { return page_elems() * sizeof(std::uint16_t); }
+  std::size_t batch() const { return batch_; }
+  std::size_t query_heads() const { return query_heads_; }
+  std::size_t kv_heads() const { return kv_heads_; }
+
+  sa_paged_kv view() const {
+    sa_paged_kv v{};
+    v.pool = pool_.get();
+    v.block_table = table_.get();
+    v.seq_len = seq_len_.get();
+    v.sealed = sealed_.get();
+    v.generation = generation_.get();
+    v.reps = reps_.get();
+    v.num_pages = static_cast<int64_t>(num_pages_);
+    v.batch = static_cast<int32_t>(batch_);
+    v.table_stride = static_cast<int32_t>(table_stride_);
+    v.rep_heads = static_cast<int32_t>(rep_heads_);
+    v.rep_stride = static_cast<int32_t>(rep_stride_);
+    v.query_heads = static_cast<int32_t>(query_heads_);
+    v.kv_heads = static_cast<int32_t>(kv_heads_);
+    v.head_dim = static_cast<int32_t>(head_dim_);
+    return v;
+  }
+
+  DeviceArray<std::uint16_t>& pool() { return pool_; }
+  DeviceArray<int32_t>& block_table() { return table_; }
+  DeviceArray<int32_t>& seq_len() { return seq_len_; }
+  DeviceArray<int32_t>& sealed() { return sealed_; }
+  DeviceArray<int32_t>& generation() { return generation_; }
+  DeviceArray<float>& reps() { return reps_; }
+
+  // Append one token per sequence (fp32 K/V [batch][kv_heads][head_dim] on
+  // the device) and seal full blocks beyond local_tokens of tail.
+  void append_seal(const float* k, const float* v, int local_tokens, hipStream_t stream = nullptr,
+                   int32_t* status = nullptr) {
+    const sa_paged_kv kv = view();
+    check(sa_hip_append_seal(&kv, k, v, local_tokens, status, stream), "append_seal");
+  }
+  void append_seal_f16(const std::uint16_t* k, const std::uint16_t* v, int local_tokens,
+                       hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = view();
+    check(sa_hip_append_seal_f16(&kv, k, v, local_tokens, status, stream), "append_seal_f16");
+  }
+  // Seal every complete block beyond local_tokens of tail (after a prefill).
+  void seal(int local_tokens, hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = view();
+    check(sa_hip_seal(&kv, local_tokens, status, stream), "seal");
+  }
+
+ private:
+  std::size_t batch_, query_heads_, kv_heads_, head_dim_, table_stride_, num_pages_, rep_heads_, rep_stride_;
+  DeviceArray<std::uint16_t> pool_;
+  DeviceArray<int32_t> table_, seq_len_, sealed_, generation_;
+  DeviceArray<float> reps_;
+};
+
+// Budgeted selection + sparse decode attention with the scratch they need.
+class SparseDecoder {
+ public:
+  SparseDecoder(const PagedKvPool& pool, sa_select_params params, int splits = 0)
+      : params_(params),
+        splits_(splits > 0 ? splits
+                           : sa_hip_attention_default_splits(static_cast<int32_t>(pool.batch()),
+                                                             static_cast<int32_t>(pool.kv_heads()),
+                                                             params.budget_blocks + 2)),
+        selected_(pool.batch() * params.select_groups * params.sel_stride),
+        counts_(pool.batch() * params.select_groups),
+        workspace_bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),
+                                                          static_cast<int32_t>(pool.query_heads()),
+                                                          static_cast<int32_t>(pool.kv_heads()), 128, splits_)),
+        workspace_((workspace_bytes_ + 3) / 4) {}
+
+  // Score every sealed block against the query [batch][query_heads][128]
+  // (device) and select per group; ids stay on the device.
+  void select(const PagedKvPool& pool, const float* query, hipStream_t stream = nullptr,
+              float* scores = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_score_select(&kv, query, &params_, selected_.get(), counts_.get(), scores, status, stream),
+          "score_select");
+  }
+  // out [batch][query_heads][128] fp32 (device).
+  void attend(const PagedKvPool& pool, const float* query, float scale, float* out,
+              hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_sparse_decode_attention(&kv, query, selected_.get(), counts_.get(), params_.select_groups,
+                                         params_.sel_stride, scale, out, workspace_.get(), workspace_bytes_,
+                                         splits_, status, stream),
+          "sparse_decode_attention");
+  }
+
+  const DeviceArray<int32_t>& selected() const { return selected_; }
+  const DeviceArray<int32_t>& counts() const { return counts_; }
+  DeviceArray<int32_t>& selected() { return selected_; }
+  DeviceArray<int32_t>& counts() { return counts_; }
+  int splits() const { return splits_; }
+
+ private:
+  sa_select_params params_;
+  int splits_;
+  DeviceArray<int32_t> selected_, counts_;
+  std::size_t workspace_bytes_;
+  DeviceArray<float> workspace_;
+};
+
+struct Correction {
+  std::size_t hits{};
+  std::vector<int32_t> misses;
+  std::vector<int32_t> replacement_slots;
+};
+
+// Host set logic of a history prediction versus the selection.
+inline Correction compare_prediction(const std::vector<int32_t>& predicted, const std::vector<int32_t>& oracle) {
+  if (predicted.size() != oracle.size())
+    throw std::runtime_error("prediction correction cardinality mismatch");
+  Correction c;
+  c.misses.resize(predicted.size());
+  c.replacement_slots.resize(predicted.size());
+  int32_t hits = 0, misses = 0;
+  check(sa_hip_compare_prediction(predicted.data(), oracle.data(), static_cast<int32_t>(predicted.size()), &hits,
+                                  c.misses.data(), c.replacement_slots.data(), &misses),
+        "compare_prediction");
+  c.hits = static_cast<std::size_t>(hits);
+  c.misses.resize(static_cast<std::size_t>(misses));
+  c.replacement_slots.resize(static_cast<std::size_t>(misses));
+  return c;
+}
+
+// Copy stream + completion event for miss-correction slot fills from pinned
+// host memory; the compute stream orders itself after the fills on the
+// device (hipStreamWaitEvent), not with a host barrier.
+class MissCorrector {
+ public:
+  MissCorrector() {
+    hip_check(hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking), "hipStreamCreate copy");
+    hip_check(hipEventCreateWithFlags(&done_, hipEventDisableTiming), "hipEventCreate");
+  }
+  ~MissCorrector() {
+    if (done_) (void)hipEventDestroy(done_);
+    if (copy_) (void)hipStreamDestroy(copy_);
+  }
+  MissCorrector(const MissCorrector&) = delete;
+  MissCorrector& operator=(const MissCorrector&) = delete;
+
+  void fill(std::uint16_t* pool, std::size_t page_bytes, const std::vector<int32_t>& dst_pages,
+            const void* pinned_src, const std::vector<int64_t>& src_blocks) {
+    if (dst_pages.size() != src_blocks.size()) throw std::runtime_error("fill: page/block count mismatch");
+    check(sa_hip_fill_pages_async(pool, static_cast<int64_t>(page_bytes), dst_pages.data(), pinned_src,
+                                  src_blocks.data(), static_cast<int32_t>(dst_pages.size()), copy_, done_),
+          "fill_pages_async");
+  }
+  // Make `compute` wait (on the device) for the last fill.
+  void order(hipStream_t compute) { check(sa_hip_stream_wait_event(compute, done_), "stream_wait_event"); }
+  hipStream_t copy_stream() const { return copy_; }
+
+ private:
+  hipStream_t copy_{};
+  hipEvent_t done_{};
+};
+
+}  // namespace solidattention::hip

@@ -158,6 +158,25 @@ __global__ void consume_checksum_kernel(const float* input, int32_t elements, fl
   checksum[0] = value;
 }
 
+// C0 transport smoke transform: out[i] = in[i] ^ mask (the reference's
+// kv_transform, cpp/src/cuda_backend.cpp:40-46), 16 bytes per lane.
+__global__ __launch_bounds__(kThreads) void xor_bytes_kernel(const uint8_t* in, uint8_t* out, uint64_t bytes,
+                                                             uint8_t mask) {
+  const uint32_t m4 = 0x01010101u * mask;
+  const uint64_t vecs = bytes / 16;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < vecs;
+       i += static_cast<uint64_t>(gridDim.x) * kThreads) {
+    uint4 v = reinterpret_cast<const uint4*>(in)[i];
+    v.x ^= m4;
+    v.y ^= m4;
+    v.z ^= m4;
+    v.w ^= m4;
+    reinterpret_cast<uint4*>(out)[i] = v;
+  }
+  if (blockIdx.x == 0)
+    for (uint64_t i = vecs * 16 + threadIdx.x; i < bytes; i += kThreads) out[i] = in[i] ^ mask;
+}
+
 int grid_for(int64_t items, int per_block) {
   const int64_t g = (items + per_block - 1) / per_block;
   return static_cast<int>(g < 1 ? 1 : (g > 65536 ? 65536 : g));
@@ -217,6 +236,14 @@ hipError_t launch_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed, u
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_synthetic_f32_kernel, dim3(grid_for(count, kThreads * 8)), dim3(kThreads), 0,
                      stream, dst, count, mix64(seed), first_index);
+  return hipGetLastError();
+}
+
+hipError_t launch_xor_bytes(const uint8_t* input, uint8_t* output, uint64_t bytes, uint8_t mask,
+                            hipStream_t stream) {
+  if (bytes == 0) return hipSuccess;
+  hipLaunchKernelGGL(xor_bytes_kernel, dim3(grid_for(static_cast<int64_t>(bytes / 16 + 1), kThreads * 4)),
+                     dim3(kThreads), 0, stream, input, output, bytes, mask);
   return hipGetLastError();
 }
 

@@ -101,5 +101,7 @@ hipError_t launch_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed,
                                      uint64_t first_index, hipStream_t stream);
 hipError_t launch_consume_checksum(const float* input, int32_t elements, float* checksum,
                                    hipStream_t stream);
+hipError_t launch_xor_bytes(const uint8_t* input, uint8_t* output, uint64_t bytes, uint8_t mask,
+                            hipStream_t stream);
 
 }  // namespace sa
