@@ -127,3 +127,18 @@ def test_compare_prediction_cardinality_mismatch(oracle_lib):
     # a prediction with a duplicate cannot be corrected slot-for-slot
     st, _, _, _ = oracle_lib.compare_prediction([0, 0, 2, 15], [0, 1, 2, 15])
     assert st != 0
+
+
+def test_topk_argmax_python_test_indices(oracle_lib):
+    """The reference's tail test (tests/test_kv_lifecycle.py:22-37) expects
+    representative indices [7, 9, 11, 13] for scores 10/9/8/7 at those tokens."""
+    import numpy as np
+    scores = np.zeros(32, np.float32)
+    scores[[7, 9, 11, 13]] = [10, 9, 8, 7]
+    top = np.zeros(4, np.uint64)
+    oracle_lib.lib().sao_topk_argmax(scores.ctypes.data, 32, 4, top.ctypes.data)
+    assert top.tolist() == [7, 9, 11, 13]
+    # ties resolve to the first maximum, as the argmax-first loop does
+    flat = np.ones(32, np.float32)
+    oracle_lib.lib().sao_topk_argmax(flat.ctypes.data, 32, 4, top.ctypes.data)
+    assert top.tolist() == [0, 1, 2, 3]
