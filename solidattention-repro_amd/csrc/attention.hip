@@ -17,11 +17,11 @@
 // query heads of the group reuse every K/V register (v_fma_mix_f32 consumes
 // the FP16 halves directly), so KV bytes are read from HBM once per group.
 // No MFMA: decode attention is a matrix-vector product (about 2 flop per KV
-// byte at G=2).  Measured on MI355X at B=64/16K, one workgroup per
-// (sequence, KV head) with 4 waves of ~16 pages each streams the selected
-// pages at ~5.3 TB/s; the same access pattern with no arithmetic reads at
-// ~5.8 TB/s and a plain contiguous read at ~6.3 TB/s, so latency is hidden
-// by the 8-10 waves per CU and a register-prefetch variant did not help.
+// byte at G=2).  Measured on MI355X at B=64/16K: one workgroup of 8 waves per
+// (sequence, KV head), ~8 pages per wave, with non-temporal page loads
+// streams the selected pages at ~6.1 TB/s (plain loads: 5.3 TB/s; a plain
+// contiguous read of the pool: 6.4 TB/s); a register-prefetch variant and a
+// fused last-workgroup merge were both slower.
 #include "sa_device.hpp"
 #include "sa_internal.hpp"
 
@@ -29,8 +29,11 @@ namespace sa {
 namespace {
 
 constexpr int D = kHeadDim;
-constexpr int kWavesPerGroup = 4;                 // waves per workgroup
-constexpr int kThreads = kWavesPerGroup * kWave;  // 256
+// Waves per workgroup: 8, except 4 for G = 8 whose 8 accumulator sets need
+// the larger per-wave register budget of a 4-wave workgroup.
+template <int G>
+constexpr int waves_per_group() { return G >= 8 ? 4 : 8; }
+constexpr int kMergeThreads = 256;
 constexpr int kLanesPerRow = D / 8;               // 16 lanes x 8 halves = one 256 B row
 constexpr int kRows = kWave / kLanesPerRow;       // 4 rows per wave-wide load
 constexpr int kIters = kPageTokens / kRows;       // 8 tokens per lane per page
@@ -129,16 +132,15 @@ __device__ inline void load_page(const Params& p, const PageRef& pr, int64_t hea
   const uint16_t* kbase = p.pool + pr.page * p.page_elems + head_off;
   if (pr.valid == kPageTokens) {
 #pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
-      vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
-    }
+    for (int it = 0; it < kIters; ++it) kr[it] = load_stream16(kbase + it * step4);
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) vr[it] = load_stream16(kbase + it * step4 + v_off);
   } else {
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
       if (it * kRows + row < pr.valid) {
-        kr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4);
-        vr[it] = *reinterpret_cast<const uint4*>(kbase + it * step4 + v_off);
+        kr[it] = load_stream16(kbase + it * step4);
+        vr[it] = load_stream16(kbase + it * step4 + v_off);
       } else {
         kr[it] = make_uint4(0, 0, 0, 0);
         vr[it] = make_uint4(0, 0, 0, 0);
@@ -206,7 +208,9 @@ __device__ inline void process_page(const uint4 (&kr)[kIters], const uint4 (&vr)
 }
 
 template <int G>
-__global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const Params p) {
+__global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_attention_kernel(const Params p) {
+  constexpr int kWavesPerGroup = waves_per_group<G>();
+  constexpr int kThreads = kWavesPerGroup * kWave;
   const int g = blockIdx.x;
   const int b = blockIdx.y;
   const int z = blockIdx.z;
@@ -344,7 +348,8 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_attention_kernel(const
 
 // Log-sum-exp merge of the split partial results of one (sequence, KV head).
 template <int G>
-__global__ __launch_bounds__(kThreads) void merge_partials_kernel(const Params p) {
+__global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const Params p) {
+  constexpr int kThreads = kMergeThreads;
   const int g = blockIdx.x;
   const int b = blockIdx.y;
   const float* base =
@@ -371,10 +376,10 @@ __global__ __launch_bounds__(kThreads) void merge_partials_kernel(const Params p
 template <int G>
 hipError_t launch_g(const Params& p, int batch, hipStream_t stream) {
   const dim3 grid(p.kv_heads, batch, p.splits);
-  hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(waves_per_group<G>() * kWave), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
-  hipLaunchKernelGGL(merge_partials_kernel<G>, dim3(p.kv_heads, batch), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(merge_partials_kernel<G>, dim3(p.kv_heads, batch), dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -87,15 +87,15 @@ size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads, int3
 }
 
 int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads, int32_t pages_per_group_hint) {
-  // One workgroup (4 waves) per (sequence, KV head) streams best once there
+  // One workgroup (8 waves) per (sequence, KV head) streams best once there
   // are >= 512 of them (two per CU): at B=64, 8 KV heads, 65 pages per group
-  // that measures 5.3 TB/s against 4.8-4.6 TB/s with 3-8 splits plus the
-  // merge.  Smaller batches split the page list until ~512 workgroups exist,
-  // keeping at least ~4 pages per wave.
+  // splits of 2-4 plus the merge kernel measured 3-7% slower than 1.
+  // Smaller batches split the page list until ~512 workgroups exist, keeping
+  // at least ~4 pages per wave.
   const int64_t pages = std::max<int32_t>(pages_per_group_hint, 1);
   const int64_t groups = static_cast<int64_t>(std::max(batch, 1)) * std::max(kv_heads, 1);
   int64_t splits = 1;
-  while (groups * splits < 512 && (splits * 2) * 4 * 4 <= pages) splits *= 2;
+  while (groups * splits < 512 && (splits * 2) * 8 * 4 <= pages) splits *= 2;
   return static_cast<int32_t>(std::min<int64_t>(splits, 64));
 }
 

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
       for (int d0 = 0; d0 < D; d0 += kBatch) {
         float rv[kBatch];
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) rv[k] = r[static_cast<int64_t>(d0 + k) * p.rep_stride];
+        for (int k = 0; k < kBatch; ++k) rv[k] = load_stream_f32(r + static_cast<int64_t>(d0 + k) * p.rep_stride);
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
 #pragma unroll
