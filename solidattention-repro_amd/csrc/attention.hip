@@ -29,10 +29,11 @@ namespace sa {
 namespace {
 
 constexpr int D = kHeadDim;
-// Waves per workgroup: 8, except 4 for G = 8 whose 8 accumulator sets need
-// the larger per-wave register budget of a 4-wave workgroup.
+// Waves per workgroup: 8 for G <= 2 (123 VGPRs: two 8-wave workgroups per
+// CU); 4 for G >= 4, whose larger accumulator sets (161+ VGPRs) would leave
+// room for only one 8-wave workgroup per CU.
 template <int G>
-constexpr int waves_per_group() { return G >= 8 ? 4 : 8; }
+constexpr int waves_per_group() { return G >= 4 ? 4 : 8; }
 constexpr int kMergeThreads = 256;
 constexpr int kLanesPerRow = D / 8;               // 16 lanes x 8 halves = one 256 B row
 constexpr int kRows = kWave / kLanesPerRow;       // 4 rows per wave-wide load
