@@ -122,6 +122,26 @@ int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query,
                                    size_t workspace_bytes, int32_t splits,
                                    int32_t* status, void* stream);
 
+/* Split-phase attention, for schedules that attend the blocks already
+ * resident while missing blocks are still being copied in (the overlap the
+ * reference gets from its copy stream, pipeline_main.cpp:811-848).  Each
+ * call attends its own id list (plus the tail when include_tail) with
+ * `splits` workgroups per (sequence, KV head) and writes their partial
+ * records to [split_base, split_base + splits) of a workspace sized by
+ * sa_hip_attention_workspace_bytes(..., total_splits) (total_splits >= 2);
+ * once calls have written all total_splits records, sa_hip_attention_merge
+ * forms `out` exactly as a single call over the union would (within fp32
+ * rounding).  The tail must be included by exactly one call. */
+int sa_hip_sparse_decode_attention_partial(
+    const sa_paged_kv* kv, const float* query, const int32_t* selected,
+    const int32_t* counts, int32_t select_groups, int32_t sel_stride,
+    float scale, int32_t include_tail, void* workspace,
+    size_t workspace_bytes, int32_t split_base, int32_t splits,
+    int32_t total_splits, int32_t* status, void* stream);
+int sa_hip_attention_merge(const sa_paged_kv* kv, const void* workspace,
+                           size_t workspace_bytes, int32_t total_splits,
+                           float* out, void* stream);
+
 /* Attention over a contiguous token-major K/V-interleaved buffer of
  * `tokens` tokens (the AttentionProblem layout, backend.hpp:18-31); the
  * device kernel of AcceleratorBackend::attention (cuda_backend.cpp:70-158)

@@ -61,8 +61,12 @@ struct Params {
   int32_t kv_per_sel;
   int32_t query_heads;
   int32_t kv_heads;
-  int32_t splits;
-  float qscale;  // softmax scale * log2(e)
+  int32_t splits;        // workgroups per (sequence, KV head) in this launch
+  int32_t part_base;     // first partial record written by this launch
+  int32_t part_total;    // partial records per (sequence, KV head) in the workspace
+  int32_t include_tail;  // attend the unsealed tail too
+  int32_t direct;        // write the normalised output instead of a partial record
+  float qscale;          // softmax scale * log2(e)
 };
 
 __device__ inline void unpack8(const uint4& w, float (&f)[8]) {
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_at
       if (L.n_sel < 0 || L.n_sel > p.sel_stride) L.n_sel = 0;
     }
   }
-  const int64_t tail_tokens = L.len - static_cast<int64_t>(L.sealed) * kPageTokens;
+  const int64_t tail_tokens = p.include_tail ? L.len - static_cast<int64_t>(L.sealed) * kPageTokens : 0;
   L.total = L.n_sel + static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
 
   // ---- query: dims [8c, 8c+8) of each head of the group, pre-scaled -------
@@ -333,10 +337,10 @@ __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_at
       }
     }
     const int qh = g * G + h;
-    if (p.splits == 1) {
+    if (p.direct) {
       p.out[(static_cast<int64_t>(b) * p.query_heads + qh) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
     } else {
-      float* rec = p.part + (((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits + z) * G + h) *
+      float* rec = p.part + (((static_cast<int64_t>(b) * p.kv_heads + g) * p.part_total + p.part_base + z) * G + h) *
                                 part_stride(D);
       if (d == 0) {
         rec[0] = mx;
@@ -354,15 +358,15 @@ __global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const Par
   const int g = blockIdx.x;
   const int b = blockIdx.y;
   const float* base =
-      p.part + ((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits) * G * part_stride(D);
+      p.part + ((static_cast<int64_t>(b) * p.kv_heads + g) * p.part_total) * G * part_stride(D);
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
     const int h = o / D;
     const int d = o % D;
     float mx = kNegInf;
-    for (int zz = 0; zz < p.splits; ++zz) mx = fmaxf(mx, base[(zz * G + h) * part_stride(D)]);
+    for (int zz = 0; zz < p.part_total; ++zz) mx = fmaxf(mx, base[(zz * G + h) * part_stride(D)]);
     float lw = 0.0f, aw = 0.0f;
     if (mx != kNegInf) {
-      for (int zz = 0; zz < p.splits; ++zz) {
+      for (int zz = 0; zz < p.part_total; ++zz) {
         const float* rec = base + (zz * G + h) * part_stride(D);
         if (rec[0] == kNegInf) continue;
         const float f = __builtin_amdgcn_exp2f(rec[0] - mx);
@@ -374,12 +378,15 @@ __global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const Par
   }
 }
 
+// mode 0: attention (+ merge when split); 1: partial records only; 2: merge only.
 template <int G>
-hipError_t launch_g(const Params& p, int batch, hipStream_t stream) {
-  const dim3 grid(p.kv_heads, batch, p.splits);
-  hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(waves_per_group<G>() * kWave), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.splits == 1) return e;
+hipError_t launch_g(const Params& p, int batch, int mode, hipStream_t stream) {
+  if (mode != 2) {
+    const dim3 grid(p.kv_heads, batch, p.splits);
+    hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(waves_per_group<G>() * kWave), 0, stream, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || mode == 1 || p.direct) return e;
+  }
   hipLaunchKernelGGL(merge_partials_kernel<G>, dim3(p.kv_heads, batch), dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
@@ -409,13 +416,24 @@ hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t strea
   p.query_heads = a.query_heads;
   p.kv_heads = a.kv_heads;
   p.splits = a.splits;
+  if (a.mode == 0) {
+    p.part_base = 0;
+    p.part_total = a.splits;
+    p.include_tail = 1;
+    p.direct = a.splits == 1;
+  } else {
+    p.part_base = a.part_base;
+    p.part_total = a.part_total;
+    p.include_tail = a.include_tail;
+    p.direct = 0;
+  }
   p.qscale = a.scale * 1.4426950408889634f;
   const int group = a.query_heads / a.kv_heads;
   switch (group) {
-    case 1: return launch_g<1>(p, a.batch, stream);
-    case 2: return launch_g<2>(p, a.batch, stream);
-    case 4: return launch_g<4>(p, a.batch, stream);
-    case 8: return launch_g<8>(p, a.batch, stream);
+    case 1: return launch_g<1>(p, a.batch, a.mode, stream);
+    case 2: return launch_g<2>(p, a.batch, a.mode, stream);
+    case 4: return launch_g<4>(p, a.batch, a.mode, stream);
+    case 8: return launch_g<8>(p, a.batch, a.mode, stream);
     default: return hipErrorInvalidValue;
   }
 }

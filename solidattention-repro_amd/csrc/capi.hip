@@ -147,6 +147,73 @@ int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query, co
                           workspace_bytes, splits, status, stream, 0);
 }
 
+int sa_hip_sparse_decode_attention_partial(const sa_paged_kv* kv, const float* query, const int32_t* selected,
+                                           const int32_t* counts, int32_t select_groups, int32_t sel_stride,
+                                           float scale, int32_t include_tail, void* workspace,
+                                           size_t workspace_bytes, int32_t split_base, int32_t splits,
+                                           int32_t total_splits, int32_t* status, void* stream) {
+  if (int e = check_geometry(kv, "attention_partial")) return e;
+  if (!query || !selected || !counts || !workspace)
+    return fail(SA_HIP_EINVAL, "attention_partial: null query/selected/counts/workspace");
+  if (!aligned16(query)) return fail(SA_HIP_EINVAL, "attention_partial: query must be 16-byte aligned");
+  if (select_groups <= 0 || kv->kv_heads % select_groups != 0)
+    return fail(SA_HIP_EINVAL, "attention_partial: select_groups must divide kv_heads");
+  if (sel_stride <= 0) return fail(SA_HIP_EINVAL, "attention_partial: sel_stride must be positive");
+  if (total_splits < 2 || splits < 1 || split_base < 0 || split_base + splits > total_splits)
+    return fail(SA_HIP_EINVAL, "attention_partial: splits [%d, %d) outside [0, %d) (total_splits >= 2)", split_base,
+                split_base + splits, total_splits);
+  const size_t need =
+      sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, total_splits);
+  if (workspace_bytes < need)
+    return fail(SA_HIP_EINVAL, "attention_partial: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  sa::AttnLaunch a{};
+  a.pool = kv->pool;
+  a.table = kv->block_table;
+  a.seq_len = kv->seq_len;
+  a.sealed = kv->sealed;
+  a.selected = selected;
+  a.counts = counts;
+  a.query = query;
+  a.part = static_cast<float*>(workspace);
+  a.status = status;
+  a.num_pages = kv->num_pages;
+  a.batch = kv->batch;
+  a.table_stride = kv->table_stride;
+  a.sel_stride = sel_stride;
+  a.select_groups = select_groups;
+  a.query_heads = kv->query_heads;
+  a.kv_heads = kv->kv_heads;
+  a.splits = splits;
+  a.scale = scale;
+  a.mode = 1;
+  a.part_base = split_base;
+  a.part_total = total_splits;
+  a.include_tail = include_tail ? 1 : 0;
+  return check_hip(sa::launch_sparse_decode_attention(a, as_stream(stream)), "attention_partial launch");
+}
+
+int sa_hip_attention_merge(const sa_paged_kv* kv, const void* workspace, size_t workspace_bytes,
+                           int32_t total_splits, float* out, void* stream) {
+  if (int e = check_geometry(kv, "attention_merge")) return e;
+  if (!workspace || !out) return fail(SA_HIP_EINVAL, "attention_merge: null workspace/out");
+  if (total_splits < 2) return fail(SA_HIP_EINVAL, "attention_merge: total_splits must be >= 2");
+  const size_t need =
+      sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, total_splits);
+  if (workspace_bytes < need)
+    return fail(SA_HIP_EINVAL, "attention_merge: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  sa::AttnLaunch a{};
+  a.out = out;
+  a.part = static_cast<float*>(const_cast<void*>(workspace));
+  a.batch = kv->batch;
+  a.query_heads = kv->query_heads;
+  a.kv_heads = kv->kv_heads;
+  a.select_groups = 1;
+  a.splits = total_splits;
+  a.mode = 2;
+  a.part_total = total_splits;
+  return check_hip(sa::launch_sparse_decode_attention(a, as_stream(stream)), "attention_merge launch");
+}
+
 static int32_t contiguous_splits(int64_t tokens, int32_t kv_heads) {
   const int64_t pages = (tokens + SA_HIP_PAGE_TOKENS - 1) / SA_HIP_PAGE_TOKENS;
   return sa_hip_attention_default_splits(1, kv_heads, static_cast<int32_t>(std::min<int64_t>(pages, 1 << 30)));

@@ -40,6 +40,13 @@ struct AttnLaunch {
   int32_t kv_heads;
   int32_t splits;
   float scale;
+  // 0: full attention (+ merge when splits > 1); 1: partial records
+  // [part_base, part_base + splits) of part_total only; 2: merge of
+  // part_total records only.
+  int32_t mode;
+  int32_t part_base;
+  int32_t part_total;
+  int32_t include_tail;
 };
 
 hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t stream);

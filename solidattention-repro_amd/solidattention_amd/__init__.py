@@ -55,6 +55,9 @@ EXPORTS = {
     "sa_hip_attention_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
     "sa_hip_attention_default_splits": (_I32, [_I32, _I32, _I32]),
     "sa_hip_sparse_decode_attention": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _P, _P]),
+    "sa_hip_sparse_decode_attention_partial": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _I32, _P, _SZ, _I32, _I32,
+                                                         _I32, _P, _P]),
+    "sa_hip_attention_merge": (C.c_int, [_KV, _P, _SZ, _I32, _P, _P]),
     "sa_hip_contiguous_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "sa_hip_attention_contiguous": (C.c_int, [_P, _P, _I64, _I32, _I32, _I32, _F, _P, _P, _SZ, _P]),
     "sa_hip_consume_checksum": (C.c_int, [_P, _I32, _P, _P]),
@@ -200,6 +203,26 @@ def sparse_decode_attention(kv: PagedKV, query, selected, counts, scale, out=Non
         C.byref(s), _ptr(query), _ptr(selected), _ptr(counts), select_groups, sel_stride, C.c_float(scale),
         _ptr(out), _ptr(workspace) if nbytes else None, nbytes, splits, _ptr(status), _stream(stream)),
         "sparse_decode_attention")
+    return out
+
+
+def sparse_decode_attention_partial(kv: PagedKV, query, selected, counts, scale, include_tail, workspace,
+                                    split_base, splits, total_splits, status=None, stream=None):
+    """Partial records [split_base, split_base + splits) of total_splits."""
+    select_groups, sel_stride = selected.shape[1], selected.shape[2]
+    s = kv.struct()
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().sa_hip_sparse_decode_attention_partial(
+        C.byref(s), _ptr(query), _ptr(selected), _ptr(counts), select_groups, sel_stride, C.c_float(scale),
+        1 if include_tail else 0, _ptr(workspace), nbytes, split_base, splits, total_splits, _ptr(status),
+        _stream(stream)), "sparse_decode_attention_partial")
+
+
+def attention_merge(kv: PagedKV, workspace, total_splits, out, stream=None):
+    s = kv.struct()
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().sa_hip_attention_merge(C.byref(s), _ptr(workspace), nbytes, total_splits, _ptr(out),
+                                       _stream(stream)), "attention_merge")
     return out
 
 

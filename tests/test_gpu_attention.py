@@ -160,3 +160,37 @@ def test_bad_page_is_flagged_not_read(hip):
     hip.sparse_decode_attention(kv, to_dev(case.query), to_dev(sel), to_dev(cnt), SCALE, status=st)
     torch.cuda.synchronize()
     assert int(st.item()) & hip.STATUS_BAD_PAGE
+
+
+def test_split_phase_partial_and_merge(hip):
+    """Hits-first schedule: attend one part of the selection (with the tail),
+    then the rest, then merge; equals attention over the whole selection."""
+    case = make_case(47, 3, 16, 8, [32 * 60 + 7, 32 * 41, 32 * 80 + 31])
+    sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, 3, 16, 8, D, 8, case.rep_stride, 8, 24, 2,
+                                    3)
+    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, sel, cnt, 8,
+                                      case.query, 3, 16, 8, D, SCALE)
+    # split every (seq, group) list into its even and odd positions
+    first = np.full_like(sel, -1)
+    second = np.full_like(sel, -1)
+    c1 = np.zeros_like(cnt)
+    c2 = np.zeros_like(cnt)
+    for b in range(3):
+        for g in range(8):
+            ids = sel[b, g, : cnt[b, g]]
+            a, z = ids[0::2], ids[1::2]
+            first[b, g, : len(a)] = a
+            second[b, g, : len(z)] = z
+            c1[b, g], c2[b, g] = len(a), len(z)
+    kv = device_kv(case)
+    total = 3
+    ws, _ = hip.attention_workspace(kv, total)
+    q = to_dev(case.query)
+    st = status_tensor()
+    hip.sparse_decode_attention_partial(kv, q, to_dev(first), to_dev(c1), SCALE, True, ws, 0, 2, total, status=st)
+    hip.sparse_decode_attention_partial(kv, q, to_dev(second), to_dev(c2), SCALE, False, ws, 2, 1, total, status=st)
+    out = torch.empty((3, 16, D), dtype=torch.float32, device="cuda")
+    hip.attention_merge(kv, ws, total, out)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    assert_close_2e3(out.cpu().numpy(), expect)
