@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--cpu-sample-seqs", type=int, default=0, help="sequences in the CPU sample (0 = auto)")
     ap.add_argument("--check-seqs", type=int, default=2, help="sequences parity-checked against the oracle")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (no HIP graph replay)")
+    ap.add_argument("--workload", default="decode", choices=["decode", "correction"],
+                    help="decode: the headline decode step; correction: long-context miss correction "
+                         "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
                     help="also run one plain page copy of PAGES pages (HBM counter calibration)")
     return ap.parse_args()
@@ -109,6 +112,10 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU: the KV-cache hot path is measured at its "
                                    "real per-GPU shape; --gpus must be 1"}))
         sys.exit(2)
+    if args.workload == "correction":
+        import bench_correction
+        bench_correction.run(args)
+        return
     import numpy as np
     import torch
 
