@@ -53,7 +53,7 @@ def run(args):
     EPS = 0.36                             # query random-walk step (~75% coverage)
     layers = args.layers or 2
     steps, warmup = args.steps, args.warmup
-    total_steps = warmup + 2 * steps + 1
+    total_steps = warmup + 3 * steps + 1
     assert total_steps < PAGE, "the tail page must not seal during the run"
     torch.cuda.set_device(0)
     dev = torch.device("cuda")
@@ -125,14 +125,17 @@ def run(args):
     log(f"setup {time.time() - t0:.1f}s: {layers} layers, host store {layers * B * TS * page_bytes / 2**30:.1f} GiB pinned")
 
     host_tables = [torch.from_numpy(ly["table"]).pin_memory() for ly in Ls]
+    host_fill = [torch.zeros((2, B * BUDGET), dtype=torch.int64).pin_memory() for _ in Ls]
+    for ly in Ls:
+        ly["fill_lists"] = torch.zeros((2, B * BUDGET), dtype=torch.int64, device=dev)
+        ly["dst32"] = torch.zeros(B * BUDGET, dtype=torch.int32, device=dev)
     host_lists = [torch.zeros((4, B, BUDGET), dtype=torch.int32).pin_memory() for _ in Ls]
     host_counts = [torch.zeros((2, B), dtype=torch.int32).pin_memory() for _ in Ls]
-    stats = {"overlapped": [], "serial": []}
     miss_total = [0]
     sel_total = [0]
     copy_events = []
 
-    def step(s, mode):
+    def step(s, mode, fill):
         for li, ly in enumerate(Ls):
             kv = ly["kv"]
             sa.append_seal(kv, ly["knew"][s], ly["vnew"][s], 0, status=status)
@@ -169,9 +172,23 @@ def run(args):
             # has completed; the hit phase reads other slots, so the copies
             # start at once
             c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if fill == "gather":
+                # the fill kernel reads its page lists from device memory,
+                # uploaded on the copy stream itself
+                hd = host_fill[li]
+                hd[0, : len(dst_pages)] = torch.tensor(dst_pages, dtype=torch.int64)
+                hd[1, : len(src_blocks)] = torch.tensor(src_blocks, dtype=torch.int64)
+                with torch.cuda.stream(copy_stream):
+                    ly["fill_lists"].copy_(hd, non_blocking=True)
+                    ly["dst32"].copy_(ly["fill_lists"][0].to(torch.int32))
             c0.record(copy_stream)
-            sa.fill_pages_async(kv.pool, page_bytes, dst_pages, ly["store"].data_ptr(), src_blocks, copy_stream,
-                                ly["done"])
+            if fill == "gather":
+                sa.fill_pages_gather_async(kv.pool, page_bytes, kv.num_pages, ly["dst32"], ly["store"].data_ptr(),
+                                           B * TS, ly["fill_lists"][1], len(dst_pages), copy_stream, ly["done"],
+                                           status=status)
+            else:
+                sa.fill_pages_async(kv.pool, page_bytes, dst_pages, ly["store"].data_ptr(), src_blocks, copy_stream,
+                                    ly["done"])
             c1.record(copy_stream)
             copy_events.append((c0, c1, len(dst_pages)))
             if mode == "overlapped":
@@ -188,24 +205,25 @@ def run(args):
         torch.cuda.synchronize()
 
     for s in range(warmup):
-        step(s, "overlapped")
+        step(s, "overlapped", "gather")
     miss_total[0] = sel_total[0] = 0
     copy_events.clear()
     results = {}
     s = warmup
-    for mode in ("serial", "overlapped"):
+    schedules = (("serial", "memcpy"), ("overlapped", "memcpy"), ("overlapped", "gather"))
+    for mode, fill in schedules:
         m0, t_all = miss_total[0], 0.0
         n_copy_ms, n_copy_pages = 0.0, 0
         ev0 = len(copy_events)
         for _ in range(steps):
             t = time.perf_counter()
-            step(s, mode)
+            step(s, mode, fill)
             t_all += time.perf_counter() - t
             s += 1
         for c0, c1, n in copy_events[ev0:]:
             n_copy_ms += c0.elapsed_time(c1)
             n_copy_pages += n
-        results[mode] = {"us_per_layer": round(t_all / steps / layers * 1e6, 1),
+        results[f"{mode}_{fill}"] = {"us_per_layer": round(t_all / steps / layers * 1e6, 1),
                          "misses_per_layer": round((miss_total[0] - m0) / steps / layers, 1),
                          "h2d_gbps": round(n_copy_pages * page_bytes / max(n_copy_ms, 1e-9) / 1e6, 1),
                          "h2d_us_per_layer": round(n_copy_ms * 1000 / steps / layers, 1)}
@@ -239,7 +257,7 @@ def run(args):
         "workload": "long-context miss correction, Qwen3-8B shape, B=8, 131072 tokens, budget 128 blocks",
         "layers": layers, "steps": steps, "warmup": warmup,
         "history_coverage": round(coverage, 4),
-        "overlapped": results["overlapped"], "serial": results["serial"],
+        "schedules": results,
         "page_bytes": page_bytes,
         "checks": {"resident_set_equals_selection": sets_ok, "slot_bytes_equal_store": bytes_ok,
                    "attention_within_2e-3": att_ok, "attention_max_abs_err": float(err.max())},

@@ -227,6 +227,19 @@ int sa_hip_fill_pages_async(uint16_t* pool, int64_t page_bytes,
                             const void* src_base, const int64_t* src_blocks,
                             int32_t count, void* copy_stream,
                             void* done_event);
+/* The same fills as one kernel on copy_stream that reads the pinned host
+ * memory (src_base must come from hipHostMalloc / pinned allocation, holding
+ * src_blocks_total pages) through its device mapping; dst_pages_dev and
+ * src_blocks_dev are device arrays.  Entries outside [0, num_pages) or
+ * [0, src_blocks_total) are skipped and flagged in status. */
+int sa_hip_fill_pages_gather_async(uint16_t* pool, int64_t page_bytes,
+                                   int64_t num_pages,
+                                   const int32_t* dst_pages_dev,
+                                   const void* src_base,
+                                   int64_t src_blocks_total,
+                                   const int64_t* src_blocks_dev,
+                                   int32_t count, int32_t* status,
+                                   void* copy_stream, void* done_event);
 int sa_hip_stream_wait_event(void* stream, void* event);
 
 /* ---- synthetic data ------------------------------------------------------ */

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 namespace {
 
@@ -384,15 +385,23 @@ int sa_hip_compare_prediction(const int32_t* predicted, const int32_t* oracle, i
   return SA_HIP_OK;
 }
 
+static int fill_args_ok(uint16_t* pool, int64_t page_bytes, const int32_t* dst_pages, const void* src_base,
+                        const int64_t* src_blocks, int32_t count, const char* op) {
+  if (count < 0 || (count > 0 && (!pool || !dst_pages || !src_base || !src_blocks)) || page_bytes <= 0 ||
+      page_bytes % 16 != 0)
+    return fail(SA_HIP_EINVAL, "%s: bad arguments", op);
+  for (int32_t i = 0; i < count; ++i)
+    if (dst_pages[i] < 0 || src_blocks[i] < 0)
+      return fail(SA_HIP_EINVAL, "%s: negative page/block index at %d", op, i);
+  return SA_HIP_OK;
+}
+
 int sa_hip_fill_pages_async(uint16_t* pool, int64_t page_bytes, const int32_t* dst_pages, const void* src_base,
                             const int64_t* src_blocks, int32_t count, void* copy_stream, void* done_event) {
-  if (count < 0 || (count > 0 && (!pool || !dst_pages || !src_base || !src_blocks)) || page_bytes <= 0)
-    return fail(SA_HIP_EINVAL, "fill_pages_async: bad arguments");
+  if (int e = fill_args_ok(pool, page_bytes, dst_pages, src_base, src_blocks, count, "fill_pages_async")) return e;
   auto* dst = reinterpret_cast<uint8_t*>(pool);
   const auto* src = static_cast<const uint8_t*>(src_base);
   for (int32_t i = 0; i < count; ++i) {
-    if (dst_pages[i] < 0 || src_blocks[i] < 0)
-      return fail(SA_HIP_EINVAL, "fill_pages_async: negative page/block index at %d", i);
     if (int e = check_hip(hipMemcpyAsync(dst + static_cast<int64_t>(dst_pages[i]) * page_bytes,
                                          src + src_blocks[i] * page_bytes, static_cast<size_t>(page_bytes),
                                          hipMemcpyHostToDevice, as_stream(copy_stream)),
@@ -402,6 +411,30 @@ int sa_hip_fill_pages_async(uint16_t* pool, int64_t page_bytes, const int32_t* d
   if (done_event)
     return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(done_event), as_stream(copy_stream)),
                      "fill_pages_async: hipEventRecord");
+  return SA_HIP_OK;
+}
+
+int sa_hip_fill_pages_gather_async(uint16_t* pool, int64_t page_bytes, int64_t num_pages,
+                                   const int32_t* dst_pages_dev, const void* src_base, int64_t src_blocks_total,
+                                   const int64_t* src_blocks_dev, int32_t count, int32_t* status, void* copy_stream,
+                                   void* done_event) {
+  if (count < 0 || (count > 0 && (!pool || !dst_pages_dev || !src_base || !src_blocks_dev)) || page_bytes <= 0 ||
+      page_bytes % 16 != 0)
+    return fail(SA_HIP_EINVAL, "fill_pages_gather_async: bad arguments");
+  void* src_dev = nullptr;
+  if (count > 0) {
+    if (int e = check_hip(hipHostGetDevicePointer(&src_dev, const_cast<void*>(src_base), 0),
+                          "fill_pages_gather_async: hipHostGetDevicePointer (source must be pinned host memory)"))
+      return e;
+    if (int e = check_hip(sa::launch_fill_from_host(pool, page_bytes, num_pages, dst_pages_dev,
+                                                    static_cast<const uint8_t*>(src_dev), src_blocks_total,
+                                                    src_blocks_dev, count, status, as_stream(copy_stream)),
+                          "fill_pages_gather_async launch"))
+      return e;
+  }
+  if (done_event)
+    return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(done_event), as_stream(copy_stream)),
+                     "fill_pages_gather_async: hipEventRecord");
   return SA_HIP_OK;
 }
 

@@ -158,6 +158,28 @@ __global__ void consume_checksum_kernel(const float* input, int32_t elements, fl
   checksum[0] = value;
 }
 
+// Miss-correction fill from pinned host memory mapped into the device
+// address space: one workgroup-row per missing page reads its 128 KiB over
+// PCIe with 16-byte loads and writes the slot.  One launch replaces one
+// hipMemcpyAsync per page.
+__global__ __launch_bounds__(kThreads) void fill_from_host_kernel(uint4* pool, int64_t page_vecs, int64_t num_pages,
+                                                                  const int32_t* dst_pages, const uint4* src,
+                                                                  int64_t src_total, const int64_t* src_blocks,
+                                                                  int32_t* status) {
+  const int i = blockIdx.y;
+  const int64_t page = dst_pages[i];
+  const int64_t blk = src_blocks[i];
+  if (page < 0 || page >= num_pages || blk < 0 || blk >= src_total) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) flag_status(status, kStatusBadPage);
+    return;
+  }
+  const uint4* s = src + blk * page_vecs;
+  uint4* d = pool + page * page_vecs;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; e < page_vecs;
+       e += static_cast<int64_t>(gridDim.x) * kThreads)
+    d[e] = s[e];
+}
+
 // C0 transport smoke transform: out[i] = in[i] ^ mask (the reference's
 // kv_transform, cpp/src/cuda_backend.cpp:40-46), 16 bytes per lane.
 __global__ __launch_bounds__(kThreads) void xor_bytes_kernel(const uint8_t* in, uint8_t* out, uint64_t bytes,
@@ -236,6 +258,17 @@ hipError_t launch_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed, u
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_synthetic_f32_kernel, dim3(grid_for(count, kThreads * 8)), dim3(kThreads), 0,
                      stream, dst, count, mix64(seed), first_index);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_from_host(uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* dst_pages,
+                                 const uint8_t* src_dev, int64_t src_total, const int64_t* src_blocks, int32_t count,
+                                 int32_t* status, hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  const int64_t vecs = page_bytes / 16;
+  const dim3 grid(grid_for(vecs, kThreads * 8), count);
+  hipLaunchKernelGGL(fill_from_host_kernel, grid, dim3(kThreads), 0, stream, reinterpret_cast<uint4*>(pool), vecs,
+                     num_pages, dst_pages, reinterpret_cast<const uint4*>(src_dev), src_total, src_blocks, status);
   return hipGetLastError();
 }
 

@@ -108,6 +108,9 @@ hipError_t launch_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed,
                                      uint64_t first_index, hipStream_t stream);
 hipError_t launch_consume_checksum(const float* input, int32_t elements, float* checksum,
                                    hipStream_t stream);
+hipError_t launch_fill_from_host(uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* dst_pages,
+                                 const uint8_t* src_dev, int64_t src_total, const int64_t* src_blocks, int32_t count,
+                                 int32_t* status, hipStream_t stream);
 hipError_t launch_xor_bytes(const uint8_t* input, uint8_t* output, uint64_t bytes, uint8_t mask,
                             hipStream_t stream);
 

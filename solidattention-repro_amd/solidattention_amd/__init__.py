@@ -68,6 +68,7 @@ EXPORTS = {
     "sa_hip_gather_pages": (C.c_int, [_P, _I64, _I64, _P, _I32, _P, _P, _P]),
     "sa_hip_compare_prediction": (C.c_int, [_P, _P, _I32, _P, _P, _P, _P]),
     "sa_hip_fill_pages_async": (C.c_int, [_P, _I64, _P, _P, _P, _I32, _P, _P]),
+    "sa_hip_fill_pages_gather_async": (C.c_int, [_P, _I64, _I64, _P, _P, _I64, _P, _I32, _P, _P, _P]),
     "sa_hip_stream_wait_event": (C.c_int, [_P, _P]),
     "sa_hip_fill_synthetic_f16": (C.c_int, [_P, _I64, C.c_uint64, C.c_uint64, _P]),
     "sa_hip_fill_synthetic_f32": (C.c_int, [_P, _I64, C.c_uint64, C.c_uint64, _P]),
@@ -302,6 +303,15 @@ def fill_pages_async(pool, page_bytes, dst_pages, src_base_ptr, src_blocks, copy
     check(lib().sa_hip_fill_pages_async(_ptr(pool), page_bytes, d.ctypes.data_as(_P), C.c_void_p(src_base_ptr),
                                         s.ctypes.data_as(_P), len(d), C.c_void_p(copy_stream.cuda_stream), ev),
           "fill_pages_async")
+
+
+def fill_pages_gather_async(pool, page_bytes, num_pages, dst_pages_dev, src_base_ptr, src_total, src_blocks_dev,
+                            count, copy_stream, done_event=None, status=None):
+    ev = None if done_event is None else C.c_void_p(done_event.cuda_event)
+    check(lib().sa_hip_fill_pages_gather_async(_ptr(pool), page_bytes, num_pages, _ptr(dst_pages_dev),
+                                               C.c_void_p(src_base_ptr), src_total, _ptr(src_blocks_dev), count,
+                                               _ptr(status), C.c_void_p(copy_stream.cuda_stream), ev),
+          "fill_pages_gather_async")
 
 
 def stream_wait_event(stream, event):

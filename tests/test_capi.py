@@ -88,3 +88,11 @@ def test_invalid_arguments_fail_before_any_launch():
     rc = L.sa_hip_score_select(C.byref(kv), C.c_void_p(16), C.byref(p), C.c_void_p(16), C.c_void_p(16), None,
                                None, None)
     assert rc == -1 and b"budget" in L.sa_hip_last_error()
+
+
+def test_loads_next_to_torch_hip_runtime():
+    """Inside a torch process the HIP runtime is torch's own libamdhip64; the
+    library must not need symbol versions newer than that runtime has."""
+    import torch  # noqa: F401  (loads torch's HIP runtime first)
+    import solidattention_amd as sa
+    C.CDLL(sa.LIB_PATH)

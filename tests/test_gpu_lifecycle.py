@@ -151,3 +151,41 @@ def test_miss_correction_copy_stream(hip):
         compute.synchronize()
         assert torch.equal(pool.cpu(), store[resident])
     assert misses_total == 24
+
+
+def test_miss_fill_gather_kernel_from_pinned_memory(hip):
+    """The one-launch fill reads pinned host pages through their device
+    mapping; slot bytes equal the store; bad pages are flagged, not read."""
+    rng = np.random.default_rng(8)
+    n_blocks, slots = 48, 20
+    page_elems = 32 * 2 * 8 * 128
+    store = torch.from_numpy(rng.integers(0, 65536, size=(n_blocks, page_elems)).astype(np.uint16).view(np.int16))
+    store = store.pin_memory()
+    pool = torch.zeros((slots, page_elems), dtype=torch.int16, device="cuda")
+    dst = np.array([3, 7, 0, 19, 11], np.int32)
+    src = np.array([40, 2, 17, 33, 5], np.int64)
+    copy_stream = torch.cuda.Stream()
+    done = torch.cuda.Event()
+    done.record(copy_stream)
+    st = status_tensor()
+    hip.fill_pages_gather_async(pool, page_elems * 2, slots, to_dev(dst), store.data_ptr(), n_blocks, to_dev(src),
+                                len(dst), copy_stream, done, status=st)
+    hip.stream_wait_event(torch.cuda.current_stream(), done)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    got = pool.cpu()
+    for d_, s_ in zip(dst, src):
+        assert torch.equal(got[d_], store[s_])
+    untouched = sorted(set(range(slots)) - set(dst.tolist()))
+    assert (got[untouched] == 0).all()
+    bad = np.array([slots + 5], np.int32)
+    hip.fill_pages_gather_async(pool, page_elems * 2, slots, to_dev(bad), store.data_ptr(), n_blocks, to_dev(src[:1]),
+                                1, copy_stream, done, status=st)
+    copy_stream.synchronize()
+    assert int(st.item()) & hip.STATUS_BAD_PAGE
+    st.zero_()
+    far = np.array([n_blocks + 3], np.int64)  # beyond the store: skipped, never read
+    hip.fill_pages_gather_async(pool, page_elems * 2, slots, to_dev(dst[:1]), store.data_ptr(), n_blocks, to_dev(far),
+                                1, copy_stream, done, status=st)
+    copy_stream.synchronize()
+    assert int(st.item()) & hip.STATUS_BAD_PAGE
