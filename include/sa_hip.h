@@ -74,13 +74,19 @@ typedef struct sa_paged_kv {
  *                  selected (the clamp of selection.py:120).
  *   init_blocks    always-selected leading blocks [0, init).
  *   local_blocks   always-selected trailing sealed blocks [n-local, n).
- *   sel_stride     row stride of the selected[] output (>= budget_blocks). */
+ *   sel_stride     row stride of the selected[] output (>= budget_blocks).
+ *   budgets        optional device array [batch] of per-sequence budgets
+ *                  (mixed-budget serving); each must lie in
+ *                  [init + local, sel_stride], otherwise that sequence selects
+ *                  nothing and status bit 16 is set.  NULL: budget_blocks. */
 typedef struct sa_select_params {
   int32_t select_groups;
   int32_t budget_blocks;
   int32_t init_blocks;
   int32_t local_blocks;
   int32_t sel_stride;
+  int32_t reserved;
+  const int32_t* budgets;
 } sa_select_params;
 
 /* ---- library ------------------------------------------------------------ */

@@ -291,6 +291,7 @@ int sa_hip_score_select(const sa_paged_kv* kv, const float* query, const sa_sele
   l.rep_stride = kv->rep_stride;
   l.select_groups = s.select_groups;
   l.budget = s.budget_blocks;
+  l.budgets = s.budgets;
   l.init_blocks = s.init_blocks;
   l.local_blocks = s.local_blocks;
   l.sel_stride = s.sel_stride;

@@ -21,6 +21,7 @@ enum StatusBits : int32_t {
   kStatusBadBlock = 2,      // logical block outside the table / sealed range
   kStatusBadLength = 4,     // seq_len / sealed inconsistent
   kStatusCapacity = 8,      // representative or table capacity exceeded
+  kStatusBadBudget = 16,    // per-sequence budget outside [init + local, sel_stride]
 };
 
 __device__ inline void flag_status(int32_t* status, int32_t bits) {

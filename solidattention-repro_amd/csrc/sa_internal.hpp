@@ -66,6 +66,7 @@ struct SelectLaunch {
   int32_t rep_stride;
   int32_t select_groups;
   int32_t budget;
+  const int32_t* budgets;
   int32_t init_blocks;
   int32_t local_blocks;
   int32_t sel_stride;

@@ -41,6 +41,7 @@ struct Params {
   int32_t select_groups;
   int32_t heads_per_sel;
   int32_t budget;
+  const int32_t* budgets;  // optional per-sequence budgets
   int32_t init_blocks;
   int32_t local_blocks;
   int32_t sel_stride;
@@ -144,10 +145,21 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   const int init_n = p.init_blocks < n ? p.init_blocks : n;
   const int local_n = p.local_blocks < n ? p.local_blocks : n;
   const int local_first = n - local_n;
-  const bool take_all = p.budget >= n;
+  int budget = p.budget;
+  if (p.budgets) {
+    budget = p.budgets[b];
+    if (budget < p.init_blocks + p.local_blocks || budget > p.sel_stride || budget <= 0) {
+      if (tid == 0) {
+        flag_status(p.status, kStatusBadBudget);
+        p.counts[out_row] = 0;
+      }
+      return;
+    }
+  }
+  const bool take_all = budget >= n;
   const int overlap = init_n > local_first ? init_n - local_first : 0;
   const int forced = init_n + local_n - overlap;
-  const int k = take_all ? 0 : p.budget - forced;
+  const int k = take_all ? 0 : budget - forced;
 
   // ---- radix select of the k-th best candidate key ------------------------
   uint32_t threshold = 0xffffffffu;
@@ -240,6 +252,7 @@ hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
   p.select_groups = s.select_groups;
   p.heads_per_sel = s.query_heads / s.select_groups;
   p.budget = s.budget;
+  p.budgets = s.budgets;
   p.init_blocks = s.init_blocks;
   p.local_blocks = s.local_blocks;
   p.sel_stride = s.sel_stride;

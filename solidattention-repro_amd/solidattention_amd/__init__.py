@@ -21,6 +21,7 @@ STATUS_BAD_PAGE = 1
 STATUS_BAD_BLOCK = 2
 STATUS_BAD_LENGTH = 4
 STATUS_CAPACITY = 8
+STATUS_BAD_BUDGET = 16
 
 
 class SaHipError(RuntimeError):
@@ -42,7 +43,7 @@ class SelectParamsStruct(C.Structure):
     """Mirror of sa_select_params (include/sa_hip.h)."""
     _fields_ = [("select_groups", C.c_int32), ("budget_blocks", C.c_int32),
                 ("init_blocks", C.c_int32), ("local_blocks", C.c_int32),
-                ("sel_stride", C.c_int32)]
+                ("sel_stride", C.c_int32), ("reserved", C.c_int32), ("budgets", C.c_void_p)]
 
 
 # name -> (restype, argtypes)
@@ -163,7 +164,8 @@ class PagedKV:
 
 
 def score_select(kv: PagedKV, query, select_groups, budget, init, local, selected=None, counts=None,
-                 scores=None, status=None, sel_stride=None, stream=None):
+                 scores=None, status=None, sel_stride=None, stream=None, budgets=None):
+    """budgets: optional device int32 [batch] of per-sequence budgets."""
     import torch
     sel_stride = sel_stride or budget
     dev = query.device
@@ -171,7 +173,8 @@ def score_select(kv: PagedKV, query, select_groups, budget, init, local, selecte
         selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
     if counts is None:
         counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
-    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
     s = kv.struct()
     check(lib().sa_hip_score_select(C.byref(s), _ptr(query), C.byref(params), _ptr(selected), _ptr(counts),
                                     _ptr(scores), _ptr(status), _stream(stream)), "score_select")
