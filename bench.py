@@ -54,6 +54,10 @@ def parse():
     ap.add_argument("--cpu-sample-seqs", type=int, default=0, help="sequences in the CPU sample (0 = auto)")
     ap.add_argument("--check-seqs", type=int, default=2, help="sequences parity-checked against the oracle")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (no HIP graph replay)")
+    ap.add_argument("--launches", type=int, default=1, choices=[1, 2, 3],
+                    help="kernel launches per layer: 1 = the fused decode step (append + seal + select + attend), "
+                         "2 = append_seal then the fused select + attend, 3 = append_seal, score_select, attention "
+                         "(1 and 2 fall back to 3 where the fused kernel does not apply)")
     ap.add_argument("--workload", default="decode", choices=["decode", "correction"],
                     help="decode: the headline decode step; correction: long-context miss correction "
                          "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage)")
@@ -147,18 +151,37 @@ def main():
     n_ev = total_steps * layers
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_ev)]
 
-    def step(s, record):
-        for l, ly in enumerate(L):
-            e = ev[s * layers + l] if record else None
-            if e: e[0].record(stream)
-            sa.append_seal(ly.kv, ly.knew[s], ly.vnew[s], 0, status=status)
-            if e: e[1].record(stream)
+    fusable = splits == 1 and sa.select_attend_fused(L[0].kv, hkv, splits)
+    launches = args.launches if fusable else 3
+    step_ws, _ = sa.decode_step_workspace(L[0].kv, splits)
+
+    def layer_launches(ly, s, e=None):
+        """One layer of one decode step; e = 4 timing events (append, select, attention)."""
+        if e: e[0].record(stream)
+        if launches == 1:
+            sa.decode_step(ly.kv, ly.knew[s], ly.vnew[s], 0, ly.q[s], hkv, budget, init, local, scale, step_ws,
+                           selected=ly.selected, counts=ly.counts, out=ly.out, splits=1, status=status)
+            if e:
+                for x in e[1:]:
+                    x.record(stream)
+            return
+        sa.append_seal(ly.kv, ly.knew[s], ly.vnew[s], 0, status=status)
+        if e: e[1].record(stream)
+        if launches == 2:
+            sa.select_attend(ly.kv, ly.q[s], hkv, budget, init, local, scale, selected=ly.selected,
+                             counts=ly.counts, out=ly.out, splits=1, status=status)
+            if e: e[2].record(stream)
+        else:
             sa.score_select(ly.kv, ly.q[s], hkv, budget, init, local, selected=ly.selected, counts=ly.counts,
                             status=status)
             if e: e[2].record(stream)
             sa.sparse_decode_attention(ly.kv, ly.q[s], ly.selected, ly.counts, scale, out=ly.out, splits=splits,
                                        workspace=workspace, status=status)
-            if e: e[3].record(stream)
+        if e: e[3].record(stream)
+
+    def step(s, record):
+        for l, ly in enumerate(L):
+            layer_launches(ly, s, ev[s * layers + l] if record else None)
 
     if args.calibrate_copy:
         # a plain copy of known size: PAGES x 128 KiB read and written once
@@ -219,21 +242,36 @@ def main():
     sel_us = 1000.0 * sum(sel) / len(sel)
     app_us = 1000.0 * sum(app) / len(app)
 
-    # attention launch duration for the roofline: back-to-back launches of the
-    # attention kernel of every layer (last step's inputs) between two events
-    # on the bench stream, so the figure matches the kernel trace's average
+    # duration of the dominant kernel for the roofline: back-to-back launches
+    # of that kernel for every layer between two events on the bench stream,
+    # so the figure matches the kernel trace's average.  1 launch: the decode
+    # step kernel (one more token appended per launch; the tables have room);
+    # 2: the select+attend kernel; 3: the attention kernel.  Each reads the
+    # selected pages; 1 and 2 also the representatives of every sealed block.
     reps = 4
     s_last = last_step
     start.record(stream)
     for _ in range(reps):
         for ly in L:
-            sa.sparse_decode_attention(ly.kv, ly.q[s_last], ly.selected, ly.counts, scale, out=ly.out,
-                                       splits=splits, workspace=workspace, status=status)
+            if launches == 1:
+                sa.decode_step(ly.kv, ly.knew[s_last], ly.vnew[s_last], 0, ly.q[s_last], hkv, budget, init, local,
+                               scale, step_ws, selected=ly.selected, counts=ly.counts, out=ly.out, splits=1,
+                               status=status)
+            elif launches == 2:
+                sa.select_attend(ly.kv, ly.q[s_last], hkv, budget, init, local, scale, selected=ly.selected,
+                                 counts=ly.counts, out=ly.out, splits=1, status=status)
+            else:
+                sa.sparse_decode_attention(ly.kv, ly.q[s_last], ly.selected, ly.counts, scale, out=ly.out,
+                                           splits=splits, workspace=workspace, status=status)
     end.record(stream)
     torch.cuda.synchronize()
-    att_kernel_us = 1000.0 * start.elapsed_time(end) / (reps * layers)
+    if int(status.item()) != 0:
+        raise SystemExit(f"device status flagged {int(status.item())}")
+    kernel_us = 1000.0 * start.elapsed_time(end) / (reps * layers)
 
-    # algorithmic bytes of one attention launch: selected KV + tail KV + q + out + ids/table entries
+    # algorithmic bytes of one launch: selected KV + tail KV + q + out + ids,
+    # plus the fp32 representatives of every sealed block (select+attend) and
+    # the appended token (decode step: fp32 K/V read, FP16 K/V written)
     seq_len = L[-1].kv.seq_len.cpu().numpy().astype(np.int64)
     sealed = L[-1].kv.sealed.cpu().numpy().astype(np.int64)
     counts = L[-1].counts.cpu().numpy().astype(np.int64)
@@ -242,12 +280,18 @@ def main():
     att_bytes = int(counts.sum() * PAGE * kv_tok_bytes + (tail.sum() * hkv) * kv_tok_bytes +
                     batch * hq * D * 4 * 2 + counts.sum() * 8)
     rep_bytes = int(sealed.sum() * hkv * D * 4)
-    layer_bytes = att_bytes + rep_bytes
-    achieved = att_bytes / (att_kernel_us * 1e-6) / 1e9
+    append_bytes = batch * hkv * D * 2 * (4 + 2)
+    layer_bytes = att_bytes + rep_bytes + append_bytes
+    kernel_bytes = {1: layer_bytes, 2: att_bytes + rep_bytes, 3: att_bytes}[launches]
+    achieved = kernel_bytes / (kernel_us * 1e-6) / 1e9
     layer_gbps = layer_bytes / (us_per_layer * 1e-6) / 1e9
-    log(f"attention {att_kernel_us:.2f} us back-to-back ({achieved:.0f} GB/s; {att_us:.2f} us event-bracketed in "
-        f"the step), select {sel_us:.2f} us, append {app_us:.2f} us, layer {us_per_layer:.2f} us")
-    traffic = measured_traffic(args.config, splits)
+    log(f"{launches} launch(es) per layer: dominant kernel {kernel_us:.2f} us back-to-back ({achieved:.0f} GB/s); "
+        f"event-bracketed append {app_us:.2f} / select {sel_us:.2f} / attention {att_us:.2f} us; "
+        f"layer {us_per_layer:.2f} us")
+    grp = hq // hkv
+    kernel_name = {1: f"decode_kernel<{grp},{grp},true,false>", 2: f"decode_kernel<{grp},{grp},false,false>",
+                   3: f"sparse_decode_attention_kernel<{grp}>"}[launches]
+    traffic = measured_traffic(args.config, kernel_name)
 
     parity = check_parity(sa, np, torch, L[-1], args, scale, hkv, budget, init, local, last_step)
     cpu = None if args.no_cpu_baseline else cpu_baseline(np, torch, L[0], args, budget, init, local, scale)
@@ -268,32 +312,38 @@ def main():
         "config": {"workload": f"{model} attention shape decode step: append+seal, score+select, sparse GQA "
                                f"attention", "layers": layers, "batch": batch, "query_heads": hq,
                    "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
-                   "init_blocks": init, "local_blocks": local, "page_tokens": PAGE, "splits": splits},
+                   "init_blocks": init, "local_blocks": local, "page_tokens": PAGE, "splits": splits,
+                   "launches_per_layer": launches},
         "tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
         "launch": "hip graph per decode step" if graph else "eager",
         "eager_us_per_layer": round(eager_ms * 1000.0 / args.steps / layers, 3),
         "achieved_layer_hbm_gbps": round(layer_gbps, 1),
-        "kernels_us": {"attention": round(att_kernel_us, 3), "attention_in_step": round(att_us, 3),
-                       "score_select": round(sel_us, 3), "append_seal": round(app_us, 3)},
+        "kernels_us": ({"decode_step": round(kernel_us, 3), "decode_step_in_step": round(app_us, 3)}
+                       if launches == 1 else
+                       {"select_attend": round(kernel_us, 3), "select_attend_in_step": round(sel_us, 3),
+                        "append_seal": round(app_us, 3)} if launches == 2 else
+                       {"attention": round(kernel_us, 3), "attention_in_step": round(att_us, 3),
+                        "score_select": round(sel_us, 3), "append_seal": round(app_us, 3)}),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": f"sparse_decode_attention_kernel<{hq // hkv}>", "algorithmic_bytes": att_bytes,
-                     "launch_us": round(att_kernel_us, 3)},
+                     "kernel": kernel_name, "algorithmic_bytes": kernel_bytes,
+                     "launch_us": round(kernel_us, 3)},
         "parity": parity,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
 
-def measured_traffic(config, splits):
-    """HBM bytes per attention launch from the committed rocprofv3 --pmc
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
     summary for this workload (FETCH_SIZE scaled by the copy-kernel
     calibration, plus WRITE_SIZE); None when no summary matches."""
-    path = os.path.join(ROOT, "profiles", "sparse_decode_attention_qwen3-0.6b_b64_16k.traffic.json")
-    if config != "qwen3-0.6b-b64-16k" or splits != 1 or not os.path.exists(path):
+    path = os.path.join(ROOT, "profiles", f"decode_step_{config}.traffic.json")
+    if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        entry = json.load(f).get("kernels", {}).get(kernel)
+    return None if entry is None else entry.get("traffic_bytes_per_launch")
 
 
 def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local, s):

@@ -179,6 +179,63 @@ int sa_hip_score_select(const sa_paged_kv* kv, const float* query,
                         int32_t* counts, float* scores, int32_t* status,
                         void* stream);
 
+/* ---- R3 + R6 fused: one layer's select-then-attend ----------------------- */
+
+/* sa_hip_score_select(kv, query, params, selected, counts, NULL, status)
+ * followed by sa_hip_sparse_decode_attention(kv, query, selected, counts,
+ * params->select_groups, params->sel_stride, scale, out, workspace,
+ * workspace_bytes, splits, status): the same selected ids and counts (bit-
+ * exact) and the same attention output (within fp32 rounding).  When
+ * sa_hip_select_attend_fused() is 1 (select_groups == kv_heads, 1 or 2 query
+ * heads per KV head, splits == 1) it runs as ONE launch, one workgroup per
+ * (sequence, KV head) that scores, selects, keeps the ids on chip and
+ * attends; otherwise as the two launches.  splits >= 1; workspace as for
+ * sa_hip_sparse_decode_attention.  Replaces the reference's per-layer
+ * select -> pack -> attention sequence (selection_main.cpp:178-230;
+ * pipeline_main.cpp:803-876) with selection on the GPU. */
+int sa_hip_select_attend_fused(const sa_paged_kv* kv,
+                               const sa_select_params* params, int32_t splits);
+int sa_hip_select_attend(const sa_paged_kv* kv, const float* query,
+                         const sa_select_params* params, float scale,
+                         int32_t* selected, int32_t* counts, float* out,
+                         void* workspace, size_t workspace_bytes,
+                         int32_t splits, int32_t* status, void* stream);
+
+/* ---- R8/R9/R4 + R3 + R6 fused: one layer's whole decode step ------------- */
+
+/* Workspace of sa_hip_decode_step: `batch` int32 arrival counters (padded
+ * to 256 bytes) followed by the attention's split records.  The caller
+ * zeroes it ONCE before the first call; every call leaves the counters at
+ * zero again.  Calls sharing a workspace must not run concurrently. */
+size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv,
+                                          int32_t splits);
+
+/* sa_hip_append_seal(kv, k, v, local_tokens) followed by
+ * sa_hip_select_attend(kv, query, params, scale, selected, counts, out, ...):
+ * the same page bytes, representatives, seq_len/sealed/generation, selected
+ * ids (bit-exact) and attention output (within fp32 rounding).  When
+ * sa_hip_select_attend_fused() is 1 it is ONE launch: each (sequence, KV
+ * head) workgroup appends and seals its own head, then scores, selects and
+ * attends; the last workgroup of a sequence to arrive writes its counters.
+ * Otherwise it runs the three launches.  The _f16 variant takes raw FP16
+ * K/V bits like sa_hip_append_seal_f16.  Replaces the reference's per-layer
+ * decode sequence of append_fp16_kv (qwen_layer_main.cpp:270-281 via
+ * qwen_chain_main.cpp:390-391), the tail seal (kv_lifecycle_main.cpp:92-113),
+ * select_shared_blocks and the sparse attention (qwen_chain_main.cpp:393-395). */
+int sa_hip_decode_step(const sa_paged_kv* kv, const float* k, const float* v,
+                       int32_t local_tokens, const float* query,
+                       const sa_select_params* params, float scale,
+                       int32_t* selected, int32_t* counts, float* out,
+                       void* workspace, size_t workspace_bytes,
+                       int32_t splits, int32_t* status, void* stream);
+int sa_hip_decode_step_f16(const sa_paged_kv* kv, const uint16_t* k,
+                           const uint16_t* v, int32_t local_tokens,
+                           const float* query, const sa_select_params* params,
+                           float scale, int32_t* selected, int32_t* counts,
+                           float* out, void* workspace,
+                           size_t workspace_bytes, int32_t splits,
+                           int32_t* status, void* stream);
+
 /* ---- R8/R9/R4: decode append, seal, representative ---------------------- */
 
 /* Append one token per sequence at position seq_len[b] (fp32 K/V converted

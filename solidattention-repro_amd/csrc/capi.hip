@@ -257,45 +257,175 @@ int sa_hip_consume_checksum(const float* input, int32_t elements, float* checksu
 
 // ---- selection ---------------------------------------------------------------
 
-int sa_hip_score_select(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
-                        int32_t* selected, int32_t* counts, float* scores, int32_t* status, void* stream) {
-  if (int e = check_geometry(kv, "score_select")) return e;
-  if (int e = check_reps(kv, "score_select")) return e;
+static int lifecycle_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
+                            const uint16_t* v16, int32_t local_tokens, int append, int32_t* status,
+                            void* stream, const char* op);
+
+static int select_launch(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
+                         int32_t* selected, int32_t* counts, float* scores, int32_t* status, const char* op,
+                         sa::SelectLaunch* l) {
+  if (int e = check_geometry(kv, op)) return e;
+  if (int e = check_reps(kv, op)) return e;
   if (!params || !query || !selected || !counts)
-    return fail(SA_HIP_EINVAL, "score_select: null params/query/selected/counts");
+    return fail(SA_HIP_EINVAL, "%s: null params/query/selected/counts", op);
   const sa_select_params& s = *params;
   if (s.select_groups <= 0 || kv->kv_heads % s.select_groups != 0)
-    return fail(SA_HIP_EINVAL, "score_select: select_groups must divide kv_heads");
+    return fail(SA_HIP_EINVAL, "%s: select_groups must divide kv_heads", op);
   const int heads_per_sel = kv->query_heads / s.select_groups;
   if (heads_per_sel > sa::kMaxSelectHeads)
-    return fail(SA_HIP_EINVAL, "score_select: %d query heads per selection group exceeds %d", heads_per_sel,
+    return fail(SA_HIP_EINVAL, "%s: %d query heads per selection group exceeds %d", op, heads_per_sel,
                 sa::kMaxSelectHeads);
   if (s.budget_blocks <= 0 || s.init_blocks < 0 || s.local_blocks < 0 ||
       s.init_blocks + s.local_blocks > s.budget_blocks)
-    return fail(SA_HIP_EINVAL, "score_select: invalid representative selection dimensions "
-                               "(budget %d, init %d, local %d)", s.budget_blocks, s.init_blocks, s.local_blocks);
+    return fail(SA_HIP_EINVAL, "%s: invalid representative selection dimensions "
+                               "(budget %d, init %d, local %d)", op, s.budget_blocks, s.init_blocks, s.local_blocks);
   if (s.sel_stride < s.budget_blocks)
-    return fail(SA_HIP_EINVAL, "score_select: sel_stride %d < budget %d", s.sel_stride, s.budget_blocks);
-  sa::SelectLaunch l{};
-  l.query = query;
-  l.reps = kv->reps;
-  l.sealed = kv->sealed;
-  l.selected = selected;
-  l.counts = counts;
-  l.scores = scores;
-  l.status = status;
-  l.batch = kv->batch;
-  l.query_heads = kv->query_heads;
-  l.kv_heads = kv->kv_heads;
-  l.rep_heads = kv->rep_heads;
-  l.rep_stride = kv->rep_stride;
-  l.select_groups = s.select_groups;
-  l.budget = s.budget_blocks;
-  l.budgets = s.budgets;
-  l.init_blocks = s.init_blocks;
-  l.local_blocks = s.local_blocks;
-  l.sel_stride = s.sel_stride;
+    return fail(SA_HIP_EINVAL, "%s: sel_stride %d < budget %d", op, s.sel_stride, s.budget_blocks);
+  *l = sa::SelectLaunch{};
+  l->query = query;
+  l->reps = kv->reps;
+  l->sealed = kv->sealed;
+  l->selected = selected;
+  l->counts = counts;
+  l->scores = scores;
+  l->status = status;
+  l->batch = kv->batch;
+  l->query_heads = kv->query_heads;
+  l->kv_heads = kv->kv_heads;
+  l->rep_heads = kv->rep_heads;
+  l->rep_stride = kv->rep_stride;
+  l->select_groups = s.select_groups;
+  l->budget = s.budget_blocks;
+  l->budgets = s.budgets;
+  l->init_blocks = s.init_blocks;
+  l->local_blocks = s.local_blocks;
+  l->sel_stride = s.sel_stride;
+  return SA_HIP_OK;
+}
+
+int sa_hip_score_select(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
+                        int32_t* selected, int32_t* counts, float* scores, int32_t* status, void* stream) {
+  sa::SelectLaunch l;
+  if (int e = select_launch(kv, query, params, selected, counts, scores, status, "score_select", &l)) return e;
   return check_hip(sa::launch_score_select(l, as_stream(stream)), "score_select launch");
+}
+
+int sa_hip_select_attend_fused(const sa_paged_kv* kv, const sa_select_params* params, int32_t splits) {
+  if (!kv || !params) return 0;
+  return splits == 1 && sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups) ? 1 : 0;
+}
+
+static sa::SelectAttendLaunch fused_launch(const sa_paged_kv* kv, const sa::SelectLaunch& l, float scale,
+                                           float* out) {
+  sa::SelectAttendLaunch f{};
+  f.pool = kv->pool;
+  f.table = kv->block_table;
+  f.seq_len = kv->seq_len;
+  f.sealed = kv->sealed;
+  f.generation = kv->generation;
+  f.reps = kv->reps;
+  f.query = l.query;
+  f.selected = l.selected;
+  f.counts = l.counts;
+  f.out = out;
+  f.status = l.status;
+  f.num_pages = kv->num_pages;
+  f.batch = kv->batch;
+  f.table_stride = kv->table_stride;
+  f.query_heads = kv->query_heads;
+  f.kv_heads = kv->kv_heads;
+  f.rep_heads = kv->rep_heads;
+  f.rep_stride = kv->rep_stride;
+  f.budget = l.budget;
+  f.budgets = l.budgets;
+  f.init_blocks = l.init_blocks;
+  f.local_blocks = l.local_blocks;
+  f.sel_stride = l.sel_stride;
+  f.scale = scale;
+  return f;
+}
+
+int sa_hip_select_attend(const sa_paged_kv* kv, const float* query, const sa_select_params* params, float scale,
+                         int32_t* selected, int32_t* counts, float* out, void* workspace, size_t workspace_bytes,
+                         int32_t splits, int32_t* status, void* stream) {
+  sa::SelectLaunch l;
+  if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, "select_attend", &l)) return e;
+  if (!out) return fail(SA_HIP_EINVAL, "select_attend: null out");
+  if (!aligned16(query)) return fail(SA_HIP_EINVAL, "select_attend: query must be 16-byte aligned");
+  if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "select_attend: splits out of range");
+  if (!sa_hip_select_attend_fused(kv, params, splits)) {
+    if (int e = check_hip(sa::launch_score_select(l, as_stream(stream)), "select_attend: score_select launch"))
+      return e;
+    return attention_common(kv, query, selected, counts, params->select_groups, params->sel_stride, scale, out,
+                            workspace, workspace_bytes, splits, status, stream, 0);
+  }
+  const sa::SelectAttendLaunch f = fused_launch(kv, l, scale, out);
+  return check_hip(sa::launch_select_attend(f, as_stream(stream)), "select_attend launch");
+}
+
+// Decode-step workspace: [batch] int32 arrival counters (padded to 256 B),
+// then the attention's split records when the step is not fused.
+static size_t arrive_bytes(int32_t batch) { return (static_cast<size_t>(batch) * 4 + 255) / 256 * 256; }
+
+size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv, int32_t splits) {
+  if (!kv || kv->batch <= 0) return 0;
+  return arrive_bytes(kv->batch) +
+         sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
+}
+
+static int decode_step_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
+                              const uint16_t* v16, int32_t local_tokens, const float* query,
+                              const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
+                              float* out, void* workspace, size_t workspace_bytes, int32_t splits, int32_t* status,
+                              void* stream, const char* op) {
+  sa::SelectLaunch l;
+  if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, op, &l)) return e;
+  if (!out) return fail(SA_HIP_EINVAL, "%s: null out", op);
+  if (!aligned16(query)) return fail(SA_HIP_EINVAL, "%s: query must be 16-byte aligned", op);
+  if (local_tokens < 0) return fail(SA_HIP_EINVAL, "%s: local_tokens must be >= 0", op);
+  if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "%s: splits out of range", op);
+  const void* ka = k16 ? static_cast<const void*>(k16) : static_cast<const void*>(k);
+  const void* va = v16 ? static_cast<const void*>(v16) : static_cast<const void*>(v);
+  if (!ka || !va) return fail(SA_HIP_EINVAL, "%s: null k/v", op);
+  if (!aligned16(ka) || !aligned16(va)) return fail(SA_HIP_EINVAL, "%s: k/v must be 16-byte aligned", op);
+  const size_t need = sa_hip_decode_step_workspace_bytes(kv, splits);
+  if (!workspace || workspace_bytes < need)
+    return fail(SA_HIP_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, need, workspace_bytes);
+  if (!aligned16(workspace)) return fail(SA_HIP_EINVAL, "%s: workspace must be 16-byte aligned", op);
+  const size_t ab = arrive_bytes(kv->batch);
+  if (!sa_hip_select_attend_fused(kv, params, splits)) {
+    if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op)) return e;
+    if (int e = check_hip(sa::launch_score_select(l, as_stream(stream)), "decode_step: score_select launch"))
+      return e;
+    return attention_common(kv, query, selected, counts, params->select_groups, params->sel_stride, scale, out,
+                            static_cast<uint8_t*>(workspace) + ab, workspace_bytes - ab, splits, status, stream, 0);
+  }
+  sa::SelectAttendLaunch f = fused_launch(kv, l, scale, out);
+  f.append = 1;
+  f.local_tokens = local_tokens;
+  f.k = k;
+  f.v = v;
+  f.k16 = k16;
+  f.v16 = v16;
+  f.arrive = static_cast<int32_t*>(workspace);
+  return check_hip(sa::launch_select_attend(f, as_stream(stream)), "decode_step launch");
+}
+
+int sa_hip_decode_step(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
+                       const float* query, const sa_select_params* params, float scale, int32_t* selected,
+                       int32_t* counts, float* out, void* workspace, size_t workspace_bytes, int32_t splits,
+                       int32_t* status, void* stream) {
+  return decode_step_common(kv, k, v, nullptr, nullptr, local_tokens, query, params, scale, selected, counts, out,
+                            workspace, workspace_bytes, splits, status, stream, "decode_step");
+}
+
+int sa_hip_decode_step_f16(const sa_paged_kv* kv, const uint16_t* k, const uint16_t* v, int32_t local_tokens,
+                           const float* query, const sa_select_params* params, float scale, int32_t* selected,
+                           int32_t* counts, float* out, void* workspace, size_t workspace_bytes, int32_t splits,
+                           int32_t* status, void* stream) {
+  if (!k || !v) return fail(SA_HIP_EINVAL, "decode_step_f16: null k/v");
+  return decode_step_common(kv, nullptr, nullptr, k, v, local_tokens, query, params, scale, selected, counts, out,
+                            workspace, workspace_bytes, splits, status, stream, "decode_step_f16");
 }
 
 // ---- append / seal -------------------------------------------------------------

@@ -74,6 +74,48 @@ struct SelectLaunch {
 
 hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream);
 
+// Fused (append + seal +) score + select + attend, one workgroup per
+// (sequence, KV head); select_groups is kv_heads.  Supported for 1 or 2
+// query heads per KV head.
+struct SelectAttendLaunch {
+  const uint16_t* pool;
+  const int32_t* table;
+  int32_t* seq_len;
+  int32_t* sealed;
+  int32_t* generation;
+  float* reps;
+  const float* query;
+  int32_t* selected;
+  int32_t* counts;
+  float* out;
+  int32_t* status;
+  int64_t num_pages;
+  int32_t batch;
+  int32_t table_stride;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t rep_heads;
+  int32_t rep_stride;
+  int32_t budget;
+  const int32_t* budgets;
+  int32_t init_blocks;
+  int32_t local_blocks;
+  int32_t sel_stride;
+  float scale;
+  // decode step: append one token per sequence (fp32 k/v or FP16 k16/v16),
+  // seal, then select + attend; arrive = [batch] zeroed arrival counters
+  int32_t append;
+  int32_t local_tokens;
+  const float* k;
+  const float* v;
+  const uint16_t* k16;
+  const uint16_t* v16;
+  int32_t* arrive;
+};
+
+bool select_attend_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups);
+hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream);
+
 struct LifecycleLaunch {
   uint16_t* pool;
   const int32_t* table;

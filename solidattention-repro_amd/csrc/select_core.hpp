@@ -1,0 +1,340 @@
+// select_core.hpp — device building blocks of block-representative scoring
+// and budgeted top-k selection (gfx950), bit-exact with the reference's
+// select_shared_blocks (cpp/src/selection.cpp:96-147) applied to each
+// selection group.  Shared by the selection kernel and the fused
+// select + attend kernel.  The including translation unit must be compiled
+// with -ffp-contract=off (every product and sum rounded separately, as in the
+// g++-built reference, which contains no FMA).
+//
+// Scoring: one lane per block.  Representatives are stored head_dim-major
+// ([rep head][d][block]), so for a fixed d the lanes of a wave read 64
+// consecutive floats (coalesced) while each lane keeps the reference's
+// sequential per-(head, block) dot order (selection.cpp:108-118).
+//
+// Selection: scores become order-preserving 32-bit keys (with -0.0 folded
+// onto +0.0, since the reference's `>` comparator treats them as equal).  A
+// 4-pass 8-bit radix select finds the key T of the k-th best candidate; all
+// candidates above T are taken plus the lowest-id candidates equal to T, which
+// is exactly what a stable descending sort followed by a greedy fill picks
+// (selection.cpp:128-142).  Output ids are compacted in ascending order with
+// wave ballots (selection.cpp:143-145).
+#pragma once
+
+#include "sa_device.hpp"
+#include "sa_internal.hpp"
+
+namespace sa {
+namespace sel {
+
+constexpr int D = kHeadDim;
+
+__device__ inline uint32_t order_key(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u << 1) == 0u) u = 0u;  // -0.0 and +0.0 compare equal
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Where the representatives and query of one (sequence, selection group) are.
+struct ScoreArgs {
+  const float* query;   // [batch][query_heads][D]
+  const float* reps;    // [batch][rep_heads][D][rep_stride]
+  int32_t b;
+  int32_t h_first;      // first query head of the group
+  int32_t heads_per_sel;
+  int32_t query_heads;
+  int32_t group;        // query heads per KV head
+  int32_t rep_heads;
+  int32_t rep_stride;
+};
+
+// q rows of the group's heads into LDS (q_s: heads_per_sel * D floats).
+template <int kThreads>
+__device__ inline void load_query(const ScoreArgs& a, float* q_s) {
+  const float* q = a.query + (static_cast<int64_t>(a.b) * a.query_heads + a.h_first) * D;
+  for (int e = threadIdx.x; e < a.heads_per_sel * D; e += kThreads) q_s[e] = q[e];
+}
+
+// keys[blk] = order_key(score of block blk) for blk < n; scores (optional)
+// receives the fp32 scores.  GR = query heads sharing one representative row
+// (the group size when representatives are per KV head, else 1).  q_s must
+// be visible to the workgroup.
+template <int GR, int kThreads>
+__device__ inline void score_blocks(const ScoreArgs& a, const float* q_s, int n, uint32_t* keys, float* scores) {
+  const float heads_f = static_cast<float>(a.heads_per_sel);
+  constexpr int kBatch = 64;
+  // One block per lane.  The 128 representative values of a block are loaded
+  // in two batches of 64 independent loads before the sequential chains run,
+  // so the latency of the HBM reads is paid twice per block, not per d.
+  for (int blk = threadIdx.x; blk < n; blk += kThreads) {
+    // An opaque zero offset keeps the query reads inside the loop: hoisted
+    // out of it, the heads_per_sel x 128 query values would be held in
+    // registers (and spilled) across all blocks of the lane.
+    int qoff = 0;
+    asm volatile("" : "+s"(qoff));
+    float score = 0.0f;
+    for (int h0 = 0; h0 < a.heads_per_sel; h0 += GR) {
+      const int h = a.h_first + h0;
+      const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
+      const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * a.rep_stride + blk;
+      float dot[GR];
+#pragma unroll
+      for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
+#pragma unroll
+      for (int d0 = 0; d0 < D; d0 += kBatch) {
+        float rv[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) rv[k] = load_stream_f32(r + static_cast<int64_t>(d0 + k) * a.rep_stride);
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+#pragma unroll
+          for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[qoff + (h0 + j) * D + d0 + k] * rv[k];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
+    }
+    keys[blk] = order_key(score);
+    if (scores) scores[blk] = score;
+  }
+}
+
+// The budget split of one selection: forced blocks [0, init_n) and
+// [local_first, n), k dynamic picks among the rest (0 when all are taken).
+struct Budget {
+  int init_n;
+  int local_first;
+  int k;
+  bool take_all;
+  bool bad;  // per-sequence budget outside [init + local, sel_stride]
+};
+
+__device__ inline Budget budget_split(int n, int budget, const int32_t* budgets, int b, int init_blocks,
+                                      int local_blocks, int sel_stride) {
+  Budget r{};
+  if (budgets) {
+    budget = budgets[b];
+    if (budget < init_blocks + local_blocks || budget > sel_stride || budget <= 0) {
+      r.bad = true;
+      return r;
+    }
+  }
+  r.init_n = init_blocks < n ? init_blocks : n;
+  const int local_n = local_blocks < n ? local_blocks : n;
+  r.local_first = n - local_n;
+  r.take_all = budget >= n;
+  const int overlap = r.init_n > r.local_first ? r.init_n - r.local_first : 0;
+  const int forced = r.init_n + local_n - overlap;
+  r.k = r.take_all ? 0 : budget - forced;
+  return r;
+}
+
+// LDS of the radix select and the compaction.
+template <int kWaves>
+struct SelectSmem {
+  uint32_t hist[2][256];
+  int counts[2][2][kWaves];
+  uint32_t prefix;
+  uint32_t remaining;
+};
+
+// Key T of the k-th best candidate among blocks [init_n, local_first)
+// (k > 0) and how many candidates equal to T the selection takes.  4 passes
+// of 8 bits; the histogram of the next pass is cleared while the current
+// one fills, so each pass costs two workgroup barriers.  All threads call it.
+template <int kThreads>
+__device__ inline void radix_threshold(const uint32_t* keys, const Budget& bs, SelectSmem<kThreads / kWave>& sm,
+                                       uint32_t& threshold, uint32_t& equal_take) {
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  for (int e = tid; e < 256; e += kThreads) sm.hist[0][e] = 0;
+  __syncthreads();
+  uint32_t prefix = 0, mask = 0, remaining = static_cast<uint32_t>(bs.k);
+  int buf = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int blk = bs.init_n + tid; blk < bs.local_first; blk += kThreads) {
+      const uint32_t key = keys[blk];
+      if ((key & mask) == prefix) atomicAdd(&sm.hist[buf][(key >> shift) & 255u], 1u);
+    }
+    for (int e = tid; e < 256; e += kThreads) sm.hist[buf ^ 1][e] = 0;
+    __syncthreads();
+    if (tid < kWave) {
+      // lane covers digits 255-4*lane .. 252-4*lane (descending)
+      uint32_t c[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[q] = sm.hist[buf][255 - 4 * lane - q];
+      const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+      uint32_t incl = mine;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t t = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += t;
+      }
+      uint32_t before = incl - mine;  // candidates in higher digits
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (before < remaining && before + c[q] >= remaining) {
+          sm.prefix = prefix | (static_cast<uint32_t>(255 - 4 * lane - q) << shift);
+          sm.remaining = remaining - before;
+        }
+        before += c[q];
+      }
+    }
+    __syncthreads();
+    prefix = sm.prefix;
+    remaining = sm.remaining;
+    mask |= 255u << shift;
+    buf ^= 1;
+  }
+  threshold = prefix;
+  equal_take = remaining;
+}
+
+// Ascending compaction of the selected ids into out_ids (global, row of
+// sel_stride) and, when lds_ids is non-null, into lds_ids as well (which may
+// alias keys: an id is written at a position <= its block, after every key
+// of its 512-block chunk has been read).  One barrier per chunk.  Returns the
+// number of selected blocks (clamped to sel_stride).  All threads call it.
+template <int kThreads>
+__device__ inline int compact_ids(const uint32_t* keys, int n, const Budget& bs, uint32_t threshold,
+                                  uint32_t equal_take, int32_t* out_ids, int sel_stride, int32_t* lds_ids,
+                                  SelectSmem<kThreads / kWave>& sm) {
+  constexpr int kWaves = kThreads / kWave;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  int taken_eq = 0, written = 0, par = 0;
+  for (int base = 0; base < n; base += kThreads) {
+    const int blk = base + tid;
+    const bool valid = blk < n;
+    const bool is_forced = valid && (bs.take_all || blk < bs.init_n || blk >= bs.local_first);
+    const uint32_t key = valid ? keys[blk] : 0u;
+    const bool cand = valid && !is_forced && bs.k > 0;
+    const bool is_eq = cand && key == threshold;
+    const bool sure = is_forced || (cand && key > threshold);
+    const uint64_t m_sure = __ballot(sure);
+    const uint64_t m_eq = __ballot(is_eq);
+    if (lane == 0) {
+      sm.counts[par][0][wave] = __popcll(m_sure);
+      sm.counts[par][1][wave] = __popcll(m_eq);
+    }
+    __syncthreads();
+    // every wave derives every wave's take count: the sure blocks plus as
+    // many of its equal-key blocks as the lowest-id-first rule leaves room for
+    int eq_off = 0, take_off = 0, eq_tot = 0, take_tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int cs = sm.counts[par][0][w];
+      const int ce = sm.counts[par][1][w];
+      int room = static_cast<int>(equal_take) - taken_eq - eq_tot;
+      room = room < 0 ? 0 : (room > ce ? ce : room);
+      const int tw = cs + room;
+      if (w < wave) {
+        eq_off += ce;
+        take_off += tw;
+      }
+      eq_tot += ce;
+      take_tot += tw;
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    const int eq_rank = taken_eq + eq_off + __popcll(m_eq & below);
+    const bool take = sure || (is_eq && eq_rank < static_cast<int>(equal_take));
+    const uint64_t m_take = __ballot(take);
+    const int pos = written + take_off + __popcll(m_take & below);
+    if (take && pos < sel_stride) {
+      out_ids[pos] = blk;
+      if (lds_ids) lds_ids[pos] = blk;
+    }
+    taken_eq += eq_tot;
+    written += take_tot;
+    par ^= 1;
+  }
+  return written < sel_stride ? written : sel_stride;
+}
+
+// ---- single-wave variants ----------------------------------------------------
+// The same radix select and compaction run by ONE wave with no workgroup
+// barrier, so the other waves of the workgroup can stream pages meanwhile.
+// LDS operations of one wave execute in program order; the workgroup fences
+// below only make the compiler wait for them.
+
+__device__ inline void lds_order() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup"); }
+
+__device__ inline void radix_threshold_wave(const uint32_t* keys, const Budget& bs, uint32_t* hist,
+                                            uint32_t& threshold, uint32_t& equal_take) {
+  const int lane = threadIdx.x % kWave;
+  uint32_t prefix = 0, mask = 0, remaining = static_cast<uint32_t>(bs.k);
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int e = lane; e < 256; e += kWave) hist[e] = 0;
+    lds_order();
+    for (int blk = bs.init_n + lane; blk < bs.local_first; blk += kWave) {
+      const uint32_t key = keys[blk];
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    lds_order();
+    // lane covers digits 255-4*lane .. 252-4*lane (descending)
+    uint32_t c[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c[q] = hist[255 - 4 * lane - q];
+    const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+    uint32_t incl = mine;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t t = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += t;
+    }
+    uint32_t before = incl - mine;
+    uint32_t digit = 0, rem = 0;
+    bool found = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (before < remaining && before + c[q] >= remaining) {
+        digit = 255 - 4 * lane - q;
+        rem = remaining - before;
+        found = true;
+      }
+      before += c[q];
+    }
+    // exactly one lane finds the digit (0 < remaining <= candidates left)
+    const uint64_t fm = __ballot(found);
+    const int src = fm ? __builtin_ctzll(fm) : 0;
+    prefix |= static_cast<uint32_t>(__shfl(static_cast<int>(digit), src, kWave)) << shift;
+    remaining = static_cast<uint32_t>(__shfl(static_cast<int>(rem), src, kWave));
+    mask |= 255u << shift;
+    lds_order();
+  }
+  threshold = prefix;
+  equal_take = remaining;
+}
+
+// Single-wave ascending compaction; lds_ids may alias keys (an id lands at a
+// position <= its block after the keys of its 64-block chunk were read).
+__device__ inline int compact_ids_wave(const uint32_t* keys, int n, const Budget& bs, uint32_t threshold,
+                                       uint32_t equal_take, int32_t* out_ids, int sel_stride, int32_t* lds_ids) {
+  const int lane = threadIdx.x % kWave;
+  const uint64_t below = (1ull << lane) - 1ull;
+  int taken_eq = 0, written = 0;
+  for (int base = 0; base < n; base += kWave) {
+    const int blk = base + lane;
+    const bool valid = blk < n;
+    const bool is_forced = valid && (bs.take_all || blk < bs.init_n || blk >= bs.local_first);
+    const uint32_t key = valid ? keys[blk] : 0u;
+    const bool cand = valid && !is_forced && bs.k > 0;
+    const bool is_eq = cand && key == threshold;
+    const bool sure = is_forced || (cand && key > threshold);
+    const uint64_t m_eq = __ballot(is_eq);
+    const int eq_rank = taken_eq + __popcll(m_eq & below);
+    const bool take = sure || (is_eq && eq_rank < static_cast<int>(equal_take));
+    const uint64_t m_take = __ballot(take);
+    const int pos = written + __popcll(m_take & below);
+    if (take && pos < sel_stride) {
+      out_ids[pos] = blk;
+      lds_ids[pos] = blk;
+    }
+    taken_eq += __popcll(m_eq);
+    written += __popcll(m_take);
+  }
+  return written < sel_stride ? written : sel_stride;
+}
+
+}  // namespace sel
+}  // namespace sa

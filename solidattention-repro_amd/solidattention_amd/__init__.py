@@ -63,6 +63,14 @@ EXPORTS = {
     "sa_hip_attention_contiguous": (C.c_int, [_P, _P, _I64, _I32, _I32, _I32, _F, _P, _P, _SZ, _P]),
     "sa_hip_consume_checksum": (C.c_int, [_P, _I32, _P, _P]),
     "sa_hip_score_select": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _P, _P]),
+    "sa_hip_select_attend_fused": (C.c_int, [_KV, C.POINTER(SelectParamsStruct), _I32]),
+    "sa_hip_select_attend": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P, _SZ, _I32, _P,
+                                       _P]),
+    "sa_hip_decode_step_workspace_bytes": (_SZ, [_KV, _I32]),
+    "sa_hip_decode_step": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P, _SZ,
+                                     _I32, _P, _P]),
+    "sa_hip_decode_step_f16": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P,
+                                         _SZ, _I32, _P, _P]),
     "sa_hip_append_seal": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_append_seal_f16": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_seal": (C.c_int, [_KV, _I32, _P, _P]),
@@ -179,6 +187,72 @@ def score_select(kv: PagedKV, query, select_groups, budget, init, local, selecte
     check(lib().sa_hip_score_select(C.byref(s), _ptr(query), C.byref(params), _ptr(selected), _ptr(counts),
                                     _ptr(scores), _ptr(status), _stream(stream)), "score_select")
     return selected, counts
+
+
+def select_attend(kv: PagedKV, query, select_groups, budget, init, local, scale, selected=None, counts=None,
+                  out=None, splits=1, workspace=None, status=None, sel_stride=None, stream=None, budgets=None):
+    """score_select followed by sparse_decode_attention; one fused launch when
+    select_attend_fused() says so.  Returns (selected, counts, out)."""
+    import torch
+    sel_stride = sel_stride or budget
+    dev = query.device
+    if selected is None:
+        selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=dev)
+    nbytes = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, splits)
+    if workspace is None and nbytes:
+        workspace = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
+    s = kv.struct()
+    check(lib().sa_hip_select_attend(C.byref(s), _ptr(query), C.byref(params), C.c_float(scale), _ptr(selected),
+                                     _ptr(counts), _ptr(out), _ptr(workspace) if nbytes else None, nbytes, splits,
+                                     _ptr(status), _stream(stream)), "select_attend")
+    return selected, counts, out
+
+
+def decode_step_workspace(kv: PagedKV, splits=1, device="cuda"):
+    """Zeroed workspace for decode_step (arrival counters + split records)."""
+    import torch
+    n = lib().sa_hip_decode_step_workspace_bytes(C.byref(kv.struct()), splits)
+    return torch.zeros(max(n // 4, 1), dtype=torch.int32, device=device), n
+
+
+def decode_step(kv: PagedKV, k, v, local_tokens, query, select_groups, budget, init, local, scale, workspace,
+                selected=None, counts=None, out=None, splits=1, status=None, sel_stride=None, stream=None,
+                budgets=None):
+    """append_seal + score_select + sparse_decode_attention for one layer; one
+    fused launch when select_attend_fused() says so.  k, v: fp32 (converted
+    round-to-nearest-even) or uint16 FP16 bits, [batch, kv_heads, head_dim].
+    workspace: from decode_step_workspace() (kept zeroed between calls).
+    Returns (selected, counts, out)."""
+    import torch
+    sel_stride = sel_stride or budget
+    dev = query.device
+    if selected is None:
+        selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=dev)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
+    s = kv.struct()
+    nbytes = workspace.numel() * workspace.element_size()
+    fn = lib().sa_hip_decode_step_f16 if k.dtype == torch.uint16 else lib().sa_hip_decode_step
+    check(fn(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(query), C.byref(params), C.c_float(scale),
+             _ptr(selected), _ptr(counts), _ptr(out), _ptr(workspace), nbytes, splits, _ptr(status),
+             _stream(stream)), "decode_step")
+    return selected, counts, out
+
+
+def select_attend_fused(kv: PagedKV, select_groups, splits=1) -> bool:
+    params = SelectParamsStruct(select_groups, 1, 0, 0, 1, 0, None)
+    s = kv.struct()
+    return bool(lib().sa_hip_select_attend_fused(C.byref(s), C.byref(params), splits))
 
 
 def attention_workspace(kv: PagedKV, splits, device="cuda"):

@@ -1,0 +1,266 @@
+"""GPU parity: the fused score + select + attend launch (sa_hip_select_attend).
+
+Its selection must be bit-exact with the oracle (which is bit-exact with the
+reference's select_shared_blocks, cpp/src/selection.cpp:96-147, per KV
+group) and its attention within 2e-3 of the oracle's fp32 attention
+(attention_reference, cpp/src/attention_reference.cpp:55-96).  The fused
+kernel runs the same attention code as the separate attention kernel, with
+the pages visited in another order, so their outputs agree to fp32 rounding.
+
+decode_step adds the append + seal (kv_lifecycle_main.cpp:31-45, 92-113;
+append_fp16_kv, qwen_layer_main.cpp:270-281) to the same launch: page bytes,
+representatives and counters must be bit-exact with the oracle after every
+step."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import assert_close_2e3, device_kv, status_tensor, to_dev
+from paged_case import D, PAGE, make_case
+
+pytestmark = pytest.mark.gpu
+
+SCALE = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+
+
+def oracle_step(case, budget, init, local, sel_stride, budgets=None):
+    esel = np.full((case.batch, case.hkv, sel_stride), -1, np.int32)
+    ecnt = np.zeros((case.batch, case.hkv), np.int32)
+    for b in range(case.batch):
+        bud = budget if budgets is None else int(budgets[b])
+        s_, c_ = O.paged_score_select(case.query[b:b + 1], case.reps[b:b + 1], case.sealed[b:b + 1], 1, case.hq,
+                                      case.hkv, D, case.rep_heads, case.rep_stride, case.hkv, bud, init, local,
+                                      sel_stride=sel_stride)
+        esel[b], ecnt[b] = s_[0], c_[0]
+    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, esel, ecnt, case.hkv,
+                                      case.query, case.batch, case.hq, case.hkv, D, SCALE)
+    return esel, ecnt, expect
+
+
+def run_fused(hip, case, budget, init, local, sel_stride=None, budgets=None, splits=1):
+    sel_stride = sel_stride or budget
+    kv = device_kv(case)
+    st = status_tensor()
+    q = to_dev(case.query)
+    bud = None if budgets is None else to_dev(budgets)
+    sel, cnt, out = hip.select_attend(kv, q, case.hkv, budget, init, local, SCALE, status=st, sel_stride=sel_stride,
+                                      budgets=bud, splits=splits)
+    # the same step as two separate launches
+    sel2, cnt2 = hip.score_select(kv, q, case.hkv, budget, init, local, status=st, sel_stride=sel_stride,
+                                  budgets=bud)
+    out2 = hip.sparse_decode_attention(kv, q, sel2, cnt2, SCALE, splits=splits, status=st)
+    torch.cuda.synchronize()
+    return (sel.cpu().numpy(), cnt.cpu().numpy(), out.cpu().numpy(), sel2.cpu().numpy(), cnt2.cpu().numpy(),
+            out2.cpu().numpy(), int(st.item()), hip.select_attend_fused(kv, case.hkv, splits))
+
+
+def check(hip, case, budget, init, local, sel_stride=None, budgets=None, splits=1, expect_fused=True):
+    sel_stride = sel_stride or budget
+    sel, cnt, out, sel2, cnt2, out2, status, fused = run_fused(hip, case, budget, init, local, sel_stride, budgets,
+                                                               splits)
+    assert status == 0
+    assert fused == expect_fused
+    esel, ecnt, expect = oracle_step(case, budget, init, local, sel_stride, budgets)
+    assert np.array_equal(cnt, ecnt)
+    assert np.array_equal(cnt2, ecnt)
+    for b in range(case.batch):
+        for g in range(case.hkv):
+            c = int(ecnt[b, g])
+            assert sel[b, g, :c].tolist() == esel[b, g, :c].tolist(), (b, g)
+            assert sel2[b, g, :c].tolist() == esel[b, g, :c].tolist(), (b, g)
+    assert np.isfinite(out).all()
+    assert_close_2e3(out, expect)
+    close_fp32(out, out2)
+
+
+def close_fp32(a, b):
+    """Same attention computed with another page order: fp32 rounding only."""
+    err = np.abs(a.astype(np.float64) - b)
+    assert (err <= 1e-5 + 1e-5 * np.abs(b)).all(), f"max diff {err.max():.3e}"
+
+
+@pytest.mark.parametrize("group,hkv,rep_heads", [(2, 8, None), (2, 8, 16), (1, 8, None), (2, 4, None)])
+def test_fused_shapes(hip, group, hkv, rep_heads):
+    print(f"case: group={group} hkv={hkv} rep_heads={rep_heads}", flush=True)
+    case = make_case(700 + group + hkv, 4, group * hkv, hkv, [32 * 512 + 7, 32 * 300 + 17, 32 * 64, 32 * 13 + 31],
+                     planted=8, rep_heads=rep_heads)
+    check(hip, case, 64, 4, 8)
+
+
+def test_fused_falls_back_for_four_heads_per_kv_head(hip):
+    """G=4 (Qwen3-8B shape) runs as the two launches; results are the same."""
+    case = make_case(710, 3, 32, 8, [32 * 200 + 3, 32 * 90, 32 * 20 + 1], planted=8)
+    check(hip, case, 32, 2, 4, expect_fused=False)
+
+
+def test_fused_split_request_runs_separately(hip):
+    case = make_case(711, 2, 16, 8, [32 * 150 + 5, 32 * 40])
+    check(hip, case, 24, 2, 4, splits=3, expect_fused=False)
+
+
+@pytest.mark.parametrize("lengths", [[5, 31, 32, 33], [32 * 3, 32 * 11 + 2, 32 * 12, 32 * 17 + 31]])
+def test_short_sequences_overlap_and_clamp(hip, lengths):
+    """No sealed block, init/local overlap, budget >= blocks."""
+    print(f"case: lengths={lengths}", flush=True)
+    case = make_case(712, len(lengths), 16, 8, lengths)
+    check(hip, case, 12, 4, 8)
+
+
+def test_many_blocks_and_ties(hip):
+    """4096 blocks per sequence (several compaction chunks) and quantised
+    representatives with many equal scores."""
+    case = make_case(713, 2, 16, 8, [32 * 4096, 32 * 1537 + 9])
+    rng = np.random.default_rng(9)
+    case.reps[:] = (rng.integers(-1, 2, size=case.reps.shape) * 0.5).astype(np.float32)
+    case.query[:] = (rng.integers(-1, 2, size=case.query.shape) * 0.25).astype(np.float32)
+    check(hip, case, 128, 4, 8)
+
+
+def test_stress_budgets_outliers(hip):
+    """Mixed lengths, a shared fragmented pool, per-sequence budgets in
+    {16, 64, all blocks} and 1% of tokens at +-60000."""
+    rng = np.random.default_rng(714)
+    batch = 8
+    lengths = (rng.integers(1024, 8192, size=batch) // 32 * 32).astype(np.int64)
+    case = make_case(715, batch, 16, 8, lengths.tolist(), outliers=0.01, spare_pages=64)
+    n_blocks = case.sealed.astype(np.int64)
+    choice = rng.integers(0, 3, size=batch)
+    budgets = np.where(choice == 0, 16, np.where(choice == 1, 64, n_blocks)).astype(np.int32)
+    budgets[0] = n_blocks[0]
+    print(f"case: lengths={lengths.tolist()} budgets={budgets.tolist()}", flush=True)
+    check(hip, case, 64, 4, 8, sel_stride=int(n_blocks.max()), budgets=budgets)
+
+
+def test_capacity_and_bad_budget_flags(hip):
+    """A sequence with more sealed blocks than rep_stride selects nothing and
+    attends its tail only; a bad per-sequence budget is flagged the same way
+    as by score_select."""
+    case = make_case(716, 2, 16, 8, [32 * 40 + 3, 32 * 30])
+    kv = device_kv(case)
+    q = to_dev(case.query)
+    st = status_tensor()
+    budgets = to_dev(np.array([20, 10], np.int32))  # 10 < init + local
+    sel, cnt, out = hip.select_attend(kv, q, 8, 20, 4, 8, SCALE, status=st, sel_stride=20, budgets=budgets)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_BAD_BUDGET
+    c = cnt.cpu().numpy()
+    assert (c[1] == 0).all() and (c[0] == 20).all()
+    kv.sealed.copy_(to_dev(np.array([case.rep_stride + 1, 30], np.int32)))
+    kv.seq_len.copy_(to_dev(np.array([32 * (case.rep_stride + 1) + 3, 32 * 30], np.int32)))
+    st.zero_()
+    sel, cnt, out = hip.select_attend(kv, q, 8, 20, 4, 8, SCALE, status=st, sel_stride=20)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    assert (cnt.cpu().numpy()[0] == 0).all()
+
+
+# ---- decode_step: append + seal + select + attend ----------------------------
+
+def oracle_decode(case, k, v, local_tokens, budget, init, local, sel_stride, k16=None, v16=None):
+    """The oracle's step: append, seal, then select + attend per KV group."""
+    if k16 is not None:
+        O.paged_append(case.pool, PAGE, case.table, case.seq_len, k16=k16, v16=v16, batch=case.batch, hkv=case.hkv,
+                       d=D)
+    else:
+        O.paged_append(case.pool, PAGE, case.table, case.seq_len, k=k, v=v, batch=case.batch, hkv=case.hkv, d=D)
+    O.paged_seal(case.pool, PAGE, case.table, case.seq_len, case.sealed, case.generation, case.reps,
+                 case.rep_heads, case.rep_stride, case.batch, case.hq, case.hkv, D, local_tokens)
+    return oracle_step(case, budget, init, local, sel_stride)
+
+
+def check_state(kv, case):
+    from gpu_util import pool_numpy
+    assert np.array_equal(kv.seq_len.cpu().numpy(), case.seq_len)
+    assert np.array_equal(kv.sealed.cpu().numpy(), case.sealed)
+    assert np.array_equal(kv.generation.cpu().numpy(), case.generation)
+    assert np.array_equal(pool_numpy(kv), case.pool)
+    assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
+
+
+@pytest.mark.parametrize("local_tokens,rep_heads", [(0, None), (32, None), (0, 16)])
+def test_decode_steps_bit_exact(hip, local_tokens, rep_heads):
+    """40 decode steps across seal boundaries (tails start at 30, 0 and 13
+    tokens), each step one launch; state, ids and outputs checked per step."""
+    print(f"case: local_tokens={local_tokens} rep_heads={rep_heads}", flush=True)
+    case = make_case(720 + local_tokens, 3, 16, 8, [32 * 70 + 30, 32 * 20, 32 * 9 + 13], table_stride=80,
+                     local_tokens=local_tokens, rep_heads=rep_heads, planted=4)
+    kv = device_kv(case)
+    assert hip.select_attend_fused(kv, 8)
+    ws, _ = hip.decode_step_workspace(kv)
+    st = status_tensor()
+    rng = np.random.default_rng(11)
+    budget, init, local = 16, 2, 3
+    for step in range(40):
+        k = (rng.standard_normal((3, 8, D)) * 2).astype(np.float32)
+        v = (rng.standard_normal((3, 8, D)) * 2).astype(np.float32)
+        case.query[:] = rng.standard_normal(case.query.shape).astype(np.float32)
+        sel, cnt, out = hip.decode_step(kv, to_dev(k), to_dev(v), local_tokens, to_dev(case.query), 8, budget, init,
+                                        local, SCALE, ws, status=st)
+        esel, ecnt, expect = oracle_decode(case, k, v, local_tokens, budget, init, local, budget)
+        torch.cuda.synchronize()
+        assert int(st.item()) == 0, step
+        got_sel, got_cnt = sel.cpu().numpy(), cnt.cpu().numpy()
+        assert np.array_equal(got_cnt, ecnt), step
+        for b in range(3):
+            for g in range(8):
+                assert got_sel[b, g, : ecnt[b, g]].tolist() == esel[b, g, : ecnt[b, g]].tolist(), (step, b, g)
+        assert_close_2e3(out.cpu().numpy(), expect)
+        if step % 13 == 0 or step == 39:
+            check_state(kv, case)
+    assert int(ws.abs().sum().item()) == 0, "arrival counters must be left at zero"
+
+
+def test_decode_step_f16_and_two_launch_fallback(hip):
+    """Raw FP16 input; and G=4 (fallback: three launches) gives the oracle's
+    state and outputs as well."""
+    for hq, seed in ((16, 730), (32, 731)):
+        case = make_case(seed, 2, hq, 8, [32 * 40 + 31, 32 * 12 + 2], table_stride=48)
+        kv = device_kv(case)
+        assert hip.select_attend_fused(kv, 8) == (hq == 16)
+        ws, _ = hip.decode_step_workspace(kv)
+        st = status_tensor()
+        rng = np.random.default_rng(seed)
+        for step in range(3):
+            k16 = (rng.standard_normal((2, 8, D)) * 3).astype(np.float16).view(np.uint16)
+            v16 = (rng.standard_normal((2, 8, D)) * 3).astype(np.float16).view(np.uint16)
+            sel, cnt, out = hip.decode_step(kv, to_dev(k16.view(np.int16)).view(torch.uint16),
+                                            to_dev(v16.view(np.int16)).view(torch.uint16), 0, to_dev(case.query), 8,
+                                            12, 2, 2, SCALE, ws, status=st)
+            esel, ecnt, expect = oracle_decode(case, None, None, 0, 12, 2, 2, 12, k16=k16, v16=v16)
+            torch.cuda.synchronize()
+            assert int(st.item()) == 0
+            assert np.array_equal(cnt.cpu().numpy(), ecnt)
+            got_sel = sel.cpu().numpy()
+            for b in range(2):
+                for g in range(8):
+                    assert got_sel[b, g, : ecnt[b, g]].tolist() == esel[b, g, : ecnt[b, g]].tolist()
+            assert_close_2e3(out.cpu().numpy(), expect)
+        check_state(kv, case)
+
+
+def test_decode_step_capacity_leaves_counters(hip):
+    """No page for the new token: flagged, nothing appended or sealed, and the
+    step still selects and attends the existing tokens."""
+    case = make_case(732, 2, 16, 8, [32 * 4, 32 * 2 + 5], table_stride=4)
+    kv = device_kv(case)
+    ws, _ = hip.decode_step_workspace(kv)
+    st = status_tensor()
+    z = torch.zeros((2, 8, D), dtype=torch.float32, device="cuda")
+    sel, cnt, out = hip.decode_step(kv, z, z, 0, to_dev(case.query), 8, 4, 1, 1, SCALE, ws, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    assert kv.seq_len.cpu().numpy().tolist() == [32 * 4, 32 * 2 + 6]
+    esel, ecnt, expect = oracle_step_after_partial_append(case)
+    assert np.array_equal(cnt.cpu().numpy(), ecnt)
+    assert_close_2e3(out.cpu().numpy(), expect)
+    assert int(ws.abs().sum().item()) == 0
+
+
+def oracle_step_after_partial_append(case):
+    """Sequence 0 has no page left (unchanged); sequence 1 appends a zero token."""
+    z = np.zeros((1, 8, D), np.float32)
+    seq1 = case.seq_len[1:2].copy()
+    O.paged_append(case.pool, PAGE, case.table[1:2], seq1, k=z, v=z, batch=1, hkv=8, d=D)
+    case.seq_len[1] = seq1[0]
+    return oracle_step(case, 4, 1, 1, 4)
