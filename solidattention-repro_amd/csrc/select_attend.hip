@@ -144,6 +144,26 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   int64_t len = p.seq_len[b];
   int n = p.sealed[b];
 
+  // ---- 0. start the representative stream: the first batch of this thread's
+  // first block, for blocks sealed before this step (a seal below only adds
+  // blocks, whose representatives are loaded after it) --------------------------
+  sel::ScoreArgs a{};
+  a.query = p.query;
+  a.reps = p.reps;
+  a.b = b;
+  a.h_first = g * G;
+  a.heads_per_sel = G;
+  a.query_heads = p.query_heads;
+  a.group = G;
+  a.rep_heads = p.rep_heads;
+  a.rep_stride = p.rep_stride;
+  // (with one representative row per query head the group's G rows would
+  // keep the prefetched batch live across the second row: not prefetched)
+  constexpr bool kPrefetch = GR == G;
+  const bool have_pre = kPrefetch && n >= 0 && n <= p.rep_stride && n <= kMaxSelectBlocks && tid < n;
+  float pre[sel::kScoreBatch];
+  if (have_pre) sel::score_prefetch(a, tid, pre);
+
   // ---- 1. append + seal (decode step) ---------------------------------------
   if (APPEND) {
     const int gen = p.generation ? p.generation[b] : 0;
@@ -162,31 +182,26 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
 
   attn::WaveState<G> st;
   const attn::LaneGeom lg = attn::lane_geom(p.v, g, lane);
-  st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
 
   // ---- 2. score + select ------------------------------------------------------
-  int pre = 0;  // local blocks [n - pre, n) attended by waves 1..pre during the selection
+  int pre_pages = 0;  // local blocks [n - pre_pages, n) attended by waves 1.. during the selection
   if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) {
+    st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
     if (tid == 0) {
       flag_status(p.v.status, kStatusCapacity);
       p.counts[out_row] = 0;
       s_count = 0;
     }
   } else {
-    sel::ScoreArgs a{};
-    a.query = p.query;
-    a.reps = p.reps;
-    a.b = b;
-    a.h_first = g * G;
-    a.heads_per_sel = G;
-    a.query_heads = p.query_heads;
-    a.group = G;
-    a.rep_heads = p.rep_heads;
-    a.rep_stride = p.rep_stride;
     sel::load_query<kThreads>(a, q_s);
     __syncthreads();
-    sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr);
+    if (kPrefetch) {
+      sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr, pre, have_pre);
+    } else {
+      sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr);
+    }
     __syncthreads();
+    st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
     const sel::Budget bs =
         sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
     if (bs.bad) {
@@ -197,7 +212,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
       }
     } else {
       const int local_n = p.local_blocks < n ? p.local_blocks : n;
-      pre = local_n < kWaves - 1 ? local_n : kWaves - 1;
+      pre_pages = local_n < kWaves - 1 ? local_n : kWaves - 1;
       if (wave == 0) {
         uint32_t threshold = 0xffffffffu, equal_take = 0;
         if (bs.k > 0) sel::radix_threshold_wave(keys, bs, hist, threshold, equal_take);
@@ -208,7 +223,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
           p.counts[out_row] = count;
           s_count = count;
         }
-      } else if (wave <= pre) {
+      } else if (wave <= pre_pages) {
         // forced local block n - wave: selected whatever the scores
         const int64_t logical = n - wave;
         const int64_t page = table_page(p.v, b, logical);
@@ -226,7 +241,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   attn::PageList L{reinterpret_cast<const int32_t*>(keys), 0, 0, 0, 0};
   L.len = len;
   L.sealed = n;
-  L.n_sel = s_count - pre;  // the last `pre` ids are n - pre .. n - 1, already attended
+  L.n_sel = s_count - pre_pages;  // the last pre_pages ids are n - pre_pages .. n - 1, already attended
   if (L.sealed < 0 || L.len < static_cast<int64_t>(L.sealed) * kPageTokens) {
     flag_status(p.v.status, kStatusBadLength);
     if (L.sealed < 0) L.sealed = 0;

@@ -54,45 +54,96 @@ __device__ inline void load_query(const ScoreArgs& a, float* q_s) {
   for (int e = threadIdx.x; e < a.heads_per_sel * D; e += kThreads) q_s[e] = q[e];
 }
 
-// keys[blk] = order_key(score of block blk) for blk < n; scores (optional)
-// receives the fp32 scores.  GR = query heads sharing one representative row
-// (the group size when representatives are per KV head, else 1).  q_s must
-// be visible to the workgroup.
-template <int GR, int kThreads>
-__device__ inline void score_blocks(const ScoreArgs& a, const float* q_s, int n, uint32_t* keys, float* scores) {
+constexpr int kScoreBatch = 64;
+
+// Issue the first batch of representative loads of block `blk` (d 0..63 of
+// the group's first representative row) before the query is in LDS, so the
+// representative stream starts while the caller does other work.
+__device__ inline void score_prefetch(const ScoreArgs& a, int blk, float (&rv)[kScoreBatch]) {
+  const int rh = a.rep_heads == a.query_heads ? a.h_first : a.h_first / a.group;
+  const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * a.rep_stride + blk;
+#pragma unroll
+  for (int k = 0; k < kScoreBatch; ++k) rv[k] = load_stream_f32(r + static_cast<int64_t>(k) * a.rep_stride);
+}
+
+// Score of block blk (sequential fp32, no contraction).  FIRST: the block is
+// this thread's first, whose first batch lives in rv0 (loaded here unless
+// have_pre says score_prefetch() already issued it).
+template <int GR, bool FIRST>
+__device__ inline float score_one(const ScoreArgs& a, const float* q_s, int blk, float (&rv0)[kScoreBatch],
+                                  bool have_pre) {
+  // An opaque zero offset keeps the query reads inside the block loop:
+  // hoisted out of it, the heads_per_sel x 128 query values would be held in
+  // registers (and spilled) across all blocks of the lane.
+  int qoff = 0;
+  asm volatile("" : "+s"(qoff));
   const float heads_f = static_cast<float>(a.heads_per_sel);
-  constexpr int kBatch = 64;
-  // One block per lane.  The 128 representative values of a block are loaded
-  // in two batches of 64 independent loads before the sequential chains run,
-  // so the latency of the HBM reads is paid twice per block, not per d.
-  for (int blk = threadIdx.x; blk < n; blk += kThreads) {
-    // An opaque zero offset keeps the query reads inside the loop: hoisted
-    // out of it, the heads_per_sel x 128 query values would be held in
-    // registers (and spilled) across all blocks of the lane.
-    int qoff = 0;
-    asm volatile("" : "+s"(qoff));
-    float score = 0.0f;
-    for (int h0 = 0; h0 < a.heads_per_sel; h0 += GR) {
-      const int h = a.h_first + h0;
-      const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
-      const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * a.rep_stride + blk;
-      float dot[GR];
+  float score = 0.0f;
+  for (int h0 = 0; h0 < a.heads_per_sel; h0 += GR) {
+    const int h = a.h_first + h0;
+    const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
+    const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * a.rep_stride + blk;
+    float dot[GR];
 #pragma unroll
-      for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
+    for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
 #pragma unroll
-      for (int d0 = 0; d0 < D; d0 += kBatch) {
-        float rv[kBatch];
+    for (int d0 = 0; d0 < D; d0 += kScoreBatch) {
+      if (FIRST && d0 == 0 && h0 == 0) {
+        if (!have_pre) {
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) rv[k] = load_stream_f32(r + static_cast<int64_t>(d0 + k) * a.rep_stride);
+          for (int k = 0; k < kScoreBatch; ++k) rv0[k] = load_stream_f32(r + static_cast<int64_t>(k) * a.rep_stride);
+        }
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
+        for (int k = 0; k < kScoreBatch; ++k) {
+#pragma unroll
+          for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[qoff + (h0 + j) * D + k] * rv0[k];
+        }
+      } else {
+        float rv[kScoreBatch];
+#pragma unroll
+        for (int k = 0; k < kScoreBatch; ++k) rv[k] = load_stream_f32(r + static_cast<int64_t>(d0 + k) * a.rep_stride);
+#pragma unroll
+        for (int k = 0; k < kScoreBatch; ++k) {
 #pragma unroll
           for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[qoff + (h0 + j) * D + d0 + k] * rv[k];
         }
       }
-#pragma unroll
-      for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
     }
+#pragma unroll
+    for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
+  }
+  return score;
+}
+
+// keys[blk] = order_key(score of block blk) for blk < n; scores (optional)
+// receives the fp32 scores.  GR = query heads sharing one representative row
+// (the group size when representatives are per KV head, else 1).  q_s must
+// be visible to the workgroup.  One block per lane; the 128 representative
+// values of a block are loaded in two batches of 64 independent loads before
+// the sequential chains run, so the latency of the HBM reads is paid twice
+// per block, not per d.  rv0 holds the first batch of the thread's first
+// block when have_pre (see score_prefetch()).
+template <int GR, int kThreads>
+__device__ inline void score_blocks(const ScoreArgs& a, const float* q_s, int n, uint32_t* keys, float* scores,
+                                    float (&rv0)[kScoreBatch], bool have_pre) {
+  int blk = threadIdx.x;
+  if (blk < n) {
+    const float score = score_one<GR, true>(a, q_s, blk, rv0, have_pre);
+    keys[blk] = order_key(score);
+    if (scores) scores[blk] = score;
+  }
+  for (blk += kThreads; blk < n; blk += kThreads) {
+    const float score = score_one<GR, false>(a, q_s, blk, rv0, false);
+    keys[blk] = order_key(score);
+    if (scores) scores[blk] = score;
+  }
+}
+
+template <int GR, int kThreads>
+__device__ inline void score_blocks(const ScoreArgs& a, const float* q_s, int n, uint32_t* keys, float* scores) {
+  float unused[kScoreBatch];
+  for (int blk = threadIdx.x; blk < n; blk += kThreads) {
+    const float score = score_one<GR, false>(a, q_s, blk, unused, false);
     keys[blk] = order_key(score);
     if (scores) scores[blk] = score;
   }
