@@ -10,6 +10,12 @@
 //                              (selection.hpp:24-29, selection.cpp:96-147)
 //   SparseDecoder::attend      attention_reference over the selected blocks
 //                              and the tail (attention_reference.cpp:55-96)
+//   SparseDecoder::select_attend  select then attend (one launch where the
+//                              fused kernel applies)
+//   SparseDecoder::decode_step append + seal, select, attend: one layer's
+//                              decode step (qwen_chain_main.cpp:390-395 with
+//                              selection on the GPU), one launch where the
+//                              fused kernel applies
 //   MissCorrector              CudaPipeline::correct_and_wait without the
 //                              host barrier (pipeline_main.cpp:305-331)
 //   compare_prediction         pipeline_main.cpp:686-717
@@ -164,7 +170,9 @@ class SparseDecoder {
         workspace_bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),
                                                           static_cast<int32_t>(pool.query_heads()),
                                                           static_cast<int32_t>(pool.kv_heads()), 128, splits_)),
-        workspace_((workspace_bytes_ + 3) / 4) {}
+        workspace_((workspace_bytes_ + 3) / 4),
+        step_workspace_bytes_(step_bytes(pool, splits_)),
+        step_workspace_((step_workspace_bytes_ + 3) / 4) {}
 
   // Score every sealed block against the query [batch][query_heads][128]
   // (device) and select per group; ids stay on the device.
@@ -184,6 +192,29 @@ class SparseDecoder {
           "sparse_decode_attention");
   }
 
+  // select() then attend(): one launch when fused() is true.
+  void select_attend(const PagedKvPool& pool, const float* query, float scale, float* out,
+                     hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_select_attend(&kv, query, &params_, scale, selected_.get(), counts_.get(), out, workspace_.get(),
+                               workspace_bytes_, splits_, status, stream),
+          "select_attend");
+  }
+  // One layer's decode step: pool.append_seal(k, v, local_tokens) then
+  // select_attend(); one launch when fused() is true.  k, v: fp32
+  // [batch][kv_heads][128] on the device.
+  void decode_step(const PagedKvPool& pool, const float* k, const float* v, int local_tokens, const float* query,
+                   float scale, float* out, hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_decode_step(&kv, k, v, local_tokens, query, &params_, scale, selected_.get(), counts_.get(), out,
+                             step_workspace_.get(), step_workspace_bytes_, splits_, status, stream),
+          "decode_step");
+  }
+  bool fused(const PagedKvPool& pool) const {
+    const sa_paged_kv kv = pool.view();
+    return sa_hip_select_attend_fused(&kv, &params_, splits_) != 0;
+  }
+
   const DeviceArray<int32_t>& selected() const { return selected_; }
   const DeviceArray<int32_t>& counts() const { return counts_; }
   DeviceArray<int32_t>& selected() { return selected_; }
@@ -196,6 +227,15 @@ class SparseDecoder {
   DeviceArray<int32_t> selected_, counts_;
   std::size_t workspace_bytes_;
   DeviceArray<float> workspace_;
+  // decode-step workspace: arrival counters (zeroed here; every step leaves
+  // them zero) and split records
+  std::size_t step_workspace_bytes_;
+  DeviceArray<int32_t> step_workspace_;
+
+  static std::size_t step_bytes(const PagedKvPool& pool, int splits) {
+    const sa_paged_kv kv = pool.view();
+    return sa_hip_decode_step_workspace_bytes(&kv, splits);
+  }
 };
 
 struct Correction {

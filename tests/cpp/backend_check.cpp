@@ -246,6 +246,76 @@ void check_lifecycle() {
   record("lifecycle_sealed_bytes_exact", bytes_ok ? "true" : "false", bytes_ok);
 }
 
+// Decode steps through SparseDecoder::decode_step (one fused launch per
+// step at G=2): 4 sequences, 34 steps across seal boundaries, against the
+// oracle's append, seal, select and attention (qwen_chain_main.cpp:390-395,
+// kv_lifecycle_main.cpp:92-113, selection.cpp:96-147).
+void check_decode_step() {
+  const std::size_t batch = 4, hq = 16, hkv = 8, d = 128, stride = 24, pages = batch * stride;
+  const std::size_t budget = 8, steps = 34;
+  sa::hip::PagedKvPool pool(batch, hq, hkv, stride, pages);
+  const std::size_t page_elems = pool.page_elems();
+  std::vector<std::uint16_t> host_pool(pages * page_elems);
+  sao_synth_fill_half(31, 0, host_pool.size(), host_pool.data());
+  std::vector<int32_t> table(batch * stride);
+  for (std::size_t i = 0; i < table.size(); ++i) table[i] = static_cast<int32_t>((i * 37 + 11) % pages);
+  std::vector<int32_t> seq_len = {32 * 9 + 30, 32 * 12, 32 * 5 + 7, 32 * 16 + 1};
+  std::vector<int32_t> sealed(batch, 0), gen(batch, 0);
+  const std::size_t rep_stride = (stride + 3) / 4 * 4;
+  std::vector<float> reps(batch * hkv * d * rep_stride, 0.0f);
+  sao_paged_seal(host_pool.data(), 32, table.data(), stride, seq_len.data(), sealed.data(), gen.data(),
+                 reps.data(), hkv, rep_stride, batch, hq, hkv, d, 0);
+  pool.pool().upload(host_pool);
+  pool.block_table().upload(table);
+  pool.seq_len().upload(seq_len);
+  pool.sealed().upload(sealed);
+  pool.generation().upload(gen);
+  pool.reps().upload(reps);
+  sa::hip::SparseDecoder dec(pool, sa_select_params{static_cast<int32_t>(hkv), static_cast<int32_t>(budget), 1, 2,
+                                                    static_cast<int32_t>(budget), 0, nullptr});
+  record("decode_step_fused", dec.fused(pool) ? "true" : "false", dec.fused(pool));
+  sa::hip::DeviceArray<float> dk(batch * hkv * d), dv(batch * hkv * d), dq(batch * hq * d), dout(batch * hq * d);
+  std::vector<float> k(batch * hkv * d), v(batch * hkv * d), q(batch * hq * d), out(batch * hq * d);
+  std::vector<int32_t> sel(batch * hkv * budget), cnt(batch * hkv);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(d));
+  bool ids_ok = true;
+  double max_err = 0.0;
+  for (std::size_t step = 0; step < steps; ++step) {
+    sao_synth_fill_float(1000 + step, 0, k.size(), k.data());
+    sao_synth_fill_float(2000 + step, 0, v.size(), v.data());
+    sao_synth_fill_float(3000 + step, 0, q.size(), q.data());
+    dk.upload(k);
+    dv.upload(v);
+    dq.upload(q);
+    dec.decode_step(pool, dk.get(), dv.get(), 0, dq.get(), scale, dout.get());
+    sao_paged_append(host_pool.data(), 32, table.data(), stride, seq_len.data(), k.data(), v.data(), nullptr, nullptr,
+                     batch, hkv, d);
+    sao_paged_seal(host_pool.data(), 32, table.data(), stride, seq_len.data(), sealed.data(), gen.data(),
+                   reps.data(), hkv, rep_stride, batch, hq, hkv, d, 0);
+    sao_paged_score_select(q.data(), reps.data(), sealed.data(), batch, hq, hkv, d, hkv, rep_stride, hkv, budget, 1,
+                           2, sel.data(), cnt.data(), budget, nullptr);
+    sao_paged_sparse_attention(host_pool.data(), 32, table.data(), stride, seq_len.data(), sealed.data(), sel.data(),
+                               cnt.data(), budget, hkv, q.data(), batch, hq, hkv, d, scale, out.data());
+    const auto gsel = dec.selected().download();
+    const auto gcnt = dec.counts().download();
+    const auto gout = dout.download();
+    for (std::size_t r = 0; r < batch * hkv; ++r) {
+      ids_ok &= gcnt[r] == cnt[r];
+      for (int i = 0; i < cnt[r] && ids_ok; ++i) ids_ok &= gsel[r * budget + i] == sel[r * budget + i];
+    }
+    for (std::size_t i = 0; i < out.size(); ++i)
+      max_err = std::max(max_err, std::abs(static_cast<double>(out[i]) - gout[i]) /
+                                      std::max(1.0, std::abs(static_cast<double>(out[i]))));
+  }
+  const bool state_ok = pool.seq_len().download() == seq_len && pool.sealed().download() == sealed &&
+                        pool.generation().download() == gen && pool.pool().download() == host_pool;
+  const auto greps = pool.reps().download();
+  const bool reps_ok = std::memcmp(greps.data(), reps.data(), reps.size() * sizeof(float)) == 0;
+  record("decode_step_selected_ids_exact", ids_ok ? "true" : "false", ids_ok);
+  record("decode_step_state_bytes_exact", state_ok && reps_ok ? "true" : "false", state_ok && reps_ok);
+  record("decode_step_max_rel_error", num(max_err), max_err <= 2e-3);
+}
+
 }  // namespace
 
 int main() {
@@ -258,6 +328,7 @@ int main() {
     check_c1(*backend, 4096, "c1_4096_tokens");
     check_c2(*backend);
     check_lifecycle();
+    check_decode_step();
     g_json << "\n}\n";
     std::cout << g_json.str();
     return g_ok ? 0 : 2;
