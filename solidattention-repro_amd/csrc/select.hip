@@ -2,18 +2,18 @@
 // (gfx950), bit-exact with the reference's select_shared_blocks
 // (cpp/src/selection.cpp:96-147) applied to each selection group.  The
 // scoring, radix select and compaction are in select_core.hpp; this kernel
-// runs them with one 8-wave workgroup per (sequence, selection group), so
-// 512 blocks (a 16K-token sequence) are scored in one pass.  This file is
-// compiled with -ffp-contract=off.
+// runs them with one workgroup per (sequence, selection group) of 8 or 16
+// waves.  A lane scores its blocks one after the other, and every workgroup
+// waits for its slowest lane, so the launch picks the width with the fewer
+// (rounds of resident workgroups) x (blocks per lane): 8 waves (two
+// workgroups per CU) at B=64 / 16K, 16 waves (one per CU, one block per
+// lane) at B=32 / 32K.  This file is compiled with -ffp-contract=off.
 #include "select_core.hpp"
 
 namespace sa {
 namespace {
 
 using namespace sel;
-
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / kWave;
 
 struct Params {
   const float* query;
@@ -36,8 +36,9 @@ struct Params {
   int32_t sel_stride;
 };
 
-template <int GR>
+template <int GR, int kThreads>
 __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) {
+  constexpr int kWaves = kThreads / kWave;
   const int sg = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
@@ -87,9 +88,34 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   if (tid == 0) p.counts[out_row] = count;
 }
 
+int compute_units() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// 16 waves when (rounds x blocks per lane) is smaller than with 8 waves;
+// resident workgroups per CU: two of 8 waves, one of 16.
+bool wide_select(int64_t workgroups, int64_t blocks) {
+  const int64_t cus = compute_units();
+  const int64_t narrow = ((workgroups + 2 * cus - 1) / (2 * cus)) * ((blocks + 511) / 512);
+  const int64_t wide = ((workgroups + cus - 1) / cus) * ((blocks + 1023) / 1024);
+  return wide < narrow;
+}
+
 template <int GR>
 void launch_gr(const Params& p, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL(score_select_kernel<GR>, grid, dim3(kThreads), 0, stream, p);
+  if (wide_select(static_cast<int64_t>(grid.x) * grid.y, p.rep_stride)) {
+    hipLaunchKernelGGL((score_select_kernel<GR, 1024>), grid, dim3(1024), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((score_select_kernel<GR, 512>), grid, dim3(512), 0, stream, p);
+  }
 }
 
 }  // namespace
