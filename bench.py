@@ -142,6 +142,10 @@ def main():
 
     status = torch.zeros(1, dtype=torch.int32, device="cuda")
     pages_hint = budget + 2
+    # the fused launch (splits 1) where it applies and fills the device; the
+    # separate attention launch splits its page lists by default_splits
+    fused_ok = (args.splits in (0, 1) and sa.select_attend_fused(L[0].kv, hkv, 1)
+                and (args.splits == 1 or sa.select_attend_default_splits(L[0].kv, hkv, budget) == 1))
     splits = args.splits or sa.default_splits(batch, hkv, pages_hint)
     ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(batch, hq, hkv, D, splits)
     workspace = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
@@ -151,9 +155,10 @@ def main():
     n_ev = total_steps * layers
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_ev)]
 
-    fusable = splits == 1 and sa.select_attend_fused(L[0].kv, hkv, splits)
-    launches = args.launches if fusable else 3
-    step_ws, _ = sa.decode_step_workspace(L[0].kv, splits)
+    launches = args.launches if fused_ok else 3
+    if launches < 3:
+        splits = 1
+    step_ws, _ = sa.decode_step_workspace(L[0].kv, 1)
 
     def layer_launches(ly, s, e=None):
         """One layer of one decode step; e = 4 timing events (append, select, attention)."""

@@ -195,6 +195,13 @@ int sa_hip_score_select(const sa_paged_kv* kv, const float* query,
  * pipeline_main.cpp:803-876) with selection on the GPU. */
 int sa_hip_select_attend_fused(const sa_paged_kv* kv,
                                const sa_select_params* params, int32_t splits);
+/* The split count to pass to sa_hip_select_attend / sa_hip_decode_step: 1
+ * (the fused launch) when the fused kernel applies and its workgroups fill
+ * the device (batch x kv_heads >= 2 x CUs); otherwise
+ * sa_hip_attention_default_splits(batch, kv_heads, budget_blocks + 2) for the
+ * separate launches. */
+int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv,
+                                            const sa_select_params* params);
 int sa_hip_select_attend(const sa_paged_kv* kv, const float* query,
                          const sa_select_params* params, float scale,
                          int32_t* selected, int32_t* counts, float* out,

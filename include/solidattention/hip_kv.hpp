@@ -171,7 +171,8 @@ class SparseDecoder {
                                                           static_cast<int32_t>(pool.query_heads()),
                                                           static_cast<int32_t>(pool.kv_heads()), 128, splits_)),
         workspace_((workspace_bytes_ + 3) / 4),
-        step_workspace_bytes_(step_bytes(pool, splits_)),
+        step_splits_(fused_splits(pool, params, splits)),
+        step_workspace_bytes_(step_bytes(pool, step_splits_)),
         step_workspace_((step_workspace_bytes_ + 3) / 4) {}
 
   // Score every sealed block against the query [batch][query_heads][128]
@@ -196,8 +197,11 @@ class SparseDecoder {
   void select_attend(const PagedKvPool& pool, const float* query, float scale, float* out,
                      hipStream_t stream = nullptr, int32_t* status = nullptr) {
     const sa_paged_kv kv = pool.view();
-    check(sa_hip_select_attend(&kv, query, &params_, scale, selected_.get(), counts_.get(), out, workspace_.get(),
-                               workspace_bytes_, splits_, status, stream),
+    // the split records of the non-fused path sit after the arrival counters
+    const std::size_t skip = arrive_bytes(pool.batch());
+    check(sa_hip_select_attend(&kv, query, &params_, scale, selected_.get(), counts_.get(), out,
+                               step_workspace_.get() + skip / 4, step_workspace_bytes_ - skip, step_splits_, status,
+                               stream),
           "select_attend");
   }
   // One layer's decode step: pool.append_seal(k, v, local_tokens) then
@@ -207,12 +211,12 @@ class SparseDecoder {
                    float scale, float* out, hipStream_t stream = nullptr, int32_t* status = nullptr) {
     const sa_paged_kv kv = pool.view();
     check(sa_hip_decode_step(&kv, k, v, local_tokens, query, &params_, scale, selected_.get(), counts_.get(), out,
-                             step_workspace_.get(), step_workspace_bytes_, splits_, status, stream),
+                             step_workspace_.get(), step_workspace_bytes_, step_splits_, status, stream),
           "decode_step");
   }
   bool fused(const PagedKvPool& pool) const {
     const sa_paged_kv kv = pool.view();
-    return sa_hip_select_attend_fused(&kv, &params_, splits_) != 0;
+    return sa_hip_select_attend_fused(&kv, &params_, step_splits_) != 0;
   }
 
   const DeviceArray<int32_t>& selected() const { return selected_; }
@@ -227,15 +231,26 @@ class SparseDecoder {
   DeviceArray<int32_t> selected_, counts_;
   std::size_t workspace_bytes_;
   DeviceArray<float> workspace_;
-  // decode-step workspace: arrival counters (zeroed here; every step leaves
-  // them zero) and split records
+  // select_attend / decode_step: the fused launch where it applies and
+  // fills the device (unless the caller fixed the splits), with a workspace
+  // of arrival counters (zeroed here; every step leaves them zero) and split
+  // records
+  int step_splits_;
   std::size_t step_workspace_bytes_;
   DeviceArray<int32_t> step_workspace_;
 
+  static int fused_splits(const PagedKvPool& pool, const sa_select_params& params, int splits) {
+    if (splits > 0) return splits;
+    const sa_paged_kv kv = pool.view();
+    return sa_hip_select_attend_default_splits(&kv, &params);
+  }
   static std::size_t step_bytes(const PagedKvPool& pool, int splits) {
     const sa_paged_kv kv = pool.view();
     return sa_hip_decode_step_workspace_bytes(&kv, splits);
   }
+  // the decode-step workspace starts with one int32 arrival counter per
+  // sequence, padded to 256 bytes (sa_hip_decode_step_workspace_bytes)
+  static std::size_t arrive_bytes(std::size_t batch) { return (batch * 4 + 255) / 256 * 256; }
 };
 
 struct Correction {

@@ -74,6 +74,9 @@ struct SelectLaunch {
 
 hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream);
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int compute_units();
+
 // Fused (append + seal +) score + select + attend, one workgroup per
 // (sequence, KV head); select_groups is kv_heads.  Supported for 1 or 2
 // query heads per KV head.

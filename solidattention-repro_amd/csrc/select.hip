@@ -88,18 +88,6 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   if (tid == 0) p.counts[out_row] = count;
 }
 
-int compute_units() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // 16 waves when (rounds x blocks per lane) is smaller than with 8 waves;
 // resident workgroups per CU: two of 8 waves, one of 16.
 bool wide_select(int64_t workgroups, int64_t blocks) {
@@ -119,6 +107,18 @@ void launch_gr(const Params& p, dim3 grid, hipStream_t stream) {
 }
 
 }  // namespace
+
+int compute_units() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
   Params p{};

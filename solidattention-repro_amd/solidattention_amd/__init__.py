@@ -64,6 +64,7 @@ EXPORTS = {
     "sa_hip_consume_checksum": (C.c_int, [_P, _I32, _P, _P]),
     "sa_hip_score_select": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _P, _P]),
     "sa_hip_select_attend_fused": (C.c_int, [_KV, C.POINTER(SelectParamsStruct), _I32]),
+    "sa_hip_select_attend_default_splits": (_I32, [_KV, C.POINTER(SelectParamsStruct)]),
     "sa_hip_select_attend": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P, _SZ, _I32, _P,
                                        _P]),
     "sa_hip_decode_step_workspace_bytes": (_SZ, [_KV, _I32]),
@@ -247,6 +248,13 @@ def decode_step(kv: PagedKV, k, v, local_tokens, query, select_groups, budget, i
              _ptr(selected), _ptr(counts), _ptr(out), _ptr(workspace), nbytes, splits, _ptr(status),
              _stream(stream)), "decode_step")
     return selected, counts, out
+
+
+def select_attend_default_splits(kv: PagedKV, select_groups, budget) -> int:
+    """1 where the fused launch applies and fills the device, else the split
+    count of the separate attention launch."""
+    params = SelectParamsStruct(select_groups, budget, 0, 0, budget, 0, None)
+    return int(lib().sa_hip_select_attend_default_splits(C.byref(kv.struct()), C.byref(params)))
 
 
 def select_attend_fused(kv: PagedKV, select_groups, splits=1) -> bool:

@@ -88,9 +88,11 @@ def test_fused_shapes(hip, group, hkv, rep_heads):
     check(hip, case, 64, 4, 8)
 
 
-def test_fused_falls_back_for_four_heads_per_kv_head(hip):
-    """G=4 (Qwen3-8B shape) runs as the two launches; results are the same."""
-    case = make_case(710, 3, 32, 8, [32 * 200 + 3, 32 * 90, 32 * 20 + 1], planted=8)
+@pytest.mark.parametrize("hq", [32, 64])
+def test_fused_falls_back_for_four_or_eight_heads_per_kv_head(hip, hq):
+    """G=4 (Qwen3-8B shape) and G=8 run as the two launches; results are the
+    same."""
+    case = make_case(710 + hq, 3, hq, 8, [32 * 200 + 3, 32 * 90, 32 * 20 + 1], planted=8)
     check(hip, case, 32, 2, 4, expect_fused=False)
 
 
@@ -178,15 +180,16 @@ def check_state(kv, case):
     assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
 
 
-@pytest.mark.parametrize("local_tokens,rep_heads", [(0, None), (32, None), (0, 16)])
-def test_decode_steps_bit_exact(hip, local_tokens, rep_heads):
+@pytest.mark.parametrize("local_tokens,rep_heads,hq", [(0, None, 16), (32, None, 16), (0, 16, 16), (0, None, 32),
+                                                      (32, 32, 32)])
+def test_decode_steps_bit_exact(hip, local_tokens, rep_heads, hq):
     """40 decode steps across seal boundaries (tails start at 30, 0 and 13
     tokens), each step one launch; state, ids and outputs checked per step."""
-    print(f"case: local_tokens={local_tokens} rep_heads={rep_heads}", flush=True)
-    case = make_case(720 + local_tokens, 3, 16, 8, [32 * 70 + 30, 32 * 20, 32 * 9 + 13], table_stride=80,
+    print(f"case: local_tokens={local_tokens} rep_heads={rep_heads} hq={hq}", flush=True)
+    case = make_case(720 + local_tokens + hq, 3, hq, 8, [32 * 70 + 30, 32 * 20, 32 * 9 + 13], table_stride=80,
                      local_tokens=local_tokens, rep_heads=rep_heads, planted=4)
     kv = device_kv(case)
-    assert hip.select_attend_fused(kv, 8)
+    assert hip.select_attend_fused(kv, 8) == (hq == 16)  # G=4: the three-launch fallback
     ws, _ = hip.decode_step_workspace(kv)
     st = status_tensor()
     rng = np.random.default_rng(11)
@@ -211,10 +214,10 @@ def test_decode_steps_bit_exact(hip, local_tokens, rep_heads):
     assert int(ws.abs().sum().item()) == 0, "arrival counters must be left at zero"
 
 
-def test_decode_step_f16_and_two_launch_fallback(hip):
-    """Raw FP16 input; and G=4 (fallback: three launches) gives the oracle's
-    state and outputs as well."""
-    for hq, seed in ((16, 730), (32, 731)):
+def test_decode_step_f16_and_three_launch_fallback(hip):
+    """Raw FP16 input at G=2 (fused), and G=4 and G=8 (fallback: three
+    launches) give the oracle's state and outputs."""
+    for hq, seed in ((16, 730), (32, 731), (64, 733)):
         case = make_case(seed, 2, hq, 8, [32 * 40 + 31, 32 * 12 + 2], table_stride=48)
         kv = device_kv(case)
         assert hip.select_attend_fused(kv, 8) == (hq == 16)
