@@ -263,6 +263,40 @@ int sa_hip_append_seal_f16(const sa_paged_kv* kv, const uint16_t* k,
 int sa_hip_seal(const sa_paged_kv* kv, int32_t local_tokens, int32_t* status,
                 void* stream);
 
+/* ---- R4 (InfLLM, prefill): local-causal block representatives ------------ */
+
+/* Workspace for sa_hip_local_causal_representatives: the window
+ * probabilities and the received mass, tokens x query_heads x
+ * (local_window + 1) floats. */
+size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads,
+                                           int32_t local_window);
+
+/* The reference's build_local_causal_representatives (selection.hpp:19-22,
+ * selection.cpp:12-94) on the GPU: every query position attends its local
+ * causal window of `local_window` keys (fp32 softmax over sequential fp32
+ * dots, scale 1/sqrt(head_dim)); each key's received mass is summed over the
+ * queries in order; per 32-token block the `topk` keys with the most mass
+ * (stable: ties keep token order) are averaged in rank order.
+ *   prompt_queries  [query_heads][tokens][head_dim] fp32 (device)
+ *   kv              [tokens][2][kv_heads][head_dim] FP16 bits (device, the
+ *                   reference's interleaved token format)
+ * Outputs (device, each optional, at least one given): values
+ * [query_heads][blocks][head_dim] (the reference's layout), offsets
+ * [query_heads][blocks][topk] int32 (the reference's chosen_token_offsets),
+ * reps [query_heads][head_dim][rep_stride] (one sequence's slice of
+ * sa_paged_kv.reps with rep_heads = query_heads), received
+ * [query_heads][tokens].  The exponential is a fixed double-precision
+ * evaluation (the reference's std::exp is glibc expf): identical chosen
+ * tokens and representative bits on the reference's fixtures; a softmax
+ * value can differ from the reference's in its last bit.  Limits:
+ * head_dim 128, block_tokens 32, local_window <= 256. */
+int sa_hip_local_causal_representatives(
+    const float* prompt_queries, const uint16_t* kv, int64_t tokens,
+    int32_t query_heads, int32_t kv_heads, int32_t head_dim,
+    int32_t block_tokens, int32_t local_window, int32_t topk, float* values,
+    int32_t* offsets, float* reps, int32_t rep_stride, float* received,
+    void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- R5: gather / pack --------------------------------------------------- */
 
 /* out + i * page_bytes <- pool + pages[i] * page_bytes for i < count (device

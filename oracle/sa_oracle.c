@@ -194,10 +194,40 @@ int sao_attention_reference(const uint16_t* kv, const float* query,
 /* ------------------------------------------------------------------------ */
 
 /* cpp/src/selection.cpp:12-94. */
-int sao_build_local_causal_representatives(
-    const float* prompt_queries, const uint16_t* kv, size_t tokens,
-    size_t query_heads, size_t kv_heads, size_t head_dim, size_t block_tokens,
-    size_t local_window, size_t topk, float* values, size_t* offsets) {
+/* exp(x) rounded to float through a fixed sequence of double operations, so
+ * the oracle and the GPU builder (which runs the same operations) agree bit
+ * for bit: Cody-Waite reduction x = k*ln2 + r with k the nearest integer to
+ * x*log2(e) and ln2 split as in fdlibm (ln2_hi has 21 trailing zero bits, so
+ * k*ln2_hi is exact), exp(r) by its Taylor series to degree 13 in Horner form
+ * (|r| <= 0.35: truncation below 1e-17 relative), then scaling by 2^k.  The
+ * double result is within ~2e-16 of exp(x), so the float is the correctly
+ * rounded exp(x) except within ~2^-29 of a rounding midpoint; glibc's expf is
+ * within 0.502 ulp, so the two agree on nearly every input (not all). */
+float sao_exp_det(float x) {
+  static const double kLn2Hi = 6.93147180369123816490e-01;
+  static const double kLn2Lo = 1.90821492927058770002e-10;
+  static const double kLog2e = 1.44269504088896338700e+00;
+  static const double kInvFact[14] = {
+      1.0, 1.0, 0.5, 1.0 / 6.0, 1.0 / 24.0, 1.0 / 120.0, 1.0 / 720.0, 1.0 / 5040.0, 1.0 / 40320.0,
+      1.0 / 362880.0, 1.0 / 3628800.0, 1.0 / 39916800.0, 1.0 / 479001600.0, 1.0 / 6227020800.0};
+  if (x != x) return x;
+  if (x < -104.0f) return 0.0f;      /* below half the smallest subnormal */
+  if (x > 89.0f) return INFINITY;    /* above the largest finite float */
+  const double xd = (double)x;
+  const double k = nearbyint(xd * kLog2e);
+  const double r = (xd - k * kLn2Hi) - k * kLn2Lo;
+  double poly = kInvFact[13];
+  for (int i = 12; i >= 0; --i) poly = poly * r + kInvFact[i];
+  return (float)ldexp(poly, (int)k);
+}
+
+/* The reference's builder (selection.cpp:12-94) with the exponential as a
+ * parameter; received (optional) gets the [Hq][tokens] attention mass. */
+static int build_lcr(const float* prompt_queries, const uint16_t* kv, size_t tokens,
+                     size_t query_heads, size_t kv_heads, size_t head_dim,
+                     size_t block_tokens, size_t local_window, size_t topk,
+                     float* values, size_t* offsets, float (*expfn)(float),
+                     float* received_out) {
   if (!prompt_queries || !kv || !values || tokens == 0 || kv_heads == 0 ||
       block_tokens == 0 || query_heads % kv_heads != 0 ||
       tokens % block_tokens != 0 || local_window == 0 || topk == 0 ||
@@ -227,7 +257,7 @@ int sao_build_local_causal_representatives(
       }
       float denominator = 0.0f;
       for (size_t w = 0; w < count; ++w) {
-        logits[w] = expf(logits[w] - maximum);
+        logits[w] = expfn(logits[w] - maximum);
         denominator += logits[w];
       }
       for (size_t w = 0; w < count; ++w)
@@ -252,10 +282,30 @@ int sao_build_local_causal_representatives(
       }
     }
   }
+  if (received_out) memcpy(received_out, received, query_heads * tokens * sizeof(float));
   free(order);
   free(logits);
   free(received);
   return SAO_OK;
+}
+
+static float expf_libm(float x) { return expf(x); }
+
+int sao_build_local_causal_representatives(
+    const float* prompt_queries, const uint16_t* kv, size_t tokens,
+    size_t query_heads, size_t kv_heads, size_t head_dim, size_t block_tokens,
+    size_t local_window, size_t topk, float* values, size_t* offsets) {
+  return build_lcr(prompt_queries, kv, tokens, query_heads, kv_heads, head_dim, block_tokens,
+                   local_window, topk, values, offsets, expf_libm, NULL);
+}
+
+int sao_build_local_causal_representatives_det(
+    const float* prompt_queries, const uint16_t* kv, size_t tokens,
+    size_t query_heads, size_t kv_heads, size_t head_dim, size_t block_tokens,
+    size_t local_window, size_t topk, float* values, size_t* offsets,
+    float* received) {
+  return build_lcr(prompt_queries, kv, tokens, query_heads, kv_heads, head_dim, block_tokens,
+                   local_window, topk, values, offsets, sao_exp_det, received);
 }
 
 int sao_mean_key_representatives(const uint16_t* kv, size_t tokens,

@@ -74,6 +74,20 @@ int sao_build_local_causal_representatives(
  * Equal to sao_build_local_causal_representatives(window=1,
  * topk=block_tokens) for every query head of the group (all received masses
  * are exactly 1, so the stable order is the natural order). */
+/* The same builder with sao_exp_det in place of expf (the GPU builder's
+ * arithmetic, bit for bit); received (optional): [Hq][tokens] attention mass
+ * each key received. */
+int sao_build_local_causal_representatives_det(
+    const float* prompt_queries, const uint16_t* kv, size_t tokens,
+    size_t query_heads, size_t kv_heads, size_t head_dim, size_t block_tokens,
+    size_t local_window, size_t topk, float* values, size_t* offsets,
+    float* received);
+
+/* exp(x) rounded to float through fixed double operations (Cody-Waite
+ * reduction, degree-13 Taylor polynomial, scaling by 2^k); the GPU builder
+ * runs the same operations. */
+float sao_exp_det(float x);
+
 int sao_mean_key_representatives(const uint16_t* kv, size_t tokens,
                                  size_t kv_heads, size_t head_dim,
                                  size_t block_tokens, float* values);

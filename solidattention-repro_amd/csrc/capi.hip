@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -436,6 +437,60 @@ int sa_hip_decode_step_f16(const sa_paged_kv* kv, const uint16_t* k, const uint1
   if (!k || !v) return fail(SA_HIP_EINVAL, "decode_step_f16: null k/v");
   return decode_step_common(kv, nullptr, nullptr, k, v, local_tokens, query, params, scale, selected, counts, out,
                             workspace, workspace_bytes, splits, status, stream, "decode_step_f16");
+}
+
+// ---- InfLLM local-causal representatives (prefill) -----------------------------
+
+size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t local_window) {
+  if (tokens <= 0 || query_heads <= 0 || local_window <= 0) return 0;
+  return sa::local_causal_workspace_bytes(tokens, query_heads, local_window);
+}
+
+int sa_hip_local_causal_representatives(const float* prompt_queries, const uint16_t* kv, int64_t tokens,
+                                        int32_t query_heads, int32_t kv_heads, int32_t head_dim,
+                                        int32_t block_tokens, int32_t local_window, int32_t topk, float* values,
+                                        int32_t* offsets, float* reps, int32_t rep_stride, float* received,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  // the reference's argument checks (selection.cpp:18-23), then this build's limits
+  if (!prompt_queries || !kv || tokens <= 0 || kv_heads <= 0 || query_heads % kv_heads != 0 ||
+      block_tokens <= 0 || tokens % block_tokens != 0 || local_window <= 0 || topk <= 0 || topk > block_tokens)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: invalid local-causal representative dimensions");
+  if (head_dim != sa::kHeadDim)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: head_dim %d unsupported (built for %d)", head_dim,
+                sa::kHeadDim);
+  if (block_tokens != SA_HIP_PAGE_TOKENS)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: block_tokens must be %d", SA_HIP_PAGE_TOKENS);
+  if (local_window > sa::kMaxLocalWindow)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: local_window %d above %d", local_window,
+                sa::kMaxLocalWindow);
+  if (tokens > (int64_t{1} << 31) / query_heads)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: tokens x query_heads too large");
+  if (!values && !reps && !offsets)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: no output given");
+  if (reps && rep_stride < tokens / block_tokens)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: rep_stride %d below the block count", rep_stride);
+  if (!aligned16(kv)) return fail(SA_HIP_EINVAL, "local_causal_representatives: kv must be 16-byte aligned");
+  const size_t need = sa_hip_local_causal_workspace_bytes(tokens, query_heads, local_window);
+  if (!workspace || workspace_bytes < need)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  sa::RepresentativeLaunch r{};
+  r.prompt_queries = prompt_queries;
+  r.kv = kv;
+  r.workspace = static_cast<float*>(workspace);
+  r.received = received;
+  r.values = values;
+  r.reps = reps;
+  r.offsets = offsets;
+  r.tokens = tokens;
+  r.query_heads = query_heads;
+  r.kv_heads = kv_heads;
+  r.window = local_window;
+  r.topk = topk;
+  r.rep_stride = rep_stride;
+  // the reference's scale: 1.0f / std::sqrt(static_cast<float>(head_dim)) (selection.cpp:26)
+  r.scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
+  return check_hip(sa::launch_local_causal_representatives(r, as_stream(stream)), "local_causal launch");
 }
 
 // ---- append / seal -------------------------------------------------------------

@@ -76,6 +76,9 @@ EXPORTS = {
     "sa_hip_append_seal_f16": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_seal": (C.c_int, [_KV, _I32, _P, _P]),
     "sa_hip_gather_pages": (C.c_int, [_P, _I64, _I64, _P, _I32, _P, _P, _P]),
+    "sa_hip_local_causal_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
+    "sa_hip_local_causal_representatives": (C.c_int, [_P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
+                                                      _I32, _P, _P, _SZ, _P]),
     "sa_hip_compare_prediction": (C.c_int, [_P, _P, _I32, _P, _P, _P, _P]),
     "sa_hip_fill_pages_async": (C.c_int, [_P, _I64, _P, _P, _P, _I32, _P, _P]),
     "sa_hip_fill_pages_gather_async": (C.c_int, [_P, _I64, _I64, _P, _P, _I64, _P, _I32, _P, _P, _P]),
@@ -339,6 +342,27 @@ def append_seal(kv: PagedKV, k, v, local_tokens, status=None, stream=None):
 def seal(kv: PagedKV, local_tokens, status=None, stream=None):
     s = kv.struct()
     check(lib().sa_hip_seal(C.byref(s), local_tokens, _ptr(status), _stream(stream)), "seal")
+
+
+def local_causal_representatives(prompt_queries, kv16, tokens, query_heads, kv_heads, window, topk, values=True,
+                                 offsets=True, reps=None, rep_stride=0, received=None, stream=None):
+    """InfLLM local-causal block representatives of a prefill (the
+    reference's build_local_causal_representatives).  prompt_queries: fp32
+    [query_heads, tokens, 128]; kv16: uint16 [tokens, 2, kv_heads, 128].
+    Returns (values [hq, blocks, 128] or None, offsets int32 [hq, blocks,
+    topk] or None); reps (optional) is filled in the d-major layout."""
+    import torch
+    dev = prompt_queries.device
+    blocks = tokens // PAGE_TOKENS
+    vals = torch.empty((query_heads, blocks, HEAD_DIM), dtype=torch.float32, device=dev) if values else None
+    offs = torch.empty((query_heads, blocks, topk), dtype=torch.int32, device=dev) if offsets else None
+    nbytes = lib().sa_hip_local_causal_workspace_bytes(tokens, query_heads, window)
+    ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
+    check(lib().sa_hip_local_causal_representatives(
+        _ptr(prompt_queries), _ptr(kv16), tokens, query_heads, kv_heads, HEAD_DIM, PAGE_TOKENS, window, topk,
+        _ptr(vals), _ptr(offs), _ptr(reps), rep_stride, _ptr(received), _ptr(ws), nbytes, _stream(stream)),
+        "local_causal_representatives")
+    return vals, offs
 
 
 def gather_pages(pool, page_bytes, num_pages, pages, out, status=None, stream=None):

@@ -1,0 +1,104 @@
+"""GPU parity: InfLLM local-causal block representatives of a prefill
+(sa_hip_local_causal_representatives), the reference's
+build_local_causal_representatives (cpp/src/selection.cpp:12-94).
+
+Bars: bit-exact (chosen offsets, representative bits, received-mass bits)
+against the oracle's builder with the same exponential
+(sao_build_local_causal_representatives_det); bit-exact offsets and
+representatives against the reference's own outputs on the committed golden
+cases and the published C2.1 offset hash; the C2.1 chain (GPU builder, then
+GPU selection) returns the published ids [0, 8, 13, 15]."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, HERE)
+
+from cases import REPRESENTATIVES, representative_inputs  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+GOLD = np.load(os.path.join(HERE, "reference_outputs.npz"), allow_pickle=False)
+
+
+def gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk, want_reps=False):
+    dq = torch.from_numpy(np.ascontiguousarray(pq)).cuda()
+    dkv = torch.from_numpy(np.ascontiguousarray(kv).view(np.int16)).cuda().view(torch.uint16)
+    received = torch.empty((hq, tokens), dtype=torch.float32, device="cuda")
+    blocks = tokens // 32
+    rep_stride = (blocks + 3) // 4 * 4
+    reps = torch.zeros((hq, 128, rep_stride), dtype=torch.float32, device="cuda") if want_reps else None
+    vals, offs = hip.local_causal_representatives(dq, dkv, tokens, hq, hkv, window, topk, reps=reps,
+                                                  rep_stride=rep_stride if want_reps else 0, received=received)
+    torch.cuda.synchronize()
+    out = (vals.cpu().numpy(), offs.cpu().numpy().astype(np.int64), received.cpu().numpy())
+    return out + ((reps.cpu().numpy()[:, :, :blocks],) if want_reps else ())
+
+
+def check_vs_det(hip, pq, kv, tokens, hq, hkv, window, topk):
+    vals, offs, rec = gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk)
+    evals, eoffs, erec = O.local_causal_representatives_det(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
+    assert np.array_equal(rec.view(np.uint32), erec.view(np.uint32)), "received mass differs"
+    assert np.array_equal(offs, eoffs.astype(np.int64)), "chosen offsets differ"
+    assert np.array_equal(vals.view(np.uint32), evals.view(np.uint32)), "representative bits differ"
+
+
+@pytest.mark.parametrize("name", sorted(REPRESENTATIVES))
+def test_gpu_builder_vs_reference_golden(hip, name):
+    c = REPRESENTATIVES[name]
+    print(f"case: representatives/{name}", flush=True)
+    pq, kv = representative_inputs(c)
+    vals, offs, _ = gpu_build(hip, pq, kv, c["tokens"], c["hq"], c["hkv"], c["window"], c["topk"])
+    assert np.array_equal(offs, GOLD[f"representatives/{name}/offsets"])
+    assert np.array_equal(vals.view(np.uint32), GOLD[f"representatives/{name}/values"])
+
+
+@pytest.mark.parametrize("window,topk,hq,hkv,tokens", [
+    (1, 1, 4, 4, 64), (2, 3, 8, 4, 96), (5, 4, 8, 2, 160), (32, 4, 16, 8, 512), (64, 8, 8, 8, 256),
+    (100, 16, 4, 1, 320), (256, 32, 8, 2, 544), (33, 32, 2, 2, 64)])
+def test_gpu_builder_vs_det_oracle(hip, window, topk, hq, hkv, tokens):
+    print(f"case: window={window} topk={topk} hq={hq} hkv={hkv} tokens={tokens}", flush=True)
+    rng = np.random.default_rng(window * 7 + tokens)
+    pq = rng.standard_normal(hq * tokens * 128).astype(np.float32)
+    kv = rng.standard_normal(tokens * 2 * hkv * 128).astype(np.float16).view(np.uint16)
+    check_vs_det(hip, pq, kv, tokens, hq, hkv, window, topk)
+
+
+def test_gpu_builder_outliers_and_ties(hip):
+    """+-60000 keys (saturated softmax rows) and repeated tokens (equal mass:
+    the stable rank keeps token order)."""
+    rng = np.random.default_rng(99)
+    tokens, hq, hkv = 128, 8, 4
+    pq = rng.standard_normal(hq * tokens * 128).astype(np.float32)
+    kv = rng.standard_normal((tokens, 2, hkv, 128)).astype(np.float16)
+    kv[rng.random(tokens) < 0.05] = np.float16(60000)
+    kv[40:56] = kv[40]  # a run of identical tokens
+    check_vs_det(hip, pq, kv.view(np.uint16).ravel(), tokens, hq, hkv, 32, 4)
+
+
+def test_gpu_c21_chain(hip):
+    """C2.1 end to end on the GPU: representatives of the reference's 512-token
+    fixture (window 32, top 4), their offset hash, then the shared selection
+    over them (budget 4 = init 1 + local 1 + 2) -> [0, 8, 13, 15]."""
+    kv, pq = O.fixture_c2(512, 16, 8, 128)
+    vals, offs, _, reps = gpu_build(hip, pq, kv, 512, 16, 8, 32, 4, want_reps=True)
+    h = 1469598103934665603
+    for o in offs.ravel():
+        h ^= int(o)
+        h = (h * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    assert h == 7873450381430813043
+    assert np.array_equal(reps.transpose(0, 2, 1).view(np.uint32), vals.view(np.uint32))
+    kvp = hip.PagedKV(1, 16, 8, table_stride=16, num_pages=16, rep_heads=16, rep_stride=16)
+    kvp.reps[0].copy_(torch.from_numpy(np.ascontiguousarray(reps)))
+    kvp.sealed.fill_(16)
+    kvp.seq_len.fill_(512)
+    query = pq.reshape(16, 512, 128)[:, 511, :].copy()
+    sel, cnt = hip.score_select(kvp, torch.from_numpy(query.reshape(1, 16, 128)).cuda(), 1, 4, 1, 1)
+    torch.cuda.synchronize()
+    assert sel[0, 0, : int(cnt.item())].cpu().numpy().tolist() == [0, 8, 13, 15]
