@@ -58,9 +58,10 @@ def parse():
                     help="kernel launches per layer: 1 = the fused decode step (append + seal + select + attend), "
                          "2 = append_seal then the fused select + attend, 3 = append_seal, score_select, attention "
                          "(1 and 2 fall back to 3 where the fused kernel does not apply)")
-    ap.add_argument("--workload", default="decode", choices=["decode", "correction"],
+    ap.add_argument("--workload", default="decode", choices=["decode", "correction", "represent"],
                     help="decode: the headline decode step; correction: long-context miss correction "
-                         "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage)")
+                         "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage); "
+                         "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
                     help="also run one plain page copy of PAGES pages (HBM counter calibration)")
     return ap.parse_args()
@@ -119,6 +120,10 @@ def main():
     if args.workload == "correction":
         import bench_correction
         bench_correction.run(args)
+        return
+    if args.workload == "represent":
+        import bench_represent
+        bench_represent.run(args)
         return
     import numpy as np
     import torch

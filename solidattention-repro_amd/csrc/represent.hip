@@ -7,9 +7,10 @@
 //      dot over head_dim, no contraction, times 1/sqrt(head_dim)), their max,
 //      exp(logit - max) and the sequential denominator, and the
 //      probabilities p = e / denominator.  Lanes: WL lanes per query (WL the
-//      power of two >= W, at most 64); lane l of a query takes the window
-//      positions w = l, l + WL, ...; the denominator is summed in window
-//      order by every lane of the query through cross-lane reads.
+//      power of two >= W / 4, at most 64); lane l of a query takes the four
+//      window positions w = l, l + WL, l + 2 WL, l + 3 WL, so each query value
+//      read from LDS serves four keys; the denominator is summed in window
+//      order by every lane of the query from the exponentials staged in LDS.
 //   2. block_topk_kernel: per (h, 32-token block), each token's received
 //      mass (the sum over the queries whose window holds it, in ascending
 //      query order, as the reference accumulates it), a stable descending
@@ -29,12 +30,20 @@ namespace sa {
 namespace {
 
 constexpr int D = kHeadDim;
-constexpr int kMaxKeysPerLane = 4;  // window <= 256
+constexpr int kMaxKeysPerLane = 4;  // window <= 4 x 64
 
 // Workgroup of the window kernel: 256 threads, at most 64 queries (32 KB of
 // staged queries).
 template <int WL>
 constexpr int window_threads() { return WL >= 4 ? 256 : 64 * WL; }
+
+// The rounded product q * k of an FP16 key: fma(q, k, +0) rounds q * k once,
+// exactly as a separate multiply does (the sum +0 only turns a -0 product into
+// +0, which no later addition to the running dot can tell apart), and lets
+// the compiler read the FP16 operand directly (v_fma_mix_f32).
+__device__ inline float mul_h(float q, uint32_t w, int hi) {
+  return __builtin_fmaf(q, hi ? hi_h2f(w) : lo_h2f(w), 0.0f);
+}
 
 // exp(x) rounded to float through fixed double operations: Cody-Waite
 // reduction (fdlibm's ln2 split), degree-13 Taylor polynomial in Horner form,
@@ -76,51 +85,82 @@ struct Params {
 };
 
 // Lanes per query: WL (a power of two, 1..64); queries per wave 64 / WL.
-template <int WL>
+// STAGE: the keys of the workgroup's windows are staged in LDS (rows padded
+// by 16 bytes so the lanes of a query, reading consecutive rows, hit
+// different banks); without it every lane reads its own 4 KiB-strided key
+// row from global memory, which the address units serialise.
+template <int WL, bool STAGE>
 __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(const Params p) {
   constexpr int kWindowThreads = window_threads<WL>();
   constexpr int kQueriesPerGroup = kWindowThreads / WL;
+  constexpr int kRowVecs = D / 8;                              // 16 uint4 per key row
+  constexpr int kMaxRows = STAGE ? kQueriesPerGroup + kMaxKeysPerLane * WL - 1 : 1;
   const int h = blockIdx.y;
   const int tid = threadIdx.x;
-  const int lane = tid % kWave;
   const int qi = tid / WL;          // query within the workgroup
   const int wl = tid % WL;          // window lane within the query
   const int g = h / (p.hq / p.hkv);
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * kQueriesPerGroup + qi;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kQueriesPerGroup;
+  const int64_t q = q0 + qi;
+  const int64_t token_elems = 2LL * p.hkv * D;
 
   __shared__ float q_s[kQueriesPerGroup][D];
+  __shared__ uint4 k_s[kMaxRows][kRowVecs + 1];
+  __shared__ __align__(16) float e_s[kQueriesPerGroup][kMaxKeysPerLane * WL];
   for (int e = tid; e < kQueriesPerGroup * D; e += kWindowThreads) {
-    const int64_t qq = static_cast<int64_t>(blockIdx.x) * kQueriesPerGroup + e / D;
+    const int64_t qq = q0 + e / D;
     q_s[e / D][e % D] = qq < p.tokens ? p.pq[(static_cast<int64_t>(h) * p.tokens + qq) * D + e % D] : 0.0f;
+  }
+  // key rows [row0, row0 + rows): every window of the workgroup's queries
+  const int64_t row0 = q0 + 1 > p.window ? q0 + 1 - p.window : 0;
+  if (STAGE) {
+    const int64_t q_last = q0 + kQueriesPerGroup - 1 < p.tokens - 1 ? q0 + kQueriesPerGroup - 1 : p.tokens - 1;
+    const int rows = static_cast<int>(q_last - row0 + 1);
+    for (int e = tid; e < rows * kRowVecs; e += kWindowThreads) {
+      const int r = e / kRowVecs;
+      const int c = e % kRowVecs;
+      k_s[r][c] = reinterpret_cast<const uint4*>(p.kv + (row0 + r) * token_elems + g * D)[c];
+    }
   }
   __syncthreads();
   if (q >= p.tokens) return;  // whole query groups leave together
 
   const int64_t start = q + 1 > p.window ? q + 1 - p.window : 0;
   const int count = static_cast<int>(q - start + 1);
-  const int64_t token_elems = 2LL * p.hkv * D;
 
-  // logits of this lane's keys w = wl + j * WL (sequential dot, no contraction)
+  // logits of this lane's keys w = wl + j * WL: sequential dots, no
+  // contraction, the four keys' chains side by side over each query chunk
+  float dot[kMaxKeysPerLane];
+  int rowk[kMaxKeysPerLane];
+  const uint4* kg[kMaxKeysPerLane];
+#pragma unroll
+  for (int j = 0; j < kMaxKeysPerLane; ++j) {
+    const int w = wl + j * WL;
+    const int wc = w < count ? w : count - 1;  // clamp: its result is dropped
+    dot[j] = 0.0f;
+    rowk[j] = static_cast<int>(start + wc - row0);
+    kg[j] = reinterpret_cast<const uint4*>(p.kv + (start + wc) * token_elems + g * D);
+  }
+#pragma unroll 2
+  for (int c = 0; c < kRowVecs; ++c) {
+    float qv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = q_s[qi][c * 8 + e];
+#pragma unroll
+    for (int j = 0; j < kMaxKeysPerLane; ++j) {
+      const uint4 kk = STAGE ? k_s[rowk[j]][c] : kg[j][c];
+      const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot[j] = dot[j] + mul_h(qv[e], kw[e >> 1], e & 1);
+    }
+  }
   float logit[kMaxKeysPerLane];
   float maximum = -__builtin_huge_valf();
 #pragma unroll
   for (int j = 0; j < kMaxKeysPerLane; ++j) {
-    const int w = wl + j * WL;
     logit[j] = -__builtin_huge_valf();
-    if (w < count) {
-      const uint4* k4 = reinterpret_cast<const uint4*>(p.kv + (start + w) * token_elems + g * D);
-      float dot = 0.0f;
-#pragma unroll 4
-      for (int c = 0; c < D / 8; ++c) {
-        const uint4 kk = k4[c];
-        const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kf = (e & 1) ? hi_h2f(kw[e >> 1]) : lo_h2f(kw[e >> 1]);
-          dot = dot + q_s[qi][c * 8 + e] * kf;
-        }
-      }
-      logit[j] = dot * p.scale;
+    if (wl + j * WL < count) {
+      logit[j] = dot[j] * p.scale;
       if (logit[j] > maximum) maximum = logit[j];
     }
   }
@@ -132,17 +172,23 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
 #pragma unroll
   for (int j = 0; j < kMaxKeysPerLane; ++j) e[j] = (wl + j * WL < count) ? exp_det(logit[j] - maximum) : 0.0f;
 
-  // denominator summed in window order, w = 0 .. count-1: key w is e[w / WL]
-  // of lane w % WL of the query (every lane of the query picks the same j)
-  const int base = lane - wl;  // first lane of this query in the wave
-  float denominator = 0.0f;
-  for (int w = 0; w < count; ++w) {
-    const int j = w / WL;
-    float src = e[0];
+  // denominator summed in window order, w = 0 .. count-1: the query's lanes
+  // put their exponentials in LDS (the query's lanes are in one wave, whose
+  // LDS operations execute in order) and every lane reads them back four at
+  // a time
 #pragma unroll
-    for (int jj = 1; jj < kMaxKeysPerLane; ++jj)
-      if (j == jj) src = e[jj];
-    denominator = denominator + __shfl(src, base + (w % WL), kWave);
+  for (int j = 0; j < kMaxKeysPerLane; ++j) e_s[qi][wl + j * WL] = e[j];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float denominator = 0.0f;
+  const float4* e4 = reinterpret_cast<const float4*>(e_s[qi]);
+  for (int w = 0; w < count; w += 4) {
+    const float4 v = e4[w / 4];
+    denominator = denominator + v.x;
+    if (w + 1 < count) denominator = denominator + v.y;
+    if (w + 2 < count) denominator = denominator + v.z;
+    if (w + 3 < count) denominator = denominator + v.w;
   }
 
   float* row = p.prob + (static_cast<int64_t>(h) * p.tokens + q) * p.window;
@@ -162,13 +208,24 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   const int64_t blocks = p.tokens / kPageTokens;
   __shared__ int order[kPageTokens];
 
+  // received mass: the probabilities of the queries t .. t+W-1 in query
+  // order, loaded 16 at a time before the sequential sum
   float r = 0.0f;
   if (lane < kPageTokens) {
     const int64_t t = static_cast<int64_t>(b) * kPageTokens + lane;
     const int64_t q_end = t + p.window - 1 < p.tokens - 1 ? t + p.window - 1 : p.tokens - 1;
-    for (int64_t q = t; q <= q_end; ++q) {
-      const int64_t start = q + 1 > p.window ? q + 1 - p.window : 0;
-      r = r + p.prob[(static_cast<int64_t>(h) * p.tokens + q) * p.window + (t - start)];
+    constexpr int kBatch = 16;
+    for (int64_t q0 = t; q0 <= q_end; q0 += kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int64_t q = q0 + i;
+        const int64_t start = q + 1 > p.window ? q + 1 - p.window : 0;
+        v[i] = q <= q_end ? p.prob[(static_cast<int64_t>(h) * p.tokens + q) * p.window + (t - start)] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i)
+        if (q0 + i <= q_end) r = r + v[i];
     }
     p.received[static_cast<int64_t>(h) * p.tokens + t] = r;
   }
@@ -195,11 +252,17 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   }
 }
 
+// Windows up to 128 keys stage their key rows in LDS (at most 135 padded
+// rows, 37 KB); longer ones read them from memory.
 template <int WL>
 void launch_window(const Params& p, hipStream_t stream) {
   constexpr int kQueriesPerGroup = window_threads<WL>() / WL;
   const dim3 grid(static_cast<unsigned>((p.tokens + kQueriesPerGroup - 1) / kQueriesPerGroup), p.hq);
-  hipLaunchKernelGGL(window_softmax_kernel<WL>, grid, dim3(window_threads<WL>()), 0, stream, p);
+  if constexpr (WL <= 32) {
+    hipLaunchKernelGGL((window_softmax_kernel<WL, true>), grid, dim3(window_threads<WL>()), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((window_softmax_kernel<WL, false>), grid, dim3(window_threads<WL>()), 0, stream, p);
+  }
 }
 
 }  // namespace
@@ -224,13 +287,13 @@ hipError_t launch_local_causal_representatives(const RepresentativeLaunch& r, hi
   p.topk = r.topk;
   p.rep_stride = r.rep_stride;
   p.scale = r.scale;
-  const int w = r.window;
-  if (w <= 1) launch_window<1>(p, stream);
-  else if (w <= 2) launch_window<2>(p, stream);
-  else if (w <= 4) launch_window<4>(p, stream);
-  else if (w <= 8) launch_window<8>(p, stream);
-  else if (w <= 16) launch_window<16>(p, stream);
-  else if (w <= 32) launch_window<32>(p, stream);
+  const int w = r.window;  // lanes per query: the power of two >= w / 4
+  if (w <= 4) launch_window<1>(p, stream);
+  else if (w <= 8) launch_window<2>(p, stream);
+  else if (w <= 16) launch_window<4>(p, stream);
+  else if (w <= 32) launch_window<8>(p, stream);
+  else if (w <= 64) launch_window<16>(p, stream);
+  else if (w <= 128) launch_window<32>(p, stream);
   else launch_window<64>(p, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
