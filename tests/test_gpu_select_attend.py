@@ -267,3 +267,53 @@ def oracle_step_after_partial_append(case):
     O.paged_append(case.pool, PAGE, case.table[1:2], seq1, k=z, v=z, batch=1, hkv=8, d=D)
     case.seq_len[1] = seq1[0]
     return oracle_step(case, 4, 1, 1, 4)
+
+
+def test_decode_step_graph_replays(hip):
+    """One decode step captured in a HIP graph and replayed 5 times (each
+    replay appends the captured token again and advances the counters), with
+    eager work and synchronisations between replays, equals 5 eager steps on
+    a copy of the state: same bytes, counters, ids and outputs, bit for bit."""
+    case = make_case(740, 4, 16, 8, [32 * 60 + 29, 32 * 33, 32 * 12 + 3, 32 * 70 + 31], table_stride=80, planted=4)
+    rng = np.random.default_rng(41)
+    k = to_dev((rng.standard_normal((4, 8, D)) * 2).astype(np.float32))
+    v = to_dev((rng.standard_normal((4, 8, D)) * 2).astype(np.float32))
+    q = to_dev(case.query)
+    outs = []
+    for mode in ("eager", "graph"):
+        kv = device_kv(case)
+        ws, _ = hip.decode_step_workspace(kv)
+        sel = torch.full((4, 8, 16), -1, dtype=torch.int32, device="cuda")
+        cnt = torch.zeros((4, 8), dtype=torch.int32, device="cuda")
+        out = torch.zeros((4, 16, D), dtype=torch.float32, device="cuda")
+        st = status_tensor()
+        step = lambda: hip.decode_step(kv, k, v, 0, q, 8, 16, 2, 3, SCALE, ws, selected=sel, counts=cnt, out=out,
+                                       status=st)
+        history = []
+        if mode == "eager":
+            for _ in range(5):
+                step()
+                torch.cuda.synchronize()
+                history.append((sel.clone(), cnt.clone(), out.clone()))
+        else:
+            side = torch.cuda.Stream()
+            with torch.cuda.stream(side):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=side):
+                    step()
+            torch.cuda.synchronize()
+            for _ in range(5):
+                g.replay()
+                torch.cuda.synchronize()
+                _ = (out * 2).sum().item()  # eager work between replays
+                history.append((sel.clone(), cnt.clone(), out.clone()))
+        assert int(st.item()) == 0
+        assert int(ws.abs().sum().item()) == 0
+        outs.append((history, kv.seq_len.cpu().numpy(), kv.sealed.cpu().numpy(), kv.generation.cpu().numpy(),
+                     kv.pool.view(torch.int16).cpu().numpy(), kv.reps.cpu().numpy()))
+    (he, *se), (hg, *sg) = outs
+    for a, b in zip(se, sg):
+        assert np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8))
+    for (s1, c1, o1), (s2, c2, o2) in zip(he, hg):
+        assert torch.equal(c1, c2) and torch.equal(s1, s2) and torch.equal(o1, o2)
+    assert int(outs[0][1][3]) == 32 * 70 + 31 + 5  # five tokens appended, a seal on the way
