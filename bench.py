@@ -58,10 +58,13 @@ def parse():
                     help="kernel launches per layer: 1 = the fused decode step (append + seal + select + attend), "
                          "2 = append_seal then the fused select + attend, 3 = append_seal, score_select, attention "
                          "(1 and 2 fall back to 3 where the fused kernel does not apply)")
-    ap.add_argument("--workload", default="decode", choices=["decode", "correction", "represent"],
+    ap.add_argument("--workload", default="decode", choices=["decode", "correction", "represent", "stress"],
                     help="decode: the headline decode step; correction: long-context miss correction "
                          "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage); "
-                         "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4)")
+                         "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4); "
+                         "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers")
+    ap.add_argument("--chunk", type=int, default=None,
+                    help="stress workload: pages per attention chunk (0 = split schedule instead)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
                     help="also run one plain page copy of PAGES pages (HBM counter calibration)")
     return ap.parse_args()
@@ -124,6 +127,10 @@ def main():
     if args.workload == "represent":
         import bench_represent
         bench_represent.run(args)
+        return
+    if args.workload == "stress":
+        import bench_stress
+        bench_stress.run(args)
         return
     import numpy as np
     import torch

@@ -128,6 +128,20 @@ int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query,
                                    size_t workspace_bytes, int32_t splits,
                                    int32_t* status, void* stream);
 
+/* The same attention for lists of very different lengths (mixed contexts
+ * and per-sequence budgets): each (sequence, KV head) page list is cut into
+ * chunks of chunk_pages pages, one workgroup each; workgroups past a short
+ * list's end contribute nothing and the last chunk takes any remainder
+ * beyond max_chunks * chunk_pages.  The partial records (max_chunks per
+ * (sequence, KV head), workspace as sa_hip_attention_workspace_bytes(...,
+ * max_chunks)) are merged with log-sum-exp.  Same result as
+ * sa_hip_sparse_decode_attention within fp32 rounding. */
+int sa_hip_sparse_decode_attention_chunked(
+    const sa_paged_kv* kv, const float* query, const int32_t* selected,
+    const int32_t* counts, int32_t select_groups, int32_t sel_stride,
+    float scale, float* out, void* workspace, size_t workspace_bytes,
+    int32_t chunk_pages, int32_t max_chunks, int32_t* status, void* stream);
+
 /* Split-phase attention, for schedules that attend the blocks already
  * resident while missing blocks are still being copied in (the overlap the
  * reference gets from its copy stream, pipeline_main.cpp:811-848).  Each

@@ -159,7 +159,9 @@ class PagedKvPool {
 // Budgeted selection + sparse decode attention with the scratch they need.
 class SparseDecoder {
  public:
-  SparseDecoder(const PagedKvPool& pool, sa_select_params params, int splits = 0)
+  // chunk_pages: page-list chunk of attend_chunked() (lists of very
+  // different lengths: mixed contexts and per-sequence budgets)
+  SparseDecoder(const PagedKvPool& pool, sa_select_params params, int splits = 0, int chunk_pages = 128)
       : params_(params),
         splits_(splits > 0 ? splits
                            : sa_hip_attention_default_splits(static_cast<int32_t>(pool.batch()),
@@ -173,7 +175,14 @@ class SparseDecoder {
         workspace_((workspace_bytes_ + 3) / 4),
         step_splits_(fused_splits(pool, params, splits)),
         step_workspace_bytes_(step_bytes(pool, step_splits_)),
-        step_workspace_((step_workspace_bytes_ + 3) / 4) {}
+        step_workspace_((step_workspace_bytes_ + 3) / 4),
+        chunk_pages_(chunk_pages),
+        max_chunks_(chunks_for(params.sel_stride, chunk_pages)),
+        chunk_workspace_bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),
+                                                                static_cast<int32_t>(pool.query_heads()),
+                                                                static_cast<int32_t>(pool.kv_heads()), 128,
+                                                                max_chunks_)),
+        chunk_workspace_((chunk_workspace_bytes_ + 3) / 4) {}
 
   // Score every sealed block against the query [batch][query_heads][128]
   // (device) and select per group; ids stay on the device.
@@ -191,6 +200,17 @@ class SparseDecoder {
                                          params_.sel_stride, scale, out, workspace_.get(), workspace_bytes_,
                                          splits_, status, stream),
           "sparse_decode_attention");
+  }
+
+  // attend() with every page list cut into chunk_pages-page chunks, one
+  // workgroup each: for batches whose lists differ widely in length.
+  void attend_chunked(const PagedKvPool& pool, const float* query, float scale, float* out,
+                      hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_sparse_decode_attention_chunked(&kv, query, selected_.get(), counts_.get(), params_.select_groups,
+                                                 params_.sel_stride, scale, out, chunk_workspace_.get(),
+                                                 chunk_workspace_bytes_, chunk_pages_, max_chunks_, status, stream),
+          "sparse_decode_attention_chunked");
   }
 
   // select() then attend(): one launch when fused() is true.
@@ -239,6 +259,18 @@ class SparseDecoder {
   std::size_t step_workspace_bytes_;
   DeviceArray<int32_t> step_workspace_;
 
+  // attend_chunked(): chunks enough for a list of every selectable block
+  // plus two tail pages (a longer list's last chunk takes the rest)
+  int chunk_pages_;
+  int max_chunks_;
+  std::size_t chunk_workspace_bytes_;
+  DeviceArray<float> chunk_workspace_;
+
+  static int chunks_for(int sel_stride, int chunk_pages) {
+    if (chunk_pages < 1) throw std::runtime_error("SparseDecoder: chunk_pages must be positive");
+    const int n = (sel_stride + 2 + chunk_pages - 1) / chunk_pages;
+    return n < 2 ? 2 : (n > 65535 ? 65535 : n);
+  }
   static int fused_splits(const PagedKvPool& pool, const sa_select_params& params, int splits) {
     if (splits > 0) return splits;
     const sa_paged_kv kv = pool.view();

@@ -7,6 +7,10 @@
 // writes a partial (max, sum, acc) record and a small second kernel merges
 // them with log-sum-exp.
 //
+// With chunk_pages > 0 the list is instead cut into chunks of that many
+// pages, one workgroup each (mixed lengths and budgets: a 2048-page list and
+// a 16-page one cost by their length).
+//
 // Measured on MI355X at B=64/16K (512 (sequence, KV head) pairs, 64 selected
 // pages + a partial tail page each): one workgroup of 8 waves per pair,
 // ~8 pages per wave, with non-temporal page loads streams the selected
@@ -47,20 +51,14 @@ struct Params {
   int32_t part_total;    // partial records per (sequence, KV head) in the workspace
   int32_t include_tail;  // attend the unsealed tail too
   int32_t direct;        // write the normalised output instead of a partial record
+  int32_t chunk_pages;   // > 0: workgroup z attends list positions [z*chunk, (z+1)*chunk)
   float qscale;          // softmax scale * log2(e)
 };
 
-template <int G>
-__global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_attention_kernel(const Params p) {
-  constexpr int kWavesPerGroup = waves_per_group<G>();
-  constexpr int kThreads = kWavesPerGroup * kWave;
-  const int g = blockIdx.x;
-  const int b = blockIdx.y;
-  const int z = blockIdx.z;
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-
-  // ---- page list of this (sequence, KV head) -------------------------------
+// The page list of (sequence b, KV head g): selected sealed blocks, then the
+// unsealed tail (when included).  Inconsistent lengths or counts are flagged
+// and clamped to what can be read safely.
+__device__ inline PageList page_list(const Params& p, int b, int g) {
   PageList L{nullptr, 0, 0, 0, 0};
   if (p.v.contig_tokens > 0) {
     L.len = p.v.contig_tokens;
@@ -80,16 +78,48 @@ __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_at
   }
   const int64_t tail_tokens = p.include_tail ? L.len - static_cast<int64_t>(L.sealed) * kPageTokens : 0;
   L.total = L.n_sel + static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
+  return L;
+}
+
+template <int G>
+__global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_attention_kernel(const Params p) {
+  constexpr int kWavesPerGroup = waves_per_group<G>();
+  constexpr int kThreads = kWavesPerGroup * kWave;
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const int z = blockIdx.z;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+
+  const PageList L = page_list(p, b, g);
+  // chunked: a chunk past the end of a short list has nothing to attend and
+  // writes no record (the merge reads only the records of existing chunks)
+  if (p.chunk_pages > 0 && z > 0 && static_cast<int64_t>(z) * p.chunk_pages >= L.total) return;
 
   const LaneGeom lg = lane_geom(p.v, g, lane);
   WaveState<G> st;
   st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
 
-  const int stride = p.splits * kWavesPerGroup;
-  for (int i = z * kWavesPerGroup + wave; i < L.total; i += stride) {
-    const PageRef pr = resolve_page(p.v, b, i, L);
-    if (pr.valid <= 0) continue;
-    st.attend(p.v, pr, lg);
+  if (p.chunk_pages > 0) {
+    // a fixed number of pages per workgroup, whatever the list length, so
+    // long and short lists cost by their length; the last workgroup takes
+    // any remainder, workgroups past the end leave an empty record
+    const int first = z * p.chunk_pages;
+    const int end = z == p.splits - 1
+                        ? L.total
+                        : static_cast<int>(min<int64_t>(L.total, static_cast<int64_t>(first) + p.chunk_pages));
+    for (int i = first + wave; i < end; i += kWavesPerGroup) {
+      const PageRef pr = resolve_page(p.v, b, i, L);
+      if (pr.valid <= 0) continue;
+      st.attend(p.v, pr, lg);
+    }
+  } else {
+    const int stride = p.splits * kWavesPerGroup;
+    for (int i = z * kWavesPerGroup + wave; i < L.total; i += stride) {
+      const PageRef pr = resolve_page(p.v, b, i, L);
+      if (pr.valid <= 0) continue;
+      st.attend(p.v, pr, lg);
+    }
   }
 
   // ---- combine the waves of the workgroup through LDS ----------------------
@@ -126,14 +156,20 @@ __global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const Par
   const int b = blockIdx.y;
   const float* base =
       p.part + ((static_cast<int64_t>(b) * p.v.kv_heads + g) * p.part_total) * G * part_stride(D);
+  // chunked: only the chunks that exist wrote records (chunk 0 always does)
+  int records = p.part_total;
+  if (p.chunk_pages > 0) {
+    const int64_t total = page_list(p, b, g).total;
+    records = static_cast<int>(min<int64_t>(p.part_total, max<int64_t>(1, (total + p.chunk_pages - 1) / p.chunk_pages)));
+  }
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
     const int h = o / D;
     const int d = o % D;
     float mx = kNegInf;
-    for (int zz = 0; zz < p.part_total; ++zz) mx = fmaxf(mx, base[(zz * G + h) * part_stride(D)]);
+    for (int zz = 0; zz < records; ++zz) mx = fmaxf(mx, base[(zz * G + h) * part_stride(D)]);
     float lw = 0.0f, aw = 0.0f;
     if (mx != kNegInf) {
-      for (int zz = 0; zz < p.part_total; ++zz) {
+      for (int zz = 0; zz < records; ++zz) {
         const float* rec = base + (zz * G + h) * part_stride(D);
         if (rec[0] == kNegInf) continue;
         const float f = __builtin_amdgcn_exp2f(rec[0] - mx);
@@ -194,6 +230,7 @@ hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t strea
     p.include_tail = a.include_tail;
     p.direct = 0;
   }
+  p.chunk_pages = a.chunk_pages;
   p.qscale = a.scale * kLog2e;
   const int group = a.query_heads / a.kv_heads;
   switch (group) {

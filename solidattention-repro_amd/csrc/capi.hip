@@ -104,7 +104,7 @@ int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads, int32_t
 static int attention_common(const sa_paged_kv* kv, const float* query, const int32_t* selected,
                             const int32_t* counts, int32_t select_groups, int32_t sel_stride, float scale,
                             float* out, void* workspace, size_t workspace_bytes, int32_t splits,
-                            int32_t* status, void* stream, int64_t contig_tokens) {
+                            int32_t* status, void* stream, int64_t contig_tokens, int32_t chunk_pages = 0) {
   sa::AttnLaunch a{};
   a.pool = kv->pool;
   a.table = kv->block_table;
@@ -126,6 +126,7 @@ static int attention_common(const sa_paged_kv* kv, const float* query, const int
   a.kv_heads = kv->kv_heads;
   a.splits = splits;
   a.scale = scale;
+  a.chunk_pages = chunk_pages;
   const size_t need =
       sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
   if (workspace_bytes < need || (need && !workspace))
@@ -147,6 +148,25 @@ int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query, co
   if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "sparse_decode_attention: splits out of range");
   return attention_common(kv, query, selected, counts, select_groups, sel_stride, scale, out, workspace,
                           workspace_bytes, splits, status, stream, 0);
+}
+
+int sa_hip_sparse_decode_attention_chunked(const sa_paged_kv* kv, const float* query, const int32_t* selected,
+                                           const int32_t* counts, int32_t select_groups, int32_t sel_stride,
+                                           float scale, float* out, void* workspace, size_t workspace_bytes,
+                                           int32_t chunk_pages, int32_t max_chunks, int32_t* status,
+                                           void* stream) {
+  if (int e = check_geometry(kv, "attention_chunked")) return e;
+  if (!query || !out || !selected || !counts)
+    return fail(SA_HIP_EINVAL, "attention_chunked: null query/out/selected/counts");
+  if (!aligned16(query)) return fail(SA_HIP_EINVAL, "attention_chunked: query must be 16-byte aligned");
+  if (select_groups <= 0 || kv->kv_heads % select_groups != 0)
+    return fail(SA_HIP_EINVAL, "attention_chunked: select_groups must divide kv_heads");
+  if (sel_stride <= 0) return fail(SA_HIP_EINVAL, "attention_chunked: sel_stride must be positive");
+  if (chunk_pages < 1) return fail(SA_HIP_EINVAL, "attention_chunked: chunk_pages must be positive");
+  if (max_chunks < 2 || max_chunks > 65535)
+    return fail(SA_HIP_EINVAL, "attention_chunked: max_chunks must lie in [2, 65535]");
+  return attention_common(kv, query, selected, counts, select_groups, sel_stride, scale, out, workspace,
+                          workspace_bytes, max_chunks, status, stream, 0, chunk_pages);
 }
 
 int sa_hip_sparse_decode_attention_partial(const sa_paged_kv* kv, const float* query, const int32_t* selected,

@@ -47,6 +47,7 @@ struct AttnLaunch {
   int32_t part_base;
   int32_t part_total;
   int32_t include_tail;
+  int32_t chunk_pages;     // > 0 (mode 0): split by chunks of pages, `splits` chunks
 };
 
 hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t stream);

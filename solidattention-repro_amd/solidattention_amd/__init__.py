@@ -59,6 +59,8 @@ EXPORTS = {
     "sa_hip_sparse_decode_attention_partial": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _I32, _P, _SZ, _I32, _I32,
                                                          _I32, _P, _P]),
     "sa_hip_attention_merge": (C.c_int, [_KV, _P, _SZ, _I32, _P, _P]),
+    "sa_hip_sparse_decode_attention_chunked": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _I32,
+                                                         _P, _P]),
     "sa_hip_contiguous_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "sa_hip_attention_contiguous": (C.c_int, [_P, _P, _I64, _I32, _I32, _I32, _F, _P, _P, _SZ, _P]),
     "sa_hip_consume_checksum": (C.c_int, [_P, _I32, _P, _P]),
@@ -292,6 +294,25 @@ def sparse_decode_attention(kv: PagedKV, query, selected, counts, scale, out=Non
         C.byref(s), _ptr(query), _ptr(selected), _ptr(counts), select_groups, sel_stride, C.c_float(scale),
         _ptr(out), _ptr(workspace) if nbytes else None, nbytes, splits, _ptr(status), _stream(stream)),
         "sparse_decode_attention")
+    return out
+
+
+def sparse_decode_attention_chunked(kv: PagedKV, query, selected, counts, scale, chunk_pages, max_chunks, out=None,
+                                    workspace=None, status=None, stream=None):
+    """Attention with every page list cut into chunks of chunk_pages pages
+    (one workgroup each, merged): for mixed lengths and budgets."""
+    import torch
+    select_groups, sel_stride = selected.shape[1], selected.shape[2]
+    if out is None:
+        out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=query.device)
+    nbytes = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, max_chunks)
+    if workspace is None:
+        workspace = torch.zeros(nbytes // 4, dtype=torch.float32, device=query.device)
+    s = kv.struct()
+    check(lib().sa_hip_sparse_decode_attention_chunked(
+        C.byref(s), _ptr(query), _ptr(selected), _ptr(counts), select_groups, sel_stride, C.c_float(scale),
+        _ptr(out), _ptr(workspace), nbytes, chunk_pages, max_chunks, _ptr(status), _stream(stream)),
+        "sparse_decode_attention_chunked")
     return out
 
 

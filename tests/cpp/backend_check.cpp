@@ -314,6 +314,20 @@ void check_decode_step() {
   record("decode_step_selected_ids_exact", ids_ok ? "true" : "false", ids_ok);
   record("decode_step_state_bytes_exact", state_ok && reps_ok ? "true" : "false", state_ok && reps_ok);
   record("decode_step_max_rel_error", num(max_err), max_err <= 2e-3);
+
+  // the chunked schedule over the last step's selection: 3-page chunks of
+  // lists of up to 9 pages, against the oracle's attention of that step
+  sa::hip::SparseDecoder chunked(pool, sa_select_params{static_cast<int32_t>(hkv), static_cast<int32_t>(budget), 1, 2,
+                                                        static_cast<int32_t>(budget), 0, nullptr},
+                                 0, 3);
+  chunked.select(pool, dq.get());
+  chunked.attend_chunked(pool, dq.get(), scale, dout.get());
+  const auto cout_ = dout.download();
+  double chunk_err = 0.0;
+  for (std::size_t i = 0; i < out.size(); ++i)
+    chunk_err = std::max(chunk_err, std::abs(static_cast<double>(out[i]) - cout_[i]) /
+                                        std::max(1.0, std::abs(static_cast<double>(out[i]))));
+  record("attend_chunked_max_rel_error", num(chunk_err), chunk_err <= 2e-3);
 }
 
 }  // namespace

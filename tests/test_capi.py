@@ -115,3 +115,24 @@ def test_local_causal_argument_checks():
     for kw in bad:
         assert call(**kw) == -1, kw
         assert L.sa_hip_last_error()
+
+
+def test_chunked_attention_argument_checks():
+    """Chunked attention refuses a non-positive chunk, fewer than two or
+    more than 65535 chunks, and a short workspace, before any launch."""
+    import solidattention_amd as sa
+    L = sa.lib()
+    fake = 4096
+    kv = sa.PagedKVStruct(fake, fake, fake, fake, fake, fake, 100, 2, 10, 8, 12, 16, 8, 128, 0)
+    need = L.sa_hip_attention_workspace_bytes(2, 16, 8, 128, 4)
+
+    def call(chunk=8, chunks=4, wsb=need, sel_stride=10):
+        return L.sa_hip_sparse_decode_attention_chunked(C.byref(kv), C.c_void_p(fake), C.c_void_p(fake),
+                                                        C.c_void_p(fake), 8, sel_stride, C.c_float(0.1),
+                                                        C.c_void_p(fake), C.c_void_p(fake), wsb, chunk, chunks,
+                                                        None, None)
+
+    for kw in [dict(chunk=0), dict(chunk=-3), dict(chunks=1), dict(chunks=65536), dict(wsb=need - 4),
+               dict(sel_stride=0)]:
+        assert call(**kw) == -1, kw
+        assert L.sa_hip_last_error()

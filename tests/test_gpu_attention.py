@@ -17,15 +17,19 @@ pytestmark = pytest.mark.gpu
 SCALE = float(np.float32(1.0) / np.sqrt(np.float32(128)))
 
 
-def run_case(hip, case, select_groups, budget, init, local, splits=None):
+def run_case(hip, case, select_groups, budget, init, local, splits=None, chunk=None):
     sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, case.batch, case.hq, case.hkv, D,
                                     case.rep_heads, case.rep_stride, select_groups, budget, init, local)
     expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, sel, cnt,
                                       select_groups, case.query, case.batch, case.hq, case.hkv, D, SCALE)
     kv = device_kv(case)
     st = status_tensor()
-    out = hip.sparse_decode_attention(kv, to_dev(case.query), to_dev(sel), to_dev(cnt), SCALE, splits=splits,
-                                      status=st)
+    if chunk:
+        out = hip.sparse_decode_attention_chunked(kv, to_dev(case.query), to_dev(sel), to_dev(cnt), SCALE,
+                                                  chunk[0], chunk[1], status=st)
+    else:
+        out = hip.sparse_decode_attention(kv, to_dev(case.query), to_dev(sel), to_dev(cnt), SCALE, splits=splits,
+                                          status=st)
     torch.cuda.synchronize()
     assert int(st.item()) == 0
     return out.cpu().numpy(), expect
@@ -45,6 +49,27 @@ def test_split_counts(hip, splits):
     case = make_case(20, 2, 16, 8, [32 * 70 + 9, 32 * 33 + 1])
     got, expect = run_case(hip, case, 8, 20, 2, 4, splits=splits)
     assert_close_2e3(got, expect)
+
+
+@pytest.mark.parametrize("chunk,max_chunks", [(1, 200), (4, 3), (5, 9), (16, 8), (64, 2)])
+def test_chunked_pages(hip, chunk, max_chunks):
+    """Lists of 41, 4, 34 and 1 pages cut into chunks: one page per chunk,
+    a last chunk taking the remainder beyond max_chunks * chunk, chunks
+    past the end of short lists, and a chunk longer than every list."""
+    print(f"case: chunk={chunk} max_chunks={max_chunks}", flush=True)
+    case = make_case(24, 4, 16, 8, [32 * 70 + 9, 32 * 3 + 5, 32 * 33 + 1, 31], planted=2)
+    got, expect = run_case(hip, case, 8, 40, 1, 2, chunk=(chunk, max_chunks))
+    assert_close_2e3(got, expect)
+
+
+def test_chunked_equals_split_within_rounding(hip):
+    """The chunked and the split schedules sum the same terms in another
+    order: equal within fp32 rounding."""
+    case = make_case(25, 3, 32, 8, [32 * 90 + 7, 32 * 12, 32 * 40 + 31])
+    a, expect = run_case(hip, case, 8, 48, 2, 3, splits=3)
+    b, _ = run_case(hip, case, 8, 48, 2, 3, chunk=(8, 7))
+    assert_close_2e3(b, expect)
+    np.testing.assert_allclose(b, a, rtol=1e-5, atol=1e-6)
 
 
 def test_workspace_reuse_across_launches(hip):

@@ -36,9 +36,14 @@ def test_stress_mixed_lengths_budgets_outliers(hip, seed):
     sel, cnt = hip.score_select(kv, q, 8, 64, INIT, LOCAL, status=st, sel_stride=sel_stride,
                                 budgets=to_dev(budgets))
     out = hip.sparse_decode_attention(kv, q, sel, cnt, SCALE, status=st)
+    # the schedule for uneven lists: 16-page chunks, enough for the longest
+    chunk = 16
+    out_c = hip.sparse_decode_attention_chunked(kv, q, sel, cnt, SCALE, chunk, (sel_stride + 1) // chunk + 1,
+                                                status=st)
     torch.cuda.synchronize()
     assert int(st.item()) == 0
     got_sel, got_cnt, got = sel.cpu().numpy(), cnt.cpu().numpy(), out.cpu().numpy()
+    got_c = out_c.cpu().numpy()
 
     esel = np.full((batch, 8, sel_stride), -1, np.int32)
     ecnt = np.zeros((batch, 8), np.int32)
@@ -51,13 +56,15 @@ def test_stress_mixed_lengths_budgets_outliers(hip, seed):
     assert np.array_equal(got_cnt, ecnt)
     expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, esel, ecnt, 8,
                                       case.query, batch, 16, 8, D, SCALE)
-    assert np.isfinite(got).all()
+    assert np.isfinite(got).all() and np.isfinite(got_c).all()
     assert_close_2e3(got, expect)
+    assert_close_2e3(got_c, expect)
     for b in np.nonzero(budgets == n_blocks)[0]:
         n = int(case.seq_len[b])
         pages = [case.pool[case.table[b, i]].reshape(PAGE, -1) for i in range(n // PAGE)]
         dense = O.attention_reference(np.concatenate(pages).ravel(), case.query[b], n, 16, 8, D, SCALE)
         assert_close_2e3(got[b], dense)
+        assert_close_2e3(got_c[b], dense)
 
 
 def test_bad_per_sequence_budget_is_flagged(hip):
@@ -71,3 +78,24 @@ def test_bad_per_sequence_budget_is_flagged(hip):
     assert int(st.item()) & hip.STATUS_BAD_BUDGET
     c = cnt.cpu().numpy()
     assert (c[1] == 0).all() and (c[0] == 20).all()
+
+
+def test_stress_full_size_one_layer(hip, capsys):
+    """The stress workload at its full size (batch 128, contexts 1K-64K, one
+    layer, ~17 GiB of pages): append + seal, per-sequence budgets and chunked
+    attention; the longest and shortest sequence and one of each budget
+    class bit-exact in selection and within 2e-3 of the oracle, full-budget
+    ones within 2e-3 of dense attention."""
+    import argparse
+    import json
+
+    import bench_stress
+    args = argparse.Namespace(layers=1, steps=1, warmup=1, seed=77, chunk=128, splits=0, check_seqs=1,
+                              no_cpu_baseline=True)
+    print("case: stress full size, 1 layer, chunk 128", flush=True)
+    bench_stress.run(args)
+    line = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
+    par = line["parity"]
+    print(par, flush=True)
+    assert par["selection_bit_exact"] and par["attention_within_2e-3"]
+    assert par["full_budget_sequences"] >= 1 and par["full_budget_equals_dense_within_2e-3"]
