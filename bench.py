@@ -63,6 +63,9 @@ def parse():
                          "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage); "
                          "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4); "
                          "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers")
+    ap.add_argument("--select", default="auto", choices=["auto", "single", "split"],
+                    help="separate selection launch: one workgroup per list, scoring split over 256-block "
+                         "workgroups, or the library's preference")
     ap.add_argument("--chunk", type=int, default=None,
                     help="stress workload: pages per attention chunk (0 = split schedule instead)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
@@ -171,6 +174,10 @@ def main():
     if launches < 3:
         splits = 1
     step_ws, _ = sa.decode_step_workspace(L[0].kv, 1)
+    split_select = args.select == "split" or (
+        args.select == "auto" and sa.score_select_split_preferred(L[0].kv, hkv, budget, init, local))
+    scores = (torch.zeros((batch, hkv, L[0].kv.rep_stride), dtype=torch.float32, device="cuda")
+              if split_select else None)
 
     def layer_launches(ly, s, e=None):
         """One layer of one decode step; e = 4 timing events (append, select, attention)."""
@@ -189,8 +196,12 @@ def main():
                              counts=ly.counts, out=ly.out, splits=1, status=status)
             if e: e[2].record(stream)
         else:
-            sa.score_select(ly.kv, ly.q[s], hkv, budget, init, local, selected=ly.selected, counts=ly.counts,
-                            status=status)
+            if split_select:
+                sa.score_select_split(ly.kv, ly.q[s], hkv, budget, init, local, selected=ly.selected,
+                                      counts=ly.counts, scores=scores, status=status)
+            else:
+                sa.score_select(ly.kv, ly.q[s], hkv, budget, init, local, selected=ly.selected, counts=ly.counts,
+                                status=status)
             if e: e[2].record(stream)
             sa.sparse_decode_attention(ly.kv, ly.q[s], ly.selected, ly.counts, scale, out=ly.out, splits=splits,
                                        workspace=workspace, status=status)
@@ -330,7 +341,8 @@ def main():
                                f"attention", "layers": layers, "batch": batch, "query_heads": hq,
                    "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
                    "init_blocks": init, "local_blocks": local, "page_tokens": PAGE, "splits": splits,
-                   "launches_per_layer": launches},
+                   "launches_per_layer": launches,
+                   "selection": None if launches < 3 else ("split" if split_select else "single")},
         "tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
         "launch": "hip graph per decode step" if graph else "eager",
         "eager_us_per_layer": round(eager_ms * 1000.0 / args.steps / layers, 3),

@@ -123,12 +123,16 @@ def run(args):
         ly["ws"] = torch.zeros(sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, TOTAL_SPLITS) // 4,
                                dtype=torch.float32, device=dev)
         ly["out"] = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
+        ly["scores"] = torch.zeros((B, 1, kv.rep_stride), dtype=torch.float32, device=dev)
         ly["done"] = torch.cuda.Event()
         ly["done"].record(copy_stream)
         Ls.append(ly)
     torch.cuda.synchronize()
     log(f"setup {time.time() - t0:.1f}s: {layers} layers, host store {layers * B * TS * page_bytes / 2**30:.1f} GiB pinned")
 
+    # 8 lists (one shared selection per sequence): the split scoring form
+    split_select = sa.score_select_split_preferred(Ls[0]["kv"], 1, BUDGET, INIT, LOCAL)
+    select_events = []
     host_tables = [torch.from_numpy(ly["table"]).pin_memory() for ly in Ls]
     host_fill = [torch.zeros((2, B * BUDGET), dtype=torch.int64).pin_memory() for _ in Ls]
     for ly in Ls:
@@ -145,8 +149,16 @@ def run(args):
         for li, ly in enumerate(Ls):
             kv = ly["kv"]
             sa.append_seal(kv, ly["knew"][s], ly["vnew"][s], 0, status=status)
-            sa.score_select(kv, ly["q"][s], 1, BUDGET, INIT, LOCAL, selected=ly["sel"], counts=ly["cnt"],
-                            status=status)
+            e_s0, e_s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e_s0.record(compute)
+            if split_select:
+                sa.score_select_split(kv, ly["q"][s], 1, BUDGET, INIT, LOCAL, selected=ly["sel"], counts=ly["cnt"],
+                                      scores=ly["scores"], status=status)
+            else:
+                sa.score_select(kv, ly["q"][s], 1, BUDGET, INIT, LOCAL, selected=ly["sel"], counts=ly["cnt"],
+                                status=status)
+            e_s1.record(compute)
+            select_events.append((e_s0, e_s1))
             ids = ly["sel"].cpu().numpy()[:, 0, :]  # synchronises the compute stream
             table = ly["table"]
             hl = host_lists[li].numpy()
@@ -269,6 +281,9 @@ def run(args):
         "workload": "long-context miss correction, Qwen3-8B shape, B=8, 131072 tokens, budget 128 blocks",
         "layers": layers, "steps": steps, "warmup": warmup,
         "history_coverage": round(coverage, 4),
+        "selection": {"form": "split" if split_select else "single",
+                      "us_per_layer": round(1000.0 * float(np.mean([a.elapsed_time(b) for a, b in select_events])),
+                                            1)},
         "schedules": results,
         "page_bytes": page_bytes,
         "checks": {"resident_set_equals_selection": sets_ok, "slot_bytes_equal_store": bytes_ok,

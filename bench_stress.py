@@ -120,6 +120,11 @@ def run(args):
     ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, splits)
     workspace = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
+    select_mode = getattr(args, "select", "auto")
+    split_select = select_mode == "split" or (
+        select_mode == "auto" and sa.score_select_split_preferred(L[0].kv, HKV, sel_stride, INIT, LOCAL, sel_stride))
+    scores = (torch.zeros((B, HKV, L[0].kv.rep_stride), dtype=torch.float32, device="cuda")
+              if split_select else None)
 
     def attend(ly, s):
         if chunk > 0:
@@ -133,8 +138,12 @@ def run(args):
         if e: e[0].record(stream)
         sa.append_seal(ly.kv, ly.knew[s], ly.vnew[s], 0, status=status)
         if e: e[1].record(stream)
-        sa.score_select(ly.kv, ly.q[s], HKV, sel_stride, INIT, LOCAL, selected=selected, counts=counts,
-                        status=status, sel_stride=sel_stride, budgets=budgets_d)
+        if split_select:
+            sa.score_select_split(ly.kv, ly.q[s], HKV, sel_stride, INIT, LOCAL, selected=selected, counts=counts,
+                                  scores=scores, status=status, sel_stride=sel_stride, budgets=budgets_d)
+        else:
+            sa.score_select(ly.kv, ly.q[s], HKV, sel_stride, INIT, LOCAL, selected=selected, counts=counts,
+                            status=status, sel_stride=sel_stride, budgets=budgets_d)
         if e: e[2].record(stream)
         attend(ly, s)
         if e: e[3].record(stream)
@@ -207,7 +216,7 @@ def run(args):
                    "budget_blocks": {"16": int((klass == 0).sum()), "64": int((klass == 1).sum()),
                                      "full": int((klass == 2).sum())},
                    "init_blocks": INIT, "local_blocks": LOCAL, "chunk_pages": chunk, "max_chunks": max_chunks,
-                   "splits": splits},
+                   "splits": splits, "selection": "split" if split_select else "single"},
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "achieved_layer_hbm_gbps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "kernels_us": {"attention": round(kernel_us, 3), "attention_in_step": round(att, 3),

@@ -193,6 +193,22 @@ int sa_hip_score_select(const sa_paged_kv* kv, const float* query,
                         int32_t* counts, float* scores, int32_t* status,
                         void* stream);
 
+/* The same selection with the scoring spread over workgroups of 256 blocks
+ * each (two launches: scores, then selection from them), for batches with
+ * few (sequence, group) lists or long ones, where one workgroup per list
+ * leaves the device idle.  scores is required ([batch][select_groups]
+ * [rep_stride] fp32, the same values sa_hip_score_select writes); ids,
+ * counts and scores are bit-identical to sa_hip_score_select's. */
+int sa_hip_score_select_split(const sa_paged_kv* kv, const float* query,
+                              const sa_select_params* params, int32_t* selected,
+                              int32_t* counts, float* scores, int32_t* status,
+                              void* stream);
+
+/* 1 when sa_hip_score_select_split is expected to be the faster form for
+ * this geometry (fewer (sequence, group) lists than compute units), else 0. */
+int sa_hip_score_select_split_preferred(const sa_paged_kv* kv,
+                                        const sa_select_params* params);
+
 /* ---- R3 + R6 fused: one layer's select-then-attend ----------------------- */
 
 /* sa_hip_score_select(kv, query, params, selected, counts, NULL, status)

@@ -331,6 +331,24 @@ int sa_hip_score_select(const sa_paged_kv* kv, const float* query, const sa_sele
   return check_hip(sa::launch_score_select(l, as_stream(stream)), "score_select launch");
 }
 
+int sa_hip_score_select_split(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
+                              int32_t* selected, int32_t* counts, float* scores, int32_t* status, void* stream) {
+  sa::SelectLaunch l;
+  if (int e = select_launch(kv, query, params, selected, counts, scores, status, "score_select_split", &l)) return e;
+  if (!scores) return fail(SA_HIP_EINVAL, "score_select_split: the scores buffer is required");
+  return check_hip(sa::launch_score_select_split(l, as_stream(stream)), "score_select_split launch");
+}
+
+int sa_hip_score_select_split_preferred(const sa_paged_kv* kv, const sa_select_params* params) {
+  if (!kv || !params || params->select_groups <= 0) return 0;
+  // measured on MI355X: spreading the scoring pays while the lists alone
+  // leave compute units idle (8 lists of 4096 blocks: 424 -> 95 us; 64 lists:
+  // 75 -> 41 us) and costs ~10% once every CU has a list (256 lists of 1024
+  // blocks: 32 -> 35 us; 1024 lists of 2048 blocks: 204 -> 220 us)
+  const int64_t lists = static_cast<int64_t>(kv->batch) * params->select_groups;
+  return lists < static_cast<int64_t>(sa::compute_units()) ? 1 : 0;
+}
+
 int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv, const sa_select_params* params) {
   if (!kv || !params) return 1;
   // the fused kernel runs two workgroups per CU; it is the better choice

@@ -74,6 +74,8 @@ struct SelectLaunch {
 };
 
 hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream);
+// scoring over chunks of 256 blocks into s.scores, then selection from them
+hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream);
 
 // Compute units of the current device (cached per device; 256 if unknown).
 int compute_units();

@@ -88,6 +88,79 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   if (tid == 0) p.counts[out_row] = count;
 }
 
+// ---- split selection: scoring spread over chunks of blocks -------------------
+// For few or very long lists, one workgroup per (sequence, selection group)
+// leaves most of the device idle while its lanes walk hundreds of blocks each.
+// The split form scores kChunkBlocks blocks per workgroup (one per lane, the
+// same score_one() arithmetic) into the fp32 scores row, then a second kernel
+// per (sequence, selection group) turns the row into keys and selects exactly
+// as score_select_kernel does.
+constexpr int kChunkBlocks = 256;
+
+template <int GR>
+__global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params p) {
+  const int sg = blockIdx.x;
+  const int b = blockIdx.y;
+  const int first = blockIdx.z * kChunkBlocks;
+  const int n = p.sealed[b];
+  // invalid lengths are flagged by the selection kernel
+  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks || first >= n) return;
+  __shared__ float q_s[kMaxSelectHeads * D];
+  ScoreArgs a{};
+  a.query = p.query;
+  a.reps = p.reps;
+  a.b = b;
+  a.h_first = sg * p.heads_per_sel;
+  a.heads_per_sel = p.heads_per_sel;
+  a.query_heads = p.query_heads;
+  a.group = p.group;
+  a.rep_heads = p.rep_heads;
+  a.rep_stride = p.rep_stride;
+  load_query<kChunkBlocks>(a, q_s);
+  __syncthreads();
+  const int blk = first + static_cast<int>(threadIdx.x);
+  if (blk < n) {
+    float unused[kScoreBatch];
+    const float score = score_one<GR, false>(a, q_s, blk, unused, false);
+    p.scores[(static_cast<int64_t>(b) * p.select_groups + sg) * p.rep_stride + blk] = score;
+  }
+}
+
+template <int kThreads>
+__global__ __launch_bounds__(kThreads) void select_scores_kernel(const Params p) {
+  constexpr int kWaves = kThreads / kWave;
+  const int sg = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  __shared__ uint32_t keys[kMaxSelectBlocks];
+  __shared__ SelectSmem<kWaves> sm;
+  const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
+  int32_t* out_ids = p.selected + out_row * p.sel_stride;
+  const int n = p.sealed[b];
+  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) {
+    if (tid == 0) {
+      flag_status(p.status, kStatusCapacity);
+      p.counts[out_row] = 0;
+    }
+    return;
+  }
+  const float* row = p.scores + out_row * p.rep_stride;
+  for (int blk = tid; blk < n; blk += kThreads) keys[blk] = order_key(row[blk]);
+  __syncthreads();
+  const Budget bs = budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
+  if (bs.bad) {
+    if (tid == 0) {
+      flag_status(p.status, kStatusBadBudget);
+      p.counts[out_row] = 0;
+    }
+    return;
+  }
+  uint32_t threshold = 0xffffffffu, equal_take = 0;
+  if (bs.k > 0) radix_threshold<kThreads>(keys, bs, sm, threshold, equal_take);
+  const int count = compact_ids<kThreads>(keys, n, bs, threshold, equal_take, out_ids, p.sel_stride, nullptr, sm);
+  if (tid == 0) p.counts[out_row] = count;
+}
+
 // 16 waves when (rounds x blocks per lane) is smaller than with 8 waves;
 // resident workgroups per CU: two of 8 waves, one of 16.
 bool wide_select(int64_t workgroups, int64_t blocks) {
@@ -106,21 +179,7 @@ void launch_gr(const Params& p, dim3 grid, hipStream_t stream) {
   }
 }
 
-}  // namespace
-
-int compute_units() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
-hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
+Params make_params(const SelectLaunch& s) {
   Params p{};
   p.query = s.query;
   p.reps = s.reps;
@@ -140,6 +199,25 @@ hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
   p.init_blocks = s.init_blocks;
   p.local_blocks = s.local_blocks;
   p.sel_stride = s.sel_stride;
+  return p;
+}
+
+}  // namespace
+
+int compute_units() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
+  const Params p = make_params(s);
   const dim3 grid(s.select_groups, s.batch);
   const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
   switch (gr) {
@@ -149,6 +227,24 @@ hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
     case 8: launch_gr<8>(p, grid, stream); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream) {
+  const Params p = make_params(s);
+  const int chunks = (s.rep_stride + kChunkBlocks - 1) / kChunkBlocks;
+  const dim3 grid(s.select_groups, s.batch, chunks);
+  const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
+  switch (gr) {
+    case 1: hipLaunchKernelGGL(score_chunk_kernel<1>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(score_chunk_kernel<2>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(score_chunk_kernel<4>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+    case 8: hipLaunchKernelGGL(score_chunk_kernel<8>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(select_scores_kernel<512>, dim3(s.select_groups, s.batch), dim3(512), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -59,6 +59,8 @@ EXPORTS = {
     "sa_hip_sparse_decode_attention_partial": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _I32, _P, _SZ, _I32, _I32,
                                                          _I32, _P, _P]),
     "sa_hip_attention_merge": (C.c_int, [_KV, _P, _SZ, _I32, _P, _P]),
+    "sa_hip_score_select_split": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _P, _P]),
+    "sa_hip_score_select_split_preferred": (C.c_int, [_KV, C.POINTER(SelectParamsStruct)]),
     "sa_hip_sparse_decode_attention_chunked": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _I32,
                                                          _P, _P]),
     "sa_hip_contiguous_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
@@ -193,6 +195,33 @@ def score_select(kv: PagedKV, query, select_groups, budget, init, local, selecte
     check(lib().sa_hip_score_select(C.byref(s), _ptr(query), C.byref(params), _ptr(selected), _ptr(counts),
                                     _ptr(scores), _ptr(status), _stream(stream)), "score_select")
     return selected, counts
+
+
+def score_select_split(kv: PagedKV, query, select_groups, budget, init, local, selected=None, counts=None,
+                       scores=None, status=None, sel_stride=None, stream=None, budgets=None):
+    """score_select with the scoring spread over 256-block workgroups; scores
+    ([batch][select_groups][rep_stride] fp32) is written and returned."""
+    import torch
+    sel_stride = sel_stride or budget
+    dev = query.device
+    if selected is None:
+        selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
+    if scores is None:
+        scores = torch.zeros((kv.batch, select_groups, kv.rep_stride), dtype=torch.float32, device=dev)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
+    s = kv.struct()
+    check(lib().sa_hip_score_select_split(C.byref(s), _ptr(query), C.byref(params), _ptr(selected), _ptr(counts),
+                                          _ptr(scores), _ptr(status), _stream(stream)), "score_select_split")
+    return selected, counts, scores
+
+
+def score_select_split_preferred(kv: PagedKV, select_groups, budget, init, local, sel_stride=None) -> bool:
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride or budget, 0, None)
+    s = kv.struct()
+    return bool(lib().sa_hip_score_select_split_preferred(C.byref(s), C.byref(params)))
 
 
 def select_attend(kv: PagedKV, query, select_groups, budget, init, local, scale, selected=None, counts=None,

@@ -136,3 +136,16 @@ def test_chunked_attention_argument_checks():
                dict(sel_stride=0)]:
         assert call(**kw) == -1, kw
         assert L.sa_hip_last_error()
+
+
+def test_split_selection_requires_scores():
+    """The split selection refuses a null scores buffer before any launch,
+    and prefers itself only when the lists leave compute units idle."""
+    import solidattention_amd as sa
+    L = sa.lib()
+    fake = 4096
+    kv = sa.PagedKVStruct(fake, fake, fake, fake, fake, fake, 100, 2, 10, 8, 12, 16, 8, 128, 0)
+    params = sa.SelectParamsStruct(8, 8, 1, 2, 8, 0, None)
+    rc = L.sa_hip_score_select_split(C.byref(kv), C.c_void_p(fake), C.byref(params), C.c_void_p(fake),
+                                     C.c_void_p(fake), None, None, None)
+    assert rc == -1 and b"scores" in L.sa_hip_last_error()

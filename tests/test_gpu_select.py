@@ -12,29 +12,36 @@ from paged_case import D, make_case
 pytestmark = pytest.mark.gpu
 
 
-def gpu_select(hip, case, select_groups, budget, init, local, sel_stride=None):
+def gpu_select(hip, case, select_groups, budget, init, local, sel_stride=None, split=False):
     kv = device_kv(case)
     sel_stride = sel_stride or budget
     scores = torch.zeros((case.batch, select_groups, case.rep_stride), dtype=torch.float32, device="cuda")
     st = status_tensor()
-    sel, cnt = hip.score_select(kv, to_dev(case.query), select_groups, budget, init, local, scores=scores,
-                                status=st, sel_stride=sel_stride)
+    if split:
+        sel, cnt, _ = hip.score_select_split(kv, to_dev(case.query), select_groups, budget, init, local,
+                                             scores=scores, status=st, sel_stride=sel_stride)
+    else:
+        sel, cnt = hip.score_select(kv, to_dev(case.query), select_groups, budget, init, local, scores=scores,
+                                    status=st, sel_stride=sel_stride)
     torch.cuda.synchronize()
     assert int(st.item()) == 0
     return sel.cpu().numpy(), cnt.cpu().numpy(), scores.cpu().numpy()
 
 
 def check(hip, case, select_groups, budget, init, local):
-    sel, cnt, sc = gpu_select(hip, case, select_groups, budget, init, local)
+    """Both forms, one workgroup per list and the split scoring, against the
+    oracle: same ids, same score bits."""
     esel, ecnt, esc = O.paged_score_select(case.query, case.reps, case.sealed, case.batch, case.hq, case.hkv, D,
                                            case.rep_heads, case.rep_stride, select_groups, budget, init, local,
                                            want_scores=True)
-    assert np.array_equal(cnt, ecnt)
-    for b in range(case.batch):
-        n = int(case.sealed[b])
-        for g in range(select_groups):
-            assert sel[b, g, : cnt[b, g]].tolist() == esel[b, g, : ecnt[b, g]].tolist(), (b, g)
-            assert np.array_equal(sc[b, g, :n].view(np.uint32), esc[b, g, :n].view(np.uint32)), (b, g)
+    for split in (False, True):
+        sel, cnt, sc = gpu_select(hip, case, select_groups, budget, init, local, split=split)
+        assert np.array_equal(cnt, ecnt), split
+        for b in range(case.batch):
+            n = int(case.sealed[b])
+            for g in range(select_groups):
+                assert sel[b, g, : cnt[b, g]].tolist() == esel[b, g, : ecnt[b, g]].tolist(), (split, b, g)
+                assert np.array_equal(sc[b, g, :n].view(np.uint32), esc[b, g, :n].view(np.uint32)), (split, b, g)
 
 
 @pytest.mark.parametrize("group,hkv", [(2, 8), (4, 8), (1, 8), (8, 2)])
@@ -107,3 +114,25 @@ def test_c21_golden_on_gpu(hip):
     case.query[0] = pq.reshape(16, 512, 128)[:, 511, :]
     sel, cnt, _ = gpu_select(hip, case, 1, 4, 1, 1)
     assert sel[0, 0, : cnt[0, 0]].tolist() == [0, 8, 13, 15]
+
+
+def test_split_capacity_flag(hip):
+    """The split form flags a sequence with more sealed blocks than
+    rep_stride and selects nothing for it, like score_select, while the
+    other sequence is selected as the oracle does."""
+    case = make_case(135, 2, 16, 8, [32 * 40 + 3, 32 * 30])
+    kv = device_kv(case)
+    kv.sealed.copy_(to_dev(np.array([case.rep_stride + 1, 30], np.int32)))
+    kv.seq_len.copy_(to_dev(np.array([32 * (case.rep_stride + 1) + 3, 32 * 30], np.int32)))
+    st = status_tensor()
+    sel, cnt, _ = hip.score_select_split(kv, to_dev(case.query), 8, 20, 4, 8, status=st, sel_stride=20)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    c = cnt.cpu().numpy()
+    assert (c[0] == 0).all()
+    esel, ecnt = O.paged_score_select(case.query[1:], case.reps[1:], case.sealed[1:], 1, 16, 8, D, 8,
+                                      case.rep_stride, 8, 20, 4, 8)
+    assert np.array_equal(c[1], ecnt[0])
+    s = sel.cpu().numpy()
+    for g in range(8):
+        assert s[1, g, : c[1, g]].tolist() == esel[0, g, : ecnt[0, g]].tolist()

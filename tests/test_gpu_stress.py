@@ -35,6 +35,8 @@ def test_stress_mixed_lengths_budgets_outliers(hip, seed):
     q = to_dev(case.query)
     sel, cnt = hip.score_select(kv, q, 8, 64, INIT, LOCAL, status=st, sel_stride=sel_stride,
                                 budgets=to_dev(budgets))
+    sel2, cnt2, _ = hip.score_select_split(kv, q, 8, 64, INIT, LOCAL, status=st, sel_stride=sel_stride,
+                                           budgets=to_dev(budgets))
     out = hip.sparse_decode_attention(kv, q, sel, cnt, SCALE, status=st)
     # the schedule for uneven lists: 16-page chunks, enough for the longest
     chunk = 16
@@ -43,6 +45,7 @@ def test_stress_mixed_lengths_budgets_outliers(hip, seed):
     torch.cuda.synchronize()
     assert int(st.item()) == 0
     got_sel, got_cnt, got = sel.cpu().numpy(), cnt.cpu().numpy(), out.cpu().numpy()
+    assert np.array_equal(cnt2.cpu().numpy(), got_cnt) and np.array_equal(sel2.cpu().numpy(), got_sel)
     got_c = out_c.cpu().numpy()
 
     esel = np.full((batch, 8, sel_stride), -1, np.int32)
@@ -78,6 +81,12 @@ def test_bad_per_sequence_budget_is_flagged(hip):
     assert int(st.item()) & hip.STATUS_BAD_BUDGET
     c = cnt.cpu().numpy()
     assert (c[1] == 0).all() and (c[0] == 20).all()
+    st2 = status_tensor()
+    _, cnt2, _ = hip.score_select_split(kv, to_dev(case.query), 8, 20, INIT, LOCAL, status=st2, sel_stride=20,
+                                        budgets=to_dev(budgets))
+    torch.cuda.synchronize()
+    assert int(st2.item()) & hip.STATUS_BAD_BUDGET
+    assert np.array_equal(cnt2.cpu().numpy(), c)
 
 
 def test_stress_full_size_one_layer(hip, capsys):
