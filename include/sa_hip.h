@@ -27,6 +27,7 @@ extern "C" {
 #define SA_HIP_OK 0
 #define SA_HIP_EINVAL (-1)   /* invalid argument / unsupported shape */
 #define SA_HIP_ERUNTIME (-2) /* HIP runtime error */
+#define SA_HIP_EIO (-3)      /* file I/O error (sa_store.h) */
 
 /* Tokens per page (and per selectable block).  Fixed: the reference's
  * 32-token blocks (selection_main.cpp:97, kv_lifecycle_main.cpp:21). */
@@ -348,6 +349,20 @@ int sa_hip_gather_pages(const uint16_t* pool, int64_t page_bytes,
 int sa_hip_compare_prediction(const int32_t* predicted, const int32_t* oracle,
                               int32_t n, int32_t* hits, int32_t* misses,
                               int32_t* replacement_slots, int32_t* miss_count);
+
+/* Seal writeback staging: on copy_stream, after after_event (a hipEvent_t
+ * recorded on the compute stream behind the step that sealed the pages;
+ * NULL: no wait), hipMemcpyAsync of pool pages pages[0..count) (host array,
+ * each in [0, num_pages)) into dst + i * page_bytes (pinned host memory),
+ * then record done_event (optional).  The store write of the staged pages
+ * (sa_store_submit_writes) starts once done_event has completed; the
+ * reference copies the sealed block out of its host tail before its
+ * O_DIRECT pwrite (kv_lifecycle_main.cpp:104-108).  For one launch instead
+ * of per-page copies, sa_hip_gather_pages writes to pinned memory too. */
+int sa_hip_pages_to_host_async(const uint16_t* pool, int64_t page_bytes,
+                               int64_t num_pages, const int32_t* pages,
+                               int32_t count, void* dst, void* copy_stream,
+                               void* after_event, void* done_event);
 
 /* Copy-stream slot fills: for i < count, hipMemcpyAsync of page_bytes from
  * pinned host memory src_base + src_blocks[i] * page_bytes into pool page

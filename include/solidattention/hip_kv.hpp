@@ -318,6 +318,7 @@ class MissCorrector {
     hip_check(hipEventCreateWithFlags(&done_, hipEventDisableTiming), "hipEventCreate");
   }
   ~MissCorrector() {
+    if (after_) (void)hipEventDestroy(after_);
     if (done_) (void)hipEventDestroy(done_);
     if (copy_) (void)hipStreamDestroy(copy_);
   }
@@ -333,11 +334,20 @@ class MissCorrector {
   }
   // Make `compute` wait (on the device) for the last fill.
   void order(hipStream_t compute) { check(sa_hip_stream_wait_event(compute, done_), "stream_wait_event"); }
+  // Make the next fills wait for the work queued so far on `s` (earlier
+  // writers or readers of the destination pages, e.g. a prefetch the compute
+  // stream was ordered after).
+  void after(hipStream_t s) {
+    if (!after_) hip_check(hipEventCreateWithFlags(&after_, hipEventDisableTiming), "hipEventCreate");
+    hip_check(hipEventRecord(after_, s), "hipEventRecord");
+    check(sa_hip_stream_wait_event(copy_, after_), "stream_wait_event");
+  }
   hipStream_t copy_stream() const { return copy_; }
 
  private:
   hipStream_t copy_{};
   hipEvent_t done_{};
+  hipEvent_t after_{};
 };
 
 }  // namespace solidattention::hip

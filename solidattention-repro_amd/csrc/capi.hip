@@ -67,6 +67,14 @@ int check_reps(const sa_paged_kv* kv, const char* op) {
 
 }  // namespace
 
+namespace sa {
+// Error reporting for the host-only parts of the library (store.cpp).
+int report_error(int code, const char* message) {
+  g_last_error = message;
+  return code;
+}
+}  // namespace sa
+
 extern "C" {
 
 const char* sa_hip_last_error(void) { return g_last_error.c_str(); }
@@ -627,6 +635,32 @@ static int fill_args_ok(uint16_t* pool, int64_t page_bytes, const int32_t* dst_p
   for (int32_t i = 0; i < count; ++i)
     if (dst_pages[i] < 0 || src_blocks[i] < 0)
       return fail(SA_HIP_EINVAL, "%s: negative page/block index at %d", op, i);
+  return SA_HIP_OK;
+}
+
+int sa_hip_pages_to_host_async(const uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* pages,
+                               int32_t count, void* dst, void* copy_stream, void* after_event, void* done_event) {
+  if (count < 0 || (count > 0 && (!pool || !pages || !dst)) || page_bytes <= 0 || page_bytes % 16 != 0)
+    return fail(SA_HIP_EINVAL, "pages_to_host_async: bad arguments");
+  for (int32_t i = 0; i < count; ++i)
+    if (pages[i] < 0 || pages[i] >= num_pages)
+      return fail(SA_HIP_EINVAL, "pages_to_host_async: page %d outside [0, %lld) at %d", pages[i],
+                  static_cast<long long>(num_pages), i);
+  hipStream_t cs = as_stream(copy_stream);
+  if (after_event)
+    if (int e = check_hip(hipStreamWaitEvent(cs, reinterpret_cast<hipEvent_t>(after_event), 0),
+                          "pages_to_host_async: hipStreamWaitEvent"))
+      return e;
+  const auto* src = reinterpret_cast<const uint8_t*>(pool);
+  auto* out = static_cast<uint8_t*>(dst);
+  for (int32_t i = 0; i < count; ++i)
+    if (int e = check_hip(hipMemcpyAsync(out + static_cast<int64_t>(i) * page_bytes,
+                                         src + static_cast<int64_t>(pages[i]) * page_bytes,
+                                         static_cast<size_t>(page_bytes), hipMemcpyDeviceToHost, cs),
+                          "pages_to_host_async: hipMemcpyAsync"))
+      return e;
+  if (done_event)
+    return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(done_event), cs), "pages_to_host_async: record");
   return SA_HIP_OK;
 }
 

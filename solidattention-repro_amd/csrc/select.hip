@@ -120,8 +120,7 @@ __global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params 
   __syncthreads();
   const int blk = first + static_cast<int>(threadIdx.x);
   if (blk < n) {
-    float unused[kScoreBatch];
-    const float score = score_one<GR, false>(a, q_s, blk, unused, false);
+    const float score = score_one_pipelined<GR>(a, q_s, blk);
     p.scores[(static_cast<int64_t>(b) * p.select_groups + sg) * p.rep_stride + blk] = score;
   }
 }

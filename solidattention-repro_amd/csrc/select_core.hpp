@@ -115,6 +115,58 @@ __device__ inline float score_one(const ScoreArgs& a, const float* q_s, int blk,
   return score;
 }
 
+// score_one() for the separate selection kernels, with the loads of the
+// next 32 representative values in flight while the current 32 are summed
+// (two 32-value buffers): memory and arithmetic overlap within each wave
+// instead of alternating across the whole workgroup.  Same operations in the
+// same order as score_one().
+constexpr int kPipeBatch = 32;
+
+template <int GR>
+__device__ inline void dot_batch(const float* q_s, int qoff, int h0, int d0, const float (&rv)[kPipeBatch],
+                                 float (&dot)[GR]) {
+#pragma unroll
+  for (int k = 0; k < kPipeBatch; ++k) {
+#pragma unroll
+    for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_s[qoff + (h0 + j) * D + d0 + k] * rv[k];
+  }
+}
+
+__device__ inline void load_batch(const float* r, int64_t stride, int d0, float (&rv)[kPipeBatch]) {
+#pragma unroll
+  for (int k = 0; k < kPipeBatch; ++k) rv[k] = load_stream_f32(r + static_cast<int64_t>(d0 + k) * stride);
+}
+
+template <int GR>
+__device__ inline float score_one_pipelined(const ScoreArgs& a, const float* q_s, int blk) {
+  static_assert(D == 4 * kPipeBatch, "four batches per representative row");
+  int qoff = 0;
+  asm volatile("" : "+s"(qoff));
+  const float heads_f = static_cast<float>(a.heads_per_sel);
+  const int64_t stride = a.rep_stride;
+  float score = 0.0f;
+  for (int h0 = 0; h0 < a.heads_per_sel; h0 += GR) {
+    const int h = a.h_first + h0;
+    const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
+    const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * stride + blk;
+    float dot[GR];
+#pragma unroll
+    for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
+    float ra[kPipeBatch], rb[kPipeBatch];
+    load_batch(r, stride, 0, ra);
+    load_batch(r, stride, kPipeBatch, rb);
+    dot_batch<GR>(q_s, qoff, h0, 0, ra, dot);
+    load_batch(r, stride, 2 * kPipeBatch, ra);
+    dot_batch<GR>(q_s, qoff, h0, kPipeBatch, rb, dot);
+    load_batch(r, stride, 3 * kPipeBatch, rb);
+    dot_batch<GR>(q_s, qoff, h0, 2 * kPipeBatch, ra, dot);
+    dot_batch<GR>(q_s, qoff, h0, 3 * kPipeBatch, rb, dot);
+#pragma unroll
+    for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
+  }
+  return score;
+}
+
 // keys[blk] = order_key(score of block blk) for blk < n; scores (optional)
 // receives the fp32 scores.  GR = query heads sharing one representative row
 // (the group size when representatives are per KV head, else 1).  q_s must
@@ -141,9 +193,8 @@ __device__ inline void score_blocks(const ScoreArgs& a, const float* q_s, int n,
 
 template <int GR, int kThreads>
 __device__ inline void score_blocks(const ScoreArgs& a, const float* q_s, int n, uint32_t* keys, float* scores) {
-  float unused[kScoreBatch];
   for (int blk = threadIdx.x; blk < n; blk += kThreads) {
-    const float score = score_one<GR, false>(a, q_s, blk, unused, false);
+    const float score = score_one_pipelined<GR>(a, q_s, blk);
     keys[blk] = order_key(score);
     if (scores) scores[blk] = score;
   }

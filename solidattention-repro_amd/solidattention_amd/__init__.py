@@ -59,6 +59,19 @@ EXPORTS = {
     "sa_hip_sparse_decode_attention_partial": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _I32, _P, _SZ, _I32, _I32,
                                                          _I32, _P, _P]),
     "sa_hip_attention_merge": (C.c_int, [_KV, _P, _SZ, _I32, _P, _P]),
+    "sa_store_open": (C.c_void_p, [C.c_char_p, _I64, _I64, _I64, _I32, _I32]),
+    "sa_store_close": (None, [_P]),
+    "sa_store_is_direct": (C.c_int, [_P]),
+    "sa_store_bytes": (_I64, [_P]),
+    "sa_store_bounced": (_I64, [_P]),
+    "sa_store_submit_reads": (_I64, [_P, _I64, _P, _I32, _P]),
+    "sa_store_submit_writes": (_I64, [_P, _I64, _P, _I32, _P]),
+    "sa_store_wait": (C.c_int, [_P, _I64]),
+    "sa_store_read_blocks": (C.c_int, [_P, _I64, _P, _I32, _P]),
+    "sa_store_write_blocks": (C.c_int, [_P, _I64, _P, _I32, _P]),
+    "sa_store_sync": (C.c_int, [_P]),
+    "sa_store_commit_marker": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p]),
+    "sa_hip_pages_to_host_async": (C.c_int, [_P, _I64, _I64, _P, _I32, _P, _P, _P, _P]),
     "sa_hip_score_select_split": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _P, _P]),
     "sa_hip_score_select_split_preferred": (C.c_int, [_KV, C.POINTER(SelectParamsStruct)]),
     "sa_hip_sparse_decode_attention_chunked": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _I32,
@@ -222,6 +235,99 @@ def score_select_split_preferred(kv: PagedKV, select_groups, budget, init, local
     params = SelectParamsStruct(select_groups, budget, init, local, sel_stride or budget, 0, None)
     s = kv.struct()
     return bool(lib().sa_hip_score_select_split_preferred(C.byref(s), C.byref(params)))
+
+
+STORE_CREATE, STORE_DIRECT = 1, 2
+
+
+class MainStore:
+    """The main KV store file (include/sa_store.h): block `block` of layer
+    `layer` at byte (layer * blocks_per_layer + block) * block_bytes.
+    Buffers are numpy arrays or tensors (pinned host memory for O_DIRECT:
+    4096-byte aligned); block ids are int64 sequences."""
+
+    def __init__(self, path, layers, blocks_per_layer, block_bytes, create=False, direct=True, threads=8):
+        flags = (STORE_CREATE if create else 0) | (STORE_DIRECT if direct else 0)
+        self.layers, self.blocks_per_layer, self.block_bytes = layers, blocks_per_layer, block_bytes
+        self.handle = lib().sa_store_open(os.fsencode(path), layers, blocks_per_layer, block_bytes, flags, threads)
+        if not self.handle:
+            raise SaHipError(f"store_open failed: {lib().sa_hip_last_error().decode(errors='replace')}")
+
+    @property
+    def direct(self) -> bool:
+        return bool(lib().sa_store_is_direct(self.handle))
+
+    @property
+    def nbytes(self) -> int:
+        return int(lib().sa_store_bytes(self.handle))
+
+    @property
+    def bounced(self) -> int:
+        return int(lib().sa_store_bounced(self.handle))
+
+    @staticmethod
+    def _ids(blocks):
+        import numpy as np
+        ids = np.ascontiguousarray(np.asarray(blocks, dtype=np.int64))
+        return ids, ids.ctypes.data_as(C.c_void_p)
+
+    @staticmethod
+    def _buf(buf):
+        return C.c_void_p(buf.data_ptr()) if hasattr(buf, "data_ptr") else buf.ctypes.data_as(C.c_void_p)
+
+    def submit_reads(self, layer, blocks, dst) -> int:
+        ids, p = self._ids(blocks)
+        bid = lib().sa_store_submit_reads(self.handle, layer, p, ids.size, self._buf(dst))
+        if bid < 0:
+            check(int(bid), "store_submit_reads")
+        return bid
+
+    def submit_writes(self, layer, blocks, src) -> int:
+        ids, p = self._ids(blocks)
+        bid = lib().sa_store_submit_writes(self.handle, layer, p, ids.size, self._buf(src))
+        if bid < 0:
+            check(int(bid), "store_submit_writes")
+        return bid
+
+    def wait(self, batch) -> None:
+        check(lib().sa_store_wait(self.handle, batch), "store_wait")
+
+    def read(self, layer, blocks, dst) -> None:
+        ids, p = self._ids(blocks)
+        check(lib().sa_store_read_blocks(self.handle, layer, p, ids.size, self._buf(dst)), "store_read_blocks")
+
+    def write(self, layer, blocks, src) -> None:
+        ids, p = self._ids(blocks)
+        check(lib().sa_store_write_blocks(self.handle, layer, p, ids.size, self._buf(src)), "store_write_blocks")
+
+    def sync(self) -> None:
+        check(lib().sa_store_sync(self.handle), "store_sync")
+
+    def close(self) -> None:
+        if self.handle:
+            lib().sa_store_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def commit_marker(directory, name, body) -> None:
+    check(lib().sa_store_commit_marker(os.fsencode(directory), name.encode(), body.encode()), "store_commit_marker")
+
+
+def pages_to_host_async(pool, page_bytes, num_pages, pages, dst, copy_stream, after_event=None, done_event=None):
+    """D2H of pool pages `pages` (host int32 sequence) into pinned `dst` on
+    copy_stream after after_event; records done_event."""
+    import numpy as np
+    ids = np.ascontiguousarray(np.asarray(pages, dtype=np.int32))
+    ev = lambda e: None if e is None else C.c_void_p(e.cuda_event if hasattr(e, "cuda_event") else e)
+    check(lib().sa_hip_pages_to_host_async(_ptr(pool), page_bytes, num_pages, ids.ctypes.data_as(C.c_void_p),
+                                           ids.size, C.c_void_p(dst.data_ptr()), _stream(copy_stream),
+                                           ev(after_event), ev(done_event)), "pages_to_host_async")
 
 
 def select_attend(kv: PagedKV, query, select_groups, budget, init, local, scale, selected=None, counts=None,

@@ -29,3 +29,26 @@ def test_cpp_backend_check(hip):
     assert m["c2_packed_kv_exact"] is True
     assert m["lifecycle_sealed_blocks"] == 448
     assert m["c1_attention_max_abs_error"] <= 2e-5
+
+
+EXE_STORE = os.path.join(ROOT, "tests", "cpp", "store_check")
+
+
+def test_cpp_store_check(hip):
+    """The store tier (solidattention/hip_store.hpp): seal writeback to the
+    main store (P1.3b.0: 448 sealed and verified, tail 32, generation 16,
+    121,110,528 bytes, commit marker) and ticketed store -> pool prefetch
+    with miss correction (P1.0: 346 misses, hit rate 0.80692, 448 verified
+    tickets, a stale ticket rejected, resident pages equal to the store)."""
+    assert os.path.exists(EXE_STORE), "tests/cpp/store_check missing: run __graft_entry__.build()"
+    print("case: tests/cpp/store_check", flush=True)
+    r = subprocess.run([EXE_STORE], capture_output=True, text=True, timeout=110)
+    print(r.stdout[-4000:])
+    print(r.stderr[-2000:])
+    assert r.returncode == 0, f"store_check exit {r.returncode}"
+    m = json.loads(r.stdout)
+    assert m["lifecycle_store_verified_reads"] == 448
+    assert m["lifecycle_store_bytes"] == 121110528
+    assert m["store_prefetch_miss_blocks"] == 346
+    assert m["store_prefetch_verified_tickets"] == 448
+    assert m["store_prefetch_stale_ticket_rejected"] is True
