@@ -58,11 +58,14 @@ def parse():
                     help="kernel launches per layer: 1 = the fused decode step (append + seal + select + attend), "
                          "2 = append_seal then the fused select + attend, 3 = append_seal, score_select, attention "
                          "(1 and 2 fall back to 3 where the fused kernel does not apply)")
-    ap.add_argument("--workload", default="decode", choices=["decode", "correction", "represent", "stress"],
+    ap.add_argument("--prefetch-blocks", type=int, default=128,
+                    help="store workload: blocks per store -> pool prefetch batch")
+    ap.add_argument("--workload", default="decode", choices=["decode", "correction", "represent", "stress", "store"],
                     help="decode: the headline decode step; correction: long-context miss correction "
                          "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage); "
                          "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4); "
-                         "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers")
+                         "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers; "
+                         "store: seal writeback behind decoding and store -> pool prefetch")
     ap.add_argument("--select", default="auto", choices=["auto", "single", "split"],
                     help="separate selection launch: one workgroup per list, scoring split over 256-block "
                          "workgroups, or the library's preference")
@@ -134,6 +137,10 @@ def main():
     if args.workload == "stress":
         import bench_stress
         bench_stress.run(args)
+        return
+    if args.workload == "store":
+        import bench_store
+        bench_store.run(args)
         return
     import numpy as np
     import torch

@@ -357,8 +357,10 @@ int sa_hip_compare_prediction(const int32_t* predicted, const int32_t* oracle,
  * then record done_event (optional).  The store write of the staged pages
  * (sa_store_submit_writes) starts once done_event has completed; the
  * reference copies the sealed block out of its host tail before its
- * O_DIRECT pwrite (kv_lifecycle_main.cpp:104-108).  For one launch instead
- * of per-page copies, sa_hip_gather_pages writes to pinned memory too. */
+ * O_DIRECT pwrite (kv_lifecycle_main.cpp:104-108).  When dst is pinned
+ * host memory the device maps (hipHostMalloc), one kernel per 256 pages
+ * writes it through the mapping (dst must then hold count * page_bytes
+ * bytes); other memory gets one hipMemcpyAsync per page. */
 int sa_hip_pages_to_host_async(const uint16_t* pool, int64_t page_bytes,
                                int64_t num_pages, const int32_t* pages,
                                int32_t count, void* dst, void* copy_stream,

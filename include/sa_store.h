@@ -6,9 +6,10 @@
  * (cpp/src/kv_lifecycle_main.cpp:73-80 and :105-108 with blocks_per_layer =
  * capacity_blocks and block = initial_blocks + sealed index;
  * cpp/src/pipeline_main.cpp:660-678 for the reads).  Writes and reads go
- * through O_DIRECT when the file system allows it (buffers and block_bytes
- * then need 4096-byte alignment; hipHostMalloc memory is page-aligned),
- * issued by a small pool of worker threads so that several blocks are in
+ * through O_DIRECT when the file system allows it (block_bytes then needs
+ * to be a multiple of 4096; a buffer O_DIRECT cannot use, unaligned or
+ * mapped by the GPU driver as hipHostMalloc memory is, goes through a
+ * page-aligned bounce buffer of the I/O thread), issued by a small pool of worker threads so that several blocks are in
  * flight at once (the reference queues them on io_uring,
  * cpp/src/uring_reader.cpp:78-122).
  *

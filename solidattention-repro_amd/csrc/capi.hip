@@ -651,14 +651,26 @@ int sa_hip_pages_to_host_async(const uint16_t* pool, int64_t page_bytes, int64_t
     if (int e = check_hip(hipStreamWaitEvent(cs, reinterpret_cast<hipEvent_t>(after_event), 0),
                           "pages_to_host_async: hipStreamWaitEvent"))
       return e;
-  const auto* src = reinterpret_cast<const uint8_t*>(pool);
-  auto* out = static_cast<uint8_t*>(dst);
-  for (int32_t i = 0; i < count; ++i)
-    if (int e = check_hip(hipMemcpyAsync(out + static_cast<int64_t>(i) * page_bytes,
-                                         src + static_cast<int64_t>(pages[i]) * page_bytes,
-                                         static_cast<size_t>(page_bytes), hipMemcpyDeviceToHost, cs),
-                          "pages_to_host_async: hipMemcpyAsync"))
+  // pinned host memory the device can address: one kernel launch per 256
+  // pages writing through the mapping; anything else: one copy per page
+  hipPointerAttribute_t attr{};
+  const bool mapped = count > 0 && hipPointerGetAttributes(&attr, dst) == hipSuccess &&
+                      attr.type == hipMemoryTypeHost && attr.devicePointer == dst;
+  (void)hipGetLastError();  // a pageable pointer leaves an error behind
+  if (mapped) {
+    if (int e = check_hip(sa::launch_pages_to_host(pool, page_bytes, pages, count, dst, cs),
+                          "pages_to_host_async: launch"))
       return e;
+  } else {
+    const auto* src = reinterpret_cast<const uint8_t*>(pool);
+    auto* out = static_cast<uint8_t*>(dst);
+    for (int32_t i = 0; i < count; ++i)
+      if (int e = check_hip(hipMemcpyAsync(out + static_cast<int64_t>(i) * page_bytes,
+                                           src + static_cast<int64_t>(pages[i]) * page_bytes,
+                                           static_cast<size_t>(page_bytes), hipMemcpyDeviceToHost, cs),
+                            "pages_to_host_async: hipMemcpyAsync"))
+        return e;
+  }
   if (done_event)
     return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(done_event), cs), "pages_to_host_async: record");
   return SA_HIP_OK;

@@ -132,6 +132,28 @@ __global__ __launch_bounds__(kThreads) void gather_pages_kernel(const uint4* poo
     dst[e] = src[e];
 }
 
+// Pages whose ids travel in the kernel arguments (no device-side list):
+// page i of the launch goes to out + i * page_vecs; out may be pinned host
+// memory (seal writeback staging), written through its device mapping.
+struct PageIdsArg {
+  int32_t ids[kPagesPerHostCopy];
+};
+
+// A few workgroups, each copying whole pages in turn: the copy runs beside
+// the decode kernels and is bound by the host link, so it holds only a few
+// compute units (every workgroup of a grid sized to the pages would sit on
+// a CU for the length of its link transfer).
+constexpr int kHostCopyGroups = 16;
+
+__global__ __launch_bounds__(kThreads) void pages_to_host_kernel(const uint4* pool, int64_t page_vecs, int count,
+                                                                 const PageIdsArg pages, uint4* out) {
+  for (int i = blockIdx.x; i < count; i += gridDim.x) {
+    const uint4* src = pool + static_cast<int64_t>(pages.ids[i]) * page_vecs;
+    uint4* dst = out + static_cast<int64_t>(i) * page_vecs;
+    for (int64_t e = threadIdx.x; e < page_vecs; e += kThreads) dst[e] = src[e];
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void fill_synthetic_f16_kernel(uint16_t* dst, int64_t count,
                                                                       uint64_t seed_mixed,
                                                                       uint64_t first) {
@@ -243,6 +265,22 @@ hipError_t launch_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t
                      reinterpret_cast<const uint4*>(pool), vecs, num_pages, pages,
                      reinterpret_cast<uint4*>(out), status);
   return hipGetLastError();
+}
+
+hipError_t launch_pages_to_host(const uint16_t* pool, int64_t page_bytes, const int32_t* pages, int32_t count,
+                                void* out, hipStream_t stream) {
+  const int64_t vecs = page_bytes / 16;
+  for (int32_t first = 0; first < count; first += kPagesPerHostCopy) {
+    const int n = count - first < kPagesPerHostCopy ? count - first : kPagesPerHostCopy;
+    PageIdsArg ids{};
+    for (int i = 0; i < n; ++i) ids.ids[i] = pages[first + i];
+    const dim3 grid(n < kHostCopyGroups ? n : kHostCopyGroups);
+    hipLaunchKernelGGL(pages_to_host_kernel, grid, dim3(kThreads), 0, stream, reinterpret_cast<const uint4*>(pool),
+                       vecs, n, ids, reinterpret_cast<uint4*>(static_cast<uint8_t*>(out) + first * page_bytes));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_fill_synthetic_f16(uint16_t* dst, int64_t count, uint64_t seed,

@@ -173,6 +173,11 @@ hipError_t launch_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t
                                const int32_t* pages, int32_t count, uint16_t* out,
                                int32_t* status, hipStream_t stream);
 
+// Pool pages to (pinned, device-mapped) host memory, ids checked by the
+// caller; one launch per kPagesPerHostCopy pages, ids in the arguments.
+constexpr int kPagesPerHostCopy = 256;
+hipError_t launch_pages_to_host(const uint16_t* pool, int64_t page_bytes, const int32_t* pages, int32_t count,
+                                void* out, hipStream_t stream);
 hipError_t launch_fill_synthetic_f16(uint16_t* dst, int64_t count, uint64_t seed,
                                      uint64_t first_index, hipStream_t stream);
 hipError_t launch_fill_synthetic_f32(float* dst, int64_t count, uint64_t seed,

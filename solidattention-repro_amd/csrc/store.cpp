@@ -102,8 +102,13 @@ struct sa_store {
         job = jobs.front();
         jobs.pop_front();
       }
-      int64_t r = transfer(fd, job.write, job.ptr, block_bytes, job.offset);
-      if (r == -EFAULT && direct) r = bounced_transfer(job);
+      int64_t r;
+      if (direct && reinterpret_cast<uintptr_t>(job.ptr) % kDirectAlign != 0) {
+        r = bounced_transfer(job);
+      } else {
+        r = transfer(fd, job.write, job.ptr, block_bytes, job.offset);
+        if (r == -EFAULT && direct) r = bounced_transfer(job);
+      }
       std::lock_guard<std::mutex> lk(mu);
       Batch& b = batches[job.batch];
       if (r != block_bytes && b.error == 0) {
@@ -122,9 +127,9 @@ struct sa_store {
     }
   }
 
-  // O_DIRECT cannot pin memory that the GPU driver mapped into the process
-  // (hipHostMalloc buffers: EFAULT); such blocks go through a page-aligned
-  // bounce buffer of the worker thread.
+  // O_DIRECT needs 4096-byte aligned buffers and cannot pin memory that the
+  // GPU driver mapped into the process (hipHostMalloc buffers: EFAULT); such
+  // blocks go through a page-aligned bounce buffer of the worker thread.
   int64_t bounced_transfer(const Job& job) {
     thread_local std::unique_ptr<char, void (*)(void*)> bounce(nullptr, std::free);
     thread_local int64_t bounce_bytes = 0;
@@ -151,8 +156,6 @@ struct sa_store {
       if (blocks[i] < 0 || blocks[i] >= blocks_per_layer)
         return fail(SA_HIP_EINVAL, "%s: block %lld outside [0, %lld)", op, static_cast<long long>(blocks[i]),
                     static_cast<long long>(blocks_per_layer));
-    if (direct && (reinterpret_cast<uintptr_t>(base) % kDirectAlign) != 0)
-      return fail(SA_HIP_EINVAL, "%s: O_DIRECT needs a 4096-byte aligned buffer", op);
     std::lock_guard<std::mutex> lk(mu);
     const int64_t id = next_batch++;
     Batch& b = batches[id];

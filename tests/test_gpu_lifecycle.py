@@ -189,3 +189,34 @@ def test_miss_fill_gather_kernel_from_pinned_memory(hip):
                                 1, copy_stream, done, status=st)
     copy_stream.synchronize()
     assert int(st.item()) & hip.STATUS_BAD_PAGE
+
+
+@pytest.mark.parametrize("pinned", [True, False])
+def test_pages_to_host_staging(hip, pinned):
+    """Seal writeback staging: pool pages to pinned host memory (one kernel
+    writing through the device mapping) or to pageable memory (one copy per
+    page), ordered after an event of the compute stream; bytes equal."""
+    import numpy as np
+    import torch
+    rng = np.random.default_rng(71)
+    npages = 300  # two launches of the pinned path (256 ids each at most)
+    kv = hip.PagedKV(1, 16, 8, 4, num_pages=npages)
+    bits = rng.integers(0, 65536, size=tuple(kv.pool.shape), dtype=np.uint16).view(np.int16)
+    kv.pool.view(torch.int16).copy_(torch.from_numpy(bits).cuda())
+    pages = rng.permutation(npages)[:260].astype(np.int32)
+    pb = kv.page_bytes
+    dst = torch.zeros(len(pages) * pb, dtype=torch.uint8)
+    if pinned:
+        dst = dst.pin_memory()
+    copy = torch.cuda.Stream()
+    after, done = torch.cuda.Event(), torch.cuda.Event()
+    after.record(torch.cuda.current_stream())
+    done.record(copy)
+    print(f"case: pinned={pinned} pages={len(pages)}", flush=True)
+    hip.pages_to_host_async(kv.pool, pb, npages, pages, dst, copy, after_event=after, done_event=done)
+    done.synchronize()
+    got = dst.numpy().reshape(len(pages), pb)
+    ref = kv.pool.view(torch.uint8).view(npages, pb).cpu().numpy()[pages]
+    assert np.array_equal(got, ref)
+    with pytest.raises(hip.SaHipError, match="outside"):
+        hip.pages_to_host_async(kv.pool, pb, npages, [npages], dst, copy)

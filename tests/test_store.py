@@ -90,9 +90,14 @@ def test_argument_and_io_errors(tmp_path):
         st.read(0, [4], buf)
     with pytest.raises(sa.SaHipError, match="block"):
         st.read(0, [-1], buf)
-    if st.direct:
-        with pytest.raises(sa.SaHipError, match="aligned"):
-            st.read(0, [0], buf[1:4097])
+    # an unaligned buffer goes through the bounce buffer under O_DIRECT
+    src = aligned(4096)
+    src[:] = deterministic_block(3, 4096)
+    st.write(1, [2], src)
+    odd = np.zeros(4097, np.uint8)
+    st.read(1, [2], odd[1:])
+    assert np.array_equal(odd[1:], src)
+    assert st.bounced == (1 if st.direct else 0)
     st.close()
     # an existing file shorter than its declared layout: a short read is an error
     with open(tmp_path / "short.bin", "wb") as f:
