@@ -393,6 +393,37 @@ int sa_hip_fill_pages_gather_async(uint16_t* pool, int64_t page_bytes,
                                    void* copy_stream, void* done_event);
 int sa_hip_stream_wait_event(void* stream, void* event);
 
+/* ---- query producer / output consumer around the attention -------------- */
+/* The reference computes these per decode token with its own kernels and
+ * cuBLAS (qwen_layer_main.cpp:125-172 rms_norm, head_rms, rope; :576-584 and
+ * :640-645 the projections and the residual add; qwen_chain_main.cpp
+ * :365-399 the decode step).  Here they run for a batch of rows (one per
+ * sequence), fp32 throughout. */
+
+/* out = x * (1 / sqrt(mean(x^2) + eps)) * w per row; width % 4 == 0. */
+int sa_hip_rms_norm(const float* x, const float* w, float* out, int32_t rows, int32_t width, float eps,
+                    void* stream);
+/* y[r][o] = sum_i x[r][i] * w[o][i] (+ residual[r][o] when non-null): the
+ * reference's cublasSgemm(CUBLAS_OP_T) on its row-major [out][in] weights.
+ * in and out multiples of 64; x and w 16-byte aligned; workspace of
+ * sa_hip_linear_workspace_bytes(rows, in, out) bytes (K-slice partial
+ * sums, added in a fixed order: deterministic). */
+size_t sa_hip_linear_workspace_bytes(int32_t rows, int32_t in, int32_t out);
+int sa_hip_linear(const float* x, const float* w, const float* residual, float* y, int32_t rows, int32_t in,
+                  int32_t out, void* workspace, size_t workspace_bytes, void* stream);
+/* The query producer of one layer for a batch of decode tokens: from the
+ * normalised hidden x [rows][hidden], q = head_rms(x wq^T) then RoPE,
+ * k = head_rms(x wk^T) then RoPE, v = x wv^T, with head_dim 128, the
+ * rotation at positions[rows] (device int32), frequencies
+ * theta^(-2i/128) correctly rounded to fp32 and the reference's NeoX pairing
+ * (d, d + 64).  Outputs [rows][heads][128] fp32, ready for
+ * sa_hip_decode_step (q) and its k/v.  hidden % 64 == 0. */
+size_t sa_hip_qkv_workspace_bytes(int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads);
+int sa_hip_qkv_project(const float* x, const float* wq, const float* wk, const float* wv, const float* q_norm,
+                       const float* k_norm, const int32_t* positions, int32_t rows, int32_t hidden,
+                       int32_t q_heads, int32_t kv_heads, float theta, float eps, float* q, float* k, float* v,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- synthetic data ------------------------------------------------------ */
 
 /* dst[i] = fp16_rne(normal(seed, first_index + i)), the generator of the

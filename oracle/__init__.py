@@ -83,6 +83,10 @@ def lib() -> C.CDLL:
         L.sao_synth_normal.argtypes = [C.c_uint64, C.c_uint64]
         L.sao_synth_fill_half.argtypes = [C.c_uint64, C.c_uint64, _SZ, _P]
         L.sao_synth_fill_float.argtypes = [C.c_uint64, C.c_uint64, _SZ, _P]
+        L.sao_rms_norm.argtypes = [_P, _P, _P, _SZ, _SZ, C.c_float]
+        L.sao_linear.argtypes = [_P, _P, _P, _P, _SZ, _SZ, _SZ]
+        L.sao_rope_inv_freq.argtypes = [C.c_float, _SZ, _P]
+        L.sao_qk_norm_rope.argtypes = [_P, _P, _P, _SZ, _SZ, _SZ, C.c_float, C.c_float]
         _oracle = L
     return _oracle
 
@@ -330,3 +334,49 @@ def p1_dense_audit(kv, prompt_queries, reps, steps, layers):
     if st != 0:
         raise ValueError("dense audit failed")
     return float(mass[0]), float(recall[0])
+
+
+# --------------------------------------------------------------------------
+# query producer / output consumer (qwen_layer_main.cpp:125-183)
+# --------------------------------------------------------------------------
+
+def rms_norm(x, w, eps=1e-6):
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    rows, width = x.shape
+    out = np.zeros_like(x)
+    if lib().sao_rms_norm(_ptr(x), _ptr(w), _ptr(out), rows, width, C.c_float(eps)) != 0:
+        raise ValueError("invalid rms_norm arguments")
+    return out
+
+
+def linear(x, w, residual=None):
+    """y = x @ w.T (+ residual); w is [out][in] as the reference stores it."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    rows, n_in = x.shape
+    n_out = w.shape[0]
+    y = np.zeros((rows, n_out), np.float32)
+    res = None if residual is None else _c(residual, np.float32)
+    if lib().sao_linear(_ptr(x), _ptr(w), _ptr(res), _ptr(y), rows, n_in, n_out) != 0:
+        raise ValueError("invalid linear arguments")
+    return y
+
+
+def rope_inv_freq(theta, head_dim):
+    f = np.zeros(head_dim // 2, np.float32)
+    lib().sao_rope_inv_freq(C.c_float(theta), head_dim, _ptr(f))
+    return f
+
+
+def qk_norm_rope(x, w, positions, theta=1e6, eps=1e-6):
+    """x [rows][heads][head_dim] -> new array: head RMS norm with w (None:
+    none), then RoPE at positions [rows] (None: none)."""
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    rows, heads, hd = x.shape
+    wv = None if w is None else _c(w, np.float32)
+    pos = None if positions is None else _c(positions, np.int32)
+    if lib().sao_qk_norm_rope(_ptr(x), _ptr(wv), _ptr(pos), rows, heads, hd, C.c_float(theta),
+                              C.c_float(eps)) != 0:
+        raise ValueError("invalid qk_norm_rope arguments")
+    return x

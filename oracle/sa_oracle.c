@@ -888,3 +888,81 @@ void sao_synth_fill_float(uint64_t seed, uint64_t first_index, size_t count,
                           float* out) {
   for (size_t i = 0; i < count; ++i) out[i] = sao_synth_normal(seed, first_index + i);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Query producer / output consumer around attention                        */
+/* (cpp/src/qwen_layer_main.cpp:125-183 kernels, :600-645 host order;       */
+/*  cpp/src/qwen_chain_main.cpp:365-399)                                    */
+/* ------------------------------------------------------------------------ */
+
+/* rms_norm (qwen_layer_main.cpp:125-143): out = x * (1/sqrt(mean(x^2) + eps))
+ * * w, sums in double here (the reference's order is a 256-thread tree). */
+int sao_rms_norm(const float* x, const float* w, float* out, size_t rows, size_t width, float eps) {
+  if (!x || !w || !out || width == 0) return -1;
+  for (size_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * width;
+    double ss = 0.0;
+    for (size_t i = 0; i < width; ++i) ss += (double)xr[i] * (double)xr[i];
+    const double inv = 1.0 / sqrt(ss / (double)width + (double)eps);
+    for (size_t i = 0; i < width; ++i) out[r * width + i] = (float)((double)xr[i] * inv * (double)w[i]);
+  }
+  return 0;
+}
+
+/* The projections (cublasSgemm with CUBLAS_OP_T on the row-major [out][in]
+ * weight, qwen_layer_main.cpp:578-584): y[r][o] = sum_i x[r][i] w[o][i]
+ * (+ residual[r][o], the residual add of :644-645), sums in double. */
+int sao_linear(const float* x, const float* w, const float* residual, float* y, size_t rows, size_t in,
+               size_t out) {
+  if (!x || !w || !y || in == 0) return -1;
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t o = 0; o < out; ++o) {
+      double acc = 0.0;
+      for (size_t i = 0; i < in; ++i) acc += (double)x[r * in + i] * (double)w[o * in + i];
+      if (residual) acc += (double)residual[r * out + o];
+      y[r * out + o] = (float)acc;
+    }
+  return 0;
+}
+
+/* RoPE frequencies: theta^(-2i/d) for i < d/2, correctly rounded to fp32
+ * (the reference evaluates powf(theta, -2.0f * i / width) on the GPU,
+ * qwen_layer_main.cpp:162-164, within its 2-ulp bound of this). */
+void sao_rope_inv_freq(float theta, size_t head_dim, float* inv_freq) {
+  for (size_t i = 0; i < head_dim / 2; ++i)
+    inv_freq[i] = (float)pow((double)theta, -2.0 * (double)i / (double)head_dim);
+}
+
+/* head_rms then rope, in place, on x [rows][heads][head_dim]
+ * (qwen_layer_main.cpp:145-172): every head row is normalised with w, then
+ * dims d and d + head_dim/2 are rotated by angle = position[r] * inv_freq[i]
+ * (fp32 product, as the reference forms it); cos and sin of that fp32 angle
+ * in double.  positions NULL: no rotation (the value projection). */
+int sao_qk_norm_rope(float* x, const float* w, const int32_t* positions, size_t rows, size_t heads,
+                     size_t head_dim, float theta, float eps) {
+  if (!x || head_dim == 0 || head_dim % 2 || head_dim > 512) return -1;
+  float inv_freq[256];
+  sao_rope_inv_freq(theta, head_dim, inv_freq);
+  const size_t half = head_dim / 2;
+  float row[512];
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t h = 0; h < heads; ++h) {
+      float* v = x + (r * heads + h) * head_dim;
+      if (w) {
+        double ss = 0.0;
+        for (size_t d = 0; d < head_dim; ++d) ss += (double)v[d] * (double)v[d];
+        const double inv = 1.0 / sqrt(ss / (double)head_dim + (double)eps);
+        for (size_t d = 0; d < head_dim; ++d) v[d] = (float)((double)v[d] * inv * (double)w[d]);
+      }
+      if (!positions) continue;
+      memcpy(row, v, head_dim * sizeof(float));
+      for (size_t d = 0; d < head_dim; ++d) {
+        const size_t i = d < half ? d : d - half;
+        const float angle = (float)positions[r] * inv_freq[i];
+        const double c = cos((double)angle), sn = sin((double)angle);
+        const double rotated = d < half ? -(double)row[d + half] : (double)row[d - half];
+        v[d] = (float)((double)row[d] * c + rotated * sn);
+      }
+    }
+  return 0;
+}

@@ -249,6 +249,16 @@ int sao_p1_dense_audit(const uint16_t* kv, const float* prompt_queries,
 
 /* ---- Synthetic data shared with the device generator ------------------- */
 
+/* Query producer / output consumer (qwen_layer_main.cpp:125-183):
+ * rms_norm, the [out][in] projections with an optional residual, and the
+ * per-head RMS norm + rotary embedding (NeoX halves). */
+int sao_rms_norm(const float* x, const float* w, float* out, size_t rows, size_t width, float eps);
+int sao_linear(const float* x, const float* w, const float* residual, float* y, size_t rows, size_t in,
+               size_t out);
+void sao_rope_inv_freq(float theta, size_t head_dim, float* inv_freq);
+int sao_qk_norm_rope(float* x, const float* w, const int32_t* positions, size_t rows, size_t heads,
+                     size_t head_dim, float theta, float eps);
+
 /* Counter-based generator.  sao_synth_normal(seed, index) is an
  * Irwin-Hall(4) approximation of N(0,1) computed with integer arithmetic and
  * one fp32 multiply, so the device generator produces the same bits. */

@@ -638,6 +638,85 @@ static int fill_args_ok(uint16_t* pool, int64_t page_bytes, const int32_t* dst_p
   return SA_HIP_OK;
 }
 
+// ---- query producer / output consumer ----------------------------------------
+
+int sa_hip_rms_norm(const float* x, const float* w, float* out, int32_t rows, int32_t width, float eps,
+                    void* stream) {
+  if (!x || !w || !out || rows <= 0 || rows > 2147483647 / 2 || width <= 0 || width % 4 != 0)
+    return fail(SA_HIP_EINVAL, "rms_norm: bad arguments (width must be a positive multiple of 4)");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out))
+    return fail(SA_HIP_EINVAL, "rms_norm: x, w and out must be 16-byte aligned");
+  return check_hip(sa::launch_rms_norm(x, w, out, rows, width, eps, as_stream(stream)), "rms_norm launch");
+}
+
+static int linear_shape_ok(int32_t rows, int32_t in, int32_t out, const char* op) {
+  if (rows <= 0 || rows > 65535 * 64 || in <= 0 || in % 64 != 0 || out <= 0 || out % 64 != 0 || out > 65535 * 64)
+    return fail(SA_HIP_EINVAL, "%s: rows %d, in %d, out %d unsupported (in and out multiples of 64)", op, rows, in,
+                out);
+  return SA_HIP_OK;
+}
+
+size_t sa_hip_linear_workspace_bytes(int32_t rows, int32_t in, int32_t out) {
+  if (rows <= 0 || in <= 0 || out <= 0) return 0;
+  return static_cast<size_t>(sa::linear_ksplit(rows, in, out)) * rows * out * sizeof(float);
+}
+
+int sa_hip_linear(const float* x, const float* w, const float* residual, float* y, int32_t rows, int32_t in,
+                  int32_t out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int e = linear_shape_ok(rows, in, out, "linear")) return e;
+  if (!x || !w || !y || !workspace) return fail(SA_HIP_EINVAL, "linear: null x/w/y/workspace");
+  if (!aligned16(x) || !aligned16(w)) return fail(SA_HIP_EINVAL, "linear: x and w must be 16-byte aligned");
+  if (workspace_bytes < sa_hip_linear_workspace_bytes(rows, in, out))
+    return fail(SA_HIP_EINVAL, "linear: workspace of %zu bytes < %zu", workspace_bytes,
+                sa_hip_linear_workspace_bytes(rows, in, out));
+  sa::LinearLaunch l{x, w, residual, y, static_cast<float*>(workspace), rows, in, out};
+  return check_hip(sa::launch_linear(l, as_stream(stream)), "linear launch");
+}
+
+size_t sa_hip_qkv_workspace_bytes(int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads) {
+  if (rows <= 0 || hidden <= 0 || q_heads <= 0 || kv_heads <= 0) return 0;
+  const int32_t out = (q_heads + 2 * kv_heads) * sa::kHeadDim;
+  return sa_hip_linear_workspace_bytes(rows, hidden, out);
+}
+
+int sa_hip_qkv_project(const float* x, const float* wq, const float* wk, const float* wv, const float* q_norm,
+                       const float* k_norm, const int32_t* positions, int32_t rows, int32_t hidden,
+                       int32_t q_heads, int32_t kv_heads, float theta, float eps, float* q, float* k, float* v,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads > 256 || kv_heads > 256)
+    return fail(SA_HIP_EINVAL, "qkv_project: bad head counts %d/%d", q_heads, kv_heads);
+  if (int e = linear_shape_ok(rows, hidden, (q_heads + 2 * kv_heads) * sa::kHeadDim, "qkv_project")) return e;
+  if (!x || !wq || !wk || !wv || !q_norm || !k_norm || !positions || !q || !k || !v || !workspace)
+    return fail(SA_HIP_EINVAL, "qkv_project: null argument");
+  if (!aligned16(x) || !aligned16(wq) || !aligned16(wk) || !aligned16(wv))
+    return fail(SA_HIP_EINVAL, "qkv_project: x and the weights must be 16-byte aligned");
+  if (!(theta > 1.0f)) return fail(SA_HIP_EINVAL, "qkv_project: rope theta must exceed 1");
+  if (workspace_bytes < sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads))
+    return fail(SA_HIP_EINVAL, "qkv_project: workspace of %zu bytes < %zu", workspace_bytes,
+                sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads));
+  sa::QkvLaunch l{};
+  l.x = x;
+  l.wq = wq;
+  l.wk = wk;
+  l.wv = wv;
+  l.q_norm = q_norm;
+  l.k_norm = k_norm;
+  l.positions = positions;
+  l.q = q;
+  l.k = k;
+  l.v = v;
+  l.workspace = static_cast<float*>(workspace);
+  l.rows = rows;
+  l.hidden = hidden;
+  l.q_heads = q_heads;
+  l.kv_heads = kv_heads;
+  l.eps = eps;
+  // theta^(-2i/128), correctly rounded (the reference's powf is within 2 ulp)
+  for (int i = 0; i < 64; ++i)
+    l.inv_freq[i] = static_cast<float>(std::pow(static_cast<double>(theta), -2.0 * i / sa::kHeadDim));
+  return check_hip(sa::launch_qkv_project(l, as_stream(stream)), "qkv_project launch");
+}
+
 int sa_hip_pages_to_host_async(const uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* pages,
                                int32_t count, void* dst, void* copy_stream, void* after_event, void* done_event) {
   if (count < 0 || (count > 0 && (!pool || !pages || !dst)) || page_bytes <= 0 || page_bytes % 16 != 0)

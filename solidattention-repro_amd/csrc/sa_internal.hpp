@@ -77,6 +77,37 @@ hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream);
 // scoring over chunks of 256 blocks into s.scores, then selection from them
 hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream);
 
+// ---- query producer / output consumer (producer.hip) -----------------------
+struct LinearLaunch {
+  const float* x;         // [rows][in]
+  const float* w;         // [out][in]
+  const float* residual;  // [rows][out] or null
+  float* y;               // [rows][out]
+  float* workspace;       // linear_ksplit(rows, in, out) * rows * out floats
+  int32_t rows, in, out;
+};
+struct QkvLaunch {
+  const float* x;         // normalised hidden [rows][hidden]
+  const float* wq;        // [q_heads*128][hidden]
+  const float* wk;        // [kv_heads*128][hidden]
+  const float* wv;
+  const float* q_norm;    // [128]
+  const float* k_norm;
+  const int32_t* positions;  // [rows]
+  float* q;               // [rows][q_heads][128]
+  float* k;               // [rows][kv_heads][128]
+  float* v;
+  float* workspace;
+  int32_t rows, hidden, q_heads, kv_heads;
+  float eps;
+  float inv_freq[64];
+};
+int linear_ksplit(int64_t rows, int64_t in, int64_t out);
+hipError_t launch_rms_norm(const float* x, const float* w, float* out, int rows, int width, float eps,
+                           hipStream_t stream);
+hipError_t launch_linear(const LinearLaunch& l, hipStream_t stream);
+hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream);
+
 // Compute units of the current device (cached per device; 256 if unknown).
 int compute_units();
 

@@ -59,6 +59,12 @@ EXPORTS = {
     "sa_hip_sparse_decode_attention_partial": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _I32, _P, _SZ, _I32, _I32,
                                                          _I32, _P, _P]),
     "sa_hip_attention_merge": (C.c_int, [_KV, _P, _SZ, _I32, _P, _P]),
+    "sa_hip_rms_norm": (C.c_int, [_P, _P, _P, _I32, _I32, _F, _P]),
+    "sa_hip_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
+    "sa_hip_linear": (C.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _SZ, _P]),
+    "sa_hip_qkv_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "sa_hip_qkv_project": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F, _F, _P, _P, _P, _P,
+                                     _SZ, _P]),
     "sa_store_open": (C.c_void_p, [C.c_char_p, _I64, _I64, _I64, _I32, _I32]),
     "sa_store_close": (None, [_P]),
     "sa_store_is_direct": (C.c_int, [_P]),
@@ -235,6 +241,53 @@ def score_select_split_preferred(kv: PagedKV, select_groups, budget, init, local
     params = SelectParamsStruct(select_groups, budget, init, local, sel_stride or budget, 0, None)
     s = kv.struct()
     return bool(lib().sa_hip_score_select_split_preferred(C.byref(s), C.byref(params)))
+
+
+def rms_norm(x, w, eps=1e-6, out=None, stream=None):
+    """x [rows][width] fp32 -> x * rsqrt(mean(x^2) + eps) * w."""
+    import torch
+    rows, width = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib().sa_hip_rms_norm(_ptr(x), _ptr(w), _ptr(out), rows, width, C.c_float(eps), _stream(stream)),
+          "rms_norm")
+    return out
+
+
+def linear(x, w, residual=None, out=None, workspace=None, stream=None):
+    """y = x @ w.T (+ residual); w is [out][in] fp32."""
+    import torch
+    rows, n_in = x.shape
+    n_out = w.shape[0]
+    if out is None:
+        out = torch.empty((rows, n_out), dtype=torch.float32, device=x.device)
+    nbytes = lib().sa_hip_linear_workspace_bytes(rows, n_in, n_out)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=x.device)
+    check(lib().sa_hip_linear(_ptr(x), _ptr(w), _ptr(residual), _ptr(out), rows, n_in, n_out, _ptr(workspace),
+                              workspace.numel() * 4, _stream(stream)), "linear")
+    return out
+
+
+def qkv_project(x, wq, wk, wv, q_norm, k_norm, positions, q_heads, kv_heads, theta=1e6, eps=1e-6, q=None, k=None,
+                v=None, workspace=None, stream=None):
+    """Normalised hidden x [rows][hidden] -> q [rows][q_heads][128] and
+    k [rows][kv_heads][128] (head RMS norm + RoPE at positions [rows]) and
+    v [rows][kv_heads][128]."""
+    import torch
+    rows, hidden = x.shape
+    dev = x.device
+    q = q if q is not None else torch.empty((rows, q_heads, HEAD_DIM), dtype=torch.float32, device=dev)
+    k = k if k is not None else torch.empty((rows, kv_heads, HEAD_DIM), dtype=torch.float32, device=dev)
+    v = v if v is not None else torch.empty((rows, kv_heads, HEAD_DIM), dtype=torch.float32, device=dev)
+    nbytes = lib().sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
+    check(lib().sa_hip_qkv_project(_ptr(x), _ptr(wq), _ptr(wk), _ptr(wv), _ptr(q_norm), _ptr(k_norm), _ptr(positions),
+                                   rows, hidden, q_heads, kv_heads, C.c_float(theta), C.c_float(eps), _ptr(q),
+                                   _ptr(k), _ptr(v), _ptr(workspace), workspace.numel() * 4, _stream(stream)),
+          "qkv_project")
+    return q, k, v
 
 
 STORE_CREATE, STORE_DIRECT = 1, 2

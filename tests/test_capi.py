@@ -149,3 +149,24 @@ def test_split_selection_requires_scores():
     rc = L.sa_hip_score_select_split(C.byref(kv), C.c_void_p(fake), C.byref(params), C.c_void_p(fake),
                                      C.c_void_p(fake), None, None, None)
     assert rc == -1 and b"scores" in L.sa_hip_last_error()
+
+
+def test_producer_argument_checks():
+    """The projections refuse shapes that are not multiples of 64, short or
+    null workspaces and a RoPE theta <= 1 before any launch."""
+    import solidattention_amd as sa
+    L = sa.lib()
+    f = C.c_void_p(4096)
+    need = L.sa_hip_linear_workspace_bytes(4, 1024, 2048)
+    assert need > 0 and need % (4 * 2048 * 4) == 0
+    assert L.sa_hip_linear(f, f, None, f, 4, 1000, 2048, f, need, None) == -1
+    assert L.sa_hip_linear(f, f, None, f, 4, 1024, 2000, f, need, None) == -1
+    assert L.sa_hip_linear(f, f, None, f, 4, 1024, 2048, f, need - 4, None) == -1
+    assert L.sa_hip_linear(f, f, None, f, 4, 1024, 2048, None, need, None) == -1
+    assert L.sa_hip_linear(f, f, None, f, 0, 1024, 2048, f, need, None) == -1
+    qn = L.sa_hip_qkv_workspace_bytes(4, 1024, 16, 8)
+    args = [f, f, f, f, f, f, f, 4, 1024, 16, 8]
+    assert L.sa_hip_qkv_project(*args, C.c_float(1.0), C.c_float(1e-6), f, f, f, f, qn, None) == -1
+    assert b"theta" in L.sa_hip_last_error()
+    assert L.sa_hip_qkv_project(*args, C.c_float(1e6), C.c_float(1e-6), f, f, f, f, qn - 4, None) == -1
+    assert L.sa_hip_rms_norm(f, f, f, 4, 1022, C.c_float(1e-6), None) == -1

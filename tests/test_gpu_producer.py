@@ -1,0 +1,126 @@
+"""GPU parity: the query producer and output consumer around the attention
+(rms_norm, the [out][in] projections, head RMS + RoPE; reference
+cpp/src/qwen_layer_main.cpp:125-172, :576-584, :640-645) against the
+oracle, and one attention layer's decode step chained through them.
+
+Bars: fp32 kernels against the oracle's float64 sums, relative to the
+largest magnitude of the result: 1e-5 for rms_norm and the projections (the
+K-slice fp32 sums of up to 2048 terms), 2e-5 for q and k after head RMS and
+RoPE (same fp32 angle, device sincos within 2 ulp); the chained layer
+output within 2e-3 (the attention's bar)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+@pytest.mark.parametrize("rows", [1, 7, 64, 130])
+def test_rms_norm(hip, rows):
+    rng = np.random.default_rng(rows)
+    x = (rng.standard_normal((rows, 1024)) * 2).astype(np.float32)
+    w = rng.standard_normal(1024).astype(np.float32)
+    got = hip.rms_norm(to_dev(x), to_dev(w), 1e-6).cpu().numpy()
+    assert rel_err(got, O.rms_norm(x, w, 1e-6)) < 1e-5
+
+
+@pytest.mark.parametrize("rows,n_in,n_out,res", [(1, 1024, 2048, False), (5, 1024, 1024, True), (64, 2048, 1024, True),
+                                                  (100, 1024, 4096, False), (130, 2048, 1024, True)])
+def test_linear(hip, rows, n_in, n_out, res):
+    print(f"case: linear rows={rows} in={n_in} out={n_out} residual={res}", flush=True)
+    rng = np.random.default_rng(rows + n_out)
+    x = rng.standard_normal((rows, n_in)).astype(np.float32)
+    w = (rng.standard_normal((n_out, n_in)) / np.sqrt(n_in)).astype(np.float32)
+    r = rng.standard_normal((rows, n_out)).astype(np.float32) if res else None
+    got = hip.linear(to_dev(x), to_dev(w), None if r is None else to_dev(r)).cpu().numpy()
+    assert rel_err(got, O.linear(x, w, r)) < 1e-5
+
+
+def make_layer(rng, hidden=1024, hq=16, hkv=8):
+    s = 1.0 / np.sqrt(hidden)
+    return dict(
+        wq=(rng.standard_normal((hq * 128, hidden)) * s).astype(np.float32),
+        wk=(rng.standard_normal((hkv * 128, hidden)) * s).astype(np.float32),
+        wv=(rng.standard_normal((hkv * 128, hidden)) * s).astype(np.float32),
+        qn=(1 + 0.1 * rng.standard_normal(128)).astype(np.float32),
+        kn=(1 + 0.1 * rng.standard_normal(128)).astype(np.float32),
+        wo=(rng.standard_normal((hidden, hq * 128)) / np.sqrt(hq * 128)).astype(np.float32),
+        inorm=(1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
+
+
+def oracle_qkv(x, L, positions, hq, hkv, theta=1e6, eps=1e-6):
+    rows = x.shape[0]
+    q = O.linear(x, L["wq"]).reshape(rows, hq, 128)
+    k = O.linear(x, L["wk"]).reshape(rows, hkv, 128)
+    v = O.linear(x, L["wv"]).reshape(rows, hkv, 128)
+    return (O.qk_norm_rope(q, L["qn"], positions, theta, eps), O.qk_norm_rope(k, L["kn"], positions, theta, eps), v)
+
+
+@pytest.mark.parametrize("rows,hq,hkv", [(1, 16, 8), (64, 16, 8), (33, 32, 8), (70, 16, 4)])
+def test_qkv_project(hip, rows, hq, hkv):
+    print(f"case: qkv rows={rows} hq={hq} hkv={hkv}", flush=True)
+    rng = np.random.default_rng(100 + rows)
+    L = make_layer(rng, 1024, hq, hkv)
+    x = rng.standard_normal((rows, 1024)).astype(np.float32)
+    pos = rng.integers(0, 131072, size=rows).astype(np.int32)
+    pos[0] = 0
+    q, k, v = hip.qkv_project(to_dev(x), to_dev(L["wq"]), to_dev(L["wk"]), to_dev(L["wv"]), to_dev(L["qn"]),
+                              to_dev(L["kn"]), to_dev(pos), hq, hkv)
+    eq, ek, ev = oracle_qkv(x, L, pos, hq, hkv)
+    assert rel_err(q.cpu().numpy(), eq) < 2e-5
+    assert rel_err(k.cpu().numpy(), ek) < 2e-5
+    assert rel_err(v.cpu().numpy(), ev) < 1e-5
+
+
+def test_attention_layer_decode_chain(hip):
+    """hidden -> rms_norm -> q/k/v (head RMS, RoPE at each sequence's
+    position) -> decode step (append k/v, seal, select, attend) -> o-proj +
+    residual, against the same chain in the oracle."""
+    from paged_case import PAGE, make_case
+    rng = np.random.default_rng(7)
+    batch, hq, hkv, hidden = 3, 16, 8, 1024
+    L = make_layer(rng, hidden, hq, hkv)
+    case = make_case(71, batch, hq, hkv, [32 * 40 + 31, 32 * 17 + 5, 32 * 25], planted=2)
+    from gpu_util import device_kv, status_tensor
+    kv = device_kv(case)
+    hid = rng.standard_normal((batch, hidden)).astype(np.float32)
+    pos = case.seq_len.astype(np.int32).copy()  # the new token's position
+    budget, init, local = 16, 1, 2
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+
+    st = status_tensor()
+    xn = hip.rms_norm(to_dev(hid), to_dev(L["inorm"]))
+    q, k, v = hip.qkv_project(xn, to_dev(L["wq"]), to_dev(L["wk"]), to_dev(L["wv"]), to_dev(L["qn"]), to_dev(L["kn"]),
+                              to_dev(pos), hq, hkv)
+    ws, _ = hip.decode_step_workspace(kv, 1)
+    sel, cnt, att = hip.decode_step(kv, k, v, 0, q, hkv, budget, init, local, scale, ws, status=st)
+    out = hip.linear(att.view(batch, hq * 128), to_dev(L["wo"]), to_dev(hid)).cpu().numpy()
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+
+    exn = O.rms_norm(hid, L["inorm"])
+    eq, ek, ev = oracle_qkv(exn, L, pos, hq, hkv)
+    # the device's q/k/v feed the oracle's attention so that its own 2e-3
+    # bar is checked on equal inputs; q/k/v themselves are checked above
+    gq, gk, gv = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+    assert rel_err(gq, eq) < 2e-5 and rel_err(gk, ek) < 2e-5 and rel_err(gv, ev) < 1e-5
+    O.paged_append(case.pool, PAGE, case.table, case.seq_len, k=gk.reshape(batch, -1), v=gv.reshape(batch, -1),
+                   batch=batch, hkv=hkv, d=128)
+    O.paged_seal(case.pool, PAGE, case.table, case.seq_len, case.sealed, case.generation, case.reps, case.rep_heads,
+                 case.rep_stride, batch, hq, hkv, 128, 0)
+    esel, ecnt = O.paged_score_select(gq, case.reps, case.sealed, batch, hq, hkv, 128, case.rep_heads,
+                                      case.rep_stride, hkv, budget, init, local)
+    eatt = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, esel, ecnt, hkv, gq,
+                                    batch, hq, hkv, 128, scale)
+    assert np.array_equal(cnt.cpu().numpy(), ecnt)
+    eout = O.linear(eatt.reshape(batch, -1), L["wo"], hid)
+    err = np.abs(out.astype(np.float64) - eout)
+    assert ((err <= 2e-3) | (err <= 2e-3 * np.abs(eout))).all(), float(err.max())
