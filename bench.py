@@ -60,12 +60,14 @@ def parse():
                          "(1 and 2 fall back to 3 where the fused kernel does not apply)")
     ap.add_argument("--prefetch-blocks", type=int, default=128,
                     help="store workload: blocks per store -> pool prefetch batch")
-    ap.add_argument("--workload", default="decode", choices=["decode", "correction", "represent", "stress", "store"],
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "correction", "represent", "stress", "store", "layer"],
                     help="decode: the headline decode step; correction: long-context miss correction "
                          "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage); "
                          "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4); "
                          "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers; "
-                         "store: seal writeback behind decoding and store -> pool prefetch")
+                         "store: seal writeback behind decoding and store -> pool prefetch; "
+                         "layer: decode step with its q/k/v producer and o-proj consumer")
     ap.add_argument("--select", default="auto", choices=["auto", "single", "split"],
                     help="separate selection launch: one workgroup per list, scoring split over 256-block "
                          "workgroups, or the library's preference")
@@ -141,6 +143,10 @@ def main():
     if args.workload == "store":
         import bench_store
         bench_store.run(args)
+        return
+    if args.workload == "layer":
+        import bench_layer
+        bench_layer.run(args)
         return
     import numpy as np
     import torch

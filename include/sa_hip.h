@@ -405,7 +405,7 @@ int sa_hip_rms_norm(const float* x, const float* w, float* out, int32_t rows, in
                     void* stream);
 /* y[r][o] = sum_i x[r][i] * w[o][i] (+ residual[r][o] when non-null): the
  * reference's cublasSgemm(CUBLAS_OP_T) on its row-major [out][in] weights.
- * in and out multiples of 64; x and w 16-byte aligned; workspace of
+ * in and out multiples of 64; x, w, residual and y 16-byte aligned; workspace of
  * sa_hip_linear_workspace_bytes(rows, in, out) bytes (K-slice partial
  * sums, added in a fixed order: deterministic). */
 size_t sa_hip_linear_workspace_bytes(int32_t rows, int32_t in, int32_t out);

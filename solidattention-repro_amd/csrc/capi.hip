@@ -665,7 +665,8 @@ int sa_hip_linear(const float* x, const float* w, const float* residual, float* 
                   int32_t out, void* workspace, size_t workspace_bytes, void* stream) {
   if (int e = linear_shape_ok(rows, in, out, "linear")) return e;
   if (!x || !w || !y || !workspace) return fail(SA_HIP_EINVAL, "linear: null x/w/y/workspace");
-  if (!aligned16(x) || !aligned16(w)) return fail(SA_HIP_EINVAL, "linear: x and w must be 16-byte aligned");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) || (residual && !aligned16(residual)))
+    return fail(SA_HIP_EINVAL, "linear: x, w, residual and y must be 16-byte aligned");
   if (workspace_bytes < sa_hip_linear_workspace_bytes(rows, in, out))
     return fail(SA_HIP_EINVAL, "linear: workspace of %zu bytes < %zu", workspace_bytes,
                 sa_hip_linear_workspace_bytes(rows, in, out));

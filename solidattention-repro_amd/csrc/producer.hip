@@ -31,7 +31,6 @@ constexpr int kSlab = 64;       // output columns per workgroup (16 per wave)
 constexpr int kMTile = 16;
 constexpr int kMTiles = 4;      // rows per workgroup: 64
 constexpr int kKStep = 16;      // k per MFMA group (4 steps of 4)
-constexpr int kKBatch = 4;      // k steps whose loads are issued together
 
 __device__ inline f32x4_t load_nt4(const float* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
@@ -87,49 +86,62 @@ struct LinearParams {
   int32_t kslice;       // k per workgroup
 };
 
+// Rows of x staged in LDS per workgroup: 64 x (kslice + 4) floats; kslice
+// at most kMaxKSlice (the 4-float pad spreads the rows over the banks).
+constexpr int kMaxKSlice = 256;
+constexpr int kXPad = 4;
+
+template <int KS>
 __global__ __launch_bounds__(kThreads) void linear_partial_kernel(const LinearParams p) {
+  static_assert(KS % 64 == 0 && KS <= kMaxKSlice, "K slice of 64..256");
+  __shared__ f32x4_t xs[kMTile * kMTiles * (KS + kXPad) / 4];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int n0 = blockIdx.x * kSlab;
   const int ks = blockIdx.y;
   const int m0 = blockIdx.z * (kMTile * kMTiles);
-  const int k_begin = ks * p.kslice;
-  // the stacked weight holding this slab (slabs never straddle two)
+  const int k_begin = ks * KS;
+  constexpr int xs_stride = (KS + kXPad) / 4;  // in float4
+  // this wave's whole w slice, issued first: 16 columns x kslice
   int wi = 0;
   if (n0 >= p.w_end[0]) wi = n0 >= p.w_end[1] ? 2 : 1;
   const int col0 = wi == 0 ? 0 : p.w_end[wi - 1];
   const int n = n0 + wave * 16 + lane % 16;  // this lane's output column (B operand column)
   const float* wrow = p.w[wi] + static_cast<int64_t>(n - col0) * p.in + k_begin + 4 * (lane / 16);
-  const float* xrow[kMTiles];
-  bool xok[kMTiles];
+  // x rows [m0, m0 + 64) x [k_begin, k_begin + KS): all loads in flight at
+  // once (coalesced, from L2), then the w slice from HBM, then x to LDS
+  constexpr int vecs = KS / 4;
+  constexpr int kXPerThread = kMTile * kMTiles * vecs / kThreads;
+  f32x4_t xr[kXPerThread];
 #pragma unroll
-  for (int t = 0; t < kMTiles; ++t) {
-    const int m = m0 + t * kMTile + lane % 16;  // A operand row
-    xok[t] = m < p.rows;
-    xrow[t] = p.x + static_cast<int64_t>(xok[t] ? m : 0) * p.in + k_begin + 4 * (lane / 16);
+  for (int i = 0; i < kXPerThread; ++i) {
+    const int e = i * kThreads + threadIdx.x;
+    const int m = m0 + e / vecs;
+    xr[i] = m < p.rows ? *reinterpret_cast<const f32x4_t*>(p.x + static_cast<int64_t>(m) * p.in + k_begin +
+                                                           4 * (e % vecs))
+                       : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
+  f32x4_t wv[KS / kKStep];
+#pragma unroll
+  for (int s = 0; s < KS / kKStep; ++s) wv[s] = load_nt4(wrow + s * kKStep);
+#pragma unroll
+  for (int i = 0; i < kXPerThread; ++i) {
+    const int e = i * kThreads + threadIdx.x;
+    xs[(e / vecs) * xs_stride + e % vecs] = xr[i];
+  }
+  __syncthreads();
+
   f32x4_t c[kMTiles];
 #pragma unroll
   for (int t = 0; t < kMTiles; ++t) c[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  for (int k = 0; k < p.kslice; k += kKStep * kKBatch) {
-    f32x4_t wv[kKBatch];
-    f32x4_t xv[kKBatch][kMTiles];
 #pragma unroll
-    for (int b = 0; b < kKBatch; ++b) {
-      wv[b] = load_nt4(wrow + k + b * kKStep);
+  for (int s = 0; s < KS / kKStep; ++s) {
 #pragma unroll
-      for (int t = 0; t < kMTiles; ++t)
-        xv[b][t] = xok[t] ? *reinterpret_cast<const f32x4_t*>(xrow[t] + k + b * kKStep)
-                          : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    for (int t = 0; t < kMTiles; ++t) {
+      // A operand: row 16 t + lane % 16, k = 16 s + 4 (lane / 16) + j
+      const f32x4_t xa = xs[(t * kMTile + lane % 16) * xs_stride + 4 * s + lane / 16];
 #pragma unroll
-    for (int b = 0; b < kKBatch; ++b) {
-#pragma unroll
-      for (int t = 0; t < kMTiles; ++t) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) c[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[b][t][j], wv[b][j], c[t], 0, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j) c[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], wv[s][j], c[t], 0, 0, 0);
     }
   }
   // D layout: lane holds rows 4 (lane / 16) + i of the tile, column lane % 16
@@ -144,16 +156,24 @@ __global__ __launch_bounds__(kThreads) void linear_partial_kernel(const LinearPa
   }
 }
 
-// out[r][o] = sum of the K-slice partials (in slice order) + residual[r][o]
+// out[r][o] = sum of the K-slice partials (in slice order) + residual[r][o];
+// 4 consecutive elements per thread, the slices' loads issued 8 at a time
 __global__ __launch_bounds__(kThreads) void linear_epilogue_kernel(const float* part, const float* residual,
                                                                    float* out, int64_t elems, int ksplit) {
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; e < elems;
-       e += static_cast<int64_t>(gridDim.x) * kThreads) {
-    float s = 0.0f;
-    for (int k = 0; k < ksplit; ++k) s += part[k * elems + e];
-    if (residual) s += residual[e];
-    out[e] = s;
+  const int64_t e = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4;
+  if (e >= elems) return;
+  f32x4_t s = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  int k = 0;
+  for (; k + 8 <= ksplit; k += 8) {
+    f32x4_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const f32x4_t*>(part + (k + i) * elems + e);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += v[i];
   }
+  for (; k < ksplit; ++k) s += *reinterpret_cast<const f32x4_t*>(part + k * elems + e);
+  if (residual) s += *reinterpret_cast<const f32x4_t*>(residual + e);
+  *reinterpret_cast<f32x4_t*>(out + e) = s;
 }
 
 struct QkvEpilogue {
@@ -221,11 +241,12 @@ int slabs_for(int out) { return out / kSlab; }
 }  // namespace
 
 int linear_ksplit(int64_t rows, int64_t in, int64_t out) {
-  // about two workgroups per CU; a slice is a multiple of 64 k
+  // the fewest K slices (partial sums are extra traffic) that give about one
+  // workgroup per CU, with slices of 64..256 k
   const int64_t mtiles = (rows + kMTile * kMTiles - 1) / (kMTile * kMTiles);
   const int64_t blocks = (out / kSlab) * mtiles;
   int64_t ks = 1;
-  while (ks * 2 * blocks <= 2 * compute_units() && in % (ks * 2 * kKStep * kKBatch) == 0) ks *= 2;
+  while (in / ks > kMaxKSlice || (ks * blocks < compute_units() && in / (ks * 2) >= 64)) ks *= 2;
   return static_cast<int>(ks);
 }
 
@@ -238,7 +259,12 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* out, int rows,
 static hipError_t launch_partials(const LinearParams& lp, hipStream_t stream) {
   const int mtiles = (lp.rows + kMTile * kMTiles - 1) / (kMTile * kMTiles);
   const dim3 grid(slabs_for(lp.out), lp.in / lp.kslice, mtiles);
-  hipLaunchKernelGGL(linear_partial_kernel, grid, dim3(kThreads), 0, stream, lp);
+  switch (lp.kslice) {
+    case 64: hipLaunchKernelGGL(linear_partial_kernel<64>, grid, dim3(kThreads), 0, stream, lp); break;
+    case 128: hipLaunchKernelGGL(linear_partial_kernel<128>, grid, dim3(kThreads), 0, stream, lp); break;
+    case 256: hipLaunchKernelGGL(linear_partial_kernel<256>, grid, dim3(kThreads), 0, stream, lp); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -255,8 +281,8 @@ hipError_t launch_linear(const LinearLaunch& l, hipStream_t stream) {
   lp.kslice = l.in / ks;
   hipError_t e = launch_partials(lp, stream);
   if (e != hipSuccess) return e;
-  const int64_t elems = static_cast<int64_t>(l.rows) * l.out;
-  const int blocks = static_cast<int>(std::min<int64_t>((elems + kThreads - 1) / kThreads, 4096));
+  const int64_t elems = static_cast<int64_t>(l.rows) * l.out;  // a multiple of 64
+  const int blocks = static_cast<int>((elems / 4 + kThreads - 1) / kThreads);
   hipLaunchKernelGGL(linear_epilogue_kernel, dim3(blocks), dim3(kThreads), 0, stream, l.workspace, l.residual,
                      l.y, elems, ks);
   return hipGetLastError();
