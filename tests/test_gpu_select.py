@@ -136,3 +136,39 @@ def test_split_capacity_flag(hip):
     s = sel.cpu().numpy()
     for g in range(8):
         assert s[1, g, : c[1, g]].tolist() == esel[0, g, : ecnt[0, g]].tolist()
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_selection_at_the_8192_block_limit(hip, split):
+    """8192 sealed blocks (256K tokens) is the selection's limit: selected
+    bit-exact with the oracle; 8193 blocks are flagged (capacity) and select
+    nothing, in both forms."""
+    rng = np.random.default_rng(140)
+    n, hq, hkv, budget = 8192, 16, 8, 128
+    rep_stride = n + 4
+    kv = hip.PagedKV(1, hq, hkv, rep_stride, num_pages=4, rep_stride=rep_stride)
+    reps = rng.standard_normal((1, hkv, D, rep_stride)).astype(np.float32)
+    kv.reps.copy_(torch.from_numpy(reps))
+    kv.sealed.fill_(n)
+    kv.seq_len.fill_(n * 32)
+    q = rng.standard_normal((1, hq, D)).astype(np.float32)
+    st = status_tensor()
+    scores = torch.zeros((1, hkv, rep_stride), dtype=torch.float32, device="cuda")
+    print(f"case: {n} blocks split={split}", flush=True)
+    fn = hip.score_select_split if split else hip.score_select
+    res = fn(kv, to_dev(q), hkv, budget, 4, 8, scores=scores, status=st)
+    sel, cnt = res[0], res[1]
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    esel, ecnt, esc = O.paged_score_select(q, reps, np.array([n], np.int32), 1, hq, hkv, D, hkv, rep_stride, hkv,
+                                           budget, 4, 8, want_scores=True)
+    assert np.array_equal(cnt.cpu().numpy(), ecnt)
+    assert np.array_equal(sel.cpu().numpy(), esel)
+    assert np.array_equal(scores.cpu().numpy()[..., :n].view(np.uint32), esc[..., :n].view(np.uint32))
+    kv.sealed.fill_(n + 1)
+    kv.seq_len.fill_((n + 1) * 32)
+    st.zero_()
+    res = fn(kv, to_dev(q), hkv, budget, 4, 8, scores=scores, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    assert (res[1].cpu().numpy() == 0).all()
