@@ -174,7 +174,7 @@ def main():
     # separate attention launch splits its page lists by default_splits
     fused_ok = (args.splits in (0, 1) and sa.select_attend_fused(L[0].kv, hkv, 1)
                 and (args.splits == 1 or sa.select_attend_default_splits(L[0].kv, hkv, budget) == 1))
-    splits = args.splits or sa.default_splits(batch, hkv, pages_hint)
+    splits = args.splits or sa.default_splits(batch, hkv, pages_hint, hq)
     ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(batch, hq, hkv, D, splits)
     workspace = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))

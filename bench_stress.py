@@ -116,7 +116,7 @@ def run(args):
         splits = max_chunks
     else:
         max_chunks = 0
-        splits = args.splits or sa.default_splits(B, HKV, int(blocks.mean()))
+        splits = args.splits or sa.default_splits(B, HKV, int(blocks.mean()), HQ)
     ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, splits)
     workspace = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()

@@ -106,7 +106,16 @@ size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads,
                                         int32_t kv_heads, int32_t head_dim,
                                         int32_t splits);
 
-/* Split count the library would pick for a launch (>= 1). */
+/* Split count the library picks for a launch (>= 1): workgroups per
+ * (sequence, KV head) until every CU holds as many as can be resident for
+ * this many query heads per KV head (two for 1-2, one for 4 and 8), keeping
+ * at least ~4 pages per wave.  No counterpart in the reference (its
+ * attention is one CPU loop per head); the split is this library's launch
+ * shape. */
+int32_t sa_hip_attention_splits_for(int32_t batch, int32_t query_heads, int32_t kv_heads,
+                                    int32_t pages_per_group_hint);
+
+/* sa_hip_attention_splits_for with 2 query heads per KV head. */
 int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads,
                                         int32_t pages_per_group_hint);
 
@@ -229,7 +238,7 @@ int sa_hip_select_attend_fused(const sa_paged_kv* kv,
 /* The split count to pass to sa_hip_select_attend / sa_hip_decode_step: 1
  * (the fused launch) when the fused kernel applies and its workgroups fill
  * the device (batch x kv_heads >= 2 x CUs); otherwise
- * sa_hip_attention_default_splits(batch, kv_heads, budget_blocks + 2) for the
+ * sa_hip_attention_splits_for(batch, query_heads, kv_heads, budget_blocks + 2) for the
  * separate launches. */
 int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv,
                                             const sa_select_params* params);

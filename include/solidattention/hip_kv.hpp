@@ -164,9 +164,10 @@ class SparseDecoder {
   SparseDecoder(const PagedKvPool& pool, sa_select_params params, int splits = 0, int chunk_pages = 128)
       : params_(params),
         splits_(splits > 0 ? splits
-                           : sa_hip_attention_default_splits(static_cast<int32_t>(pool.batch()),
-                                                             static_cast<int32_t>(pool.kv_heads()),
-                                                             params.budget_blocks + 2)),
+                           : sa_hip_attention_splits_for(static_cast<int32_t>(pool.batch()),
+                                                         static_cast<int32_t>(pool.query_heads()),
+                                                         static_cast<int32_t>(pool.kv_heads()),
+                                                         params.budget_blocks + 2)),
         selected_(pool.batch() * params.select_groups * params.sel_stride),
         counts_(pool.batch() * params.select_groups),
         workspace_bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),

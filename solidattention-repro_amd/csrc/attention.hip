@@ -26,11 +26,12 @@ namespace {
 
 using namespace attn;
 
-// Waves per workgroup: 8 for G <= 2 (123 VGPRs: two 8-wave workgroups per
-// CU); 4 for G >= 4, whose larger accumulator sets (161+ VGPRs) would leave
-// room for only one 8-wave workgroup per CU.
+// Waves per workgroup: 8 for G <= 4 (G <= 2: 123 VGPRs, two 8-wave
+// workgroups per CU; G = 4: one 8-wave workgroup per CU, bound by its
+// 8 x 16 KiB LDS page slots); 4 for G = 8, whose registers (~300) allow one
+// wave per SIMD.
 template <int G>
-constexpr int waves_per_group() { return G >= 4 ? 4 : 8; }
+constexpr int waves_per_group() { return G >= 8 ? 4 : 8; }
 constexpr int kMergeThreads = 256;
 
 struct Params {
@@ -97,25 +98,59 @@ __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_at
   if (p.chunk_pages > 0 && z > 0 && static_cast<int64_t>(z) * p.chunk_pages >= L.total) return;
 
   const LaneGeom lg = lane_geom(p.v, g, lane);
+  const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
   WaveState<G> st;
-  st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
 
+  // G = 4, 8: pages staged through LDS (a 16 KiB slot per wave, reused for
+  // the combine below) and q.K on the matrix cores; G <= 2 keeps pages in
+  // registers (two 8-wave workgroups per CU already keep enough pages in
+  // flight and the arithmetic per page is half or less)
+  constexpr bool kStaged = G == 4 || G == 8;
+  constexpr int kStageBytes = kWavesPerGroup * kStageVecs * 16;
+  constexpr int kPbufFloats = (G * 32 + G + 3) / 4 * 4;
+  constexpr int kSmemBytes = kStaged ? kStageBytes + kWavesPerGroup * kPbufFloats * 4
+                                     : static_cast<int>(sizeof(CombineSmem<G, kWavesPerGroup>));
+  static_assert(!kStaged || sizeof(CombineSmem<G, kWavesPerGroup>) <= kStageBytes, "combine fits the stage");
+  __shared__ __align__(16) unsigned char smem[kSmemBytes];
+
+  int start, end, step;
+  bool owns_last;  // this workgroup's range holds the list's last position
   if (p.chunk_pages > 0) {
     // a fixed number of pages per workgroup, whatever the list length, so
     // long and short lists cost by their length; the last workgroup takes
     // any remainder, workgroups past the end leave an empty record
     const int first = z * p.chunk_pages;
-    const int end = z == p.splits - 1
-                        ? L.total
-                        : static_cast<int>(min<int64_t>(L.total, static_cast<int64_t>(first) + p.chunk_pages));
-    for (int i = first + wave; i < end; i += kWavesPerGroup) {
-      const PageRef pr = resolve_page(p.v, b, i, L);
-      if (pr.valid <= 0) continue;
-      st.attend(p.v, pr, lg);
-    }
+    end = z == p.splits - 1 ? L.total
+                            : static_cast<int>(min<int64_t>(L.total, static_cast<int64_t>(first) + p.chunk_pages));
+    start = first + wave;
+    step = kWavesPerGroup;
+    owns_last = first < L.total && end == L.total;
   } else {
-    const int stride = p.splits * kWavesPerGroup;
-    for (int i = z * kWavesPerGroup + wave; i < L.total; i += stride) {
+    start = z * kWavesPerGroup + wave;
+    end = L.total;
+    step = p.splits * kWavesPerGroup;
+    owns_last = L.total > 0 && ((L.total - 1) / kWavesPerGroup) % p.splits == z;
+  }
+  if constexpr (kStaged) {
+    // the list's last page, when it is a partial tail page, is spread over
+    // all waves of the workgroup that owns it (row groups, register loads)
+    const bool split_last = L.total > L.n_sel && L.len % kPageTokens != 0;
+    const int walk_end = split_last ? min(end, L.total - 1) : end;
+    st.reset();
+    float* pbuf = reinterpret_cast<float*>(smem + kStageBytes) + wave * kPbufFloats;
+    st.attend_staged_mfma(p.v, b, L, start, walk_end, step, lg, lane, g,
+                          reinterpret_cast<uint4*>(smem) + wave * kStageVecs, pbuf, q_group, p.qscale);
+    if (split_last && owns_last) {
+      const PageRef pr = resolve_page(p.v, b, L.total - 1, L);
+      if (pr.valid > 0) {
+        st.load_q(q_group, p.qscale, lg.col);
+        st.template attend_rows<kWavesPerGroup>(p.v, pr, lg, wave);
+      }
+    }
+    __syncthreads();  // every wave is done with its slot before the combine reuses the area
+  } else {
+    st.init(q_group, p.qscale, lg.col);
+    for (int i = start; i < end; i += step) {
       const PageRef pr = resolve_page(p.v, b, i, L);
       if (pr.valid <= 0) continue;
       st.attend(p.v, pr, lg);
@@ -124,7 +159,7 @@ __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_at
 
   // ---- combine the waves of the workgroup through LDS ----------------------
   st.reduce_rows();
-  __shared__ CombineSmem<G, kWavesPerGroup> cs;
+  CombineSmem<G, kWavesPerGroup>& cs = *reinterpret_cast<CombineSmem<G, kWavesPerGroup>*>(smem);
   publish_wave<G, kWavesPerGroup>(st, cs, wave, lane, lg.row, lg.col);
   __syncthreads();
 

@@ -96,17 +96,29 @@ size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads, int3
   return static_cast<size_t>(batch) * kv_heads * splits * group * sa::part_stride(head_dim) * sizeof(float);
 }
 
-int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads, int32_t pages_per_group_hint) {
-  // One workgroup (8 waves) per (sequence, KV head) streams best once there
-  // are >= 512 of them (two per CU): at B=64, 8 KV heads, 65 pages per group
-  // splits of 2-4 plus the merge kernel measured 3-7% slower than 1.
-  // Smaller batches split the page list until ~512 workgroups exist, keeping
-  // at least ~4 pages per wave.
+int32_t sa_hip_attention_splits_for(int32_t batch, int32_t query_heads, int32_t kv_heads,
+                                    int32_t pages_per_group_hint) {
+  // Workgroups per (sequence, KV head) so that every CU holds as many as can
+  // be resident: two 8-wave workgroups per CU for 1-2 query heads per KV
+  // head (registers), one for 4 (its eight 16 KiB LDS page slots) and one
+  // 4-wave workgroup for 8 (registers).  Measured at B=64, 8 KV heads, G=2:
+  // splits of 2-4 plus the merge kernel ran 3-7% slower than 1; at B=32,
+  // G=4: one workgroup per list without the merge ran 52 us against 63 us
+  // for splits of 2.  Smaller batches split the page list until every
+  // resident slot is used, keeping at least ~4 pages per wave.
+  const int group = kv_heads > 0 && query_heads >= kv_heads ? query_heads / kv_heads : 1;
+  const int per_cu = group <= 2 ? 2 : 1;
+  const int waves = group >= 8 ? 4 : 8;
+  const int64_t target = static_cast<int64_t>(per_cu) * sa::compute_units();
   const int64_t pages = std::max<int32_t>(pages_per_group_hint, 1);
   const int64_t groups = static_cast<int64_t>(std::max(batch, 1)) * std::max(kv_heads, 1);
   int64_t splits = 1;
-  while (groups * splits < 512 && (splits * 2) * 8 * 4 <= pages) splits *= 2;
+  while (groups * splits < target && (splits * 2) * waves * 4 <= pages) splits *= 2;
   return static_cast<int32_t>(std::min<int64_t>(splits, 64));
+}
+
+int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads, int32_t pages_per_group_hint) {
+  return sa_hip_attention_splits_for(batch, 2 * std::max(kv_heads, 1), kv_heads, pages_per_group_hint);
 }
 
 static int attention_common(const sa_paged_kv* kv, const float* query, const int32_t* selected,
@@ -244,16 +256,17 @@ int sa_hip_attention_merge(const sa_paged_kv* kv, const void* workspace, size_t 
   return check_hip(sa::launch_sparse_decode_attention(a, as_stream(stream)), "attention_merge launch");
 }
 
-static int32_t contiguous_splits(int64_t tokens, int32_t kv_heads) {
+static int32_t contiguous_splits(int64_t tokens, int32_t query_heads, int32_t kv_heads) {
   const int64_t pages = (tokens + SA_HIP_PAGE_TOKENS - 1) / SA_HIP_PAGE_TOKENS;
-  return sa_hip_attention_default_splits(1, kv_heads, static_cast<int32_t>(std::min<int64_t>(pages, 1 << 30)));
+  return sa_hip_attention_splits_for(1, query_heads, kv_heads,
+                                     static_cast<int32_t>(std::min<int64_t>(pages, 1 << 30)));
 }
 
 size_t sa_hip_contiguous_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t kv_heads,
                                          int32_t head_dim) {
   if (tokens <= 0 || kv_heads <= 0) return 0;
   return sa_hip_attention_workspace_bytes(1, query_heads, kv_heads, head_dim,
-                                          contiguous_splits(tokens, kv_heads));
+                                          contiguous_splits(tokens, query_heads, kv_heads));
 }
 
 int sa_hip_attention_contiguous(const uint16_t* kv, const float* query, int64_t tokens, int32_t query_heads,
@@ -276,7 +289,7 @@ int sa_hip_attention_contiguous(const uint16_t* kv, const float* query, int64_t 
   view.head_dim = head_dim;
   if (int e = check_geometry(&view, "attention_contiguous")) return e;
   return attention_common(&view, query, nullptr, nullptr, 1, 1, scale, out, workspace, workspace_bytes,
-                          contiguous_splits(tokens, kv_heads), nullptr, stream, tokens);
+                          contiguous_splits(tokens, query_heads, kv_heads), nullptr, stream, tokens);
 }
 
 int sa_hip_consume_checksum(const float* input, int32_t elements, float* checksum, void* stream) {
@@ -364,7 +377,7 @@ int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv, const sa_sele
   if (sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups) &&
       static_cast<int64_t>(kv->batch) * kv->kv_heads >= 2 * static_cast<int64_t>(sa::compute_units()))
     return 1;
-  return sa_hip_attention_default_splits(kv->batch, kv->kv_heads, params->budget_blocks + 2);
+  return sa_hip_attention_splits_for(kv->batch, kv->query_heads, kv->kv_heads, params->budget_blocks + 2);
 }
 
 int sa_hip_select_attend_fused(const sa_paged_kv* kv, const sa_select_params* params, int32_t splits) {

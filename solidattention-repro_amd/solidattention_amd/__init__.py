@@ -55,6 +55,7 @@ EXPORTS = {
     "sa_hip_device_count": (C.c_int, []),
     "sa_hip_attention_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
     "sa_hip_attention_default_splits": (_I32, [_I32, _I32, _I32]),
+    "sa_hip_attention_splits_for": (_I32, [_I32, _I32, _I32, _I32]),
     "sa_hip_sparse_decode_attention": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _P, _P]),
     "sa_hip_sparse_decode_attention_partial": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _I32, _P, _SZ, _I32, _I32,
                                                          _I32, _P, _P]),
@@ -462,8 +463,12 @@ def attention_workspace(kv: PagedKV, splits, device="cuda"):
     return torch.zeros(max(n // 4, 1), dtype=torch.float32, device=device), n
 
 
-def default_splits(batch, kv_heads, pages_hint):
-    return int(lib().sa_hip_attention_default_splits(batch, kv_heads, pages_hint))
+def default_splits(batch, kv_heads, pages_hint, query_heads=None):
+    """Split count of the library for a launch; query_heads defaults to two
+    per KV head."""
+    if query_heads is None:
+        return int(lib().sa_hip_attention_default_splits(batch, kv_heads, pages_hint))
+    return int(lib().sa_hip_attention_splits_for(batch, query_heads, kv_heads, pages_hint))
 
 
 def sparse_decode_attention(kv: PagedKV, query, selected, counts, scale, out=None, splits=None,
@@ -471,7 +476,7 @@ def sparse_decode_attention(kv: PagedKV, query, selected, counts, scale, out=Non
     import torch
     select_groups, sel_stride = selected.shape[1], selected.shape[2]
     if splits is None:
-        splits = default_splits(kv.batch, kv.kv_heads, sel_stride + 2)
+        splits = default_splits(kv.batch, kv.kv_heads, sel_stride + 2, kv.query_heads)
     if out is None:
         out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=query.device)
     nbytes = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, splits)

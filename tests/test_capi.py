@@ -43,6 +43,15 @@ def test_host_only_queries():
     assert L.sa_hip_attention_workspace_bytes(64, 16, 8, 128, 1) == 0
     s = L.sa_hip_attention_default_splits(64, 8, 66)
     assert 1 <= s <= 64
+    # resident workgroups per CU (256 CUs off the GPU): two for 1-2 query
+    # heads per KV head, one 8-wave for 4, one 4-wave for 8; at least ~4
+    # pages per wave
+    assert L.sa_hip_attention_splits_for(64, 16, 8, 66) == 1 == s
+    assert L.sa_hip_attention_splits_for(32, 32, 8, 66) == 1
+    assert L.sa_hip_attention_splits_for(32, 16, 8, 66) == 2
+    assert L.sa_hip_attention_splits_for(8, 32, 8, 66) == 2
+    assert L.sa_hip_attention_splits_for(1, 64, 8, 1000) == 32
+    assert L.sa_hip_attention_splits_for(1, 32, 8, 1 << 20) == 32
 
 
 def test_compare_prediction_matches_oracle_on_p10(oracle_lib):
