@@ -14,11 +14,17 @@
 // Measured on MI355X at B=64/16K (512 (sequence, KV head) pairs, 64 selected
 // pages + a partial tail page each): one workgroup of 8 waves per pair,
 // ~8 pages per wave, with non-temporal page loads streams the selected
-// pages at ~6.0 TB/s (plain loads: 5.3 TB/s; a plain contiguous read of the
-// pool: 6.4 TB/s).  Rejected variants, measured: register prefetch of the
-// next page, a fused last-workgroup merge, prefetching the page ids of a
-// wave's pages into lanes, and spreading the partial tail page over all
-// waves (all within run-to-run noise or slower).
+// pages at ~6.0 TB/s (plain loads: 5.3 TB/s).  Reads of 16 KiB page slices
+// in random page order peak at 6.3-6.5 TB/s on this pool layout (a
+// contiguous stream: 7.2 TB/s).  Rejected variants at G <= 2, measured:
+// register prefetch of the next page, a fused last-workgroup merge,
+// prefetching the page ids of a wave's pages into lanes, and spreading the
+// partial tail page over all waves (all within run-to-run noise or slower).
+//
+// G = 4 (Qwen3-8B shape, B=32/32K, 256 pairs): LDS-staged pages with q.K on
+// the matrix cores, one 8-wave workgroup per pair and no merge, runs within
+// ~3% of the same kernel with its arithmetic removed (timing probe); the
+// register kernel with splits of 2 + merge ran ~13% slower on the same box.
 #include "attn_core.hpp"
 
 namespace sa {

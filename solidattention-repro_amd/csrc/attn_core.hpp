@@ -16,8 +16,10 @@
 // {r, r+4, ...}.  q.k partial dots are reduced across the 16 lanes of a row
 // with DPP; the G query heads of the group reuse every K/V register
 // (v_fma_mix_f32 consumes the FP16 halves directly), so KV bytes are read
-// from HBM once per group.  No MFMA: decode attention is a matrix-vector
-// product (about 2 flop per KV byte at G=2).
+// from HBM once per group.  At G <= 2 everything runs on the VALU (decode
+// attention is a matrix-vector product, about 2 flop per KV byte); at G = 4
+// and 8 the pages are staged through LDS and q.K runs on the matrix cores
+// (the staged section below), which halves the VALU work per page.
 #pragma once
 
 #include "sa_device.hpp"
