@@ -36,14 +36,16 @@ struct Params {
   int32_t sel_stride;
 };
 
-template <int GR, int kThreads>
+// QUAD: four blocks per lane with 16-byte representative loads (reps 16-byte
+// aligned, rep_stride a multiple of 4); else one block per lane.
+template <int GR, int kThreads, bool QUAD>
 __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) {
   constexpr int kWaves = kThreads / kWave;
   const int sg = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
 
-  __shared__ float q_s[kMaxSelectHeads * D];
+  __shared__ __align__(16) float q_s[kMaxSelectHeads * D];
   __shared__ uint32_t keys[kMaxSelectBlocks];
   __shared__ SelectSmem<kWaves> sm;
 
@@ -69,9 +71,14 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   a.group = p.group;
   a.rep_heads = p.rep_heads;
   a.rep_stride = p.rep_stride;
-  load_query<kThreads>(a, q_s);
+  load_query_t<kThreads>(a, q_s);
   __syncthreads();
-  score_blocks<GR, kThreads>(a, q_s, n, keys, p.scores ? p.scores + out_row * p.rep_stride : nullptr);
+  float* scores_row = p.scores ? p.scores + out_row * p.rep_stride : nullptr;
+  if constexpr (QUAD) {
+    score_blocks_quad<GR, kThreads>(a, q_s, n, keys, scores_row);
+  } else {
+    score_blocks_t<GR, kThreads>(a, q_s, n, keys, scores_row);
+  }
   __syncthreads();
 
   const Budget bs = budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
@@ -105,7 +112,7 @@ __global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params 
   const int n = p.sealed[b];
   // invalid lengths are flagged by the selection kernel
   if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks || first >= n) return;
-  __shared__ float q_s[kMaxSelectHeads * D];
+  __shared__ __align__(16) float q_s[kMaxSelectHeads * D];
   ScoreArgs a{};
   a.query = p.query;
   a.reps = p.reps;
@@ -116,11 +123,11 @@ __global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params 
   a.group = p.group;
   a.rep_heads = p.rep_heads;
   a.rep_stride = p.rep_stride;
-  load_query<kChunkBlocks>(a, q_s);
+  load_query_t<kChunkBlocks>(a, q_s);
   __syncthreads();
   const int blk = first + static_cast<int>(threadIdx.x);
   if (blk < n) {
-    const float score = score_one_pipelined<GR>(a, q_s, blk);
+    const float score = score_one_t<GR>(a, q_s, blk);
     p.scores[(static_cast<int64_t>(b) * p.select_groups + sg) * p.rep_stride + blk] = score;
   }
 }
@@ -169,12 +176,19 @@ bool wide_select(int64_t workgroups, int64_t blocks) {
   return wide < narrow;
 }
 
+bool quad_layout(const Params& p) {
+  return (reinterpret_cast<uintptr_t>(p.reps) & 15u) == 0 && p.rep_stride % 4 == 0;
+}
+
 template <int GR>
 void launch_gr(const Params& p, dim3 grid, hipStream_t stream) {
-  if (wide_select(static_cast<int64_t>(grid.x) * grid.y, p.rep_stride)) {
-    hipLaunchKernelGGL((score_select_kernel<GR, 1024>), grid, dim3(1024), 0, stream, p);
+  if (quad_layout(p)) {
+    // 4 waves score 1024 blocks per pass
+    hipLaunchKernelGGL((score_select_kernel<GR, 256, true>), grid, dim3(256), 0, stream, p);
+  } else if (wide_select(static_cast<int64_t>(grid.x) * grid.y, p.rep_stride)) {
+    hipLaunchKernelGGL((score_select_kernel<GR, 1024, false>), grid, dim3(1024), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((score_select_kernel<GR, 512>), grid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((score_select_kernel<GR, 512, false>), grid, dim3(512), 0, stream, p);
   }
 }
 

@@ -167,6 +167,174 @@ __device__ inline float score_one_pipelined(const ScoreArgs& a, const float* q_s
   return score;
 }
 
+// The same scoring with the query staged transposed: q_t[d * heads_per_sel
+// + h], so the GR heads that share a representative row are adjacent and one
+// broadcast LDS read per d feeds all of them (with q_s[h * D + d] each d
+// costs GR reads, each waited on before its multiply).  Same operations in
+// the same order as score_one(): bit-identical scores.
+template <int kThreads>
+__device__ inline void load_query_t(const ScoreArgs& a, float* q_t) {
+  const float* q = a.query + (static_cast<int64_t>(a.b) * a.query_heads + a.h_first) * D;
+  for (int e = threadIdx.x; e < a.heads_per_sel * D; e += kThreads) q_t[(e % D) * a.heads_per_sel + e / D] = q[e];
+}
+
+template <int GR>
+__device__ inline void read_q_t(const float* p, float (&qv)[GR]) {
+  if constexpr (GR == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    qv[0] = v.x;
+    qv[1] = v.y;
+    qv[2] = v.z;
+    qv[3] = v.w;
+  } else if constexpr (GR == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    qv[0] = v.x;
+    qv[1] = v.y;
+  } else {
+#pragma unroll
+    for (int j = 0; j < GR; ++j) qv[j] = p[j];
+  }
+}
+
+template <int GR>
+__device__ inline void dot_batch_t(const float* q_t, int qoff, int hps, int h0, int d0,
+                                   const float (&rv)[kPipeBatch], float (&dot)[GR]) {
+#pragma unroll
+  for (int k = 0; k < kPipeBatch; ++k) {
+    float qv[GR];
+    read_q_t<GR>(q_t + qoff + (d0 + k) * hps + h0, qv);
+#pragma unroll
+    for (int j = 0; j < GR; ++j) dot[j] = dot[j] + qv[j] * rv[k];
+  }
+}
+
+template <int GR>
+__device__ inline float score_one_t(const ScoreArgs& a, const float* q_t, int blk) {
+  static_assert(D == 4 * kPipeBatch, "four batches per representative row");
+  int qoff = 0;
+  asm volatile("" : "+s"(qoff));
+  const float heads_f = static_cast<float>(a.heads_per_sel);
+  const int hps = a.heads_per_sel;
+  const int64_t stride = a.rep_stride;
+  float score = 0.0f;
+  for (int h0 = 0; h0 < hps; h0 += GR) {
+    const int h = a.h_first + h0;
+    const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
+    const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * stride + blk;
+    float dot[GR];
+#pragma unroll
+    for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
+    float ra[kPipeBatch], rb[kPipeBatch];
+    load_batch(r, stride, 0, ra);
+    load_batch(r, stride, kPipeBatch, rb);
+    dot_batch_t<GR>(q_t, qoff, hps, h0, 0, ra, dot);
+    load_batch(r, stride, 2 * kPipeBatch, ra);
+    dot_batch_t<GR>(q_t, qoff, hps, h0, kPipeBatch, rb, dot);
+    load_batch(r, stride, 3 * kPipeBatch, rb);
+    dot_batch_t<GR>(q_t, qoff, hps, h0, 2 * kPipeBatch, ra, dot);
+    dot_batch_t<GR>(q_t, qoff, hps, h0, 3 * kPipeBatch, rb, dot);
+#pragma unroll
+    for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
+  }
+  return score;
+}
+
+template <int GR, int kThreads>
+__device__ inline void score_blocks_t(const ScoreArgs& a, const float* q_t, int n, uint32_t* keys, float* scores) {
+  for (int blk = threadIdx.x; blk < n; blk += kThreads) {
+    const float score = score_one_t<GR>(a, q_t, blk);
+    keys[blk] = order_key(score);
+    if (scores) scores[blk] = score;
+  }
+}
+
+// Four consecutive blocks per lane: one 16-byte load per d fetches the
+// lane's four representative values (rows of rep_stride floats, rep_stride a
+// multiple of 4, reps 16-byte aligned), so a wave reads 1 KiB per load
+// instruction instead of 256 B.  On the Qwen3-8B selection layout (256 lists
+// x 128 rows x 1024 blocks) the loads alone take 18 us this way against
+// 29 us with one block per lane (probe).  Each block's dot is still the
+// sequential fp32 sum over d per head, in the same order: bit-identical
+// scores.  Batches of 8 rows, double-buffered (three batches ahead measured
+// no faster).
+constexpr int kQuadBatch = 8;
+typedef float f32x4q_t __attribute__((ext_vector_type(4)));
+
+__device__ inline void load_quads(const float* r, int64_t stride, int d0, f32x4q_t (&rv)[kQuadBatch]) {
+#pragma unroll
+  for (int k = 0; k < kQuadBatch; ++k)
+    rv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4q_t*>(r + static_cast<int64_t>(d0 + k) * stride));
+}
+
+template <int GR>
+__device__ inline void dot_quads(const float* q_t, int qoff, int hps, int h0, int d0, const f32x4q_t (&rv)[kQuadBatch],
+                                 float (&dot)[GR][4]) {
+#pragma unroll
+  for (int k = 0; k < kQuadBatch; ++k) {
+    float qv[GR];
+    read_q_t<GR>(q_t + qoff + (d0 + k) * hps + h0, qv);
+#pragma unroll
+    for (int j = 0; j < GR; ++j) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dot[j][c] = dot[j][c] + qv[j] * rv[k][c];
+    }
+  }
+}
+
+template <int GR>
+__device__ inline void score_quad(const ScoreArgs& a, const float* q_t, int blk0, float (&score)[4]) {
+  static_assert(D % (2 * kQuadBatch) == 0, "whole double batches per representative row");
+  int qoff = 0;
+  asm volatile("" : "+s"(qoff));
+  const float heads_f = static_cast<float>(a.heads_per_sel);
+  const int hps = a.heads_per_sel;
+  const int64_t stride = a.rep_stride;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) score[c] = 0.0f;
+  for (int h0 = 0; h0 < hps; h0 += GR) {
+    const int h = a.h_first + h0;
+    const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
+    const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * stride + blk0;
+    float dot[GR][4];
+#pragma unroll
+    for (int j = 0; j < GR; ++j) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dot[j][c] = 0.0f;
+    }
+    f32x4q_t ra[kQuadBatch], rb[kQuadBatch];
+    load_quads(r, stride, 0, ra);
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += 2 * kQuadBatch) {
+      load_quads(r, stride, d0 + kQuadBatch, rb);
+      dot_quads<GR>(q_t, qoff, hps, h0, d0, ra, dot);
+      if (d0 + 2 * kQuadBatch < D) load_quads(r, stride, d0 + 2 * kQuadBatch, ra);
+      dot_quads<GR>(q_t, qoff, hps, h0, d0 + kQuadBatch, rb, dot);
+    }
+#pragma unroll
+    for (int j = 0; j < GR; ++j) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) score[c] = score[c] + dot[j][c] / heads_f;
+    }
+  }
+}
+
+// keys/scores of blocks [0, n), four per lane; the loads of a lane's last
+// quad may cover blocks n..rep_stride-1 (inside the row, discarded).
+template <int GR, int kThreads>
+__device__ inline void score_blocks_quad(const ScoreArgs& a, const float* q_t, int n, uint32_t* keys, float* scores) {
+  for (int blk0 = 4 * threadIdx.x; blk0 < n; blk0 += 4 * kThreads) {
+    float sc[4];
+    score_quad<GR>(a, q_t, blk0, sc);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (blk0 + c < n) {
+        keys[blk0 + c] = order_key(sc[c]);
+        if (scores) scores[blk0 + c] = sc[c];
+      }
+    }
+  }
+}
+
 // keys[blk] = order_key(score of block blk) for blk < n; scores (optional)
 // receives the fp32 scores.  GR = query heads sharing one representative row
 // (the group size when representatives are per KV head, else 1).  q_s must
