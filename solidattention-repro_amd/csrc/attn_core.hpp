@@ -422,8 +422,17 @@ struct WaveState {
     }
     const KStageOffsets ko = k_stage_offsets(v, g, lg);
 
-    float m_lane = kNegInf;  // running max of head column col (same in all 4 row groups)
-    float l_lane = 0.0f;     // this lane's share of the denominator (its 8 tokens per page)
+    // continue from the state in m/l (register layout: every row holds the
+    // running max, row r the denominator share of row group r)
+    float m_lane = m[0];  // running max of head column col (same in all 4 row groups)
+    float l_lane = l[0];  // this lane's share of the denominator (its 8 tokens per page)
+#pragma unroll
+    for (int h = 1; h < G; ++h) {
+      if (hd == h) {
+        m_lane = m[h];
+        l_lane = l[h];
+      }
+    }
     for (int base = start; base < end; base += kWave * step) {
       const int i = base + lane * step;
       PageRef mine{0, 0};

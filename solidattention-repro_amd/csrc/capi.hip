@@ -372,17 +372,22 @@ int sa_hip_score_select_split_preferred(const sa_paged_kv* kv, const sa_select_p
 
 int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv, const sa_select_params* params) {
   if (!kv || !params) return 1;
-  // the fused kernel runs two workgroups per CU; it is the better choice
-  // once it fills the device
-  if (sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups) &&
-      static_cast<int64_t>(kv->batch) * kv->kv_heads >= 2 * static_cast<int64_t>(sa::compute_units()))
+  // the fused kernel (two workgroups per CU, one at 4 query heads per KV
+  // head) is the better choice once it fills the device
+  if (sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups, params->sel_stride,
+                                  kv->reps, kv->rep_stride) &&
+      static_cast<int64_t>(kv->batch) * kv->kv_heads >=
+          sa::select_attend_per_cu(kv->query_heads, kv->kv_heads) * static_cast<int64_t>(sa::compute_units()))
     return 1;
   return sa_hip_attention_splits_for(kv->batch, kv->query_heads, kv->kv_heads, params->budget_blocks + 2);
 }
 
 int sa_hip_select_attend_fused(const sa_paged_kv* kv, const sa_select_params* params, int32_t splits) {
   if (!kv || !params) return 0;
-  return splits == 1 && sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups) ? 1 : 0;
+  return splits == 1 && sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups,
+                                                    params->sel_stride, kv->reps, kv->rep_stride)
+             ? 1
+             : 0;
 }
 
 static sa::SelectAttendLaunch fused_launch(const sa_paged_kv* kv, const sa::SelectLaunch& l, float scale,

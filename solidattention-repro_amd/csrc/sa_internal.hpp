@@ -12,6 +12,7 @@ constexpr int kHeadDim = 128;      // head_dim the tuned kernels are built for
 constexpr int kPartPad = 4;        // floats before the accumulator in a partial record
 constexpr int kMaxSelectBlocks = 8192;
 constexpr int kMaxSelectHeads = 32;
+constexpr int kMaxStagedSelected = 2048;  // selected ids per list the fused kernel at 4 heads per KV head holds
 
 // Partial-result record of one (sequence, KV head, split, query head):
 // [0] running max (log2 domain), [1] denominator, [kPartPad, kPartPad + D)
@@ -150,7 +151,12 @@ struct SelectAttendLaunch {
   int32_t* arrive;
 };
 
-bool select_attend_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups);
+// The fused kernels: 1-2 query heads per KV head (registers), or 4 (LDS-staged
+// pages; sel_stride <= kMaxStagedSelected, reps 8-byte aligned, rep_stride
+// even).  Resident workgroups per CU: 2, or 1 for 4 query heads per KV head.
+bool select_attend_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups, int32_t sel_stride,
+                             const float* reps, int32_t rep_stride);
+int select_attend_per_cu(int32_t query_heads, int32_t kv_heads);
 hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream);
 
 // InfLLM local-causal block representatives of a prefill (contiguous KV).

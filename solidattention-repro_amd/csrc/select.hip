@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   __syncthreads();
   float* scores_row = p.scores ? p.scores + out_row * p.rep_stride : nullptr;
   if constexpr (QUAD) {
-    score_blocks_quad<GR, kThreads>(a, q_s, n, keys, scores_row);
+    score_blocks_vec<GR, 4, kThreads>(a, q_s, n, keys, scores_row, tid);
   } else {
     score_blocks_t<GR, kThreads>(a, q_s, n, keys, scores_row);
   }
@@ -176,13 +176,9 @@ bool wide_select(int64_t workgroups, int64_t blocks) {
   return wide < narrow;
 }
 
-bool quad_layout(const Params& p) {
-  return (reinterpret_cast<uintptr_t>(p.reps) & 15u) == 0 && p.rep_stride % 4 == 0;
-}
-
 template <int GR>
 void launch_gr(const Params& p, dim3 grid, hipStream_t stream) {
-  if (quad_layout(p)) {
+  if (vec_layout<4>(p.reps, p.rep_stride)) {
     // 4 waves score 1024 blocks per pass
     hipLaunchKernelGGL((score_select_kernel<GR, 256, true>), grid, dim3(256), 0, stream, p);
   } else if (wide_select(static_cast<int64_t>(grid.x) * grid.y, p.rep_stride)) {

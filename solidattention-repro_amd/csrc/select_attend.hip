@@ -38,6 +38,7 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int D = kHeadDim;
+constexpr int kStagedIds = kMaxStagedSelected;
 
 struct Params {
   attn::PoolView v;
@@ -267,12 +268,156 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   }
 }
 
+
+// ---- 4 query heads per KV head: LDS-staged pages, q.K on the matrix cores --
+// One 8-wave workgroup per (sequence, KV head), one per CU (the eight 16 KiB
+// page slots).  After append + seal, all 512 threads score two blocks per lane
+// (8-byte representative loads); the keys borrow the page slots of waves 0
+// and 1.  Wave 0 then selects while waves 2..7 attend the last local blocks
+// (selected whatever the scores) through their own slots; then all waves
+// attend the rest of the selected blocks and the tail with the staged walk
+// of attn_core.hpp (pages HBM -> LDS by DMA, q.K on v_mfma_f32_16x16x32_f16).
+template <int GR, bool APPEND, bool F16>
+__global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p) {
+  constexpr int G = 4;
+  constexpr int kStageBytes = kWaves * attn::kStageVecs * 16;
+  constexpr int kPbufFloats = (G * 32 + G + 3) / 4 * 4;
+  static_assert(kMaxSelectBlocks * 4 <= 2 * attn::kStageVecs * 16, "keys fit the page slots of waves 0 and 1");
+  static_assert(sizeof(attn::CombineSmem<G, kWaves>) <= kStageBytes, "combine fits the page slots");
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+
+  __shared__ __align__(16) unsigned char smem[kStageBytes + kWaves * kPbufFloats * 4];
+  __shared__ __align__(16) float q_t[G * D];
+  __shared__ uint32_t hist[256];
+  __shared__ int32_t ids[kStagedIds];
+  __shared__ int s_count;
+  uint32_t* keys = reinterpret_cast<uint32_t*>(smem);
+  uint4* stage = reinterpret_cast<uint4*>(smem) + wave * attn::kStageVecs;
+  float* pbuf = reinterpret_cast<float*>(smem + kStageBytes) + wave * kPbufFloats;
+  const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
+
+  const int64_t out_row = static_cast<int64_t>(b) * p.v.kv_heads + g;
+  int64_t len = p.seq_len[b];
+  int n = p.sealed[b];
+
+  // ---- 1. append + seal (decode step) ---------------------------------------
+  if (APPEND) {
+    const int gen = p.generation ? p.generation[b] : 0;
+    int added = 0;
+    const bool appended = append_seal_head<G, F16>(p, b, g, len, n, added);
+    __syncthreads();  // representatives visible to the scoring below
+    if (tid == 0 && atomicAdd(&p.arrive[b], 1) == p.v.kv_heads - 1) {
+      if (appended) {
+        p.seq_len[b] = static_cast<int32_t>(len);
+        p.sealed[b] = n;
+        if (p.generation) p.generation[b] = gen + added;
+      }
+      p.arrive[b] = 0;
+    }
+  }
+
+  attn::WaveState<G> st;
+  st.reset();
+  const attn::LaneGeom lg = attn::lane_geom(p.v, g, lane);
+
+  // ---- 2. score + select; waves 2.. attend forced local blocks meanwhile -----
+  int pre_pages = 0;  // local blocks [n - pre_pages, n) attended during the selection
+  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) {
+    if (tid == 0) {
+      flag_status(p.v.status, kStatusCapacity);
+      p.counts[out_row] = 0;
+      s_count = 0;
+    }
+  } else {
+    sel::ScoreArgs a{};
+    a.query = p.query;
+    a.reps = p.reps;
+    a.b = b;
+    a.h_first = g * G;
+    a.heads_per_sel = G;
+    a.query_heads = p.query_heads;
+    a.group = G;
+    a.rep_heads = p.rep_heads;
+    a.rep_stride = p.rep_stride;
+    sel::load_query_t<kThreads>(a, q_t);
+    __syncthreads();
+    sel::score_blocks_vec<GR, 2, kThreads>(a, q_t, n, keys, nullptr, tid);
+    __syncthreads();
+    const sel::Budget bs =
+        sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
+    if (bs.bad) {
+      if (tid == 0) {
+        flag_status(p.v.status, kStatusBadBudget);
+        p.counts[out_row] = 0;
+        s_count = 0;
+      }
+    } else {
+      const int local_n = p.local_blocks < n ? p.local_blocks : n;
+      pre_pages = local_n < kWaves - 2 ? local_n : kWaves - 2;
+      if (wave == 0) {
+        uint32_t threshold = 0xffffffffu, equal_take = 0;
+        if (bs.k > 0) sel::radix_threshold_wave(keys, bs, hist, threshold, equal_take);
+        const int count = sel::compact_ids_wave(keys, n, bs, threshold, equal_take,
+                                                p.selected + out_row * p.sel_stride, p.sel_stride, ids);
+        if (lane == 0) {
+          p.counts[out_row] = count;
+          s_count = count;
+        }
+      } else if (wave >= 2 && wave - 2 < pre_pages) {
+        // local block n - pre_pages + (wave - 2), as tail position wave - 2
+        // of a list that ends with block n
+        const attn::PageList Lp{nullptr, static_cast<int64_t>(n) * kPageTokens, n - pre_pages, 0, pre_pages};
+        st.attend_staged_mfma(p.v, b, Lp, wave - 2, pre_pages, kWaves - 2, lg, lane, g, stage, pbuf, q_group,
+                              p.qscale);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. attend the other selected blocks and the tail ---------------------------
+  attn::PageList L{ids, 0, 0, 0, 0};
+  L.len = len;
+  L.sealed = n;
+  L.n_sel = s_count - pre_pages;  // the last pre_pages ids are n - pre_pages .. n - 1, already attended
+  if (L.sealed < 0 || L.len < static_cast<int64_t>(L.sealed) * kPageTokens) {
+    flag_status(p.v.status, kStatusBadLength);
+    if (L.sealed < 0) L.sealed = 0;
+    L.len = static_cast<int64_t>(L.sealed) * kPageTokens;
+  }
+  const int64_t tail_tokens = L.len - static_cast<int64_t>(L.sealed) * kPageTokens;
+  L.total = L.n_sel + static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
+  st.attend_staged_mfma(p.v, b, L, wave, L.total, kWaves, lg, lane, g, stage, pbuf, q_group, p.qscale);
+  __syncthreads();  // every wave is done with its slot before the combine reuses the area
+
+  st.reduce_rows();
+  attn::CombineSmem<G, kWaves>& cs = *reinterpret_cast<attn::CombineSmem<G, kWaves>*>(smem);
+  attn::publish_wave<G, kWaves>(st, cs, wave, lane, lg.row, lg.col);
+  __syncthreads();
+  for (int o = tid; o < G * D; o += kThreads) {
+    const int h = o / D;
+    const int d = o % D;
+    float mx, lw, aw;
+    attn::combine_element<G, kWaves>(cs, h, d, mx, lw, aw);
+    p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
+  }
+}
+
 template <bool APPEND, bool F16>
 hipError_t launch_mode(const Params& p, int batch, hipStream_t stream) {
   const int group = p.query_heads / p.v.kv_heads;
   const bool per_query_reps = p.rep_heads == p.query_heads;
   const dim3 grid(p.v.kv_heads, batch);
-  if (group == 1) {
+  if (group == 4) {
+    if (per_query_reps) {
+      hipLaunchKernelGGL((decode_kernel_staged<1, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((decode_kernel_staged<4, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
+    }
+  } else if (group == 1) {
     hipLaunchKernelGGL((decode_kernel<1, 1, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
   } else if (per_query_reps) {
     hipLaunchKernelGGL((decode_kernel<2, 1, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
@@ -284,13 +429,22 @@ hipError_t launch_mode(const Params& p, int batch, hipStream_t stream) {
 
 }  // namespace
 
-bool select_attend_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups) {
+bool select_attend_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups, int32_t sel_stride,
+                             const float* reps, int32_t rep_stride) {
   const int group = kv_heads > 0 ? query_heads / kv_heads : 0;
-  return select_groups == kv_heads && (group == 1 || group == 2);
+  if (select_groups != kv_heads) return false;
+  if (group == 1 || group == 2) return true;
+  // 4: the selected ids are held in LDS; two-block representative loads
+  return group == 4 && sel_stride <= kStagedIds && sel::vec_layout<2>(reps, rep_stride);
+}
+
+int select_attend_per_cu(int32_t query_heads, int32_t kv_heads) {
+  return kv_heads > 0 && query_heads / kv_heads == 4 ? 1 : 2;
 }
 
 hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream) {
-  if (!select_attend_supported(s.query_heads, s.kv_heads, s.kv_heads)) return hipErrorInvalidValue;
+  if (!select_attend_supported(s.query_heads, s.kv_heads, s.kv_heads, s.sel_stride, s.reps, s.rep_stride))
+    return hipErrorInvalidValue;
   if (s.append && !s.arrive) return hipErrorInvalidValue;
   Params p{};
   p.v.pool = s.pool;

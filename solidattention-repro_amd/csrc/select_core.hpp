@@ -248,91 +248,110 @@ __device__ inline void score_blocks_t(const ScoreArgs& a, const float* q_t, int 
   }
 }
 
-// Four consecutive blocks per lane: one 16-byte load per d fetches the
-// lane's four representative values (rows of rep_stride floats, rep_stride a
-// multiple of 4, reps 16-byte aligned), so a wave reads 1 KiB per load
-// instruction instead of 256 B.  On the Qwen3-8B selection layout (256 lists
-// x 128 rows x 1024 blocks) the loads alone take 18 us this way against
-// 29 us with one block per lane (probe).  Each block's dot is still the
-// sequential fp32 sum over d per head, in the same order: bit-identical
-// scores.  Batches of 8 rows, double-buffered (three batches ahead measured
-// no faster).
-constexpr int kQuadBatch = 8;
-typedef float f32x4q_t __attribute__((ext_vector_type(4)));
+// NB (2 or 4) consecutive blocks per lane: one 8- or 16-byte load per d
+// fetches the lane's NB representative values (rows of rep_stride floats,
+// rep_stride a multiple of NB, reps aligned to 4 NB bytes), so a wave reads
+// 512 B or 1 KiB per load instruction instead of 256 B.  On the Qwen3-8B
+// selection layout (256 lists x 128 rows x 1024 blocks) the loads alone take
+// 18 us with 4 blocks per lane (4 waves per list), 22 us with 2 (8 waves)
+// and 29 us with one (probe).  Each block's dot is still the sequential fp32
+// sum over d per head, in the same order: bit-identical scores.  Batches of
+// 8 rows, double-buffered (three batches ahead measured no faster).
+constexpr int kVecBatch = 8;
 
-__device__ inline void load_quads(const float* r, int64_t stride, int d0, f32x4q_t (&rv)[kQuadBatch]) {
+template <int NB>
+struct RepVec {
+  typedef float type __attribute__((ext_vector_type(NB)));
+};
+
+template <int NB>
+__device__ inline void load_vecs(const float* r, int64_t stride, int d0, typename RepVec<NB>::type (&rv)[kVecBatch]) {
+  typedef typename RepVec<NB>::type vec_t;
 #pragma unroll
-  for (int k = 0; k < kQuadBatch; ++k)
-    rv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4q_t*>(r + static_cast<int64_t>(d0 + k) * stride));
+  for (int k = 0; k < kVecBatch; ++k)
+    rv[k] = __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(r + static_cast<int64_t>(d0 + k) * stride));
 }
 
-template <int GR>
-__device__ inline void dot_quads(const float* q_t, int qoff, int hps, int h0, int d0, const f32x4q_t (&rv)[kQuadBatch],
-                                 float (&dot)[GR][4]) {
+template <int GR, int NB>
+__device__ inline void dot_vecs(const float* q_t, int qoff, int hps, int h0, int d0,
+                                const typename RepVec<NB>::type (&rv)[kVecBatch], float (&dot)[GR][NB]) {
 #pragma unroll
-  for (int k = 0; k < kQuadBatch; ++k) {
+  for (int k = 0; k < kVecBatch; ++k) {
     float qv[GR];
     read_q_t<GR>(q_t + qoff + (d0 + k) * hps + h0, qv);
 #pragma unroll
     for (int j = 0; j < GR; ++j) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dot[j][c] = dot[j][c] + qv[j] * rv[k][c];
+      for (int c = 0; c < NB; ++c) dot[j][c] = dot[j][c] + qv[j] * rv[k][c];
     }
   }
 }
 
-template <int GR>
-__device__ inline void score_quad(const ScoreArgs& a, const float* q_t, int blk0, float (&score)[4]) {
-  static_assert(D % (2 * kQuadBatch) == 0, "whole double batches per representative row");
+template <int GR, int NB>
+__device__ inline void score_vec(const ScoreArgs& a, const float* q_t, int blk0, float (&score)[NB]) {
+  static_assert(D % (2 * kVecBatch) == 0, "whole double batches per representative row");
+  typedef typename RepVec<NB>::type vec_t;
   int qoff = 0;
   asm volatile("" : "+s"(qoff));
   const float heads_f = static_cast<float>(a.heads_per_sel);
-  const int hps = a.heads_per_sel;
-  const int64_t stride = a.rep_stride;
+  // opaque like qoff: with the head count known at compile time (the fused
+  // kernel) the allocator spilled hundreds of registers
+  int hps = a.heads_per_sel;
+  asm volatile("" : "+s"(hps));
+  int64_t stride = a.rep_stride;
+  asm volatile("" : "+s"(stride));
 #pragma unroll
-  for (int c = 0; c < 4; ++c) score[c] = 0.0f;
+  for (int c = 0; c < NB; ++c) score[c] = 0.0f;
   for (int h0 = 0; h0 < hps; h0 += GR) {
     const int h = a.h_first + h0;
     const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
     const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * stride + blk0;
-    float dot[GR][4];
+    float dot[GR][NB];
 #pragma unroll
     for (int j = 0; j < GR; ++j) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dot[j][c] = 0.0f;
+      for (int c = 0; c < NB; ++c) dot[j][c] = 0.0f;
     }
-    f32x4q_t ra[kQuadBatch], rb[kQuadBatch];
-    load_quads(r, stride, 0, ra);
+    vec_t ra[kVecBatch], rb[kVecBatch];
+    load_vecs<NB>(r, stride, 0, ra);
 #pragma unroll
-    for (int d0 = 0; d0 < D; d0 += 2 * kQuadBatch) {
-      load_quads(r, stride, d0 + kQuadBatch, rb);
-      dot_quads<GR>(q_t, qoff, hps, h0, d0, ra, dot);
-      if (d0 + 2 * kQuadBatch < D) load_quads(r, stride, d0 + 2 * kQuadBatch, ra);
-      dot_quads<GR>(q_t, qoff, hps, h0, d0 + kQuadBatch, rb, dot);
+    for (int d0 = 0; d0 < D; d0 += 2 * kVecBatch) {
+      load_vecs<NB>(r, stride, d0 + kVecBatch, rb);
+      dot_vecs<GR, NB>(q_t, qoff, hps, h0, d0, ra, dot);
+      if (d0 + 2 * kVecBatch < D) load_vecs<NB>(r, stride, d0 + 2 * kVecBatch, ra);
+      dot_vecs<GR, NB>(q_t, qoff, hps, h0, d0 + kVecBatch, rb, dot);
     }
 #pragma unroll
     for (int j = 0; j < GR; ++j) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) score[c] = score[c] + dot[j][c] / heads_f;
+      for (int c = 0; c < NB; ++c) score[c] = score[c] + dot[j][c] / heads_f;
     }
   }
 }
 
-// keys/scores of blocks [0, n), four per lane; the loads of a lane's last
-// quad may cover blocks n..rep_stride-1 (inside the row, discarded).
-template <int GR, int kThreads>
-__device__ inline void score_blocks_quad(const ScoreArgs& a, const float* q_t, int n, uint32_t* keys, float* scores) {
-  for (int blk0 = 4 * threadIdx.x; blk0 < n; blk0 += 4 * kThreads) {
-    float sc[4];
-    score_quad<GR>(a, q_t, blk0, sc);
+// keys/scores of blocks [0, n), NB per lane, by the kThreads threads with
+// index tid; the loads of a lane's last group may cover blocks
+// n..rep_stride-1 (inside the row, discarded).
+template <int GR, int NB, int kThreads>
+__device__ inline void score_blocks_vec(const ScoreArgs& a, const float* q_t, int n, uint32_t* keys, float* scores,
+                                        int tid) {
+  for (int blk0 = NB * tid; blk0 < n; blk0 += NB * kThreads) {
+    float sc[NB];
+    score_vec<GR, NB>(a, q_t, blk0, sc);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NB; ++c) {
       if (blk0 + c < n) {
         keys[blk0 + c] = order_key(sc[c]);
         if (scores) scores[blk0 + c] = sc[c];
       }
     }
   }
+}
+
+// The representative layout allows NB-wide loads.
+template <int NB>
+__host__ __device__ inline bool vec_layout(const float* reps, int rep_stride) {
+  return (reinterpret_cast<uintptr_t>(reps) & (4u * NB - 1u)) == 0 && rep_stride % NB == 0;
 }
 
 // keys[blk] = order_key(score of block blk) for blk < n; scores (optional)

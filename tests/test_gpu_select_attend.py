@@ -80,7 +80,8 @@ def close_fp32(a, b):
     assert (err <= 1e-5 + 1e-5 * np.abs(b)).all(), f"max diff {err.max():.3e}"
 
 
-@pytest.mark.parametrize("group,hkv,rep_heads", [(2, 8, None), (2, 8, 16), (1, 8, None), (2, 4, None)])
+@pytest.mark.parametrize("group,hkv,rep_heads", [(2, 8, None), (2, 8, 16), (1, 8, None), (2, 4, None), (4, 8, None),
+                                                 (4, 8, 32), (4, 4, None)])
 def test_fused_shapes(hip, group, hkv, rep_heads):
     print(f"case: group={group} hkv={hkv} rep_heads={rep_heads}", flush=True)
     case = make_case(700 + group + hkv, 4, group * hkv, hkv, [32 * 512 + 7, 32 * 300 + 17, 32 * 64, 32 * 13 + 31],
@@ -89,11 +90,18 @@ def test_fused_shapes(hip, group, hkv, rep_heads):
 
 
 @pytest.mark.parametrize("hq", [32, 64])
-def test_fused_falls_back_for_four_or_eight_heads_per_kv_head(hip, hq):
-    """G=4 (Qwen3-8B shape) and G=8 run as the two launches; results are the
-    same."""
+def test_fused_at_four_fallback_at_eight_heads_per_kv_head(hip, hq):
+    """G=4 (Qwen3-8B shape) runs fused (LDS-staged pages, q.K on the matrix
+    cores); G=8 runs as the two launches; results are the same."""
     case = make_case(710 + hq, 3, hq, 8, [32 * 200 + 3, 32 * 90, 32 * 20 + 1], planted=8)
-    check(hip, case, 32, 2, 4, expect_fused=False)
+    check(hip, case, 32, 2, 4, expect_fused=hq == 32)
+
+
+def test_four_heads_odd_rep_stride_runs_separately(hip):
+    """The fused kernel at G=4 reads two representatives per 8-byte load: an
+    odd rep_stride takes the two launches, with the same results."""
+    case = make_case(709, 2, 32, 8, [32 * 60 + 5, 32 * 33], rep_stride=67, planted=4)
+    check(hip, case, 24, 2, 4, expect_fused=False)
 
 
 def test_fused_split_request_runs_separately(hip):
@@ -101,31 +109,34 @@ def test_fused_split_request_runs_separately(hip):
     check(hip, case, 24, 2, 4, splits=3, expect_fused=False)
 
 
+@pytest.mark.parametrize("hq", [16, 32])
 @pytest.mark.parametrize("lengths", [[5, 31, 32, 33], [32 * 3, 32 * 11 + 2, 32 * 12, 32 * 17 + 31]])
-def test_short_sequences_overlap_and_clamp(hip, lengths):
+def test_short_sequences_overlap_and_clamp(hip, lengths, hq):
     """No sealed block, init/local overlap, budget >= blocks."""
-    print(f"case: lengths={lengths}", flush=True)
-    case = make_case(712, len(lengths), 16, 8, lengths)
+    print(f"case: lengths={lengths} hq={hq}", flush=True)
+    case = make_case(712, len(lengths), hq, 8, lengths)
     check(hip, case, 12, 4, 8)
 
 
-def test_many_blocks_and_ties(hip):
+@pytest.mark.parametrize("hq", [16, 32])
+def test_many_blocks_and_ties(hip, hq):
     """4096 blocks per sequence (several compaction chunks) and quantised
     representatives with many equal scores."""
-    case = make_case(713, 2, 16, 8, [32 * 4096, 32 * 1537 + 9])
+    case = make_case(713, 2, hq, 8, [32 * 4096, 32 * 1537 + 9])
     rng = np.random.default_rng(9)
     case.reps[:] = (rng.integers(-1, 2, size=case.reps.shape) * 0.5).astype(np.float32)
     case.query[:] = (rng.integers(-1, 2, size=case.query.shape) * 0.25).astype(np.float32)
     check(hip, case, 128, 4, 8)
 
 
-def test_stress_budgets_outliers(hip):
+@pytest.mark.parametrize("hq", [16, 32])
+def test_stress_budgets_outliers(hip, hq):
     """Mixed lengths, a shared fragmented pool, per-sequence budgets in
     {16, 64, all blocks} and 1% of tokens at +-60000."""
     rng = np.random.default_rng(714)
     batch = 8
     lengths = (rng.integers(1024, 8192, size=batch) // 32 * 32).astype(np.int64)
-    case = make_case(715, batch, 16, 8, lengths.tolist(), outliers=0.01, spare_pages=64)
+    case = make_case(715, batch, hq, 8, lengths.tolist(), outliers=0.01, spare_pages=64)
     n_blocks = case.sealed.astype(np.int64)
     choice = rng.integers(0, 3, size=batch)
     budgets = np.where(choice == 0, 16, np.where(choice == 1, 64, n_blocks)).astype(np.int32)
@@ -189,7 +200,7 @@ def test_decode_steps_bit_exact(hip, local_tokens, rep_heads, hq):
     case = make_case(720 + local_tokens + hq, 3, hq, 8, [32 * 70 + 30, 32 * 20, 32 * 9 + 13], table_stride=80,
                      local_tokens=local_tokens, rep_heads=rep_heads, planted=4)
     kv = device_kv(case)
-    assert hip.select_attend_fused(kv, 8) == (hq == 16)  # G=4: the three-launch fallback
+    assert hip.select_attend_fused(kv, 8)  # G=2 and G=4 both run as one launch
     ws, _ = hip.decode_step_workspace(kv)
     st = status_tensor()
     rng = np.random.default_rng(11)
@@ -215,12 +226,12 @@ def test_decode_steps_bit_exact(hip, local_tokens, rep_heads, hq):
 
 
 def test_decode_step_f16_and_three_launch_fallback(hip):
-    """Raw FP16 input at G=2 (fused), and G=4 and G=8 (fallback: three
+    """Raw FP16 input at G=2 and G=4 (fused), and G=8 (fallback: three
     launches) give the oracle's state and outputs."""
     for hq, seed in ((16, 730), (32, 731), (64, 733)):
         case = make_case(seed, 2, hq, 8, [32 * 40 + 31, 32 * 12 + 2], table_stride=48)
         kv = device_kv(case)
-        assert hip.select_attend_fused(kv, 8) == (hq == 16)
+        assert hip.select_attend_fused(kv, 8) == (hq in (16, 32))
         ws, _ = hip.decode_step_workspace(kv)
         st = status_tensor()
         rng = np.random.default_rng(seed)
