@@ -30,6 +30,11 @@ HBM_PEAK_GBPS = 8000.0
 PAGE = 32
 D = 128
 
+METRICS = {
+    "qwen3-0.6b-b64-16k": "sparse decode-attn µs/layer + achieved HBM GB/s (Qwen3-0.6B shape, B=64, 16K)",
+    "qwen3-8b-b32-32k": "sparse decode-attn µs/layer + achieved HBM GB/s (Qwen3-8B shape, B=32, 32K)",
+}
+
 CONFIGS = {
     # name: (layers, batch, query_heads, kv_heads, context, budget, init, local, planted, model)
     "qwen3-0.6b-b64-16k": (28, 64, 16, 8, 16384, 64, 4, 8, 8, "Qwen3-0.6B"),
@@ -330,15 +335,19 @@ def main():
         f"event-bracketed append {app_us:.2f} / select {sel_us:.2f} / attention {att_us:.2f} us; "
         f"layer {us_per_layer:.2f} us")
     grp = hq // hkv
-    kernel_name = {1: f"decode_kernel<{grp},{grp},true,false>", 2: f"decode_kernel<{grp},{grp},false,false>",
-                   3: f"sparse_decode_attention_kernel<{grp}>"}[launches]
+    if grp == 4:  # the LDS-staged one-launch kernel (4 query heads per KV head)
+        kernel_name = {1: "decode_kernel_staged<4,true,false>", 2: "decode_kernel_staged<4,false,false>",
+                       3: "sparse_decode_attention_kernel<4>"}[launches]
+    else:
+        kernel_name = {1: f"decode_kernel<{grp},{grp},true,false>", 2: f"decode_kernel<{grp},{grp},false,false>",
+                       3: f"sparse_decode_attention_kernel<{grp}>"}[launches]
     traffic = measured_traffic(args.config, kernel_name)
 
     parity = check_parity(sa, np, torch, L[-1], args, scale, hkv, budget, init, local, last_step)
     cpu = None if args.no_cpu_baseline else cpu_baseline(np, torch, L[0], args, budget, init, local, scale)
 
     line = {
-        "metric": "sparse decode-attn µs/layer + achieved HBM GB/s (Qwen3-0.6B shape, B=64, 16K)",
+        "metric": METRICS[args.config],
         "value": round(us_per_layer, 3),
         "unit": "us/layer",
         "n_gpus": 1,
