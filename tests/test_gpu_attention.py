@@ -43,21 +43,25 @@ def test_paged_group_shapes(hip, group, hkv):
     assert_close_2e3(got, expect)
 
 
+@pytest.mark.parametrize("hq", [16, 32, 64])
 @pytest.mark.parametrize("splits", [1, 2, 3, 8, 33])
-def test_split_counts(hip, splits):
-    print(f"case: splits={splits}", flush=True)
-    case = make_case(20, 2, 16, 8, [32 * 70 + 9, 32 * 33 + 1])
+def test_split_counts(hip, splits, hq):
+    """Query heads per KV head 2 (register pages), 4 and 8 (LDS-staged
+    pages, q.K on the matrix cores) under every split count."""
+    print(f"case: splits={splits} hq={hq}", flush=True)
+    case = make_case(20, 2, hq, 8, [32 * 70 + 9, 32 * 33 + 1])
     got, expect = run_case(hip, case, 8, 20, 2, 4, splits=splits)
     assert_close_2e3(got, expect)
 
 
+@pytest.mark.parametrize("hq", [16, 32, 64])
 @pytest.mark.parametrize("chunk,max_chunks", [(1, 200), (4, 3), (5, 9), (16, 8), (64, 2)])
-def test_chunked_pages(hip, chunk, max_chunks):
+def test_chunked_pages(hip, chunk, max_chunks, hq):
     """Lists of 41, 4, 34 and 1 pages cut into chunks: one page per chunk,
     a last chunk taking the remainder beyond max_chunks * chunk, chunks
     past the end of short lists, and a chunk longer than every list."""
-    print(f"case: chunk={chunk} max_chunks={max_chunks}", flush=True)
-    case = make_case(24, 4, 16, 8, [32 * 70 + 9, 32 * 3 + 5, 32 * 33 + 1, 31], planted=2)
+    print(f"case: chunk={chunk} max_chunks={max_chunks} hq={hq}", flush=True)
+    case = make_case(24, 4, hq, 8, [32 * 70 + 9, 32 * 3 + 5, 32 * 33 + 1, 31], planted=2)
     got, expect = run_case(hip, case, 8, 40, 1, 2, chunk=(chunk, max_chunks))
     assert_close_2e3(got, expect)
 
@@ -174,6 +178,21 @@ def test_contiguous_lengths(hip, tokens):
     assert_close_2e3(out.cpu().numpy(), expect)
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 8), (16, 2)])
+@pytest.mark.parametrize("tokens", [1, 33, 1000, 4096])
+def test_contiguous_group_sizes(hip, tokens, hq, hkv):
+    """Contiguous buffers at 4 and 8 query heads per KV head: full pages
+    staged through LDS, a partial last page spread over the waves."""
+    print(f"case: tokens={tokens} hq={hq} hkv={hkv}", flush=True)
+    rng = np.random.default_rng(tokens + hq)
+    kv = rng.standard_normal(tokens * 2 * hkv * 128).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(hq * 128).astype(np.float32)
+    expect = O.attention_reference(kv, q, tokens, hq, hkv, 128, SCALE)
+    out = hip.attention_contiguous(to_dev(kv.view(np.int16)).view(torch.uint16), to_dev(q), tokens, hq, hkv, SCALE)
+    torch.cuda.synchronize()
+    assert_close_2e3(out.cpu().numpy(), expect)
+
+
 def test_bad_page_is_flagged_not_read(hip):
     case = make_case(46, 1, 16, 8, [32 * 8])
     sel = np.zeros((1, 8, 4), np.int32)
@@ -187,14 +206,16 @@ def test_bad_page_is_flagged_not_read(hip):
     assert int(st.item()) & hip.STATUS_BAD_PAGE
 
 
-def test_split_phase_partial_and_merge(hip):
+@pytest.mark.parametrize("hq", [16, 32, 64])
+def test_split_phase_partial_and_merge(hip, hq):
     """Hits-first schedule: attend one part of the selection (with the tail),
     then the rest, then merge; equals attention over the whole selection."""
-    case = make_case(47, 3, 16, 8, [32 * 60 + 7, 32 * 41, 32 * 80 + 31])
-    sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, 3, 16, 8, D, 8, case.rep_stride, 8, 24, 2,
+    print(f"case: hq={hq}", flush=True)
+    case = make_case(47, 3, hq, 8, [32 * 60 + 7, 32 * 41, 32 * 80 + 31])
+    sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, 3, hq, 8, D, 8, case.rep_stride, 8, 24, 2,
                                     3)
     expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, sel, cnt, 8,
-                                      case.query, 3, 16, 8, D, SCALE)
+                                      case.query, 3, hq, 8, D, SCALE)
     # split every (seq, group) list into its even and odd positions
     first = np.full_like(sel, -1)
     second = np.full_like(sel, -1)
@@ -214,7 +235,7 @@ def test_split_phase_partial_and_merge(hip):
     st = status_tensor()
     hip.sparse_decode_attention_partial(kv, q, to_dev(first), to_dev(c1), SCALE, True, ws, 0, 2, total, status=st)
     hip.sparse_decode_attention_partial(kv, q, to_dev(second), to_dev(c2), SCALE, False, ws, 2, 1, total, status=st)
-    out = torch.empty((3, 16, D), dtype=torch.float32, device="cuda")
+    out = torch.empty((3, hq, D), dtype=torch.float32, device="cuda")
     hip.attention_merge(kv, ws, total, out)
     torch.cuda.synchronize()
     assert int(st.item()) == 0
