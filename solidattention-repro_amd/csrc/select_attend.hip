@@ -39,6 +39,7 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int D = kHeadDim;
 constexpr int kStagedIds = kMaxStagedSelected;
+constexpr int kMaxPrePages = kWaves - 1;  // forced blocks attended during the selection (G = 4)
 
 struct Params {
   attn::PoolView v;
@@ -215,11 +216,8 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
       const int local_n = p.local_blocks < n ? p.local_blocks : n;
       pre_pages = local_n < kWaves - 1 ? local_n : kWaves - 1;
       if (wave == 0) {
-        uint32_t threshold = 0xffffffffu, equal_take = 0;
-        if (bs.k > 0) sel::radix_threshold_wave(keys, bs, hist, threshold, equal_take);
-        const int count = sel::compact_ids_wave(keys, n, bs, threshold, equal_take,
-                                                p.selected + out_row * p.sel_stride, p.sel_stride,
-                                                reinterpret_cast<int32_t*>(keys));
+        const int count = sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride,
+                                               p.sel_stride, reinterpret_cast<int32_t*>(keys));
         if (lane == 0) {
           p.counts[out_row] = count;
           s_count = count;
@@ -273,10 +271,12 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
 // One 8-wave workgroup per (sequence, KV head), one per CU (the eight 16 KiB
 // page slots).  After append + seal, all 512 threads score two blocks per lane
 // (8-byte representative loads); the keys borrow the page slots of waves 0
-// and 1.  Wave 0 then selects while waves 2..7 attend the last local blocks
-// (selected whatever the scores) through their own slots; then all waves
-// attend the rest of the selected blocks and the tail with the staged walk
-// of attn_core.hpp (pages HBM -> LDS by DMA, q.K on v_mfma_f32_16x16x32_f16).
+// and 1.  Wave 0 then selects while waves 1..7 (2..7 when the keys reach into
+// wave 1's slot) attend one forced block each (the last local blocks, then
+// init blocks: selected whatever the scores) through their own slots; then
+// all waves attend the rest of the selected blocks and the tail
+// with the staged walk of attn_core.hpp (pages HBM -> LDS by DMA, q.K on
+// v_mfma_f32_16x16x32_f16).
 template <int GR, bool APPEND, bool F16>
 __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p) {
   constexpr int G = 4;
@@ -294,6 +294,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   __shared__ __align__(16) float q_t[G * D];
   __shared__ uint32_t hist[256];
   __shared__ int32_t ids[kStagedIds];
+  __shared__ int32_t pre_ids[kMaxPrePages];
   __shared__ int s_count;
   uint32_t* keys = reinterpret_cast<uint32_t*>(smem);
   uint4* stage = reinterpret_cast<uint4*>(smem) + wave * attn::kStageVecs;
@@ -324,8 +325,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   st.reset();
   const attn::LaneGeom lg = attn::lane_geom(p.v, g, lane);
 
-  // ---- 2. score + select; waves 2.. attend forced local blocks meanwhile -----
-  int pre_pages = 0;  // local blocks [n - pre_pages, n) attended during the selection
+  // ---- 2. score + select; waves 1.. attend forced blocks meanwhile -----------
+  // pre_init init blocks [0, pre_init) and pre_local local blocks
+  // [n - pre_local, n) are attended during the selection: in the ascending
+  // selection they are the first pre_init and the last pre_local ids.
+  int pre_init = 0, pre_local = 0;
   if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) {
     if (tid == 0) {
       flag_status(p.v.status, kStatusCapacity);
@@ -346,9 +350,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
     sel::load_query_t<kThreads>(a, q_t);
     __syncthreads();
     sel::score_blocks_vec<GR, 2, kThreads>(a, q_t, n, keys, nullptr, tid);
-    __syncthreads();
     const sel::Budget bs =
         sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
+    // one forced page per wave that has a free slot: wave 1's slot is free
+    // unless the keys (4 bytes per block) reach into it (a second page per
+    // wave measured slower: each wave keeps one page in flight, so it costs a
+    // whole load latency while the selection has already ended)
+    const int pre_first = n * 4 <= attn::kStageVecs * 16 ? 1 : 2;
+    const int pre_cap = kWaves - pre_first;
+    if (!bs.bad) {
+      // local blocks not already init blocks, then init blocks
+      const int local_n = n - (bs.local_first > bs.init_n ? bs.local_first : bs.init_n);
+      pre_local = local_n < pre_cap ? local_n : pre_cap;
+      pre_init = bs.init_n < pre_cap - pre_local ? bs.init_n : pre_cap - pre_local;
+      if (tid < pre_init + pre_local) pre_ids[tid] = tid < pre_init ? tid : n - pre_local + (tid - pre_init);
+    }
+    __syncthreads();  // keys and pre_ids visible
     if (bs.bad) {
       if (tid == 0) {
         flag_status(p.v.status, kStatusBadBudget);
@@ -356,33 +373,29 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
         s_count = 0;
       }
     } else {
-      const int local_n = p.local_blocks < n ? p.local_blocks : n;
-      pre_pages = local_n < kWaves - 2 ? local_n : kWaves - 2;
+      const int pre_pages = pre_init + pre_local;
       if (wave == 0) {
-        uint32_t threshold = 0xffffffffu, equal_take = 0;
-        if (bs.k > 0) sel::radix_threshold_wave(keys, bs, hist, threshold, equal_take);
-        const int count = sel::compact_ids_wave(keys, n, bs, threshold, equal_take,
-                                                p.selected + out_row * p.sel_stride, p.sel_stride, ids);
+        const int count =
+            sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride, p.sel_stride, ids);
         if (lane == 0) {
           p.counts[out_row] = count;
           s_count = count;
         }
-      } else if (wave >= 2 && wave - 2 < pre_pages) {
-        // local block n - pre_pages + (wave - 2), as tail position wave - 2
-        // of a list that ends with block n
-        const attn::PageList Lp{nullptr, static_cast<int64_t>(n) * kPageTokens, n - pre_pages, 0, pre_pages};
-        st.attend_staged_mfma(p.v, b, Lp, wave - 2, pre_pages, kWaves - 2, lg, lane, g, stage, pbuf, q_group,
-                              p.qscale);
+      } else if (wave >= pre_first && wave - pre_first < pre_pages) {
+        const attn::PageList Lp{pre_ids, static_cast<int64_t>(n) * kPageTokens, n, pre_pages, pre_pages};
+        st.attend_staged_mfma(p.v, b, Lp, wave - pre_first, pre_pages, kWaves - pre_first, lg, lane, g, stage,
+                              pbuf, q_group, p.qscale);
       }
     }
   }
   __syncthreads();
 
   // ---- 3. attend the other selected blocks and the tail ---------------------------
-  attn::PageList L{ids, 0, 0, 0, 0};
+  attn::PageList L{ids + pre_init, 0, 0, 0, 0};
   L.len = len;
   L.sealed = n;
-  L.n_sel = s_count - pre_pages;  // the last pre_pages ids are n - pre_pages .. n - 1, already attended
+  L.n_sel = s_count - pre_init - pre_local;
+  if (L.n_sel < 0) L.n_sel = 0;
   if (L.sealed < 0 || L.len < static_cast<int64_t>(L.sealed) * kPageTokens) {
     flag_status(p.v.status, kStatusBadLength);
     if (L.sealed < 0) L.sealed = 0;

@@ -13,7 +13,9 @@
 //
 // Selection: scores become order-preserving 32-bit keys (with -0.0 folded
 // onto +0.0, since the reference's `>` comparator treats them as equal).  A
-// 4-pass 8-bit radix select finds the key T of the k-th best candidate; all
+// 4-pass 8-bit radix select (or, for one wave and up to 1024 blocks, a
+// bit-by-bit search over keys held in registers) finds the key T of the k-th
+// best candidate; all
 // candidates above T are taken plus the lowest-id candidates equal to T, which
 // is exactly what a stable descending sort followed by a greedy fill picks
 // (selection.cpp:128-142).  Output ids are compacted in ascending order with
@@ -623,6 +625,126 @@ __device__ inline int compact_ids_wave(const uint32_t* keys, int n, const Budget
     written += __popcll(m_take);
   }
   return written < sel_stride ? written : sel_stride;
+}
+
+// ---- single-wave selection with the keys in registers (n <= 64 NC) ----------
+// Lane l holds the keys of blocks l + 64 i (i < NC), each key that is not a
+// dynamic candidate replaced by 0, so one LDS read per key is all the LDS
+// traffic.  The k-th largest candidate key T is built from the top bit down:
+// T takes bit b when at least k candidates have keys >= T | 2^b, counted with
+// one wave ballot per register and scalar popcounts.  Every test value is
+// >= 1, so the masked zeros are never counted and a candidate whose key is 0
+// is ranked correctly.  The take and the ascending compaction are those of
+// compact_ids_wave.
+//
+// The compares of eight (or four) registers are issued back to back (one asm
+// block) before their scalar popcounts: compiled from ballots, each popcount
+// directly followed the compare it reads and waited out the vector pipeline
+// (about 500 cycles per step against 290 so, measured at 16 registers).
+__device__ inline int count_at_least8(uint32_t x, const uint32_t* k) {
+  uint64_t m0, m1, m2, m3, m4, m5, m6, m7;
+  asm volatile(
+      "v_cmp_le_u32_e64 %0, %8, %9\n"
+      "v_cmp_le_u32_e64 %1, %8, %10\n"
+      "v_cmp_le_u32_e64 %2, %8, %11\n"
+      "v_cmp_le_u32_e64 %3, %8, %12\n"
+      "v_cmp_le_u32_e64 %4, %8, %13\n"
+      "v_cmp_le_u32_e64 %5, %8, %14\n"
+      "v_cmp_le_u32_e64 %6, %8, %15\n"
+      "v_cmp_le_u32_e64 %7, %8, %16\n"
+      : "=&s"(m0), "=&s"(m1), "=&s"(m2), "=&s"(m3), "=&s"(m4), "=&s"(m5), "=&s"(m6), "=&s"(m7)
+      : "s"(x), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(k[4]), "v"(k[5]), "v"(k[6]), "v"(k[7]));
+  return __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3) + __popcll(m4) + __popcll(m5) + __popcll(m6) +
+         __popcll(m7);
+}
+
+__device__ inline int count_at_least4(uint32_t x, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t k3) {
+  uint64_t m0, m1, m2, m3;
+  asm volatile(
+      "v_cmp_le_u32_e64 %0, %4, %5\n"
+      "v_cmp_le_u32_e64 %1, %4, %6\n"
+      "v_cmp_le_u32_e64 %2, %4, %7\n"
+      "v_cmp_le_u32_e64 %3, %4, %8\n"
+      : "=&s"(m0), "=&s"(m1), "=&s"(m2), "=&s"(m3)
+      : "s"(x), "v"(k0), "v"(k1), "v"(k2), "v"(k3));
+  return __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
+}
+
+template <int NC>
+__device__ inline int count_at_least(const uint32_t (&kr)[NC], uint32_t x) {
+  static_assert(NC % 4 == 0, "keys per lane in fours");
+  int c = 0;
+#pragma unroll
+  for (int i = 0; i + 8 <= NC; i += 8) c += count_at_least8(x, kr + i);
+  if constexpr (NC % 8 != 0) c += count_at_least4(x, kr[NC - 4], kr[NC - 3], kr[NC - 2], kr[NC - 1]);
+  return c;
+}
+
+// keys must hold at least 64 NC entries (entries past n are read, not used).
+template <int NC>
+__device__ inline int select_ids_wave_regs(const uint32_t* keys, int n, const Budget& bs, int32_t* out_ids,
+                                           int sel_stride, int32_t* lds_ids) {
+  const int lane = threadIdx.x % kWave;
+  const bool dynamic = bs.k > 0 && !bs.take_all;
+  uint32_t kr[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) kr[i] = keys[i * kWave + lane];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int blk = i * kWave + lane;
+    const bool cand = dynamic && blk >= bs.init_n && blk < bs.local_first;
+    kr[i] = cand ? kr[i] : 0u;
+  }
+  uint32_t threshold = 0xffffffffu;
+  int equal_take = 0;
+  if (dynamic) {
+    uint32_t t = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t c = t | (1u << bit);
+      if (count_at_least<NC>(kr, c) >= bs.k) t = c;
+    }
+    threshold = t;
+    equal_take = bs.k - (t == 0xffffffffu ? 0 : count_at_least<NC>(kr, t + 1u));
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  int taken_eq = 0, written = 0;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int blk = i * kWave + lane;
+    const bool valid = blk < n;
+    const bool is_forced = valid && (bs.take_all || blk < bs.init_n || blk >= bs.local_first);
+    const bool cand = valid && !is_forced && dynamic;
+    const bool is_eq = cand && kr[i] == threshold;
+    const bool sure = is_forced || (cand && kr[i] > threshold);
+    const uint64_t m_eq = __ballot(is_eq);
+    const int eq_rank = taken_eq + __popcll(m_eq & below);
+    const bool take = sure || (is_eq && eq_rank < equal_take);
+    const uint64_t m_take = __ballot(take);
+    const int pos = written + __popcll(m_take & below);
+    if (take && pos < sel_stride) {
+      out_ids[pos] = blk;
+      lds_ids[pos] = blk;
+    }
+    taken_eq += __popcll(m_eq);
+    written += __popcll(m_take);
+  }
+  return written < sel_stride ? written : sel_stride;
+}
+
+// Single-wave selection of one list: forced blocks plus the k best
+// candidates (lowest id first among equal keys), ids ascending into out_ids
+// and lds_ids (which may alias keys).  Up to 1024 blocks the keys are held in
+// registers (keys must hold 1024 entries); longer lists take the LDS radix
+// select.  Returns the count.
+__device__ inline int select_ids_wave(const uint32_t* keys, int n, const Budget& bs, uint32_t* hist,
+                                      int32_t* out_ids, int sel_stride, int32_t* lds_ids) {
+  if (n <= 4 * kWave) return select_ids_wave_regs<4>(keys, n, bs, out_ids, sel_stride, lds_ids);
+  if (n <= 8 * kWave) return select_ids_wave_regs<8>(keys, n, bs, out_ids, sel_stride, lds_ids);
+  if (n <= 12 * kWave) return select_ids_wave_regs<12>(keys, n, bs, out_ids, sel_stride, lds_ids);
+  if (n <= 16 * kWave) return select_ids_wave_regs<16>(keys, n, bs, out_ids, sel_stride, lds_ids);
+  uint32_t threshold = 0xffffffffu, equal_take = 0;
+  if (bs.k > 0) radix_threshold_wave(keys, bs, hist, threshold, equal_take);
+  return compact_ids_wave(keys, n, bs, threshold, equal_take, out_ids, sel_stride, lds_ids);
 }
 
 }  // namespace sel

@@ -129,6 +129,29 @@ def test_many_blocks_and_ties(hip, hq):
     check(hip, case, 128, 4, 8)
 
 
+def test_four_heads_keys_past_first_slot(hip):
+    """4 query heads per KV head with 5000 sealed blocks: the keys (20 KB)
+    reach into the second page slot, so that slot's wave stays out of the
+    forced-block walk during the selection."""
+    case = make_case(717, 2, 8, 2, [32 * 5000 + 7, 32 * 4096 + 31], planted=4)
+    check(hip, case, 64, 4, 8)
+
+
+@pytest.mark.parametrize("hq", [16, 32])
+@pytest.mark.parametrize("lengths", [[32 * 256 + 5, 32 * 257, 32 * 512, 32 * 513 + 1],
+                                     [32 * 768 + 31, 32 * 1024 + 1, 32 * 1025]])
+def test_list_length_boundaries_with_ties(hip, lengths, hq):
+    """Lists of 256, 257, 512, 513, 768, 1024 and 1025 blocks (the edges of
+    the one-wave selection's 4/8/12/16 keys per lane and its LDS fallback)
+    with quantised scores: many equal keys at the threshold, many zeros."""
+    print(f"case: lengths={lengths} hq={hq}", flush=True)
+    case = make_case(714, len(lengths), hq, 8, lengths)
+    rng = np.random.default_rng(14)
+    case.reps[:] = (rng.integers(-1, 2, size=case.reps.shape) * 0.5).astype(np.float32)
+    case.query[:] = (rng.integers(-1, 2, size=case.query.shape) * 0.25).astype(np.float32)
+    check(hip, case, 64, 4, 8)
+
+
 @pytest.mark.parametrize("hq", [16, 32])
 def test_stress_budgets_outliers(hip, hq):
     """Mixed lengths, a shared fragmented pool, per-sequence budgets in
