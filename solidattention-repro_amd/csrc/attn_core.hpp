@@ -600,6 +600,61 @@ __device__ inline void publish_wave(const WaveState<G>& st, CombineSmem<G, W>& c
   }
 }
 
+// The same combination without the cross-row shuffles of reduce_rows(): every
+// lane publishes its own row's share (two 16-byte LDS writes per head) and
+// the combine adds the kRows shares of each wave.  For the staged walk, whose
+// rows all keep the same running max; 4x the LDS of CombineSmem.
+template <int G, int W>
+struct CombineRowsSmem {
+  float m[W][G];
+  float l[W][kRows][G];
+  float acc[W][kRows][G][D];
+};
+
+template <int G, int W>
+__device__ inline void publish_wave_rows(const WaveState<G>& st, CombineRowsSmem<G, W>& cs, int wave, int row,
+                                         int col) {
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float4* dst = reinterpret_cast<float4*>(&cs.acc[wave][row][h][col * 8]);
+    dst[0] = make_float4(st.acc[h][0], st.acc[h][1], st.acc[h][2], st.acc[h][3]);
+    dst[1] = make_float4(st.acc[h][4], st.acc[h][5], st.acc[h][6], st.acc[h][7]);
+  }
+  if (col == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      cs.l[wave][row][h] = st.l[h];
+      if (row == 0) cs.m[wave][h] = st.m[h];
+    }
+  }
+}
+
+template <int G, int W>
+__device__ inline void combine_element_rows(const CombineRowsSmem<G, W>& cs, int h, int d, float& mx, float& lw,
+                                            float& aw) {
+  mx = kNegInf;
+#pragma unroll
+  for (int w = 0; w < W; ++w) mx = fmaxf(mx, cs.m[w][h]);
+  lw = 0.0f;
+  aw = 0.0f;
+  if (mx != kNegInf) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float mw = cs.m[w][h];
+      if (mw == kNegInf) continue;
+      const float f = __builtin_amdgcn_exp2f(mw - mx);
+      float lr = 0.0f, ar = 0.0f;
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        lr += cs.l[w][r][h];
+        ar += cs.acc[w][r][h][d];
+      }
+      lw = __builtin_fmaf(lr, f, lw);
+      aw = __builtin_fmaf(ar, f, aw);
+    }
+  }
+}
+
 // Log-sum-exp combination of the W waves for head h, dim d: returns the
 // merged max (log2 domain), denominator and accumulator.
 template <int G, int W>

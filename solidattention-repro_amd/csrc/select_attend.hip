@@ -283,7 +283,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   constexpr int kStageBytes = kWaves * attn::kStageVecs * 16;
   constexpr int kPbufFloats = (G * 32 + G + 3) / 4 * 4;
   static_assert(kMaxSelectBlocks * 4 <= 2 * attn::kStageVecs * 16, "keys fit the page slots of waves 0 and 1");
-  static_assert(sizeof(attn::CombineSmem<G, kWaves>) <= kStageBytes, "combine fits the page slots");
+  static_assert(sizeof(attn::CombineRowsSmem<G, kWaves>) <= kStageBytes, "combine fits the page slots");
   const int g = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
@@ -406,15 +406,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   st.attend_staged_mfma(p.v, b, L, wave, L.total, kWaves, lg, lane, g, stage, pbuf, q_group, p.qscale);
   __syncthreads();  // every wave is done with its slot before the combine reuses the area
 
-  st.reduce_rows();
-  attn::CombineSmem<G, kWaves>& cs = *reinterpret_cast<attn::CombineSmem<G, kWaves>*>(smem);
-  attn::publish_wave<G, kWaves>(st, cs, wave, lane, lg.row, lg.col);
+  attn::CombineRowsSmem<G, kWaves>& cs = *reinterpret_cast<attn::CombineRowsSmem<G, kWaves>*>(smem);
+  attn::publish_wave_rows<G, kWaves>(st, cs, wave, lg.row, lg.col);
   __syncthreads();
   for (int o = tid; o < G * D; o += kThreads) {
     const int h = o / D;
     const int d = o % D;
     float mx, lw, aw;
-    attn::combine_element<G, kWaves>(cs, h, d, mx, lw, aw);
+    attn::combine_element_rows<G, kWaves>(cs, h, d, mx, lw, aw);
     p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
   }
 }
