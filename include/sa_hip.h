@@ -283,6 +283,34 @@ int sa_hip_decode_step_f16(const sa_paged_kv* kv, const uint16_t* k,
                            size_t workspace_bytes, int32_t splits,
                            int32_t* status, void* stream);
 
+/* Static scratch of sa_hip_decode_step_noalloc, per GPU: the first
+ * SA_HIP_NOALLOC_COUNTER_BYTES hold the arrival counters (one per sequence,
+ * any batch up to 65535), the rest the attention's split records. */
+#define SA_HIP_NOALLOC_SCRATCH_BYTES (4u << 20)
+#define SA_HIP_NOALLOC_COUNTER_BYTES (256u << 10)
+
+/* sa_hip_decode_step (fp32 k/v) without a workspace argument, allocating
+ * nothing: no hipMalloc, hipFree or allocating library call on any call.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Its scratch is a static device array of
+ * SA_HIP_NOALLOC_SCRATCH_BYTES on each GPU the library runs on, held until
+ * the process ends; its device address is looked up on the first call on a
+ * device.  The arrival counters are cleared by a small kernel on `stream`
+ * before every fused launch.  Limit: launches whose split records
+ * (sa_hip_decode_step_workspace_bytes(kv, splits) minus the counters) exceed
+ * SA_HIP_NOALLOC_SCRATCH_BYTES - SA_HIP_NOALLOC_COUNTER_BYTES are refused
+ * with SA_HIP_EINVAL (the fused launch, splits == 1, needs no records).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (unordered streams, or host threads) race and give wrong results; order
+ * them on one stream.  Results equal sa_hip_decode_step's. */
+int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k,
+                               const float* v, int32_t local_tokens,
+                               const float* query,
+                               const sa_select_params* params, float scale,
+                               int32_t* selected, int32_t* counts, float* out,
+                               int32_t splits, int32_t* status, void* stream);
+
 /* ---- R8/R9/R4: decode append, seal, representative ---------------------- */
 
 /* Append one token per sequence at position seq_len[b] (fp32 K/V converted

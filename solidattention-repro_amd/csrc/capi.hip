@@ -1,6 +1,7 @@
 // capi.hip — the extern "C" boundary (include/sa_hip.h): argument
 // validation, error strings, launch dispatch.  Hot entry points allocate
-// nothing; scratch comes in through workspace arguments.
+// nothing; scratch comes in through workspace arguments, or for
+// sa_hip_decode_step_noalloc from the static `scratch` array below.
 #include "sa_hip.h"
 #include "sa_internal.hpp"
 
@@ -11,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -74,6 +76,53 @@ int report_error(int code, const char* message) {
   return code;
 }
 }  // namespace sa
+
+// ---- scratch of the allocation-free decode step (sa_hip_decode_step_noalloc) ----
+// One array per GPU, held until the process ends: kNoallocCounterBytes of
+// arrival counters (65535 sequences, the batch limit) at the front, split
+// records of the unfused launches after them.  In host code `scratch` is a
+// host-side stand-in, never a device address: the device address comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+static constexpr size_t kNoallocScratchBytes = SA_HIP_NOALLOC_SCRATCH_BYTES;
+static constexpr size_t kNoallocCounterBytes = SA_HIP_NOALLOC_COUNTER_BYTES;
+static_assert(kNoallocCounterBytes >= 65535 * sizeof(int32_t), "a counter for every sequence of a batch");
+static_assert(kNoallocScratchBytes > kNoallocCounterBytes, "room for split records");
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+// Zeroes the arrival counters with vector stores (a kernel, not
+// hipMemsetAsync, so that a captured graph holds no memset node).
+__global__ void clear_counters_kernel(int32_t* counters, int32_t n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) counters[i] = 0;
+}
+
+namespace {
+
+constexpr int kNoallocMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kNoallocMaxDevices];  // device address of `scratch` per device
+
+// The device address of the current device's `scratch`, looked up on the
+// first call on that device (with the device current) and kept.
+int noalloc_scratch(void** out, const char* op) {
+  int dev = -1;
+  if (int e = check_hip(hipGetDevice(&dev), "decode_step_noalloc: hipGetDevice")) return e;
+  if (dev < 0 || dev >= kNoallocMaxDevices)
+    return fail(SA_HIP_EINVAL, "%s: device %d beyond the %d devices the scratch table holds", op, dev,
+                kNoallocMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    if (int e = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "decode_step_noalloc: hipGetSymbolAddress"))
+      return e;
+    if (!p) return fail(SA_HIP_ERUNTIME, "%s: no device address for the scratch array", op);
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return SA_HIP_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -448,11 +497,15 @@ size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv, int32_t splits)
          sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
 }
 
-static int decode_step_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
-                              const uint16_t* v16, int32_t local_tokens, const float* query,
-                              const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
-                              float* out, void* workspace, size_t workspace_bytes, int32_t splits, int32_t* status,
-                              void* stream, const char* op) {
+// The decode step on explicit scratch: `arrive` holds kv->batch arrival
+// counters, zero on entry to the fused launch, which leaves them at zero
+// (clear_arrive: zeroed here first, whatever they hold); `records` the
+// attention's split records of the unfused launches (records_bytes of them).
+static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
+                           const uint16_t* v16, int32_t local_tokens, const float* query,
+                           const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
+                           float* out, int32_t* arrive, bool clear_arrive, void* records, size_t records_bytes,
+                           int32_t splits, int32_t* status, void* stream, const char* op) {
   sa::SelectLaunch l;
   if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, op, &l)) return e;
   if (!out) return fail(SA_HIP_EINVAL, "%s: null out", op);
@@ -463,17 +516,12 @@ static int decode_step_common(const sa_paged_kv* kv, const float* k, const float
   const void* va = v16 ? static_cast<const void*>(v16) : static_cast<const void*>(v);
   if (!ka || !va) return fail(SA_HIP_EINVAL, "%s: null k/v", op);
   if (!aligned16(ka) || !aligned16(va)) return fail(SA_HIP_EINVAL, "%s: k/v must be 16-byte aligned", op);
-  const size_t need = sa_hip_decode_step_workspace_bytes(kv, splits);
-  if (!workspace || workspace_bytes < need)
-    return fail(SA_HIP_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, need, workspace_bytes);
-  if (!aligned16(workspace)) return fail(SA_HIP_EINVAL, "%s: workspace must be 16-byte aligned", op);
-  const size_t ab = arrive_bytes(kv->batch);
   if (!sa_hip_select_attend_fused(kv, params, splits)) {
     if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op)) return e;
     if (int e = check_hip(sa::launch_score_select(l, as_stream(stream)), "decode_step: score_select launch"))
       return e;
     return attention_common(kv, query, selected, counts, params->select_groups, params->sel_stride, scale, out,
-                            static_cast<uint8_t*>(workspace) + ab, workspace_bytes - ab, splits, status, stream, 0);
+                            records, records_bytes, splits, status, stream, 0);
   }
   sa::SelectAttendLaunch f = fused_launch(kv, l, scale, out);
   f.append = 1;
@@ -482,8 +530,29 @@ static int decode_step_common(const sa_paged_kv* kv, const float* k, const float
   f.v = v;
   f.k16 = k16;
   f.v16 = v16;
-  f.arrive = static_cast<int32_t*>(workspace);
+  f.arrive = arrive;
+  if (clear_arrive) {
+    hipLaunchKernelGGL(clear_counters_kernel, dim3((kv->batch + 255) / 256), dim3(256), 0, as_stream(stream),
+                       arrive, kv->batch);
+    if (int e = check_hip(hipGetLastError(), "decode_step: counter clear launch")) return e;
+  }
   return check_hip(sa::launch_select_attend(f, as_stream(stream)), "decode_step launch");
+}
+
+static int decode_step_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
+                              const uint16_t* v16, int32_t local_tokens, const float* query,
+                              const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
+                              float* out, void* workspace, size_t workspace_bytes, int32_t splits, int32_t* status,
+                              void* stream, const char* op) {
+  if (!kv || kv->batch <= 0) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv or empty batch", op);
+  const size_t need = sa_hip_decode_step_workspace_bytes(kv, splits);
+  if (!workspace || workspace_bytes < need)
+    return fail(SA_HIP_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, need, workspace_bytes);
+  if (!aligned16(workspace)) return fail(SA_HIP_EINVAL, "%s: workspace must be 16-byte aligned", op);
+  const size_t ab = arrive_bytes(kv->batch);
+  return decode_step_run(kv, k, v, k16, v16, local_tokens, query, params, scale, selected, counts, out,
+                         static_cast<int32_t*>(workspace), false, static_cast<uint8_t*>(workspace) + ab,
+                         workspace_bytes - ab, splits, status, stream, op);
 }
 
 int sa_hip_decode_step(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
@@ -501,6 +570,28 @@ int sa_hip_decode_step_f16(const sa_paged_kv* kv, const uint16_t* k, const uint1
   if (!k || !v) return fail(SA_HIP_EINVAL, "decode_step_f16: null k/v");
   return decode_step_common(kv, nullptr, nullptr, k, v, local_tokens, query, params, scale, selected, counts, out,
                             workspace, workspace_bytes, splits, status, stream, "decode_step_f16");
+}
+
+int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
+                               const float* query, const sa_select_params* params, float scale, int32_t* selected,
+                               int32_t* counts, float* out, int32_t splits, int32_t* status, void* stream) {
+  const char* op = "decode_step_noalloc";
+  if (!kv || kv->batch <= 0) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv or empty batch", op);
+  if (kv->batch > 65535) return fail(SA_HIP_EINVAL, "%s: batch %d out of range", op, kv->batch);
+  if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "%s: splits out of range", op);
+  // the fused launch needs only the counters; the unfused ones need records
+  const size_t records = sa_hip_decode_step_workspace_bytes(kv, splits) - arrive_bytes(kv->batch);
+  if (records > kNoallocScratchBytes - kNoallocCounterBytes)
+    return fail(SA_HIP_EINVAL, "%s: %zu bytes of split records exceed the %zu-byte static scratch (fewer splits "
+                "or a smaller batch, or sa_hip_decode_step with a workspace)", op, records,
+                kNoallocScratchBytes - kNoallocCounterBytes);
+  void* base = nullptr;
+  if (int e = noalloc_scratch(&base, op)) return e;
+  // the counters are cleared before the fused launch, whatever an earlier
+  // call on this GPU left in them
+  return decode_step_run(kv, k, v, nullptr, nullptr, local_tokens, query, params, scale, selected, counts, out,
+                         static_cast<int32_t*>(base), true, static_cast<uint8_t*>(base) + kNoallocCounterBytes,
+                         kNoallocScratchBytes - kNoallocCounterBytes, splits, status, stream, op);
 }
 
 // ---- InfLLM local-causal representatives (prefill) -----------------------------

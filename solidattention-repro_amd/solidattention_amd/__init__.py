@@ -96,6 +96,8 @@ EXPORTS = {
                                      _I32, _P, _P]),
     "sa_hip_decode_step_f16": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P,
                                          _SZ, _I32, _P, _P]),
+    "sa_hip_decode_step_noalloc": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P,
+                                             _I32, _P, _P]),
     "sa_hip_append_seal": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_append_seal_f16": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_seal": (C.c_int, [_KV, _I32, _P, _P]),
@@ -441,6 +443,25 @@ def decode_step(kv: PagedKV, k, v, local_tokens, query, select_groups, budget, i
     check(fn(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(query), C.byref(params), C.c_float(scale),
              _ptr(selected), _ptr(counts), _ptr(out), _ptr(workspace), nbytes, splits, _ptr(status),
              _stream(stream)), "decode_step")
+    return selected, counts, out
+
+
+NOALLOC_SCRATCH_BYTES = 4 << 20
+NOALLOC_COUNTER_BYTES = 256 << 10
+
+
+def decode_step_noalloc(kv: PagedKV, k, v, local_tokens, query, select_groups, budget, init, local, scale,
+                        selected, counts, out, splits=1, status=None, sel_stride=None, stream=None, budgets=None):
+    """decode_step without a workspace: the library's static per-GPU scratch
+    (sa_hip_decode_step_noalloc).  fp32 k/v; the caller passes the outputs.
+    Calls that overlap on one GPU race."""
+    sel_stride = sel_stride or budget
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
+    s = kv.struct()
+    check(lib().sa_hip_decode_step_noalloc(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(query), C.byref(params),
+                                           C.c_float(scale), _ptr(selected), _ptr(counts), _ptr(out), splits,
+                                           _ptr(status), _stream(stream)), "decode_step_noalloc")
     return selected, counts, out
 
 

@@ -179,3 +179,22 @@ def test_producer_argument_checks():
     assert b"theta" in L.sa_hip_last_error()
     assert L.sa_hip_qkv_project(*args, C.c_float(1e6), C.c_float(1e-6), f, f, f, f, qn - 4, None) == -1
     assert L.sa_hip_rms_norm(f, f, f, 4, 1022, C.c_float(1e-6), None) == -1
+
+
+def test_noalloc_decode_step_refuses_records_beyond_scratch():
+    """The allocation-free decode step refuses split records larger than its
+    static scratch before touching the device (safe without a GPU)."""
+    import solidattention_amd as sa
+    L = sa.lib()
+    fake = 4096
+    kv = sa.PagedKVStruct(fake, fake, fake, fake, fake, fake, 100, 64, 10, 8, 12, 16, 8, 128, 0)
+    params = sa.SelectParamsStruct(8, 8, 1, 2, 8, 0, None)
+    records = L.sa_hip_attention_workspace_bytes(64, 16, 8, 128, 64)
+    assert records > sa.NOALLOC_SCRATCH_BYTES - sa.NOALLOC_COUNTER_BYTES
+    f = C.c_void_p(fake)
+    rc = L.sa_hip_decode_step_noalloc(C.byref(kv), f, f, 0, f, C.byref(params), C.c_float(0.1), f, f, f, 64, None,
+                                      None)
+    assert rc == -1 and b"static scratch" in L.sa_hip_last_error()
+    kv.batch = 0
+    assert L.sa_hip_decode_step_noalloc(C.byref(kv), f, f, 0, f, C.byref(params), C.c_float(0.1), f, f, f, 1, None,
+                                        None) == -1
