@@ -10,8 +10,9 @@ and representative update when a page fills), score + select per KV group,
 sparse GQA decode attention over the selected blocks plus the tail.
 
 Prints one JSON line: µs/layer (value), tokens/s, achieved HBM GB/s of the
-attention kernel against MI355X peak, and the CPU baseline (the oracle's C
-restatement of the reference CPU path timed on a bounded sample).
+decode-step kernel against MI355X peak (with a measured page-copy bandwidth
+beside it), and the CPU baseline (the reference's own CPU functions, compiled from
+its sources, timed on a bounded sample).
 """
 from __future__ import annotations
 
@@ -99,8 +100,11 @@ class Layer:
         perm = torch.randperm(num_pages, generator=g, dtype=torch.int64).to(torch.int32)
         kv.block_table.copy_(perm.view(batch, table_stride))
         sa.fill_synthetic_f16(kv.pool.view(-1), seed, 0)
-        q = torch.empty((total_steps, batch, hq, D), dtype=torch.float32, device="cuda")
-        sa.fill_synthetic_f32(q.view(-1), seed + 1, 0)
+        # one query per sequence, held over every step, so that the planted
+        # blocks below score high in every timed step (new K/V per step)
+        q0 = torch.empty((batch, hq, D), dtype=torch.float32, device="cuda")
+        sa.fill_synthetic_f32(q0.view(-1), seed + 1, 0)
+        q = q0.unsqueeze(0).expand(total_steps, batch, hq, D)
         knew = torch.empty((total_steps, batch, hkv, D), dtype=torch.float32, device="cuda")
         vnew = torch.empty_like(knew)
         sa.fill_synthetic_f32(knew.view(-1), seed + 2, 0)
@@ -110,7 +114,7 @@ class Layer:
             full = ctx // PAGE
             blocks = torch.randint(0, full, (batch, hkv, planted), generator=g).cuda()
             grp = hq // hkv
-            qmean = q[0].view(batch, hkv, grp, D).mean(dim=2)  # [B, Hkv, D]
+            qmean = q0.view(batch, hkv, grp, D).mean(dim=2)  # [B, Hkv, D]
             pool16 = kv.pool.view(torch.float16)  # [pages, 32, 2, Hkv, D]
             noise = torch.empty((batch, hkv, planted, PAGE, D), dtype=torch.float32, device="cuda")
             sa.fill_synthetic_f32(noise.view(-1), seed + 4, 0)
@@ -177,7 +181,7 @@ def main():
     pages_hint = budget + 2
     # the fused launch (splits 1) where it applies and fills the device; the
     # separate attention launch splits its page lists by default_splits
-    fused_ok = (args.splits in (0, 1) and sa.select_attend_fused(L[0].kv, hkv, 1)
+    fused_ok = (args.splits in (0, 1) and sa.select_attend_fused(L[0].kv, hkv, 1, sel_stride=budget)
                 and (args.splits == 1 or sa.select_attend_default_splits(L[0].kv, hkv, budget) == 1))
     splits = args.splits or sa.default_splits(batch, hkv, pages_hint, hq)
     ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(batch, hq, hkv, D, splits)
@@ -288,32 +292,20 @@ def main():
     sel_us = 1000.0 * sum(sel) / len(sel)
     app_us = 1000.0 * sum(app) / len(app)
 
-    # duration of the dominant kernel for the roofline: back-to-back launches
-    # of that kernel for every layer between two events on the bench stream,
-    # so the figure matches the kernel trace's average.  1 launch: the decode
-    # step kernel (one more token appended per launch; the tables have room);
-    # 2: the select+attend kernel; 3: the attention kernel.  Each reads the
-    # selected pages; 1 and 2 also the representatives of every sealed block.
-    reps = 4
-    s_last = last_step
-    start.record(stream)
-    for _ in range(reps):
-        for ly in L:
-            if launches == 1:
-                sa.decode_step(ly.kv, ly.knew[s_last], ly.vnew[s_last], 0, ly.q[s_last], hkv, budget, init, local,
-                               scale, step_ws, selected=ly.selected, counts=ly.counts, out=ly.out, splits=1,
-                               status=status)
-            elif launches == 2:
-                sa.select_attend(ly.kv, ly.q[s_last], hkv, budget, init, local, scale, selected=ly.selected,
-                                 counts=ly.counts, out=ly.out, splits=1, status=status)
-            else:
-                sa.sparse_decode_attention(ly.kv, ly.q[s_last], ly.selected, ly.counts, scale, out=ly.out,
-                                           splits=splits, workspace=workspace, status=status)
-    end.record(stream)
-    torch.cuda.synchronize()
-    if int(status.item()) != 0:
-        raise SystemExit(f"device status flagged {int(status.item())}")
-    kernel_us = 1000.0 * start.elapsed_time(end) / (reps * layers)
+    # duration of the dominant kernel for the roofline, from the timed region
+    # itself (HIP events on the bench stream).  One launch per layer: the
+    # decode-step kernel is the only kernel of the step, so its average launch
+    # duration is the timed region over steps x layers launches (graph
+    # replay; it includes the dispatch gap between consecutive launches, so
+    # it bounds the kernel trace's average from above).  Eager, or two or
+    # three launches: the events around each launch of the eager timed steps.
+    if launches == 1:
+        kernel_us = us_per_layer if graph else app_us
+        assert kernel_us * layers <= ms_per_step * 1000.0 * (1 + 1e-9) or not graph
+    else:
+        kernel_us = sel_us if launches == 2 else att_us
+
+    copy_ref = copy_reference(sa, torch, L[0].kv, args.seed)
 
     # algorithmic bytes of one launch: selected KV + tail KV + q + out + ids,
     # plus the fp32 representatives of every sealed block (select+attend) and
@@ -331,9 +323,14 @@ def main():
     kernel_bytes = {1: layer_bytes, 2: att_bytes + rep_bytes, 3: att_bytes}[launches]
     achieved = kernel_bytes / (kernel_us * 1e-6) / 1e9
     layer_gbps = layer_bytes / (us_per_layer * 1e-6) / 1e9
-    log(f"{launches} launch(es) per layer: dominant kernel {kernel_us:.2f} us back-to-back ({achieved:.0f} GB/s); "
-        f"event-bracketed append {app_us:.2f} / select {sel_us:.2f} / attention {att_us:.2f} us; "
-        f"layer {us_per_layer:.2f} us")
+    if launches == 1:
+        log(f"1 launch per layer: decode step {kernel_us:.2f} us per launch in the timed region ({achieved:.0f} "
+            f"GB/s); eager with events around each launch {app_us:.2f} us; layer {us_per_layer:.2f} us")
+    else:
+        log(f"{launches} launches per layer: dominant kernel {kernel_us:.2f} us per launch ({achieved:.0f} GB/s); "
+            f"eager append {app_us:.2f} / select {sel_us:.2f} / attention {att_us:.2f} us; "
+            f"layer {us_per_layer:.2f} us")
+    log(f"copy reference: gather_pages_kernel {copy_ref['gbps']:.0f} GB/s over {copy_ref['bytes']} bytes")
     grp = hq // hkv
     if grp == 4:  # the LDS-staged one-launch kernel (4 query heads per KV head)
         kernel_name = {1: "decode_kernel_staged<4,true,false>", 2: "decode_kernel_staged<4,false,false>",
@@ -358,7 +355,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16 KV, fp32 math",
-        "data": "synthetic (seeded N(0,1) FP16 KV, 8 planted blocks per head, random permuted page tables)",
+        "data": "synthetic (seeded N(0,1) FP16 KV and queries, one query per sequence held over the steps, "
+                f"{planted} planted high-score blocks per (sequence, KV head) against it, new K/V every step, "
+                "randomly permuted page tables)",
         "config": {"workload": f"{model} attention shape decode step: append+seal, score+select, sparse GQA "
                                f"attention", "layers": layers, "batch": batch, "query_heads": hq,
                    "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
@@ -369,7 +368,7 @@ def main():
         "launch": "hip graph per decode step" if graph else "eager",
         "eager_us_per_layer": round(eager_ms * 1000.0 / args.steps / layers, 3),
         "achieved_layer_hbm_gbps": round(layer_gbps, 1),
-        "kernels_us": ({"decode_step": round(kernel_us, 3), "decode_step_in_step": round(app_us, 3)}
+        "kernels_us": ({"decode_step": round(kernel_us, 3), "decode_step_eager": round(app_us, 3)}
                        if launches == 1 else
                        {"select_attend": round(kernel_us, 3), "select_attend_in_step": round(sel_us, 3),
                         "append_seal": round(app_us, 3)} if launches == 2 else
@@ -378,11 +377,42 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": kernel_name, "algorithmic_bytes": kernel_bytes,
-                     "launch_us": round(kernel_us, 3)},
+                     "launch_us": round(kernel_us, 3),
+                     "launch_timing": ("graph-replayed timed region / (steps x layers)" if launches == 1 and graph
+                                       else "events around each launch in the eager timed steps"),
+                     "copy_reference": copy_ref},
         "parity": parity,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def copy_reference(sa, torch, kv, seed, pages=4096, reps=5):
+    """A measured bandwidth reference on the same pool: gather_pages_kernel
+    copying `pages` whole 128 KiB pages, drawn in random order from the pool,
+    into a contiguous buffer (each byte read once and written once), timed
+    with HIP events over `reps` launches on the bench stream.  A copy mixes
+    reads and writes, so a read-dominated kernel can exceed it: it is a
+    reference point on the same box, not a ceiling."""
+    n = min(pages, int(kv.num_pages))
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed + 17)
+    src = torch.randperm(int(kv.num_pages), generator=g)[:n].to(torch.int32).cuda()
+    dst = torch.empty((n, kv.page_bytes // 2), dtype=torch.int16, device="cuda").view(torch.uint16)
+    sa.gather_pages(kv.pool, kv.page_bytes, kv.num_pages, src, dst)  # warm
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        sa.gather_pages(kv.pool, kv.page_bytes, kv.num_pages, src, dst)
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = 1000.0 * start.elapsed_time(end) / reps
+    nbytes = 2 * n * kv.page_bytes
+    del dst
+    return {"kernel": "gather_pages_kernel", "what": f"copy of {n} random pool pages (read + write)",
+            "bytes": nbytes, "us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
 def measured_traffic(config, kernel):
@@ -431,17 +461,25 @@ def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local, s):
 
 
 def cpu_baseline(np, torch, ly, args, budget, init, local, scale):
-    """The oracle's restatement of the reference CPU path (score + select +
-    pack + attention per (sequence, KV group)) on a bounded sample of
-    sequences of the same workload, reported per layer of the full batch by
-    scaling with batch / sample: on one thread (as the reference runs), and
-    with one thread per sequence over the host's cores (the oracle's C calls
-    release the interpreter lock)."""
+    """The reference CPU path on a bounded sample of sequences of the same
+    workload, reported per layer of the full batch by scaling with batch /
+    sample: on one thread (as the reference runs), and with one thread per
+    sequence over the host's cores.  Per (sequence, KV group) it runs the
+    reference's select_shared_blocks (cpp/src/selection.cpp:96-147) over the
+    group's query heads, packs the selected blocks of that KV head plus the
+    tail contiguously (the placement of read_blocks_fixed,
+    uring_reader.cpp:87-95) and runs its attention_reference
+    (cpp/src/attention_reference.cpp:55-96).  kind "reference": the
+    reference's own functions compiled from its sources (oracle/_ref);
+    kind "port": the oracle's bit-identical C restatement where oracle/_ref
+    was not built.  ctypes releases the interpreter lock during each call."""
     from concurrent.futures import ThreadPoolExecutor
 
     import oracle as O
+    use_ref = O.ref_available()
     kv = ly.kv
     batch, hq, hkv = ly.batch, ly.hq, ly.hkv
+    grp = hq // hkv
     threads = max(1, min(len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count(),
                          16, batch))
     n = args.cpu_sample_seqs or threads
@@ -454,14 +492,40 @@ def cpu_baseline(np, torch, ly, args, budget, init, local, scale):
     lookup = np.zeros(int(used.max()) + 1, np.int32)
     lookup[used] = np.arange(used.size, dtype=np.int32)
     table_l = np.ascontiguousarray(lookup[np.clip(table, 0, used.max())].astype(np.int32))
-    reps = np.ascontiguousarray(kv.reps[seqs].cpu().numpy())
+    reps = kv.reps[seqs].cpu().numpy()  # [n][rep_heads][D][rep_stride]
     q = np.ascontiguousarray(ly.q[0][seqs].cpu().numpy())
+    gpu_sel = ly.selected[seqs].cpu().numpy()
+    gpu_cnt = ly.counts[seqs].cpu().numpy()
+    # the reference's representative layout, [query head][block][D] per group
+    # (a layout change done once, outside the timed region)
+    rep_g = {}
+    for b in range(n):
+        nb = int(sealed[b])
+        for g in range(hkv):
+            rows = [reps[b, g if kv.rep_heads == hkv else g * grp + j, :, :nb].T for j in range(grp)]
+            rep_g[b, g] = np.ascontiguousarray(np.stack(rows), dtype=np.float32)
+    q_g = {(b, g): np.ascontiguousarray(q[b, g * grp:(g + 1) * grp]) for b in range(n) for g in range(hkv)}
+
+    def unit(b, g):
+        nb = int(sealed[b])
+        ids, _ = O.select_shared_blocks(q_g[b, g], rep_g[b, g], grp, nb, D, budget, init, local, use_ref=use_ref)
+        tail = int(seq_len[b]) - nb * PAGE
+        tokens = len(ids) * PAGE + tail
+        packed = np.empty((tokens, 2, 1, D), np.uint16)
+        packed[: len(ids) * PAGE] = pool[table_l[b, ids], :, :, g:g + 1, :].reshape(-1, 2, 1, D)
+        if tail:
+            tp = pool[table_l[b, nb:nb + (tail + PAGE - 1) // PAGE], :, :, g:g + 1, :].reshape(-1, 2, 1, D)
+            packed[len(ids) * PAGE:] = tp[:tail]
+        O.attention_reference(packed, q_g[b, g], tokens, grp, 1, D, scale, use_ref=use_ref)
+        return ids
+
+    # cross-check: the reference's ids for the sample equal the GPU's selection
+    ids_equal = all(unit(b, g).tolist() == gpu_sel[b, g, : gpu_cnt[b, g]].tolist()
+                    for b in range(min(n, 2)) for g in range(hkv))
 
     def one(b):
-        sel, cnt = O.paged_score_select(q[b:b + 1], reps[b:b + 1], sealed[b:b + 1], 1, hq, hkv, D, kv.rep_heads,
-                                        kv.rep_stride, hkv, budget, init, local)
-        O.paged_sparse_attention(pool, PAGE, table_l[b:b + 1], seq_len[b:b + 1], sealed[b:b + 1], sel, cnt, hkv,
-                                 q[b:b + 1], 1, hq, hkv, D, scale)
+        for g in range(hkv):
+            unit(b, g)
 
     # one thread: the first two sequences, repeated for ~10 s at most
     t0 = time.perf_counter()
@@ -486,12 +550,16 @@ def cpu_baseline(np, torch, ly, args, budget, init, local, scale):
             if el > 5.0 or rounds >= 200:
                 break
     multi_us = el / (rounds * n) * batch * 1e6
-    return {"value": round(multi_us, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"{n} of {batch} sequences of one layer, one per thread on {threads} threads, x {rounds} "
-                      f"rounds (score+select+gather+attention per KV group, oracle C restatement), scaled to "
-                      f"{batch} sequences",
+    what = ("the reference's select_shared_blocks + pack + attention_reference (oracle/_ref, built from its "
+            "sources)" if use_ref else "the oracle's C restatement of select_shared_blocks + pack + "
+            "attention_reference")
+    return {"value": round(multi_us, 1), "unit": "us/layer", "cores": threads,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"{n} of {batch} sequences of one layer (all {hkv} KV groups each), one per thread on "
+                      f"{threads} threads, x {rounds} rounds, scaled to {batch} sequences; per group: {what}",
             "single_thread": {"value": round(single_us, 1), "cores": 1,
                               "sample": f"2 sequences x {loops} repeats on one thread, scaled to {batch}"},
+            "ids_equal_gpu_selection": bool(ids_equal),
             "host_cpu": _cpu_model(), "nproc": os.cpu_count()}
 
 

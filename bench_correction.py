@@ -27,8 +27,16 @@ store through its device mapping.  Reported per layer: the device critical
 path from the first fill issued to the attention output (copy-stream and
 compute-stream events on one clock), the fill bandwidth, and the host wall
 time of this Python driver (dominated by its own bookkeeping).
-Checked at the end: resident sets equal the selections, slot bytes equal the
-host store, attention matches the oracle on the resident pages.
+Acceptance, after the timed steps (the reference's serial-vs-pipelined check,
+pipeline_main.cpp:1090-1123, and its corrected-set check, :704-715): for
+`accept_steps` more steps every layer runs the overlapped schedule and, on the
+same resident state, the serial one (one attention over the whole selection);
+the two outputs agree within 2e-3 (the merge order differs, so not bit for
+bit).  Then, for every sequence of every layer: the selection equals the
+oracle's (bit-exact ids), the resident set equals the selection, every slot's
+bytes equal its host-store block, and the attention matches the oracle on the
+resident pages within 2e-3.  run() returns the result line; any failed check
+raises SystemExit (a non-zero exit status) after the line is printed.
 """
 from __future__ import annotations
 
@@ -58,7 +66,8 @@ def run(args):
     EPS = 0.36                             # query random-walk step (~75% coverage)
     layers = args.layers or 2
     steps, warmup = args.steps, args.warmup
-    total_steps = warmup + 3 * steps + 1
+    accept_steps = max(1, int(getattr(args, "accept_steps", 2) or 2))
+    total_steps = warmup + 3 * steps + accept_steps + 1
     assert total_steps < PAGE, "the tail page must not seal during the run"
     torch.cuda.set_device(0)
     dev = torch.device("cuda")
@@ -123,6 +132,9 @@ def run(args):
         ly["ws"] = torch.zeros(sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, TOTAL_SPLITS) // 4,
                                dtype=torch.float32, device=dev)
         ly["out"] = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
+        ly["out_serial"] = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
+        ly["ws_serial"] = torch.zeros(sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, 2) // 4,
+                                      dtype=torch.float32, device=dev)
         ly["scores"] = torch.zeros((B, 1, kv.rep_stride), dtype=torch.float32, device=dev)
         ly["done"] = torch.cuda.Event()
         ly["done"].record(copy_stream)
@@ -145,7 +157,9 @@ def run(args):
     copy_events = []
     crit_events = []  # (first copy issued, attention output ready) per layer step
 
-    def step(s, mode, fill):
+    serial_err = []  # per acceptance layer step: max |overlapped - serial|, and whether within 2e-3
+
+    def step(s, mode, fill, accept=False):
         for li, ly in enumerate(Ls):
             kv = ly["kv"]
             sa.append_seal(kv, ly["knew"][s], ly["vnew"][s], 0, status=status)
@@ -216,6 +230,10 @@ def run(args):
                 sa.sparse_decode_attention_partial(kv, ly["q"][s], ly["miss"], ly["missc"], scale, False, ly["ws"], 2,
                                                    2, TOTAL_SPLITS, status=status)
                 sa.attention_merge(kv, ly["ws"], TOTAL_SPLITS, ly["out"])
+                if accept:
+                    # the serial schedule's attention on the same resident state
+                    sa.sparse_decode_attention(kv, ly["q"][s], ly["sel"], ly["cnt"], scale, out=ly["out_serial"],
+                                               splits=2, workspace=ly["ws_serial"], status=status)
             else:
                 copy_stream.synchronize()  # the reference's host barrier (pipeline_main.cpp:322-323)
                 sa.sparse_decode_attention(kv, ly["q"][s], ly["sel"], ly["cnt"], scale, out=ly["out"], splits=2,
@@ -223,6 +241,12 @@ def run(args):
             e_end = torch.cuda.Event(enable_timing=True)
             e_end.record(compute)
             crit_events.append((c0, e_end))
+            if accept:
+                a = ly["out"].double()
+                b_ = ly["out_serial"].double()
+                err = (a - b_).abs()
+                ok = bool(((err <= 2e-3) | (err <= 2e-3 * b_.abs())).all().item())
+                serial_err.append((float(err.max().item()), ok))
         torch.cuda.synchronize()
 
     for s in range(warmup):
@@ -251,32 +275,49 @@ def run(args):
                          "misses_per_layer": round((miss_total[0] - m0) / steps / layers, 1),
                          "h2d_gbps": round(n_copy_pages * page_bytes / max(n_copy_ms, 1e-9) / 1e6, 1),
                          "h2d_us_per_layer": round(n_copy_ms * 1000 / steps / layers, 1)}
+    for _ in range(accept_steps):
+        step(s, "overlapped", "gather", accept=True)
+        s += 1
     if int(status.item()) != 0:
         raise SystemExit(f"device status flagged {int(status.item())}")
     coverage = 1.0 - miss_total[0] / max(sel_total[0], 1)
 
-    # checks: resident sets == selections; slot bytes == store; attention vs oracle
+    # checks on every sequence of every layer after the last step
     import oracle as O
-    ly = Ls[-1]
-    kv = ly["kv"]
-    ids = ly["sel"].cpu().numpy()[:, 0, :]
-    sets_ok = all(sorted(ly["resident"][b]) == ids[b].tolist() for b in range(B))
-    pool = kv.pool.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B * SLOTS, page_elems)
-    store = ly["store"].numpy().view(np.uint16)
-    bytes_ok = all(np.array_equal(pool[b * SLOTS + slot], store[b * TS + blk])
-                   for b in range(B) for slot, blk in enumerate(ly["resident"][b]))
-    table = kv.block_table.cpu().numpy()
-    seq_len = kv.seq_len.cpu().numpy()
-    sealed = kv.sealed.cpu().numpy()
-    cnt = ly["cnt"].cpu().numpy()
-    sel = ly["sel"].cpu().numpy()
-    qh = ly["q"][s - 1].cpu().numpy()
-    n = 2
-    expect = O.paged_sparse_attention(pool.reshape(-1), PAGE, table[:n], seq_len[:n], sealed[:n], sel[:n], cnt[:n], 1,
-                                      qh[:n], n, HQ, HKV, D, scale)
-    got = ly["out"][:n].cpu().numpy()
-    err = np.abs(got.astype(np.float64) - expect)
-    att_ok = bool(((err <= 2e-3) | (err <= 2e-3 * np.abs(expect))).all())
+    sets_ok = bytes_ok = sel_ok = att_ok = True
+    att_err = 0.0
+    for ly in Ls:
+        kv = ly["kv"]
+        ids = ly["sel"].cpu().numpy()[:, 0, :]
+        sets_ok &= all(sorted(ly["resident"][b]) == ids[b].tolist() for b in range(B))
+        pool = kv.pool.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B * SLOTS, page_elems)
+        store = ly["store"].numpy().view(np.uint16)
+        bytes_ok &= all(np.array_equal(pool[b * SLOTS + slot], store[b * TS + blk])
+                        for b in range(B) for slot, blk in enumerate(ly["resident"][b]))
+        table = kv.block_table.cpu().numpy()
+        seq_len = kv.seq_len.cpu().numpy()
+        sealed = kv.sealed.cpu().numpy()
+        cnt = ly["cnt"].cpu().numpy()
+        sel = ly["sel"].cpu().numpy()
+        qh = ly["q"][s - 1].cpu().numpy()
+        # the selection of the last step against the oracle's (bit-exact ids)
+        esel, ecnt = O.paged_score_select(qh, kv.reps.cpu().numpy(), sealed, B, HQ, HKV, D, kv.rep_heads,
+                                          kv.rep_stride, 1, BUDGET, INIT, LOCAL)
+        sel_ok &= bool(np.array_equal(cnt, ecnt)) and all(
+            sel[b, 0, : ecnt[b, 0]].tolist() == esel[b, 0, : ecnt[b, 0]].tolist() for b in range(B))
+        expect = O.paged_sparse_attention(pool.reshape(-1), PAGE, table, seq_len, sealed, sel, cnt, 1, qh, B, HQ, HKV,
+                                          D, scale)
+        got = ly["out"].cpu().numpy()
+        err = np.abs(got.astype(np.float64) - expect)
+        att_ok &= bool(((err <= 2e-3) | (err <= 2e-3 * np.abs(expect))).all())
+        att_err = max(att_err, float(err.max()))
+    checks = {"sequences": B * layers,
+              "selection_equals_oracle": bool(sel_ok),
+              "resident_set_equals_selection": bool(sets_ok), "slot_bytes_equal_store": bool(bytes_ok),
+              "attention_within_2e-3": bool(att_ok), "attention_max_abs_err": att_err,
+              "serial_equals_pipelined_within_2e-3": all(ok for _, ok in serial_err),
+              "serial_pipelined_max_abs_err": max(e for e, _ in serial_err),
+              "accept_layer_steps": len(serial_err)}
     line = {
         "workload": "long-context miss correction, Qwen3-8B shape, B=8, 131072 tokens, budget 128 blocks",
         "layers": layers, "steps": steps, "warmup": warmup,
@@ -286,7 +327,10 @@ def run(args):
                                             1)},
         "schedules": results,
         "page_bytes": page_bytes,
-        "checks": {"resident_set_equals_selection": sets_ok, "slot_bytes_equal_store": bytes_ok,
-                   "attention_within_2e-3": att_ok, "attention_max_abs_err": float(err.max())},
+        "checks": checks,
     }
     print(json.dumps(line), flush=True)
+    failed = [k for k, v in checks.items() if v is False]
+    if failed:
+        raise SystemExit(f"correction workload checks failed: {failed}")
+    return line

@@ -472,8 +472,14 @@ def select_attend_default_splits(kv: PagedKV, select_groups, budget) -> int:
     return int(lib().sa_hip_select_attend_default_splits(C.byref(kv.struct()), C.byref(params)))
 
 
-def select_attend_fused(kv: PagedKV, select_groups, splits=1) -> bool:
-    params = SelectParamsStruct(select_groups, 1, 0, 0, 1, 0, None)
+def select_attend_fused(kv: PagedKV, select_groups, splits=1, sel_stride=None, budget=None) -> bool:
+    """Whether select_attend / decode_step run as one launch for this
+    geometry.  sel_stride: the row stride of the caller's selected[] (the
+    fused launch at 4 query heads per KV head keeps up to 2048 ids per list
+    on chip); defaults to budget, which defaults to 1."""
+    budget = budget or 1
+    sel_stride = sel_stride or budget
+    params = SelectParamsStruct(select_groups, budget, 0, 0, sel_stride, 0, None)
     s = kv.struct()
     return bool(lib().sa_hip_select_attend_fused(C.byref(s), C.byref(params), splits))
 

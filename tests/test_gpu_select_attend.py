@@ -351,3 +351,45 @@ def test_decode_step_graph_replays(hip):
     for (s1, c1, o1), (s2, c2, o2) in zip(he, hg):
         assert torch.equal(c1, c2) and torch.equal(s1, s2) and torch.equal(o1, o2)
     assert int(outs[0][1][3]) == 32 * 70 + 31 + 5  # five tokens appended, a seal on the way
+
+
+def test_decode_steps_key_channel_outliers_four_heads(hip):
+    """The Qwen3-8B decode step's data through its default kernel: 32 query /
+    8 KV heads (the fused, LDS-staged G = 4 launch), keys with 4 of 128
+    channels scaled x8 (post-RoPE key outliers, in the pool and in every
+    appended token), 1024+ sealed blocks per sequence, budget 64 = 4 init +
+    8 local + 52 dynamic; 24 decode steps with seals on the way.  Ids and
+    state bit-exact, attention within 2e-3 of the oracle on every step."""
+    lengths = [32 * 1024 + 20, 32 * 1100 + 30, 32 * 1040 + 9]
+    print(f"case: G=4 channel outliers lengths={lengths}", flush=True)
+    case = make_case(761, 3, 32, 8, lengths, table_stride=1112, channel_scale=(4, 8.0))
+    kv = device_kv(case)
+    budget, init, local = 64, 4, 8
+    assert hip.select_attend_fused(kv, 8)
+    ws, _ = hip.decode_step_workspace(kv)
+    st = status_tensor()
+    rng = np.random.default_rng(62)
+    seals = 0
+    for step in range(24):
+        k = rng.standard_normal((3, 8, D)).astype(np.float32)
+        k[..., :4] *= 8.0
+        v = rng.standard_normal((3, 8, D)).astype(np.float32)
+        case.query[:] = rng.standard_normal(case.query.shape).astype(np.float32)
+        before = case.sealed.copy()
+        sel, cnt, out = hip.decode_step(kv, to_dev(k), to_dev(v), 0, to_dev(case.query), 8, budget, init, local,
+                                        SCALE, ws, status=st)
+        esel, ecnt, expect = oracle_decode(case, k, v, 0, budget, init, local, budget)
+        seals += int((case.sealed - before).sum())
+        torch.cuda.synchronize()
+        assert int(st.item()) == 0, step
+        got_sel, got_cnt = sel.cpu().numpy(), cnt.cpu().numpy()
+        assert np.array_equal(got_cnt, ecnt), step
+        assert (ecnt == budget).all()
+        for b in range(3):
+            for g in range(8):
+                assert got_sel[b, g, :budget].tolist() == esel[b, g, :budget].tolist(), (step, b, g)
+        assert_close_2e3(out.cpu().numpy(), expect)
+        if step in (0, 12, 23):
+            check_state(kv, case)
+    assert seals == 3  # one seal each, after 12, 2 and 23 appends
+    assert int(ws.abs().sum().item()) == 0
