@@ -87,7 +87,9 @@ class DeviceArray {
 };
 
 // One layer's paged FP16 KV slot pool in HBM with its block tables,
-// lengths and block representatives.
+// lengths and block representatives.  The default representative row stride
+// is a multiple of 32 floats: every [rep head][d] row starts on a 128-byte
+// line, so the scoring kernels' streaming loads fetch no line twice.
 class PagedKvPool {
  public:
   PagedKvPool(std::size_t batch, std::size_t query_heads, std::size_t kv_heads, std::size_t table_stride,
@@ -95,7 +97,7 @@ class PagedKvPool {
               std::size_t head_dim = 128)
       : batch_(batch), query_heads_(query_heads), kv_heads_(kv_heads), head_dim_(head_dim),
         table_stride_(table_stride), num_pages_(num_pages), rep_heads_(rep_heads ? rep_heads : kv_heads),
-        rep_stride_(rep_stride ? rep_stride : (table_stride + 3) / 4 * 4),
+        rep_stride_(rep_stride ? rep_stride : (table_stride + 31) / 32 * 32),
         pool_(num_pages * page_elems()), table_(batch * table_stride), seq_len_(batch), sealed_(batch),
         generation_(batch), reps_(batch * rep_heads_ * head_dim * rep_stride_) {}
 

@@ -38,6 +38,9 @@ struct Params {
 
 // QUAD: four blocks per lane with 16-byte representative loads (reps 16-byte
 // aligned, rep_stride a multiple of 4); else one block per lane.
+// LDS: the group's query rows and one key per block, sized by the launch
+// (select_smem_bytes) to the group's heads and min(rep_stride, 8192) keys, so
+// that short representative rows leave room for more resident workgroups.
 template <int GR, int kThreads, bool QUAD>
 __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) {
   constexpr int kWaves = kThreads / kWave;
@@ -45,8 +48,9 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
 
-  __shared__ __align__(16) float q_s[kMaxSelectHeads * D];
-  __shared__ uint32_t keys[kMaxSelectBlocks];
+  extern __shared__ __align__(16) float dyn_smem[];
+  float* q_s = dyn_smem;                                                   // heads_per_sel * D
+  uint32_t* keys = reinterpret_cast<uint32_t*>(dyn_smem + p.heads_per_sel * D);  // min(rep_stride, 8192)
   __shared__ SelectSmem<kWaves> sm;
 
   const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
@@ -176,15 +180,21 @@ bool wide_select(int64_t workgroups, int64_t blocks) {
   return wide < narrow;
 }
 
+size_t select_smem_bytes(const Params& p) {
+  const int keys = p.rep_stride < kMaxSelectBlocks ? p.rep_stride : kMaxSelectBlocks;
+  return (static_cast<size_t>(p.heads_per_sel) * D + (keys + 3) / 4 * 4) * sizeof(float);
+}
+
 template <int GR>
 void launch_gr(const Params& p, dim3 grid, hipStream_t stream) {
+  const size_t smem = select_smem_bytes(p);
   if (vec_layout<4>(p.reps, p.rep_stride)) {
     // 4 waves score 1024 blocks per pass
-    hipLaunchKernelGGL((score_select_kernel<GR, 256, true>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((score_select_kernel<GR, 256, true>), grid, dim3(256), smem, stream, p);
   } else if (wide_select(static_cast<int64_t>(grid.x) * grid.y, p.rep_stride)) {
-    hipLaunchKernelGGL((score_select_kernel<GR, 1024, false>), grid, dim3(1024), 0, stream, p);
+    hipLaunchKernelGGL((score_select_kernel<GR, 1024, false>), grid, dim3(1024), smem, stream, p);
   } else {
-    hipLaunchKernelGGL((score_select_kernel<GR, 512, false>), grid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((score_select_kernel<GR, 512, false>), grid, dim3(512), smem, stream, p);
   }
 }
 

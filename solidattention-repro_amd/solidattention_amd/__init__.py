@@ -156,6 +156,18 @@ def _stream(stream=None):
     return C.c_void_p(s.cuda_stream)
 
 
+REP_ROW_FLOATS = 32
+
+
+def default_rep_stride(blocks):
+    """Representative row stride for `blocks` blocks: a multiple of 32 floats,
+    so that each head_dim row of [rep head][d][block] starts on a 128-byte
+    line and a row of n blocks is fetched as ceil(4 n / 128) lines instead of
+    one line more (the scoring kernels read every row with streaming loads,
+    so a line shared by two rows is fetched twice)."""
+    return (max(int(blocks), 1) + REP_ROW_FLOATS - 1) // REP_ROW_FLOATS * REP_ROW_FLOATS
+
+
 class PagedKV:
     """Device-resident paged FP16 KV slot pool of one layer.
 
@@ -175,8 +187,9 @@ class PagedKV:
         self.table_stride = table_stride
         self.num_pages = num_pages if num_pages is not None else batch * table_stride
         self.rep_heads = rep_heads if rep_heads is not None else kv_heads
-        # a multiple of 4 lets the scoring kernel load 4 blocks per lane
-        self.rep_stride = rep_stride if rep_stride is not None else (table_stride + 3) // 4 * 4
+        # a multiple of 32 floats starts every representative row on a
+        # 128-byte line (and lets the scoring kernel load 4 blocks per lane)
+        self.rep_stride = rep_stride if rep_stride is not None else default_rep_stride(table_stride)
         dev = torch.device(device)
         if pool is None:
             pool = torch.zeros((self.num_pages, PAGE_TOKENS, 2, kv_heads, head_dim),
