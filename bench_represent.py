@@ -118,7 +118,7 @@ def check(sa, np, torch, pq, kv, reps, offs, HQ, HKV, T, W, K, blocks, rep_strid
     # the received mass of the last window: compare the blocks before it
     q = pq[:, :n].cpu().numpy()
     k = kv[:n].view(torch.int16).cpu().numpy().view(np.uint16)
-    vals, eoffs, _ = O.local_causal_representatives_det(q, k, n, HQ, HKV, D, 32, W, K)
+    vals, eoffs, _ = O.local_causal_representatives_restated(q, k, n, HQ, HKV, D, 32, W, K)
     full = n // 32 - (W + 31) // 32  # blocks whose tokens' windows end inside the prefix
     reps_ok = bool(np.array_equal(got_reps[:, :, :full].transpose(0, 2, 1).view(np.uint32),
                                   vals[:, :full].view(np.uint32)))

@@ -353,11 +353,11 @@ size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads,
  * [query_heads][blocks][topk] int32 (the reference's chosen_token_offsets),
  * reps [query_heads][head_dim][rep_stride] (one sequence's slice of
  * sa_paged_kv.reps with rep_heads = query_heads), received
- * [query_heads][tokens].  The exponential is a fixed double-precision
- * evaluation (the reference's std::exp is glibc expf): identical chosen
- * tokens and representative bits on the reference's fixtures; a softmax
- * value can differ from the reference's in its last bit.  Limits:
- * head_dim 128, block_tokens 32, local_window <= 256. */
+ * [query_heads][tokens].  The exponential restates glibc's expf (the
+ * reference's std::exp(float)): the same table, polynomial and fused
+ * multiply-adds in double, equal to it on every float, so the chosen tokens,
+ * representatives and received masses are the reference's bit for bit.
+ * Limits: head_dim 128, block_tokens 32, local_window <= 256. */
 int sa_hip_local_causal_representatives(
     const float* prompt_queries, const uint16_t* kv, int64_t tokens,
     int32_t query_heads, int32_t kv_heads, int32_t head_dim,

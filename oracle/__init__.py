@@ -56,10 +56,13 @@ def lib() -> C.CDLL:
         L.sao_half_to_float.argtypes = [C.c_uint16]
         L.sao_attention_reference.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, C.c_float, _P]
         L.sao_build_local_causal_representatives.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P]
-        L.sao_build_local_causal_representatives_det.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P,
+        L.sao_build_local_causal_representatives_restated.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P,
                                                                  _P]
-        L.sao_exp_det.restype = C.c_float
-        L.sao_exp_det.argtypes = [C.c_float]
+        L.sao_expf_glibc.restype = C.c_float
+        L.sao_expf_glibc.argtypes = [C.c_float]
+        L.sao_expf_glibc_table.argtypes = [_P]
+        L.sao_expf_glibc_mismatches.restype = C.c_longlong
+        L.sao_expf_glibc_mismatches.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
         L.sao_mean_key_representatives.argtypes = [_P, _SZ, _SZ, _SZ, _SZ, _P]
         L.sao_select_shared_blocks.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P]
         L.sao_paged_score_select.argtypes = [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _SZ, _P]
@@ -146,9 +149,9 @@ def local_causal_representatives(prompt_queries, kv, tokens, hq, hkv, d, block, 
     return values.reshape(hq, blocks, d), offsets.reshape(hq, blocks, topk)
 
 
-def local_causal_representatives_det(prompt_queries, kv, tokens, hq, hkv, d, block, window, topk):
-    """The builder with sao_exp_det in place of expf (the GPU builder's
-    arithmetic); returns (values [hq][blocks][d], offsets [hq][blocks][topk],
+def local_causal_representatives_restated(prompt_queries, kv, tokens, hq, hkv, d, block, window, topk):
+    """The builder with the restated glibc expf (sao_expf_glibc) in place of
+    libm's (the GPU builder's arithmetic); returns (values [hq][blocks][d], offsets [hq][blocks][topk],
     received [hq][tokens])."""
     prompt_queries = _c(prompt_queries, np.float32)
     kv = _c(kv, np.uint16)
@@ -156,16 +159,30 @@ def local_causal_representatives_det(prompt_queries, kv, tokens, hq, hkv, d, blo
     values = np.zeros(hq * blocks * d, np.float32)
     offsets = np.zeros(hq * blocks * topk, np.uint64)
     received = np.zeros(hq * tokens, np.float32)
-    st = lib().sao_build_local_causal_representatives_det(_ptr(prompt_queries), _ptr(kv), tokens, hq, hkv, d, block,
+    st = lib().sao_build_local_causal_representatives_restated(_ptr(prompt_queries), _ptr(kv), tokens, hq, hkv, d, block,
                                                          window, topk, _ptr(values), _ptr(offsets), _ptr(received))
     if st != 0:
         raise ValueError("invalid local-causal representative dimensions")
     return values.reshape(hq, blocks, d), offsets.reshape(hq, blocks, topk), received.reshape(hq, tokens)
 
 
-def exp_det(x):
-    f = lib().sao_exp_det
-    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+def expf_glibc(x):
+    """sao_expf_glibc elementwise over a float32 array."""
+    f = lib().sao_expf_glibc
+    x = np.asarray(x, np.float32).ravel()
+    return np.array([f(float(v)) for v in x], np.float32)
+
+
+def expf_glibc_table():
+    out = np.zeros(32, np.uint64)
+    lib().sao_expf_glibc_table(_ptr(out))
+    return [int(v) for v in out]
+
+
+def expf_glibc_mismatches(first_bits, last_bits, stride=1):
+    """Floats (bit patterns first, first + stride, ... <= last) where the
+    restated expf differs from libm's."""
+    return int(lib().sao_expf_glibc_mismatches(first_bits, last_bits, stride))
 
 
 def mean_key_representatives(kv, tokens, hkv, d, block):

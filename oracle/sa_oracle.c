@@ -194,31 +194,70 @@ int sao_attention_reference(const uint16_t* kv, const float* query,
 /* ------------------------------------------------------------------------ */
 
 /* cpp/src/selection.cpp:12-94. */
-/* exp(x) rounded to float through a fixed sequence of double operations, so
- * the oracle and the GPU builder (which runs the same operations) agree bit
- * for bit: Cody-Waite reduction x = k*ln2 + r with k the nearest integer to
- * x*log2(e) and ln2 split as in fdlibm (ln2_hi has 21 trailing zero bits, so
- * k*ln2_hi is exact), exp(r) by its Taylor series to degree 13 in Horner form
- * (|r| <= 0.35: truncation below 1e-17 relative), then scaling by 2^k.  The
- * double result is within ~2e-16 of exp(x), so the float is the correctly
- * rounded exp(x) except within ~2^-29 of a rounding midpoint; glibc's expf is
- * within 0.502 ulp, so the two agree on nearly every input (not all). */
-float sao_exp_det(float x) {
-  static const double kLn2Hi = 6.93147180369123816490e-01;
-  static const double kLn2Lo = 1.90821492927058770002e-10;
-  static const double kLog2e = 1.44269504088896338700e+00;
-  static const double kInvFact[14] = {
-      1.0, 1.0, 0.5, 1.0 / 6.0, 1.0 / 24.0, 1.0 / 120.0, 1.0 / 720.0, 1.0 / 5040.0, 1.0 / 40320.0,
-      1.0 / 362880.0, 1.0 / 3628800.0, 1.0 / 39916800.0, 1.0 / 479001600.0, 1.0 / 6227020800.0};
-  if (x != x) return x;
-  if (x < -104.0f) return 0.0f;      /* below half the smallest subnormal */
-  if (x > 89.0f) return INFINITY;    /* above the largest finite float */
+/* The reference's std::exp(float) (selection.cpp:53) is glibc's expf.  This
+ * restates the method of glibc 2.35 (sysdeps/ieee754/flt-32/e_expf.c with the
+ * data of e_exp2f_data.c, the ARM optimized-routines expf): in double,
+ * z = x * 32/ln2, k = z rounded to the nearest integer (by adding and
+ * subtracting 1.5 * 2^52), r = z - k, 2^(k/32) = 2^((k mod 32)/32) * 2^(k div 32)
+ * from a 32-entry table (gen_expf_table.py), and 2^(r/32) by a degree-3
+ * polynomial; the double result is rounded to float.  x86-64 glibc runs the
+ * variant built for FMA: r and the polynomial steps below are fused
+ * multiply-adds.  With exactly these fusions the result equals this
+ * container's libm expf on every float in [-110, 90] (all 2,240,806,914 of
+ * them; without the fusion in r, 2 differ).  Test infrastructure, restated
+ * so that the GPU builder can run the same operations. */
+static const uint64_t kExpfTab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+void sao_expf_glibc_table(uint64_t* out) { memcpy(out, kExpfTab, sizeof kExpfTab); }
+
+float sao_expf_glibc(float x) {
+  static const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
+  static const double kShift = 0x1.8p+52;
+  static const double kC0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
+  static const double kC1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0);
+  static const double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  if (x != x) return x + x;
+  if (x > 0x1.62e42ep6f) return INFINITY;  /* above log(2^128) */
+  if (x < -0x1.9fe368p6f) return 0.0f;     /* below log(2^-150) */
   const double xd = (double)x;
-  const double k = nearbyint(xd * kLog2e);
-  const double r = (xd - k * kLn2Hi) - k * kLn2Lo;
-  double poly = kInvFact[13];
-  for (int i = 12; i >= 0; --i) poly = poly * r + kInvFact[i];
-  return (float)ldexp(poly, (int)k);
+  const double z = kInvLn2N * xd;
+  const double kd_shifted = z + kShift;
+  uint64_t ki;
+  memcpy(&ki, &kd_shifted, sizeof ki);
+  const double kd = kd_shifted - kShift;
+  const double r = fma(kInvLn2N, xd, -kd);
+  uint64_t t = kExpfTab[ki % 32] + (ki << 47);
+  double s;
+  memcpy(&s, &t, sizeof s);
+  const double p = fma(kC0, r, kC1);
+  const double r2 = r * r;
+  double y = fma(kC2, r, 1.0);
+  y = fma(p, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+long long sao_expf_glibc_mismatches(uint32_t first_bits, uint32_t last_bits, uint32_t stride) {
+  long long bad = 0;
+  if (stride == 0) stride = 1;
+  for (uint64_t u = first_bits; u <= last_bits; u += stride) {
+    const uint32_t bits = (uint32_t)u;
+    float x, a, b;
+    memcpy(&x, &bits, sizeof x);
+    a = sao_expf_glibc(x);
+    b = expf(x);
+    if (memcmp(&a, &b, sizeof a) != 0) ++bad;
+  }
+  return bad;
 }
 
 /* The reference's builder (selection.cpp:12-94) with the exponential as a
@@ -299,13 +338,13 @@ int sao_build_local_causal_representatives(
                    local_window, topk, values, offsets, expf_libm, NULL);
 }
 
-int sao_build_local_causal_representatives_det(
+int sao_build_local_causal_representatives_restated(
     const float* prompt_queries, const uint16_t* kv, size_t tokens,
     size_t query_heads, size_t kv_heads, size_t head_dim, size_t block_tokens,
     size_t local_window, size_t topk, float* values, size_t* offsets,
     float* received) {
   return build_lcr(prompt_queries, kv, tokens, query_heads, kv_heads, head_dim, block_tokens,
-                   local_window, topk, values, offsets, sao_exp_det, received);
+                   local_window, topk, values, offsets, sao_expf_glibc, received);
 }
 
 int sao_mean_key_representatives(const uint16_t* kv, size_t tokens,

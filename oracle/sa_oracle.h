@@ -74,19 +74,23 @@ int sao_build_local_causal_representatives(
  * Equal to sao_build_local_causal_representatives(window=1,
  * topk=block_tokens) for every query head of the group (all received masses
  * are exactly 1, so the stable order is the natural order). */
-/* The same builder with sao_exp_det in place of expf (the GPU builder's
- * arithmetic, bit for bit); received (optional): [Hq][tokens] attention mass
- * each key received. */
-int sao_build_local_causal_representatives_det(
+/* The same builder with sao_expf_glibc in place of libm's expf (the GPU
+ * builder's arithmetic, bit for bit); received (optional): [Hq][tokens]
+ * attention mass each key received. */
+int sao_build_local_causal_representatives_restated(
     const float* prompt_queries, const uint16_t* kv, size_t tokens,
     size_t query_heads, size_t kv_heads, size_t head_dim, size_t block_tokens,
     size_t local_window, size_t topk, float* values, size_t* offsets,
     float* received);
 
-/* exp(x) rounded to float through fixed double operations (Cody-Waite
- * reduction, degree-13 Taylor polynomial, scaling by 2^k); the GPU builder
- * runs the same operations. */
-float sao_exp_det(float x);
+/* glibc 2.35's expf restated (32-entry 2^(i/32) table, degree-3 polynomial
+ * in double, the fused multiply-adds of its x86-64 FMA build); the GPU
+ * builder runs the same operations.  _table copies the 32 table entries;
+ * _mismatches counts the floats with bit patterns first, first + stride, ...
+ * <= last where it differs from libm's expf. */
+float sao_expf_glibc(float x);
+void sao_expf_glibc_table(uint64_t* out);
+long long sao_expf_glibc_mismatches(uint32_t first_bits, uint32_t last_bits, uint32_t stride);
 
 int sao_mean_key_representatives(const uint16_t* kv, size_t tokens,
                                  size_t kv_heads, size_t head_dim,

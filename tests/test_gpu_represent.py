@@ -2,9 +2,12 @@
 (sa_hip_local_causal_representatives), the reference's
 build_local_causal_representatives (cpp/src/selection.cpp:12-94).
 
-Bars: bit-exact (chosen offsets, representative bits, received-mass bits)
-against the oracle's builder with the same exponential
-(sao_build_local_causal_representatives_det); bit-exact offsets and
+The GPU builder's exponential restates glibc's expf, the reference's
+std::exp.  Bars: bit-exact chosen offsets and representative bits against the
+oracle's builder with libm's expf (the reference's own arithmetic,
+sao_build_local_causal_representatives) and, with the received-mass bits,
+against the oracle's builder with the restated expf
+(sao_build_local_causal_representatives_restated); bit-exact offsets and
 representatives against the reference's own outputs on the committed golden
 cases and the published C2.1 offset hash; the C2.1 chain (GPU builder, then
 GPU selection) returns the published ids [0, 8, 13, 15]."""
@@ -41,12 +44,16 @@ def gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk, want_reps=False):
     return out + ((reps.cpu().numpy()[:, :, :blocks],) if want_reps else ())
 
 
-def check_vs_det(hip, pq, kv, tokens, hq, hkv, window, topk):
+def check_vs_oracle(hip, pq, kv, tokens, hq, hkv, window, topk):
     vals, offs, rec = gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk)
-    evals, eoffs, erec = O.local_causal_representatives_det(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
+    evals, eoffs, erec = O.local_causal_representatives_restated(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
     assert np.array_equal(rec.view(np.uint32), erec.view(np.uint32)), "received mass differs"
     assert np.array_equal(offs, eoffs.astype(np.int64)), "chosen offsets differ"
     assert np.array_equal(vals.view(np.uint32), evals.view(np.uint32)), "representative bits differ"
+    # the reference's arithmetic: libm's expf
+    lvals, loffs = O.local_causal_representatives(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
+    assert np.array_equal(offs, loffs.astype(np.int64)), "chosen offsets differ from the libm builder"
+    assert np.array_equal(vals.view(np.uint32), lvals.view(np.uint32)), "representative bits differ from libm"
 
 
 @pytest.mark.parametrize("name", sorted(REPRESENTATIVES))
@@ -62,12 +69,12 @@ def test_gpu_builder_vs_reference_golden(hip, name):
 @pytest.mark.parametrize("window,topk,hq,hkv,tokens", [
     (1, 1, 4, 4, 64), (2, 3, 8, 4, 96), (5, 4, 8, 2, 160), (32, 4, 16, 8, 512), (64, 8, 8, 8, 256),
     (100, 16, 4, 1, 320), (256, 32, 8, 2, 544), (33, 32, 2, 2, 64)])
-def test_gpu_builder_vs_det_oracle(hip, window, topk, hq, hkv, tokens):
+def test_gpu_builder_vs_oracle(hip, window, topk, hq, hkv, tokens):
     print(f"case: window={window} topk={topk} hq={hq} hkv={hkv} tokens={tokens}", flush=True)
     rng = np.random.default_rng(window * 7 + tokens)
     pq = rng.standard_normal(hq * tokens * 128).astype(np.float32)
     kv = rng.standard_normal(tokens * 2 * hkv * 128).astype(np.float16).view(np.uint16)
-    check_vs_det(hip, pq, kv, tokens, hq, hkv, window, topk)
+    check_vs_oracle(hip, pq, kv, tokens, hq, hkv, window, topk)
 
 
 def test_gpu_builder_outliers_and_ties(hip):
@@ -79,7 +86,17 @@ def test_gpu_builder_outliers_and_ties(hip):
     kv = rng.standard_normal((tokens, 2, hkv, 128)).astype(np.float16)
     kv[rng.random(tokens) < 0.05] = np.float16(60000)
     kv[40:56] = kv[40]  # a run of identical tokens
-    check_vs_det(hip, pq, kv.view(np.uint16).ravel(), tokens, hq, hkv, 32, 4)
+    check_vs_oracle(hip, pq, kv.view(np.uint16).ravel(), tokens, hq, hkv, 32, 4)
+
+
+def test_gpu_builder_wide_logit_range(hip):
+    """Queries and keys scaled x6: window logits spread over hundreds, so the
+    exponentials cover the whole float range down to subnormals and zero."""
+    rng = np.random.default_rng(123)
+    tokens, hq, hkv = 384, 8, 2
+    pq = (rng.standard_normal(hq * tokens * 128) * 6).astype(np.float32)
+    kv = (rng.standard_normal(tokens * 2 * hkv * 128) * 6).astype(np.float16).view(np.uint16)
+    check_vs_oracle(hip, pq, kv, tokens, hq, hkv, 48, 6)
 
 
 def test_gpu_c21_chain(hip):
