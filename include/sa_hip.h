@@ -283,6 +283,51 @@ int sa_hip_decode_step_f16(const sa_paged_kv* kv, const uint16_t* k,
                            size_t workspace_bytes, int32_t splits,
                            int32_t* status, void* stream);
 
+/* ---- R4/R9 InfLLM online seal -------------------------------------------- */
+
+/* The InfLLM online seal of the reference's P1.3c.4 (online_seal_main.cpp
+ * :41-44): when a decode step seals a 32-token block, the representative of
+ * each query head h is build_local_causal_representatives (selection.hpp
+ * :19-22, selection.cpp:12-94) applied to that block alone: its 32 keys (KV
+ * head h / G), the 32 decode queries of head h issued with those tokens,
+ * block_tokens 32, local_window and topk (the reference: 32 and 4); the
+ * reference's arithmetic bit for bit (its std::exp restated, see
+ * sa_hip_local_causal_representatives).  Representatives are per query head:
+ * kv->rep_heads must equal kv->query_heads.
+ *   query_ring   [batch][query_heads][ring_tokens][head_dim] fp32 device
+ *                memory: the decode query issued with the token at position
+ *                p is kept at slot p % ring_tokens, written by the call that
+ *                appends the token.  A caller that starts decoding after a
+ *                prefill copies the prefill queries of the unsealed tail
+ *                positions into their slots first.
+ *   ring_tokens  >= local_tokens + 32 (the whole tail). */
+typedef struct sa_online_seal {
+  float* query_ring;
+  int32_t ring_tokens;
+  int32_t local_window;
+  int32_t topk;
+  int32_t reserved;
+} sa_online_seal;
+
+/* sa_hip_append_seal (fp32 K/V) that also keeps the step's queries
+ * ([batch][query_heads][head_dim]) in the ring and seals with the online
+ * representative instead of the mean key. */
+int sa_hip_append_seal_online(const sa_paged_kv* kv, const float* k,
+                              const float* v, int32_t local_tokens,
+                              const float* query, const sa_online_seal* seal,
+                              int32_t* status, void* stream);
+
+/* sa_hip_decode_step (fp32 K/V) with the online seal: one launch where
+ * sa_hip_select_attend_fused() is 1, else sa_hip_append_seal_online, the
+ * selection and the attention.  Same workspace as sa_hip_decode_step. */
+int sa_hip_decode_step_online(const sa_paged_kv* kv, const float* k,
+                              const float* v, int32_t local_tokens,
+                              const float* query, const sa_online_seal* seal,
+                              const sa_select_params* params, float scale,
+                              int32_t* selected, int32_t* counts, float* out,
+                              void* workspace, size_t workspace_bytes,
+                              int32_t splits, int32_t* status, void* stream);
+
 /* Static scratch of sa_hip_decode_step_noalloc, per GPU: the first
  * SA_HIP_NOALLOC_COUNTER_BYTES hold the arrival counters (one per sequence,
  * any batch up to 65535), the rest the attention's split records. */

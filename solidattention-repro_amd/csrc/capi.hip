@@ -350,7 +350,27 @@ int sa_hip_consume_checksum(const float* input, int32_t elements, float* checksu
 
 static int lifecycle_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
                             const uint16_t* v16, int32_t local_tokens, int append, int32_t* status,
-                            void* stream, const char* op);
+                            void* stream, const char* op, const float* query = nullptr,
+                            const sa_online_seal* seal = nullptr);
+
+// The InfLLM online seal's arguments: a query ring that holds every token of
+// the tail (local + 32), a window >= 1, top-k within a block, one
+// representative per query head, and this step's queries.
+static int online_check(const sa_paged_kv* kv, const sa_online_seal* seal, const float* query,
+                        int32_t local_tokens, const char* op) {
+  if (!seal || !seal->query_ring) return fail(SA_HIP_EINVAL, "%s: null online seal / query ring", op);
+  if (!query) return fail(SA_HIP_EINVAL, "%s: null query", op);
+  if (local_tokens < 0 || static_cast<int64_t>(seal->ring_tokens) < static_cast<int64_t>(local_tokens) + 32)
+    return fail(SA_HIP_EINVAL, "%s: ring_tokens %d must hold the tail (local_tokens %d + 32)", op,
+                seal->ring_tokens, local_tokens);
+  if (seal->local_window < 1) return fail(SA_HIP_EINVAL, "%s: local_window must be >= 1", op);
+  if (seal->topk < 1 || seal->topk > SA_HIP_PAGE_TOKENS)
+    return fail(SA_HIP_EINVAL, "%s: topk %d outside [1, 32]", op, seal->topk);
+  if (kv->rep_heads != kv->query_heads)
+    return fail(SA_HIP_EINVAL, "%s: the online seal writes one representative per query head "
+                "(rep_heads must equal query_heads)", op);
+  return SA_HIP_OK;
+}
 
 static int select_launch(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
                          int32_t* selected, int32_t* counts, float* scores, int32_t* status, const char* op,
@@ -505,7 +525,8 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
                            const uint16_t* v16, int32_t local_tokens, const float* query,
                            const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
                            float* out, int32_t* arrive, bool clear_arrive, void* records, size_t records_bytes,
-                           int32_t splits, int32_t* status, void* stream, const char* op) {
+                           int32_t splits, int32_t* status, void* stream, const char* op,
+                           const sa_online_seal* seal = nullptr) {
   sa::SelectLaunch l;
   if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, op, &l)) return e;
   if (!out) return fail(SA_HIP_EINVAL, "%s: null out", op);
@@ -516,8 +537,10 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
   const void* va = v16 ? static_cast<const void*>(v16) : static_cast<const void*>(v);
   if (!ka || !va) return fail(SA_HIP_EINVAL, "%s: null k/v", op);
   if (!aligned16(ka) || !aligned16(va)) return fail(SA_HIP_EINVAL, "%s: k/v must be 16-byte aligned", op);
+  if (seal)
+    if (int e = online_check(kv, seal, query, local_tokens, op)) return e;
   if (!sa_hip_select_attend_fused(kv, params, splits)) {
-    if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op)) return e;
+    if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op, query, seal)) return e;
     if (int e = check_hip(sa::launch_score_select(l, as_stream(stream)), "decode_step: score_select launch"))
       return e;
     return attention_common(kv, query, selected, counts, params->select_groups, params->sel_stride, scale, out,
@@ -531,6 +554,13 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
   f.k16 = k16;
   f.v16 = v16;
   f.arrive = arrive;
+  if (seal) {
+    f.ring = seal->query_ring;
+    f.ring_tokens = seal->ring_tokens;
+    f.window = seal->local_window;
+    f.topk = seal->topk;
+    f.seal_scale = 1.0f / sqrtf(static_cast<float>(kv->head_dim));
+  }
   if (clear_arrive) {
     hipLaunchKernelGGL(clear_counters_kernel, dim3((kv->batch + 255) / 256), dim3(256), 0, as_stream(stream),
                        arrive, kv->batch);
@@ -570,6 +600,23 @@ int sa_hip_decode_step_f16(const sa_paged_kv* kv, const uint16_t* k, const uint1
   if (!k || !v) return fail(SA_HIP_EINVAL, "decode_step_f16: null k/v");
   return decode_step_common(kv, nullptr, nullptr, k, v, local_tokens, query, params, scale, selected, counts, out,
                             workspace, workspace_bytes, splits, status, stream, "decode_step_f16");
+}
+
+int sa_hip_decode_step_online(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
+                              const float* query, const sa_online_seal* seal, const sa_select_params* params,
+                              float scale, int32_t* selected, int32_t* counts, float* out, void* workspace,
+                              size_t workspace_bytes, int32_t splits, int32_t* status, void* stream) {
+  const char* op = "decode_step_online";
+  if (!seal) return fail(SA_HIP_EINVAL, "%s: null online seal", op);
+  if (!kv || kv->batch <= 0) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv or empty batch", op);
+  const size_t need = sa_hip_decode_step_workspace_bytes(kv, splits);
+  if (!workspace || workspace_bytes < need)
+    return fail(SA_HIP_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, need, workspace_bytes);
+  if (!aligned16(workspace)) return fail(SA_HIP_EINVAL, "%s: workspace must be 16-byte aligned", op);
+  const size_t ab = arrive_bytes(kv->batch);
+  return decode_step_run(kv, k, v, nullptr, nullptr, local_tokens, query, params, scale, selected, counts, out,
+                         static_cast<int32_t*>(workspace), false, static_cast<uint8_t*>(workspace) + ab,
+                         workspace_bytes - ab, splits, status, stream, op, seal);
 }
 
 int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
@@ -652,7 +699,7 @@ int sa_hip_local_causal_representatives(const float* prompt_queries, const uint1
 
 static int lifecycle_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
                             const uint16_t* v16, int32_t local_tokens, int append, int32_t* status,
-                            void* stream, const char* op) {
+                            void* stream, const char* op, const float* query, const sa_online_seal* seal) {
   if (int e = check_geometry(kv, op)) return e;
   if (int e = check_reps(kv, op)) return e;
   if (local_tokens < 0) return fail(SA_HIP_EINVAL, "%s: local_tokens must be >= 0", op);
@@ -683,7 +730,24 @@ static int lifecycle_common(const sa_paged_kv* kv, const float* k, const float* 
   l.kv_heads = kv->kv_heads;
   l.local_tokens = local_tokens;
   l.append = append;
+  if (seal) {
+    if (!append || k16) return fail(SA_HIP_EINVAL, "%s: the online seal needs an fp32 append", op);
+    if (int e = online_check(kv, seal, query, local_tokens, op)) return e;
+    l.query = query;
+    l.ring = seal->query_ring;
+    l.ring_tokens = seal->ring_tokens;
+    l.window = seal->local_window;
+    l.topk = seal->topk;
+    l.seal_scale = 1.0f / sqrtf(static_cast<float>(kv->head_dim));
+  }
   return check_hip(sa::launch_append_seal(l, as_stream(stream)), op);
+}
+
+int sa_hip_append_seal_online(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
+                              const float* query, const sa_online_seal* seal, int32_t* status, void* stream) {
+  if (!seal) return fail(SA_HIP_EINVAL, "append_seal_online: null online seal");
+  return lifecycle_common(kv, k, v, nullptr, nullptr, local_tokens, 1, status, stream, "append_seal_online", query,
+                          seal);
 }
 
 int sa_hip_append_seal(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,

@@ -11,7 +11,10 @@
 // sealed-count advance: the block stays in its page.  The representative is
 // the mean key of the block (sum of its 32 keys in token order, divided by
 // 32), i.e. the reference's build_local_causal_representatives with window 1
-// and top-k 32 (cpp/src/selection.cpp:12-94), bit-exact.
+// and top-k 32 (cpp/src/selection.cpp:12-94), bit-exact; or, for the InfLLM
+// online seal, the builder itself over the sealed block and the decode
+// queries issued with its tokens (online_seal.hpp).
+#include "online_seal.hpp"
 #include "sa_device.hpp"
 #include "sa_internal.hpp"
 
@@ -43,6 +46,8 @@ struct Params {
   int32_t group;
   int32_t local_tokens;
   int32_t append;
+  const float* query;     // online seal: this step's decode queries [batch][query_heads][D]
+  online::Args online;
 };
 
 __device__ inline int64_t table_page(const Params& p, int b, int64_t logical) {
@@ -51,10 +56,14 @@ __device__ inline int64_t table_page(const Params& p, int b, int64_t logical) {
   return (page >= 0 && page < p.num_pages) ? page : -1;
 }
 
+// ONLINE: keep each appended token's decode queries in the ring and seal
+// with the local-causal representative of every query head.
+template <bool ONLINE>
 __global__ __launch_bounds__(kThreads) void append_seal_kernel(const Params p) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   int64_t len = p.seq_len[b];
+  __shared__ float seal_smem[ONLINE ? online::kSmemFloats : 1];
 
   if (p.append) {
     const int64_t page = table_page(p, b, len / kPageTokens);
@@ -79,6 +88,7 @@ __global__ __launch_bounds__(kThreads) void append_seal_kernel(const Params p) {
       *reinterpret_cast<ushort4*>(dst + e) = kk;
       *reinterpret_cast<ushort4*>(dst + p.width + e) = vv;
     }
+    if (ONLINE) online::store_queries(p.online, p.query, b, 0, p.online.query_heads, len, tid, kThreads);
     len += 1;
     // The seal below may read the token just written by other threads.
     __syncthreads();
@@ -94,6 +104,18 @@ __global__ __launch_bounds__(kThreads) void append_seal_kernel(const Params p) {
       break;
     }
     const uint16_t* src = p.pool + page * p.page_elems;
+    if (ONLINE) {
+      // one representative per query head (rep_heads == query_heads)
+      for (int h = 0; h < p.online.query_heads; ++h) {
+        const int g = h / (p.online.query_heads / (p.width / D));
+        online::seal_head<kThreads>(p.online, b, h, src + g * D, p.token_elems, s * kPageTokens,
+                                    p.reps + (static_cast<int64_t>(b) * p.rep_heads + h) * D * p.rep_stride + s,
+                                    p.rep_stride, seal_smem);
+      }
+      ++s;
+      ++added;
+      continue;
+    }
     for (int o = tid; o < p.width; o += kThreads) {  // o = kv_head * D + d
       float sum = 0.0f;
 #pragma unroll 8
@@ -251,7 +273,13 @@ hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream) {
   p.group = l.rep_heads == l.kv_heads ? 1 : l.query_heads / l.kv_heads;
   p.local_tokens = l.local_tokens;
   p.append = l.append;
-  hipLaunchKernelGGL(append_seal_kernel, dim3(l.batch), dim3(kThreads), 0, stream, p);
+  if (l.ring) {
+    p.query = l.query;
+    p.online = online::Args{l.ring, l.ring_tokens, l.window, l.topk, l.query_heads, l.seal_scale};
+    hipLaunchKernelGGL(append_seal_kernel<true>, dim3(l.batch), dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(append_seal_kernel<false>, dim3(l.batch), dim3(kThreads), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

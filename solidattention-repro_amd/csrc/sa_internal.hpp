@@ -149,6 +149,12 @@ struct SelectAttendLaunch {
   const uint16_t* k16;
   const uint16_t* v16;
   int32_t* arrive;
+  // InfLLM online seal (decode step; ring non-null, rep_heads == query_heads)
+  float* ring;
+  int32_t ring_tokens;
+  int32_t window;
+  int32_t topk;
+  float seal_scale;
 };
 
 // The fused kernels: 1-2 query heads per KV head (registers), or 4 (LDS-staged
@@ -202,6 +208,16 @@ struct LifecycleLaunch {
   int32_t kv_heads;
   int32_t local_tokens;
   int32_t append;   // 0: seal only
+  // InfLLM online seal (ring non-null; rep_heads == query_heads): the
+  // decode queries [batch][query_heads][D] of this step are kept in
+  // ring[batch][query_heads][ring_tokens][D] and a sealed block's
+  // representative is the local-causal builder over the block
+  const float* query;
+  float* ring;
+  int32_t ring_tokens;
+  int32_t window;
+  int32_t topk;
+  float seal_scale;
 };
 
 hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream);

@@ -30,6 +30,7 @@
 // This file is compiled with -ffp-contract=off (scoring and seal sums are
 // bit-exact); the attention writes its fused multiply-adds explicitly.
 #include "attn_core.hpp"
+#include "online_seal.hpp"
 #include "select_core.hpp"
 
 namespace sa {
@@ -66,6 +67,7 @@ struct Params {
   int32_t sel_stride;
   int32_t local_tokens;
   float qscale;  // softmax scale * log2(e)
+  online::Args online;  // InfLLM online seal (ring non-null)
 };
 
 __device__ inline int64_t table_page(const attn::PoolView& v, int b, int64_t logical) {
@@ -76,9 +78,13 @@ __device__ inline int64_t table_page(const attn::PoolView& v, int b, int64_t log
 
 // Append head g of the new token and seal filled blocks for head g.  Returns
 // whether the token was appended (false: no page for it, nothing changes);
-// len and n are advanced in place.
-template <int G, bool F16>
-__device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& len, int& n, int& added) {
+// len and n are advanced in place.  ONLINE: the decode queries of the
+// group's heads are kept in the ring and a sealed block's representative of
+// each of them is the local-causal builder over the block (seal_smem: LDS
+// the caller does not use yet, online::kSmemFloats floats).
+template <int G, bool F16, bool ONLINE = false>
+__device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& len, int& n, int& added,
+                                        float* seal_smem = nullptr) {
   const int tid = threadIdx.x;
   const int64_t page = table_page(p.v, b, len / kPageTokens);
   if (page < 0) {
@@ -101,8 +107,9 @@ __device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& 
                     (len % kPageTokens) * p.v.token_elems + is_v * p.v.kv_heads * D + g * D + e;
     *reinterpret_cast<ushort4*>(dst) = h;
   }
+  if (ONLINE) online::store_queries(p.online, p.query, b, g * G, G, len, tid, kThreads);
   len += 1;
-  __syncthreads();  // the new token is visible to the seal below
+  __syncthreads();  // the new token (and its queries) visible to the seal below
   const int rg = p.rep_heads == p.v.kv_heads ? 1 : G;  // representative rows of head g
   while (len >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens) {
     const int64_t sp = n < p.rep_stride ? table_page(p.v, b, n) : -1;
@@ -110,7 +117,16 @@ __device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& 
       if (tid == 0) flag_status(p.v.status, kStatusCapacity);
       break;
     }
-    if (tid < D) {
+    if (ONLINE) {
+      // rep_heads == query_heads: one representative per query head
+      for (int j = 0; j < G; ++j) {
+        const int h = g * G + j;
+        online::seal_head<kThreads>(p.online, b, h, p.v.pool + sp * p.v.page_elems + g * D, p.v.token_elems,
+                                    static_cast<int64_t>(n) * kPageTokens,
+                                    p.reps + (static_cast<int64_t>(b) * p.rep_heads + h) * D * p.rep_stride + n,
+                                    p.rep_stride, seal_smem);
+      }
+    } else if (tid < D) {
       const uint16_t* src = p.v.pool + sp * p.v.page_elems + g * D + tid;
       float sum = 0.0f;
 #pragma unroll 8
@@ -128,7 +144,7 @@ __device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& 
 // G = query heads per KV head; GR = query heads sharing one representative
 // row (G for per-KV-head representatives, 1 for per-query-head ones);
 // APPEND: decode step (append + seal first); F16: raw FP16 K/V input.
-template <int G, int GR, bool APPEND, bool F16>
+template <int G, int GR, bool APPEND, bool F16, bool ONLINE = false>
 __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   const int g = blockIdx.x;
   const int b = blockIdx.y;
@@ -170,7 +186,8 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   if (APPEND) {
     const int gen = p.generation ? p.generation[b] : 0;
     int added = 0;
-    const bool appended = append_seal_head<G, F16>(p, b, g, len, n, added);
+    const bool appended =
+        append_seal_head<G, F16, ONLINE>(p, b, g, len, n, added, reinterpret_cast<float*>(keys));
     __syncthreads();  // representatives visible to the scoring below
     if (tid == 0 && atomicAdd(&p.arrive[b], 1) == p.v.kv_heads - 1) {
       if (appended) {
@@ -277,7 +294,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
 // all waves attend the rest of the selected blocks and the tail
 // with the staged walk of attn_core.hpp (pages HBM -> LDS by DMA, q.K on
 // v_mfma_f32_16x16x32_f16).
-template <int GR, bool APPEND, bool F16>
+template <int GR, bool APPEND, bool F16, bool ONLINE = false>
 __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p) {
   constexpr int G = 4;
   constexpr int kStageBytes = kWaves * attn::kStageVecs * 16;
@@ -309,7 +326,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   if (APPEND) {
     const int gen = p.generation ? p.generation[b] : 0;
     int added = 0;
-    const bool appended = append_seal_head<G, F16>(p, b, g, len, n, added);
+    const bool appended =
+        append_seal_head<G, F16, ONLINE>(p, b, g, len, n, added, reinterpret_cast<float*>(smem));
     __syncthreads();  // representatives visible to the scoring below
     if (tid == 0 && atomicAdd(&p.arrive[b], 1) == p.v.kv_heads - 1) {
       if (appended) {
@@ -418,6 +436,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   }
 }
 
+// Decode step with the InfLLM online seal (fp32 K/V, one representative per
+// query head).
+hipError_t launch_online(const Params& p, int batch, hipStream_t stream) {
+  const int group = p.query_heads / p.v.kv_heads;
+  const dim3 grid(p.v.kv_heads, batch);
+  if (p.rep_heads != p.query_heads) return hipErrorInvalidValue;
+  if (group == 4) {
+    hipLaunchKernelGGL((decode_kernel_staged<1, true, false, true>), grid, dim3(kThreads), 0, stream, p);
+  } else if (group == 1) {
+    hipLaunchKernelGGL((decode_kernel<1, 1, true, false, true>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((decode_kernel<2, 1, true, false, true>), grid, dim3(kThreads), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
 template <bool APPEND, bool F16>
 hipError_t launch_mode(const Params& p, int batch, hipStream_t stream) {
   const int group = p.query_heads / p.v.kv_heads;
@@ -491,6 +525,11 @@ hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream)
   p.sel_stride = s.sel_stride;
   p.local_tokens = s.local_tokens;
   p.qscale = s.scale * attn::kLog2e;
+  if (s.ring) {
+    if (!s.append || s.k16) return hipErrorInvalidValue;
+    p.online = online::Args{s.ring, s.ring_tokens, s.window, s.topk, s.query_heads, s.seal_scale};
+    return launch_online(p, s.batch, stream);
+  }
   if (!s.append) return launch_mode<false, false>(p, s.batch, stream);
   return s.k16 ? launch_mode<true, true>(p, s.batch, stream) : launch_mode<true, false>(p, s.batch, stream);
 }

@@ -46,6 +46,12 @@ class SelectParamsStruct(C.Structure):
                 ("sel_stride", C.c_int32), ("reserved", C.c_int32), ("budgets", C.c_void_p)]
 
 
+class OnlineSealStruct(C.Structure):
+    """Mirror of sa_online_seal (include/sa_hip.h)."""
+    _fields_ = [("query_ring", C.c_void_p), ("ring_tokens", C.c_int32), ("local_window", C.c_int32),
+                ("topk", C.c_int32), ("reserved", C.c_int32)]
+
+
 # name -> (restype, argtypes)
 _P, _I32, _I64, _SZ, _F = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t, C.c_float
 _KV = C.POINTER(PagedKVStruct)
@@ -96,6 +102,9 @@ EXPORTS = {
                                      _I32, _P, _P]),
     "sa_hip_decode_step_f16": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P,
                                          _SZ, _I32, _P, _P]),
+    "sa_hip_append_seal_online": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(OnlineSealStruct), _P, _P]),
+    "sa_hip_decode_step_online": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(OnlineSealStruct),
+                                            C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P, _SZ, _I32, _P, _P]),
     "sa_hip_decode_step_noalloc": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P,
                                              _I32, _P, _P]),
     "sa_hip_append_seal": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
@@ -456,6 +465,54 @@ def decode_step(kv: PagedKV, k, v, local_tokens, query, select_groups, budget, i
     check(fn(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(query), C.byref(params), C.c_float(scale),
              _ptr(selected), _ptr(counts), _ptr(out), _ptr(workspace), nbytes, splits, _ptr(status),
              _stream(stream)), "decode_step")
+    return selected, counts, out
+
+
+class OnlineSeal:
+    """The InfLLM online seal's query ring ([batch, query_heads, ring_tokens,
+    128] fp32 on the device) and builder parameters (sa_online_seal)."""
+
+    def __init__(self, kv: PagedKV, ring_tokens=PAGE_TOKENS, window=PAGE_TOKENS, topk=4, device="cuda"):
+        import torch
+        self.ring = torch.zeros((kv.batch, kv.query_heads, ring_tokens, kv.head_dim), dtype=torch.float32,
+                                device=device)
+        self.ring_tokens, self.window, self.topk = ring_tokens, window, topk
+
+    def struct(self) -> OnlineSealStruct:
+        return OnlineSealStruct(self.ring.data_ptr(), self.ring_tokens, self.window, self.topk, 0)
+
+
+def append_seal_online(kv: PagedKV, k, v, local_tokens, query, seal: OnlineSeal, status=None, stream=None):
+    s = kv.struct()
+    o = seal.struct()
+    check(lib().sa_hip_append_seal_online(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(query), C.byref(o),
+                                          _ptr(status), _stream(stream)), "append_seal_online")
+
+
+def decode_step_online(kv: PagedKV, k, v, local_tokens, query, seal: OnlineSeal, select_groups, budget, init, local,
+                       scale, workspace, selected=None, counts=None, out=None, splits=1, status=None,
+                       sel_stride=None, stream=None, budgets=None):
+    """decode_step (fp32 k/v) with the InfLLM online seal: the step's queries
+    go to seal.ring and a sealed block gets the local-causal representative
+    of every query head (kv.rep_heads == kv.query_heads)."""
+    import torch
+    sel_stride = sel_stride or budget
+    dev = query.device
+    if selected is None:
+        selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=dev)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
+    s = kv.struct()
+    o = seal.struct()
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().sa_hip_decode_step_online(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(query), C.byref(o),
+                                          C.byref(params), C.c_float(scale), _ptr(selected), _ptr(counts), _ptr(out),
+                                          _ptr(workspace), nbytes, splits, _ptr(status), _stream(stream)),
+          "decode_step_online")
     return selected, counts, out
 
 

@@ -82,3 +82,44 @@ def make_case(seed, batch, hq, hkv, lengths, table_stride=None, rep_heads=None, 
                  D, local_tokens)
     return PagedCase(batch, hq, hkv, table_stride, num_pages, pool, table, seq_len, sealed, generation, reps,
                      query, rep_heads, rep_stride, local_tokens)
+
+
+def oracle_select_attend(case, budget, init, local, sel_stride, scale, budgets=None):
+    """The oracle's per-KV-group selection and sparse attention of one step."""
+    esel = np.full((case.batch, case.hkv, sel_stride), -1, np.int32)
+    ecnt = np.zeros((case.batch, case.hkv), np.int32)
+    for b in range(case.batch):
+        bud = budget if budgets is None else int(budgets[b])
+        s_, c_ = O.paged_score_select(case.query[b:b + 1], case.reps[b:b + 1], case.sealed[b:b + 1], 1, case.hq,
+                                      case.hkv, D, case.rep_heads, case.rep_stride, case.hkv, bud, init, local,
+                                      sel_stride=sel_stride)
+        esel[b], ecnt[b] = s_[0], c_[0]
+    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, esel, ecnt, case.hkv,
+                                      case.query, case.batch, case.hq, case.hkv, D, scale)
+    return esel, ecnt, expect
+
+
+def oracle_online_append_seal(case, ring, k, v, query, local_tokens, window, topk, use_ref=False):
+    """The InfLLM online seal on the oracle (the reference's P1.3c.4 step,
+    online_seal_main.cpp:41-44): append one token per sequence, keep its
+    decode queries in ring[b][h][pos % ring_tokens], then seal while the tail
+    holds local_tokens + 32 tokens, each sealed block's representative of
+    query head h being build_local_causal_representatives over that block
+    alone (its 32 keys and the 32 queries of its tokens)."""
+    ring_tokens = ring.shape[2]
+    pos = case.seq_len.copy()
+    O.paged_append(case.pool, PAGE, case.table, case.seq_len, k=k, v=v, batch=case.batch, hkv=case.hkv, d=D)
+    for b in range(case.batch):
+        if case.seq_len[b] > pos[b]:
+            ring[b, :, pos[b] % ring_tokens, :] = query[b]
+    for b in range(case.batch):
+        while case.seq_len[b] >= (case.sealed[b] + 1) * PAGE + local_tokens:
+            n = int(case.sealed[b])
+            block_kv = case.pool[case.table[b, n]]  # [32][2][hkv][128]: the reference's token format
+            slots = [(n * PAGE + t) % ring_tokens for t in range(PAGE)]
+            block_q = np.ascontiguousarray(ring[b][:, slots, :])  # [hq][32][128]
+            vals, _ = O.local_causal_representatives(block_q, block_kv, PAGE, case.hq, case.hkv, D, PAGE, window,
+                                                     topk, use_ref=use_ref)
+            case.reps[b, :, :, n] = vals[:, 0, :]
+            case.sealed[b] += 1
+            case.generation[b] += 1
