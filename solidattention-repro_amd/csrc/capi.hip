@@ -823,15 +823,18 @@ int sa_hip_rms_norm(const float* x, const float* w, float* out, int32_t rows, in
 }
 
 static int linear_shape_ok(int32_t rows, int32_t in, int32_t out, const char* op) {
-  if (rows <= 0 || rows > 65535 * 64 || in <= 0 || in % 64 != 0 || out <= 0 || out % 64 != 0 || out > 65535 * 64)
-    return fail(SA_HIP_EINVAL, "%s: rows %d, in %d, out %d unsupported (in and out multiples of 64)", op, rows, in,
-                out);
+  if (rows <= 0 || rows > 65535 * 64 || in <= 0 || in % 256 != 0 || out <= 0 || out % 64 != 0 ||
+      out > 65535 * 16)
+    return fail(SA_HIP_EINVAL, "%s: rows %d, in %d, out %d unsupported (in a multiple of 256, out of 64)", op,
+                rows, in, out);
   return SA_HIP_OK;
 }
 
 size_t sa_hip_linear_workspace_bytes(int32_t rows, int32_t in, int32_t out) {
   if (rows <= 0 || in <= 0 || out <= 0) return 0;
-  return static_cast<size_t>(sa::linear_ksplit(rows, in, out)) * rows * out * sizeof(float);
+  const int ks = sa::linear_ksplit(rows, in, out);
+  return sa::linear_counter_bytes(rows, out) +
+         (ks > 1 ? static_cast<size_t>(ks) * rows * out * sizeof(float) : 0);
 }
 
 int sa_hip_linear(const float* x, const float* w, const float* residual, float* y, int32_t rows, int32_t in,
@@ -843,33 +846,38 @@ int sa_hip_linear(const float* x, const float* w, const float* residual, float* 
   if (workspace_bytes < sa_hip_linear_workspace_bytes(rows, in, out))
     return fail(SA_HIP_EINVAL, "linear: workspace of %zu bytes < %zu", workspace_bytes,
                 sa_hip_linear_workspace_bytes(rows, in, out));
+  if (!aligned16(workspace)) return fail(SA_HIP_EINVAL, "linear: workspace must be 16-byte aligned");
   sa::LinearLaunch l{x, w, residual, y, static_cast<float*>(workspace), rows, in, out};
   return check_hip(sa::launch_linear(l, as_stream(stream)), "linear launch");
 }
 
 size_t sa_hip_qkv_workspace_bytes(int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads) {
   if (rows <= 0 || hidden <= 0 || q_heads <= 0 || kv_heads <= 0) return 0;
-  const int32_t out = (q_heads + 2 * kv_heads) * sa::kHeadDim;
-  return sa_hip_linear_workspace_bytes(rows, hidden, out);
+  const int64_t out = static_cast<int64_t>(q_heads + 2 * kv_heads) * sa::kHeadDim;
+  return sa::qkv_counter_bytes(rows, q_heads, kv_heads) + static_cast<size_t>(rows) * out * sizeof(float);
 }
 
-int sa_hip_qkv_project(const float* x, const float* wq, const float* wk, const float* wv, const float* q_norm,
-                       const float* k_norm, const int32_t* positions, int32_t rows, int32_t hidden,
-                       int32_t q_heads, int32_t kv_heads, float theta, float eps, float* q, float* k, float* v,
-                       void* workspace, size_t workspace_bytes, void* stream) {
+static int qkv_common(const float* x, const float* gain, float in_eps, const float* wq, const float* wk,
+                      const float* wv, const float* q_norm, const float* k_norm, const int32_t* positions,
+                      int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads, float theta, float eps,
+                      float* q, float* k, float* v, void* workspace, size_t workspace_bytes, void* stream,
+                      const char* op) {
   if (q_heads <= 0 || kv_heads <= 0 || q_heads > 256 || kv_heads > 256)
-    return fail(SA_HIP_EINVAL, "qkv_project: bad head counts %d/%d", q_heads, kv_heads);
-  if (int e = linear_shape_ok(rows, hidden, (q_heads + 2 * kv_heads) * sa::kHeadDim, "qkv_project")) return e;
+    return fail(SA_HIP_EINVAL, "%s: bad head counts %d/%d", op, q_heads, kv_heads);
+  if (int e = linear_shape_ok(rows, hidden, (q_heads + 2 * kv_heads) * sa::kHeadDim, op)) return e;
   if (!x || !wq || !wk || !wv || !q_norm || !k_norm || !positions || !q || !k || !v || !workspace)
-    return fail(SA_HIP_EINVAL, "qkv_project: null argument");
-  if (!aligned16(x) || !aligned16(wq) || !aligned16(wk) || !aligned16(wv))
-    return fail(SA_HIP_EINVAL, "qkv_project: x and the weights must be 16-byte aligned");
-  if (!(theta > 1.0f)) return fail(SA_HIP_EINVAL, "qkv_project: rope theta must exceed 1");
+    return fail(SA_HIP_EINVAL, "%s: null argument", op);
+  if (!aligned16(x) || !aligned16(wq) || !aligned16(wk) || !aligned16(wv) || (gain && !aligned16(gain)) ||
+      !aligned16(v) || !aligned16(workspace))
+    return fail(SA_HIP_EINVAL, "%s: x, the weights, v and the workspace must be 16-byte aligned", op);
+  if (!(theta > 1.0f)) return fail(SA_HIP_EINVAL, "%s: rope theta must exceed 1", op);
   if (workspace_bytes < sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads))
-    return fail(SA_HIP_EINVAL, "qkv_project: workspace of %zu bytes < %zu", workspace_bytes,
+    return fail(SA_HIP_EINVAL, "%s: workspace of %zu bytes < %zu", op, workspace_bytes,
                 sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads));
   sa::QkvLaunch l{};
   l.x = x;
+  l.gain = gain;
+  l.in_eps = in_eps;
   l.wq = wq;
   l.wk = wk;
   l.wv = wv;
@@ -888,7 +896,25 @@ int sa_hip_qkv_project(const float* x, const float* wq, const float* wk, const f
   // theta^(-2i/128), correctly rounded (the reference's powf is within 2 ulp)
   for (int i = 0; i < 64; ++i)
     l.inv_freq[i] = static_cast<float>(std::pow(static_cast<double>(theta), -2.0 * i / sa::kHeadDim));
-  return check_hip(sa::launch_qkv_project(l, as_stream(stream)), "qkv_project launch");
+  return check_hip(sa::launch_qkv_project(l, as_stream(stream)), op);
+}
+
+int sa_hip_qkv_project(const float* x, const float* wq, const float* wk, const float* wv, const float* q_norm,
+                       const float* k_norm, const int32_t* positions, int32_t rows, int32_t hidden,
+                       int32_t q_heads, int32_t kv_heads, float theta, float eps, float* q, float* k, float* v,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  return qkv_common(x, nullptr, 0.0f, wq, wk, wv, q_norm, k_norm, positions, rows, hidden, q_heads, kv_heads, theta,
+                    eps, q, k, v, workspace, workspace_bytes, stream, "qkv_project");
+}
+
+int sa_hip_qkv_project_rms(const float* hidden_rows, const float* input_norm, float input_eps, const float* wq,
+                           const float* wk, const float* wv, const float* q_norm, const float* k_norm,
+                           const int32_t* positions, int32_t rows, int32_t hidden, int32_t q_heads,
+                           int32_t kv_heads, float theta, float eps, float* q, float* k, float* v, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!input_norm) return fail(SA_HIP_EINVAL, "qkv_project_rms: null input_norm");
+  return qkv_common(hidden_rows, input_norm, input_eps, wq, wk, wv, q_norm, k_norm, positions, rows, hidden, q_heads,
+                    kv_heads, theta, eps, q, k, v, workspace, workspace_bytes, stream, "qkv_project_rms");
 }
 
 int sa_hip_pages_to_host_async(const uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* pages,

@@ -84,11 +84,13 @@ struct LinearLaunch {
   const float* w;         // [out][in]
   const float* residual;  // [rows][out] or null
   float* y;               // [rows][out]
-  float* workspace;       // linear_ksplit(rows, in, out) * rows * out floats
+  float* workspace;       // linear_counter_bytes, then (ks > 1) ks * rows * out floats; zero once
   int32_t rows, in, out;
 };
 struct QkvLaunch {
-  const float* x;         // normalised hidden [rows][hidden]
+  const float* x;         // hidden [rows][hidden]: normalised, or raw with gain
+  const float* gain;      // optional input RMSNorm weight [hidden] (folded into the projection)
+  float in_eps;
   const float* wq;        // [q_heads*128][hidden]
   const float* wk;        // [kv_heads*128][hidden]
   const float* wv;
@@ -104,6 +106,9 @@ struct QkvLaunch {
   float inv_freq[64];
 };
 int linear_ksplit(int64_t rows, int64_t in, int64_t out);
+// arrival counters at the front of the projection workspaces (256-byte padded)
+size_t linear_counter_bytes(int64_t rows, int64_t out);
+size_t qkv_counter_bytes(int64_t rows, int q_heads, int kv_heads);
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, int rows, int width, float eps,
                            hipStream_t stream);
 hipError_t launch_linear(const LinearLaunch& l, hipStream_t stream);

@@ -72,6 +72,8 @@ EXPORTS = {
     "sa_hip_qkv_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "sa_hip_qkv_project": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F, _F, _P, _P, _P, _P,
                                      _SZ, _P]),
+    "sa_hip_qkv_project_rms": (C.c_int, [_P, _P, _F, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F, _F, _P,
+                                         _P, _P, _P, _SZ, _P]),
     "sa_store_open": (C.c_void_p, [C.c_char_p, _I64, _I64, _I64, _I32, _I32]),
     "sa_store_close": (None, [_P]),
     "sa_store_is_direct": (C.c_int, [_P]),
@@ -287,18 +289,19 @@ def linear(x, w, residual=None, out=None, workspace=None, stream=None):
     if out is None:
         out = torch.empty((rows, n_out), dtype=torch.float32, device=x.device)
     nbytes = lib().sa_hip_linear_workspace_bytes(rows, n_in, n_out)
-    if workspace is None:
-        workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=x.device)
+    if workspace is None:  # zeroed once: its arrival counters start at zero
+        workspace = torch.zeros(max(nbytes // 4, 1), dtype=torch.float32, device=x.device)
     check(lib().sa_hip_linear(_ptr(x), _ptr(w), _ptr(residual), _ptr(out), rows, n_in, n_out, _ptr(workspace),
                               workspace.numel() * 4, _stream(stream)), "linear")
     return out
 
 
 def qkv_project(x, wq, wk, wv, q_norm, k_norm, positions, q_heads, kv_heads, theta=1e6, eps=1e-6, q=None, k=None,
-                v=None, workspace=None, stream=None):
+                v=None, workspace=None, stream=None, input_norm=None, input_eps=1e-6):
     """Normalised hidden x [rows][hidden] -> q [rows][q_heads][128] and
     k [rows][kv_heads][128] (head RMS norm + RoPE at positions [rows]) and
-    v [rows][kv_heads][128]."""
+    v [rows][kv_heads][128].  With input_norm, x is the raw hidden and its
+    RMSNorm (weight input_norm) runs in the same launch."""
     import torch
     rows, hidden = x.shape
     dev = x.device
@@ -306,12 +309,19 @@ def qkv_project(x, wq, wk, wv, q_norm, k_norm, positions, q_heads, kv_heads, the
     k = k if k is not None else torch.empty((rows, kv_heads, HEAD_DIM), dtype=torch.float32, device=dev)
     v = v if v is not None else torch.empty((rows, kv_heads, HEAD_DIM), dtype=torch.float32, device=dev)
     nbytes = lib().sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads)
-    if workspace is None:
-        workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
-    check(lib().sa_hip_qkv_project(_ptr(x), _ptr(wq), _ptr(wk), _ptr(wv), _ptr(q_norm), _ptr(k_norm), _ptr(positions),
-                                   rows, hidden, q_heads, kv_heads, C.c_float(theta), C.c_float(eps), _ptr(q),
-                                   _ptr(k), _ptr(v), _ptr(workspace), workspace.numel() * 4, _stream(stream)),
-          "qkv_project")
+    if workspace is None:  # zeroed once: its arrival counters start at zero
+        workspace = torch.zeros(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
+    if input_norm is None:
+        check(lib().sa_hip_qkv_project(_ptr(x), _ptr(wq), _ptr(wk), _ptr(wv), _ptr(q_norm), _ptr(k_norm),
+                                       _ptr(positions), rows, hidden, q_heads, kv_heads, C.c_float(theta),
+                                       C.c_float(eps), _ptr(q), _ptr(k), _ptr(v), _ptr(workspace),
+                                       workspace.numel() * 4, _stream(stream)), "qkv_project")
+    else:
+        check(lib().sa_hip_qkv_project_rms(_ptr(x), _ptr(input_norm), C.c_float(input_eps), _ptr(wq), _ptr(wk),
+                                           _ptr(wv), _ptr(q_norm), _ptr(k_norm), _ptr(positions), rows, hidden,
+                                           q_heads, kv_heads, C.c_float(theta), C.c_float(eps), _ptr(q), _ptr(k),
+                                           _ptr(v), _ptr(workspace), workspace.numel() * 4, _stream(stream)),
+              "qkv_project_rms")
     return q, k, v
 
 

@@ -4,10 +4,11 @@ cpp/src/qwen_layer_main.cpp:125-172, :576-584, :640-645) against the
 oracle, and one attention layer's decode step chained through them.
 
 Bars: fp32 kernels against the oracle's float64 sums, relative to the
-largest magnitude of the result: 1e-5 for rms_norm and the projections (the
-K-slice fp32 sums of up to 2048 terms), 2e-5 for q and k after head RMS and
-RoPE (same fp32 angle, device sincos within 2 ulp); the chained layer
-output within 2e-3 (the attention's bar)."""
+largest magnitude of the result: 1e-5 for rms_norm and the projections (fp32
+sums of up to 2048 terms in a fixed order), 2e-5 for q and k after head RMS
+and RoPE (same fp32 angle, device sincos within 2 ulp), also with the input
+RMSNorm folded into the q/k/v launch; the chained layer output within 2e-3
+(the attention's bar)."""
 import numpy as np
 import pytest
 import torch
@@ -78,6 +79,47 @@ def test_qkv_project(hip, rows, hq, hkv):
     assert rel_err(q.cpu().numpy(), eq) < 2e-5
     assert rel_err(k.cpu().numpy(), ek) < 2e-5
     assert rel_err(v.cpu().numpy(), ev) < 1e-5
+
+
+@pytest.mark.parametrize("rows,hq,hkv", [(1, 16, 8), (64, 16, 8), (33, 32, 8), (130, 16, 4)])
+def test_qkv_project_with_input_rms(hip, rows, hq, hkv):
+    """The input RMSNorm folded into the q/k/v launch equals rms_norm then
+    the projections (oracle, float64) within the same bars."""
+    print(f"case: qkv+rms rows={rows} hq={hq} hkv={hkv}", flush=True)
+    rng = np.random.default_rng(200 + rows)
+    L = make_layer(rng, 1024, hq, hkv)
+    hid = (rng.standard_normal((rows, 1024)) * 3).astype(np.float32)
+    pos = rng.integers(0, 131072, size=rows).astype(np.int32)
+    q, k, v = hip.qkv_project(to_dev(hid), to_dev(L["wq"]), to_dev(L["wk"]), to_dev(L["wv"]), to_dev(L["qn"]),
+                              to_dev(L["kn"]), to_dev(pos), hq, hkv, input_norm=to_dev(L["inorm"]))
+    eq, ek, ev = oracle_qkv(O.rms_norm(hid, L["inorm"]), L, pos, hq, hkv)
+    assert rel_err(q.cpu().numpy(), eq) < 2e-5
+    assert rel_err(k.cpu().numpy(), ek) < 2e-5
+    assert rel_err(v.cpu().numpy(), ev) < 1e-5
+
+
+def test_projection_workspaces_reused(hip):
+    """Three calls in a row on one zeroed workspace each (the arrival
+    counters must come back to zero): every result equals the oracle."""
+    rng = np.random.default_rng(9)
+    L = make_layer(rng, 1024, 16, 8)
+    qkv_ws = torch.zeros(hip.lib().sa_hip_qkv_workspace_bytes(64, 1024, 16, 8) // 4, dtype=torch.float32,
+                         device="cuda")
+    lin_ws = torch.zeros(hip.lib().sa_hip_linear_workspace_bytes(64, 2048, 1024) // 4, dtype=torch.float32,
+                         device="cuda")
+    for it in range(3):
+        hid = rng.standard_normal((64, 1024)).astype(np.float32)
+        att = rng.standard_normal((64, 2048)).astype(np.float32)
+        pos = rng.integers(0, 4096, size=64).astype(np.int32)
+        q, k, v = hip.qkv_project(to_dev(hid), to_dev(L["wq"]), to_dev(L["wk"]), to_dev(L["wv"]), to_dev(L["qn"]),
+                                  to_dev(L["kn"]), to_dev(pos), 16, 8, workspace=qkv_ws,
+                                  input_norm=to_dev(L["inorm"]))
+        y = hip.linear(to_dev(att), to_dev(L["wo"]), to_dev(hid), workspace=lin_ws)
+        eq, ek, ev = oracle_qkv(O.rms_norm(hid, L["inorm"]), L, pos, 16, 8)
+        assert rel_err(q.cpu().numpy(), eq) < 2e-5, it
+        assert rel_err(k.cpu().numpy(), ek) < 2e-5, it
+        assert rel_err(v.cpu().numpy(), ev) < 1e-5, it
+        assert rel_err(y.cpu().numpy(), O.linear(att, L["wo"], hid)) < 1e-5, it
 
 
 def test_attention_layer_decode_chain(hip):
