@@ -223,6 +223,40 @@ __device__ inline int64_t readlane64(int64_t x, int k) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Pages start, start + step, ... (< end) of a page list, for the staged
+// walk: the lanes resolve 64 positions at a time; positions that resolve to
+// no page (flagged) are skipped.
+struct ListPages {
+  const PoolView& v;
+  int b;
+  const PageList& L;
+  int pos;
+  int end;
+  int step;
+  int lane;
+  PageRef batch{0, 0};  // lane l: position pos_batch + l * step
+  int k = 0;
+  int n = 0;
+
+  __device__ inline PageRef next(bool) {
+    for (;;) {
+      if (k >= n) {
+        if (pos >= end) return PageRef{0, 0};
+        const int i = pos + lane * step;
+        batch = i < end ? resolve_page(v, b, i, L) : PageRef{0, 0};
+        n = min(kWave, (end - pos + step - 1) / step);
+        pos += kWave * step;
+        k = 0;
+      }
+      PageRef r;
+      r.valid = __builtin_amdgcn_readlane(batch.valid, k);
+      r.page = readlane64(batch.page, k);
+      ++k;
+      if (r.valid > 0) return r;
+    }
+  }
+};
+
 // Online-softmax state of one wave for the G query heads of a KV group.
 template <int G>
 struct WaveState {
@@ -370,6 +404,18 @@ struct WaveState {
   __device__ inline void attend_staged_mfma(const PoolView& v, int b, const PageList& L, int start, int end,
                                             int step, const LaneGeom& lg, int lane, int g, uint4* stage,
                                             float* pbuf, const float* q_group, float qscale) {
+    ListPages src{v, b, L, start, end, step, lane};
+    attend_staged(v, src, lg, lane, g, stage, pbuf, q_group, qscale);
+  }
+
+  // The staged walk over the pages a source hands out: src.next(wait)
+  // returns the next page to attend (valid > 0), valid == 0 when the source
+  // is exhausted, or (only with wait == false) valid < 0 when the next page
+  // is not known yet.  One page is in flight while the previous one is
+  // computed.
+  template <class Src>
+  __device__ inline void attend_staged(const PoolView& v, Src& src, const LaneGeom& lg, int lane, int g,
+                                       uint4* stage, float* pbuf, const float* q_group, float qscale) {
     static_assert(G == 4 || G == 8, "G high and G low head columns fill the 16 MFMA columns");
     typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
     typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -433,118 +479,112 @@ struct WaveState {
         l_lane = l[h];
       }
     }
-    for (int base = start; base < end; base += kWave * step) {
-      const int i = base + lane * step;
-      PageRef mine{0, 0};
-      if (i < end) mine = resolve_page(v, b, i, L);
-      const int n = min(kWave, (end - base + step - 1) / step);
-      int next_valid = __builtin_amdgcn_readlane(mine.valid, 0);
-      if (next_valid > 0) stage_page(v, readlane64(mine.page, 0), next_valid, lg, ko, stage);
-      for (int k = 0; k < n; ++k) {
-        const int valid = next_valid;
-        uint4 ka[2][4], vr[kIters];
-        if (valid > 0) {
-          wait_staged();
+    PageRef cur = src.next(true);
+    if (cur.valid > 0) stage_page(v, cur.page, cur.valid, lg, ko, stage);
+    while (cur.valid > 0) {
+      const int valid = cur.valid;
+      uint4 ka[2][4], vr[kIters];
+      wait_staged();
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) ka[t][kk] = stage[kidx[t][kk]];
-          }
+        for (int kk = 0; kk < 4; ++kk) ka[t][kk] = stage[kidx[t][kk]];
+      }
 #pragma unroll
-          for (int it = 0; it < kIters; ++it) vr[it] = stage[(kIters + it) * kWave + lane];
-          wait_lds_reads();
-        }
-        if (k + 1 < n) {
-          next_valid = __builtin_amdgcn_readlane(mine.valid, k + 1);
-          if (next_valid > 0) stage_page(v, readlane64(mine.page, k + 1), next_valid, lg, ko, stage);
-        }
-        if (valid <= 0) continue;
+      for (int it = 0; it < kIters; ++it) vr[it] = stage[(kIters + it) * kWave + lane];
+      wait_lds_reads();
+      PageRef nxt = src.next(false);
+      if (nxt.valid > 0) stage_page(v, nxt.page, nxt.valid, lg, ko, stage);
 
-        // S for this lane's 8 tokens 8 kq + 4 t + i (log2 domain)
-        f32x4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      // S for this lane's 8 tokens 8 kq + 4 t + i (log2 domain)
+      f32x4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, ka[0][kk]), qb[kk], s0, 0, 0, 0);
-          s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, ka[1][kk]), qb[kk], s1, 0, 0, 0);
-        }
-        float sv[8];
+      for (int kk = 0; kk < 4; ++kk) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, ka[0][kk]), qb[kk], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, ka[1][kk]), qb[kk], s1, 0, 0, 0);
+      }
+      float sv[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sv[r] = (s0[r] + dpp_f<0x100 + G>(s0[r])) * sinv;  // row_shl:G: the low-half column
-          sv[4 + r] = (s1[r] + dpp_f<0x100 + G>(s1[r])) * sinv;
-        }
-        if (valid < kPageTokens) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            if (8 * kq + 4 * (e >> 2) + (e & 3) >= valid) sv[e] = kNegInf;
-          }
-        }
-        float pmax = kNegInf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pmax = fmaxf(pmax, sv[e]);
-        pmax = fmaxf(pmax, shfl_xor_f(pmax, 16));
-        pmax = fmaxf(pmax, shfl_xor_f(pmax, 32));
-        const float mn = fmaxf(m_lane, pmax);
-        const float corr = (m_lane == mn) ? 1.0f : __builtin_amdgcn_exp2f(m_lane - mn);
-        const float base_m = (mn == kNegInf) ? 0.0f : mn;
-        m_lane = mn;
-        float lsum = l_lane * corr;
+      for (int r = 0; r < 4; ++r) {
+        sv[r] = (s0[r] + dpp_f<0x100 + G>(s0[r])) * sinv;  // row_shl:G: the low-half column
+        sv[4 + r] = (s1[r] + dpp_f<0x100 + G>(s1[r])) * sinv;
+      }
+      if (valid < kPageTokens) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          sv[e] = __builtin_amdgcn_exp2f(sv[e] - base_m);
-          lsum += sv[e];
-        }
-        l_lane = lsum;
-        // probabilities to the P.V order: token 8 kq + 4 t + r is row r of
-        // row group 2 kq + t
-        if (col < G) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<float2*>(pbuf + (col * 4 + r) * kIters + 2 * kq) = make_float2(sv[r], sv[4 + r]);
-          if (kq == 0) pbuf[G * 32 + col] = corr;
-        }
-        // the wave's LDS operations complete in issue order: the reads below
-        // see the writes above
-        __builtin_amdgcn_wave_barrier();
-        float p[G][kIters];
-        float cr[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          const float4 a = *reinterpret_cast<const float4*>(pbuf + (h * 4 + lg.row) * kIters);
-          const float4 c = *reinterpret_cast<const float4*>(pbuf + (h * 4 + lg.row) * kIters + 4);
-          p[h][0] = a.x; p[h][1] = a.y; p[h][2] = a.z; p[h][3] = a.w;
-          p[h][4] = c.x; p[h][5] = c.y; p[h][6] = c.z; p[h][7] = c.w;
-        }
-#pragma unroll
-        for (int h = 0; h < G; h += 4) {
-          const float4 c = *reinterpret_cast<const float4*>(pbuf + G * 32 + h);
-          cr[h] = c.x; cr[h + 1] = c.y; cr[h + 2] = c.z; cr[h + 3] = c.w;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (valid < kPageTokens) {
-          // rows past the tail were not staged: their slot holds stale bytes
-#pragma unroll
-          for (int it = 0; it < kIters; ++it) {
-            if (it * kRows + lg.row >= valid) vr[it] = make_uint4(0, 0, 0, 0);
-          }
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[h][j] *= cr[h];
-        }
-        // P.V, each V half converted at its use (v_fma_mix_f32)
-#pragma unroll
-        for (int it = 0; it < kIters; ++it) {
-          const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float vj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
-#pragma unroll
-            for (int h = 0; h < G; ++h) acc[h][j] = __builtin_fmaf(p[h][it], vj, acc[h][j]);
-          }
+          if (8 * kq + 4 * (e >> 2) + (e & 3) >= valid) sv[e] = kNegInf;
         }
       }
+      float pmax = kNegInf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pmax = fmaxf(pmax, sv[e]);
+      pmax = fmaxf(pmax, shfl_xor_f(pmax, 16));
+      pmax = fmaxf(pmax, shfl_xor_f(pmax, 32));
+      const float mn = fmaxf(m_lane, pmax);
+      const float corr = (m_lane == mn) ? 1.0f : __builtin_amdgcn_exp2f(m_lane - mn);
+      const float base_m = (mn == kNegInf) ? 0.0f : mn;
+      m_lane = mn;
+      float lsum = l_lane * corr;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sv[e] = __builtin_amdgcn_exp2f(sv[e] - base_m);
+        lsum += sv[e];
+      }
+      l_lane = lsum;
+      // probabilities to the P.V order: token 8 kq + 4 t + r is row r of
+      // row group 2 kq + t
+      if (col < G) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<float2*>(pbuf + (col * 4 + r) * kIters + 2 * kq) = make_float2(sv[r], sv[4 + r]);
+        if (kq == 0) pbuf[G * 32 + col] = corr;
+      }
+      // the wave's LDS operations complete in issue order: the reads below
+      // see the writes above
+      __builtin_amdgcn_wave_barrier();
+      float p[G][kIters];
+      float cr[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float4 a = *reinterpret_cast<const float4*>(pbuf + (h * 4 + lg.row) * kIters);
+        const float4 c = *reinterpret_cast<const float4*>(pbuf + (h * 4 + lg.row) * kIters + 4);
+        p[h][0] = a.x; p[h][1] = a.y; p[h][2] = a.z; p[h][3] = a.w;
+        p[h][4] = c.x; p[h][5] = c.y; p[h][6] = c.z; p[h][7] = c.w;
+      }
+#pragma unroll
+      for (int h = 0; h < G; h += 4) {
+        const float4 c = *reinterpret_cast<const float4*>(pbuf + G * 32 + h);
+        cr[h] = c.x; cr[h + 1] = c.y; cr[h + 2] = c.z; cr[h + 3] = c.w;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (valid < kPageTokens) {
+        // rows past the tail were not staged: their slot holds stale bytes
+#pragma unroll
+        for (int it = 0; it < kIters; ++it) {
+          if (it * kRows + lg.row >= valid) vr[it] = make_uint4(0, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] *= cr[h];
+      }
+      // P.V, each V half converted at its use (v_fma_mix_f32)
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float vj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
+#pragma unroll
+          for (int h = 0; h < G; ++h) acc[h][j] = __builtin_fmaf(p[h][it], vj, acc[h][j]);
+        }
+      }
+      if (nxt.valid < 0) {
+        nxt = src.next(true);
+        if (nxt.valid > 0) stage_page(v, nxt.page, nxt.valid, lg, ko, stage);
+      }
+      cur = nxt;
     }
     // hand the statistics to the register layout: every row keeps the same
     // max; row r takes the denominator share of row group r, so that

@@ -24,8 +24,8 @@
 //
 // Sequence counters: the 8 workgroups of a sequence all read seq_len,
 // sealed and generation; the last of them to arrive (a per-sequence arrival
-// counter in the caller's workspace, left at zero) writes the new values,
-// so no workgroup can read an updated counter.
+// counter in the caller's workspace, left at zero) writes the new values at
+// its end, so no workgroup can read an updated counter.
 //
 // This file is compiled with -ffp-contract=off (scoring and seal sums are
 // bit-exact); the attention writes its fused multiply-adds explicitly.
@@ -40,7 +40,6 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int D = kHeadDim;
 constexpr int kStagedIds = kMaxStagedSelected;
-constexpr int kMaxPrePages = kWaves - 1;  // forced blocks attended during the selection (G = 4)
 
 struct Params {
   attn::PoolView v;
@@ -82,6 +81,32 @@ __device__ inline int64_t table_page(const attn::PoolView& v, int b, int64_t log
 // group's heads are kept in the ring and a sealed block's representative of
 // each of them is the local-causal builder over the block (seal_smem: LDS
 // the caller does not use yet, online::kSmemFloats floats).
+// Head g of the new token as FP16 bits, four values per lane of one wave:
+// lanes 0..31 hold K values 4 l .. 4 l + 3, lanes 32..63 the V values.
+template <bool F16>
+__device__ inline ushort4 token_quad(const Params& p, int b, int g, int lane) {
+  const int is_v = lane / 32;
+  const int e = (lane % 32) * 4;
+  const int64_t src = (static_cast<int64_t>(b) * p.v.kv_heads + g) * D + e;
+  if (F16) return *reinterpret_cast<const ushort4*>((is_v ? p.v16 : p.k16) + src);
+  const float4 f = *reinterpret_cast<const float4*>((is_v ? p.vv : p.k) + src);
+  return make_ushort4(f2h_rne(f.x), f2h_rne(f.y), f2h_rne(f.z), f2h_rne(f.w));
+}
+
+__device__ inline void store_token_quad(const Params& p, int64_t page, int64_t pos, int g, int lane, ushort4 h) {
+  const int is_v = lane / 32;
+  const int e = (lane % 32) * 4;
+  uint16_t* dst = const_cast<uint16_t*>(p.v.pool) + page * p.v.page_elems + (pos % kPageTokens) * p.v.token_elems +
+                  is_v * p.v.kv_heads * D + g * D + e;
+  *reinterpret_cast<ushort4*>(dst) = h;
+}
+
+// Whether appending one token at position len seals a block (len + 1 tokens
+// reach block n's end plus the local tail).
+__device__ inline bool append_seals(const Params& p, int64_t len, int n) {
+  return len + 1 >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens;
+}
+
 template <int G, bool F16, bool ONLINE = false>
 __device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& len, int& n, int& added,
                                         float* seal_smem = nullptr) {
@@ -91,25 +116,12 @@ __device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& 
     if (tid == 0) flag_status(p.v.status, kStatusCapacity);
     return false;
   }
-  if (tid < kWave) {
-    // lanes 0..31: 4 K values each, lanes 32..63: 4 V values each
-    const int is_v = tid / 32;
-    const int e = (tid % 32) * 4;
-    const int64_t src = (static_cast<int64_t>(b) * p.v.kv_heads + g) * D + e;
-    ushort4 h;
-    if (F16) {
-      h = *reinterpret_cast<const ushort4*>((is_v ? p.v16 : p.k16) + src);
-    } else {
-      const float4 f = *reinterpret_cast<const float4*>((is_v ? p.vv : p.k) + src);
-      h = make_ushort4(f2h_rne(f.x), f2h_rne(f.y), f2h_rne(f.z), f2h_rne(f.w));
-    }
-    uint16_t* dst = const_cast<uint16_t*>(p.v.pool) + page * p.v.page_elems +
-                    (len % kPageTokens) * p.v.token_elems + is_v * p.v.kv_heads * D + g * D + e;
-    *reinterpret_cast<ushort4*>(dst) = h;
-  }
+  if (tid < kWave) store_token_quad(p, page, len, g, tid, token_quad<F16>(p, b, g, tid));
   if (ONLINE) online::store_queries(p.online, p.query, b, g * G, G, len, tid, kThreads);
   len += 1;
-  __syncthreads();  // the new token (and its queries) visible to the seal below
+  // the new token (and its queries) visible to the seal below; without a
+  // seal nothing in this workgroup reads them
+  if (len >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens) __syncthreads();
   const int rg = p.rep_heads == p.v.kv_heads ? 1 : G;  // representative rows of head g
   while (len >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens) {
     const int64_t sp = n < p.rep_stride ? table_page(p.v, b, n) : -1;
@@ -141,6 +153,27 @@ __device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& 
   return true;
 }
 
+// Sequence counters of one decode step.  Every workgroup of sequence b reads
+// seq_len, sealed and generation at its start and adds 1 to arrive[b] after
+// its append; the workgroup that brings the count to kv_heads (all others
+// have read the counters by then) writes the new values and clears the count.
+struct SeqCommit {
+  int gen = 0;
+  int added = 0;
+  int arrived = -1;
+  bool appended = false;
+};
+
+__device__ inline void commit_sequence(const Params& p, int b, int64_t len, int n, const SeqCommit& c) {
+  if (c.arrived != p.v.kv_heads - 1) return;
+  if (c.appended) {
+    p.seq_len[b] = static_cast<int32_t>(len);
+    p.sealed[b] = n;
+    if (p.generation) p.generation[b] = c.gen + c.added;
+  }
+  p.arrive[b] = 0;
+}
+
 // G = query heads per KV head; GR = query heads sharing one representative
 // row (G for per-KV-head representatives, 1 for per-query-head ones);
 // APPEND: decode step (append + seal first); F16: raw FP16 K/V input.
@@ -159,6 +192,9 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   __shared__ int s_count;
 
   const int64_t out_row = static_cast<int64_t>(b) * p.v.kv_heads + g;
+  // the group's query rows, loaded at entry (their latency overlaps the append)
+  const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
+  const float q_entry = tid < G * D ? q_group[tid] : 0.0f;
   int64_t len = p.seq_len[b];
   int n = p.sealed[b];
 
@@ -183,20 +219,15 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   if (have_pre) sel::score_prefetch(a, tid, pre);
 
   // ---- 1. append + seal (decode step) ---------------------------------------
+  // The arrival count is read at the end of the kernel, so that its round
+  // trip overlaps the scoring; the representatives a seal wrote are visible
+  // to the scoring after the query barrier below.
+  SeqCommit commit{};
   if (APPEND) {
-    const int gen = p.generation ? p.generation[b] : 0;
-    int added = 0;
-    const bool appended =
-        append_seal_head<G, F16, ONLINE>(p, b, g, len, n, added, reinterpret_cast<float*>(keys));
-    __syncthreads();  // representatives visible to the scoring below
-    if (tid == 0 && atomicAdd(&p.arrive[b], 1) == p.v.kv_heads - 1) {
-      if (appended) {
-        p.seq_len[b] = static_cast<int32_t>(len);
-        p.sealed[b] = n;
-        if (p.generation) p.generation[b] = gen + added;
-      }
-      p.arrive[b] = 0;
-    }
+    commit.gen = p.generation ? p.generation[b] : 0;
+    commit.appended =
+        append_seal_head<G, F16, ONLINE>(p, b, g, len, n, commit.added, reinterpret_cast<float*>(keys));
+    if (tid == 0) commit.arrived = atomicAdd(&p.arrive[b], 1);
   }
 
   attn::WaveState<G> st;
@@ -212,7 +243,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
       s_count = 0;
     }
   } else {
-    sel::load_query<kThreads>(a, q_s);
+    if (tid < G * D) q_s[tid] = q_entry;
     __syncthreads();
     if (kPrefetch) {
       sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr, pre, have_pre);
@@ -281,6 +312,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
     attn::combine_element<G, kWaves>(cs, h, d, mx, lw, aw);
     p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
   }
+  if (APPEND && tid == 0) commit_sequence(p, b, len, n, commit);
 }
 
 
@@ -288,19 +320,117 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
 // One 8-wave workgroup per (sequence, KV head), one per CU (the eight 16 KiB
 // page slots).  After append + seal, all 512 threads score two blocks per lane
 // (8-byte representative loads); the keys borrow the page slots of waves 0
-// and 1.  Wave 0 then selects while waves 1..7 (2..7 when the keys reach into
-// wave 1's slot) attend one forced block each (the last local blocks, then
-// init blocks: selected whatever the scores) through their own slots; then
-// all waves attend the rest of the selected blocks and the tail
-// with the staged walk of attn_core.hpp (pages HBM -> LDS by DMA, q.K on
-// v_mfma_f32_16x16x32_f16).
+// and 1.  Then every wave walks pages with the staged walk of attn_core.hpp
+// (pages HBM -> LDS by DMA, q.K on v_mfma_f32_16x16x32_f16), claiming list
+// positions one at a time from an LDS counter:
+//   * positions [0, F): the forced blocks (init, then local: selected
+//     whatever the scores; at most kEarly), whose pages the last wave looked
+//     up while it scored;
+//   * positions [F, F + late): the other selected blocks, then the tail
+//     pages, listed by wave 0 after its selection.
+// Waves 1..7 start on the forced blocks while wave 0 selects; a wave that
+// claims a late position before the list is out waits for it (an LDS flag
+// that wave 0 sets on every path).  No wave idles at a barrier between the
+// selection and the walk, and the waves end within about a page of each
+// other.
+constexpr int kEarly = 64;      // forced blocks looked up before the selection
+constexpr int kTailPages = 64;  // tail pages listed by wave 0 (more are looked up when claimed)
+
+// Page of logical block blk of sequence b, or -1 (flagged) if there is none.
+__device__ inline int64_t lookup_page(const attn::PoolView& v, int b, int64_t blk) {
+  if (v.contig_tokens > 0) return blk;
+  if (blk < 0 || blk >= v.table_stride) {
+    flag_status(v.status, kStatusBadBlock);
+    return -1;
+  }
+  const int64_t page = v.table[static_cast<int64_t>(b) * v.table_stride + blk];
+  if (page < 0 || page >= v.num_pages) {
+    flag_status(v.status, kStatusBadPage);
+    return -1;
+  }
+  return page;
+}
+
+// LDS state of the claimed walk.
+struct ClaimSmem {
+  int next;        // next position to claim
+  int late_ready;  // 1 once wave 0 has listed the late positions
+  int late_n;      // late positions: selected blocks, then tail pages
+  int late_mid;    // of which selected blocks
+  int32_t early[kEarly];
+  int32_t late[kStagedIds + kTailPages];  // the selected ids, then (in place) the late pages
+};
+
+__device__ inline void wait_late(ClaimSmem& cs) {
+  while (__hip_atomic_load(&cs.late_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+    __builtin_amdgcn_s_sleep(1);
+}
+
+// Page source of the staged walk: claims positions (see above); all values
+// wave-uniform.
+struct ClaimPages {
+  ClaimSmem& cs;
+  const attn::PoolView& v;
+  int b;
+  int lane;
+  int F;        // forced positions listed early
+  int n;        // sealed blocks
+  int64_t len;  // tokens (after this step's append)
+  int pending = -1;
+  bool ready = false;
+
+  __device__ inline attn::PageRef next(bool wait) {
+    for (;;) {
+      int c;
+      if (pending >= 0) {
+        c = pending;
+        pending = -1;
+      } else {
+        int x = 0;
+        if (lane == 0) x = __hip_atomic_fetch_add(&cs.next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        c = __builtin_amdgcn_readfirstlane(x);
+      }
+      if (c < F) {
+        const int32_t page = __builtin_amdgcn_readfirstlane(cs.early[c]);
+        if (page >= 0) return attn::PageRef{page, kPageTokens};
+        continue;
+      }
+      if (!ready) {
+        if (!wait) {
+          pending = c;
+          return attn::PageRef{0, -1};
+        }
+        wait_late(cs);
+        ready = true;
+      }
+      const int j = c - F;
+      const int late_n = __builtin_amdgcn_readfirstlane(cs.late_n);
+      if (j >= late_n) return attn::PageRef{0, 0};
+      const int mid = __builtin_amdgcn_readfirstlane(cs.late_mid);
+      if (j < mid) {
+        const int32_t page = __builtin_amdgcn_readfirstlane(cs.late[j]);
+        if (page >= 0) return attn::PageRef{page, kPageTokens};
+        continue;
+      }
+      const int k = j - mid;
+      const int64_t left = len - static_cast<int64_t>(n + k) * kPageTokens;
+      const int valid = left < kPageTokens ? static_cast<int>(left) : kPageTokens;
+      const int64_t page = k < kTailPages ? static_cast<int64_t>(__builtin_amdgcn_readfirstlane(cs.late[j]))
+                                          : lookup_page(v, b, static_cast<int64_t>(n) + k);
+      if (page >= 0 && valid > 0) return attn::PageRef{page, valid};
+    }
+  }
+};
+
 template <int GR, bool APPEND, bool F16, bool ONLINE = false>
 __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p) {
   constexpr int G = 4;
   constexpr int kStageBytes = kWaves * attn::kStageVecs * 16;
   constexpr int kPbufFloats = (G * 32 + G + 3) / 4 * 4;
-  static_assert(kMaxSelectBlocks * 4 <= 2 * attn::kStageVecs * 16, "keys fit the page slots of waves 0 and 1");
+  constexpr int kSlotBytes = attn::kStageVecs * 16;
+  static_assert(kMaxSelectBlocks * 4 <= 2 * kSlotBytes, "keys fit the page slots of waves 0 and 1");
   static_assert(sizeof(attn::CombineRowsSmem<G, kWaves>) <= kStageBytes, "combine fits the page slots");
+  static_assert(kEarly <= kWave, "one lane per early lookup");
   const int g = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
@@ -310,51 +440,63 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   __shared__ __align__(16) unsigned char smem[kStageBytes + kWaves * kPbufFloats * 4];
   __shared__ __align__(16) float q_t[G * D];
   __shared__ uint32_t hist[256];
-  __shared__ int32_t ids[kStagedIds];
-  __shared__ int32_t pre_ids[kMaxPrePages];
-  __shared__ int s_count;
+  __shared__ ClaimSmem cl;
   uint32_t* keys = reinterpret_cast<uint32_t*>(smem);
   uint4* stage = reinterpret_cast<uint4*>(smem) + wave * attn::kStageVecs;
   float* pbuf = reinterpret_cast<float*>(smem + kStageBytes) + wave * kPbufFloats;
   const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
 
   const int64_t out_row = static_cast<int64_t>(b) * p.v.kv_heads + g;
+  // the group's query rows, loaded at entry (their latency overlaps the append)
+  const float q_entry = q_group[tid % (G * D)];
   int64_t len = p.seq_len[b];
   int n = p.sealed[b];
 
-  // ---- 1. append + seal (decode step) ---------------------------------------
+  // ---- 1. append + seal (decode step; arrival read at the end, as above) ------
+  // A step that seals a block appends and seals here, before the scoring.
+  // Otherwise nothing reads the new token before the page walk: wave 0
+  // stores it at the start of the walk phase, before it lists the tail (the
+  // tail page's id and the token are loaded now; their latency overlaps the
+  // scoring).
+  SeqCommit commit{};
+  bool deferred = false;
+  int64_t tail_page = -1;
+  ushort4 token{};
   if (APPEND) {
-    const int gen = p.generation ? p.generation[b] : 0;
-    int added = 0;
-    const bool appended =
-        append_seal_head<G, F16, ONLINE>(p, b, g, len, n, added, reinterpret_cast<float*>(smem));
-    __syncthreads();  // representatives visible to the scoring below
-    if (tid == 0 && atomicAdd(&p.arrive[b], 1) == p.v.kv_heads - 1) {
-      if (appended) {
-        p.seq_len[b] = static_cast<int32_t>(len);
-        p.sealed[b] = n;
-        if (p.generation) p.generation[b] = gen + added;
-      }
-      p.arrive[b] = 0;
+    commit.gen = p.generation ? p.generation[b] : 0;
+    if (append_seals(p, len, n)) {
+      commit.appended =
+          append_seal_head<G, F16, ONLINE>(p, b, g, len, n, commit.added, reinterpret_cast<float*>(smem));
+    } else {
+      deferred = true;
+      tail_page = table_page(p.v, b, len / kPageTokens);
+      if (wave == 0) token = token_quad<F16>(p, b, g, lane);
     }
+    if (tid == 0) commit.arrived = atomicAdd(&p.arrive[b], 1);
   }
 
   attn::WaveState<G> st;
   st.reset();
   const attn::LaneGeom lg = attn::lane_geom(p.v, g, lane);
 
-  // ---- 2. score + select; waves 1.. attend forced blocks meanwhile -----------
-  // pre_init init blocks [0, pre_init) and pre_local local blocks
-  // [n - pre_local, n) are attended during the selection: in the ascending
-  // selection they are the first pre_init and the last pre_local ids.
-  int pre_init = 0, pre_local = 0;
-  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) {
-    if (tid == 0) {
-      flag_status(p.v.status, kStatusCapacity);
-      p.counts[out_row] = 0;
-      s_count = 0;
-    }
-  } else {
+  // ---- 2. score; the forced blocks' pages looked up meanwhile ----------------
+  const bool n_ok = n >= 0 && n <= p.rep_stride && n <= kMaxSelectBlocks;
+  const sel::Budget bs =
+      n_ok ? sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride)
+           : sel::Budget{0, 0, 0, false, true};
+  // forced blocks: [0, init_f) and [n - local_f, n); every block if all are taken
+  int init_f = 0, local_f = 0;
+  if (!bs.bad) {
+    init_f = bs.take_all ? n : bs.init_n;
+    local_f = bs.take_all ? 0 : n - (bs.local_first > bs.init_n ? bs.local_first : bs.init_n);
+  }
+  const int e_init = init_f < kEarly ? init_f : kEarly;
+  const int e_local = local_f < kEarly - e_init ? local_f : kEarly - e_init;
+  const int F = e_init + e_local;
+  int32_t early_page = -1;
+  if (wave == kWaves - 1 && lane < F)
+    early_page = static_cast<int32_t>(lookup_page(p.v, b, lane < e_init ? lane : n - e_local + (lane - e_init)));
+  if (n_ok) {
     sel::ScoreArgs a{};
     a.query = p.query;
     a.reps = p.reps;
@@ -365,63 +507,84 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
     a.group = G;
     a.rep_heads = p.rep_heads;
     a.rep_stride = p.rep_stride;
-    sel::load_query_t<kThreads>(a, q_t);
+    static_assert(G * D == kThreads, "one query element per thread");
+    q_t[(tid % D) * G + tid / D] = q_entry;
     __syncthreads();
     sel::score_blocks_vec<GR, 2, kThreads>(a, q_t, n, keys, nullptr, tid);
-    const sel::Budget bs =
-        sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
-    // one forced page per wave that has a free slot: wave 1's slot is free
-    // unless the keys (4 bytes per block) reach into it (a second page per
-    // wave measured slower: each wave keeps one page in flight, so it costs a
-    // whole load latency while the selection has already ended)
-    const int pre_first = n * 4 <= attn::kStageVecs * 16 ? 1 : 2;
-    const int pre_cap = kWaves - pre_first;
-    if (!bs.bad) {
-      // local blocks not already init blocks, then init blocks
-      const int local_n = n - (bs.local_first > bs.init_n ? bs.local_first : bs.init_n);
-      pre_local = local_n < pre_cap ? local_n : pre_cap;
-      pre_init = bs.init_n < pre_cap - pre_local ? bs.init_n : pre_cap - pre_local;
-      if (tid < pre_init + pre_local) pre_ids[tid] = tid < pre_init ? tid : n - pre_local + (tid - pre_init);
+  }
+  if (ONLINE && deferred && tail_page >= 0) {
+    // the group's query rows of this step to the ring (read by later seals)
+    const int64_t slot = len % p.online.ring_tokens;
+    const int h = g * G + tid / D;
+    p.online.ring[((static_cast<int64_t>(b) * p.online.query_heads + h) * p.online.ring_tokens + slot) * D +
+                  tid % D] = q_entry;
+  }
+  if (wave == kWaves - 1) cl.early[lane] = early_page;
+  if (tid == 0) {
+    cl.next = 0;
+    cl.late_ready = 0;
+  }
+  if (deferred && tail_page >= 0) {
+    commit.appended = true;
+    len += 1;
+  }
+  // the tail after this step's append (the walk's view: a length below the
+  // sealed blocks is flagged and walked as no tail)
+  int wn = n;
+  int64_t wlen = len;
+  if (wn < 0 || wlen < static_cast<int64_t>(wn) * kPageTokens) {
+    if (tid == 0) flag_status(p.v.status, kStatusBadLength);
+    if (wn < 0) wn = 0;
+    wlen = static_cast<int64_t>(wn) * kPageTokens;
+  }
+  const int64_t tail_tokens = wlen - static_cast<int64_t>(wn) * kPageTokens;
+  const int tail_pages = static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
+  __syncthreads();  // keys, the early pages and the claim counter visible
+
+  // ---- 3. select (wave 0) and walk (every wave, claimed positions) -------------
+  if (wave == 0) {
+    if (deferred) {
+      if (tail_page >= 0) store_token_quad(p, tail_page, len - 1, g, lane, token);
+      else if (lane == 0) flag_status(p.v.status, kStatusCapacity);
     }
-    __syncthreads();  // keys and pre_ids visible
-    if (bs.bad) {
-      if (tid == 0) {
-        flag_status(p.v.status, kStatusBadBudget);
+    int count = 0;
+    if (!n_ok || bs.bad) {
+      if (lane == 0) {
+        flag_status(p.v.status, n_ok ? kStatusBadBudget : kStatusCapacity);
         p.counts[out_row] = 0;
-        s_count = 0;
       }
     } else {
-      const int pre_pages = pre_init + pre_local;
-      if (wave == 0) {
-        const int count =
-            sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride, p.sel_stride, ids);
-        if (lane == 0) {
-          p.counts[out_row] = count;
-          s_count = count;
-        }
-      } else if (wave >= pre_first && wave - pre_first < pre_pages) {
-        const attn::PageList Lp{pre_ids, static_cast<int64_t>(n) * kPageTokens, n, pre_pages, pre_pages};
-        st.attend_staged_mfma(p.v, b, Lp, wave - pre_first, pre_pages, kWaves - pre_first, lg, lane, g, stage,
-                              pbuf, q_group, p.qscale);
-      }
+      count = sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride, p.sel_stride, cl.late);
+      if (lane == 0) p.counts[out_row] = count;
     }
+    // late positions: the selected blocks not listed early, then the tail
+    // pages; in place over the ids (position j reads id e_init + j >= j)
+    const int mid = count - F > 0 ? count - F : 0;
+    const int listed = mid + (tail_pages < kTailPages ? tail_pages : kTailPages);
+    for (int j0 = 0; j0 < listed; j0 += kWave) {
+      const int j = j0 + lane;
+      int64_t page = -1;
+      if (j < mid) {
+        page = lookup_page(p.v, b, cl.late[e_init + j]);
+      } else if (j < listed) {
+        page = lookup_page(p.v, b, static_cast<int64_t>(wn) + (j - mid));
+      }
+      __builtin_amdgcn_wave_barrier();  // every lane has read its id before any lane writes
+      if (j < listed) cl.late[j] = static_cast<int32_t>(page);
+    }
+    if (lane == 0) {
+      cl.late_mid = mid;
+      cl.late_n = mid + tail_pages;
+    }
+    // the appended token has reached memory before a wave can claim the tail
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    if (lane == 0) __hip_atomic_store(&cl.late_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  __syncthreads();
-
-  // ---- 3. attend the other selected blocks and the tail ---------------------------
-  attn::PageList L{ids + pre_init, 0, 0, 0, 0};
-  L.len = len;
-  L.sealed = n;
-  L.n_sel = s_count - pre_init - pre_local;
-  if (L.n_sel < 0) L.n_sel = 0;
-  if (L.sealed < 0 || L.len < static_cast<int64_t>(L.sealed) * kPageTokens) {
-    flag_status(p.v.status, kStatusBadLength);
-    if (L.sealed < 0) L.sealed = 0;
-    L.len = static_cast<int64_t>(L.sealed) * kPageTokens;
-  }
-  const int64_t tail_tokens = L.len - static_cast<int64_t>(L.sealed) * kPageTokens;
-  L.total = L.n_sel + static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
-  st.attend_staged_mfma(p.v, b, L, wave, L.total, kWaves, lg, lane, g, stage, pbuf, q_group, p.qscale);
+  const bool waits = wave != 0 && wave * kSlotBytes < n * 4;  // the keys reach into this wave's page slot
+  if (waits) wait_late(cl);
+  ClaimPages src{cl, p.v, b, lane, F, wn, wlen};
+  src.ready = wave == 0 || waits;
+  st.attend_staged(p.v, src, lg, lane, g, stage, pbuf, q_group, p.qscale);
   __syncthreads();  // every wave is done with its slot before the combine reuses the area
 
   attn::CombineRowsSmem<G, kWaves>& cs = *reinterpret_cast<attn::CombineRowsSmem<G, kWaves>*>(smem);
@@ -434,6 +597,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
     attn::combine_element_rows<G, kWaves>(cs, h, d, mx, lw, aw);
     p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
   }
+  if (APPEND && tid == 0) commit_sequence(p, b, len, n, commit);
 }
 
 // Decode step with the InfLLM online seal (fp32 K/V, one representative per
