@@ -74,9 +74,10 @@ def parse():
                          "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers; "
                          "store: seal writeback behind decoding and store -> pool prefetch; "
                          "layer: decode step with its q/k/v producer and o-proj consumer")
-    ap.add_argument("--select", default="auto", choices=["auto", "single", "split"],
+    ap.add_argument("--select", default="auto", choices=["auto", "single", "split", "chunked"],
                     help="separate selection launch: one workgroup per list, scoring split over 256-block "
-                         "workgroups, or the library's preference")
+                         "workgroups (two launches), lists in chunks of 1024-2048 blocks (one launch), or the default "
+                         "(stress workload: chunked; decode workload: the library's preference)")
     ap.add_argument("--chunk", type=int, default=None,
                     help="stress workload: pages per attention chunk (0 = split schedule instead)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
@@ -200,6 +201,8 @@ def main():
         args.select == "auto" and sa.score_select_split_preferred(L[0].kv, hkv, budget, init, local))
     scores = (torch.zeros((batch, hkv, L[0].kv.rep_stride), dtype=torch.float32, device="cuda")
               if split_select else None)
+    select_ws = (sa.score_select_chunked_workspace(L[0].kv, hkv, budget, init, local)[0]
+                 if args.select == "chunked" else None)
 
     def layer_launches(ly, s, e=None):
         """One layer of one decode step; e = 4 timing events (append, select, attention)."""
@@ -221,6 +224,9 @@ def main():
             if split_select:
                 sa.score_select_split(ly.kv, ly.q[s], hkv, budget, init, local, selected=ly.selected,
                                       counts=ly.counts, scores=scores, status=status)
+            elif select_ws is not None:
+                sa.score_select_chunked(ly.kv, ly.q[s], hkv, budget, init, local, select_ws, selected=ly.selected,
+                                        counts=ly.counts, status=status)
             else:
                 sa.score_select(ly.kv, ly.q[s], hkv, budget, init, local, selected=ly.selected, counts=ly.counts,
                                 status=status)
@@ -363,7 +369,8 @@ def main():
                    "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
                    "init_blocks": init, "local_blocks": local, "page_tokens": PAGE, "splits": splits,
                    "launches_per_layer": launches,
-                   "selection": None if launches < 3 else ("split" if split_select else "single")},
+                   "selection": None if launches < 3 else ("split" if split_select else
+                                                          "chunked" if select_ws is not None else "single")},
         "tokens_per_s": round(batch / (ms_per_step * 1e-3), 1),
         "launch": "hip graph per decode step" if graph else "eager",
         "eager_us_per_layer": round(eager_ms * 1000.0 / args.steps / layers, 3),

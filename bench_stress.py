@@ -120,11 +120,15 @@ def run(args):
     ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, splits)
     workspace = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
+    # mixed lengths: the chunked selection (long lists spread over workgroups)
     select_mode = getattr(args, "select", "auto")
-    split_select = select_mode == "split" or (
-        select_mode == "auto" and sa.score_select_split_preferred(L[0].kv, HKV, sel_stride, INIT, LOCAL, sel_stride))
+    if select_mode == "auto":
+        select_mode = "chunked"
+    split_select = select_mode == "split"
     scores = (torch.zeros((B, HKV, L[0].kv.rep_stride), dtype=torch.float32, device="cuda")
               if split_select else None)
+    select_ws = (sa.score_select_chunked_workspace(L[0].kv, HKV, sel_stride, INIT, LOCAL, sel_stride)[0]
+                 if select_mode == "chunked" else None)
 
     def attend(ly, s):
         if chunk > 0:
@@ -141,6 +145,9 @@ def run(args):
         if split_select:
             sa.score_select_split(ly.kv, ly.q[s], HKV, sel_stride, INIT, LOCAL, selected=selected, counts=counts,
                                   scores=scores, status=status, sel_stride=sel_stride, budgets=budgets_d)
+        elif select_ws is not None:
+            sa.score_select_chunked(ly.kv, ly.q[s], HKV, sel_stride, INIT, LOCAL, select_ws, selected=selected,
+                                    counts=counts, status=status, sel_stride=sel_stride, budgets=budgets_d)
         else:
             sa.score_select(ly.kv, ly.q[s], HKV, sel_stride, INIT, LOCAL, selected=selected, counts=counts,
                             status=status, sel_stride=sel_stride, budgets=budgets_d)
@@ -216,7 +223,7 @@ def run(args):
                    "budget_blocks": {"16": int((klass == 0).sum()), "64": int((klass == 1).sum()),
                                      "full": int((klass == 2).sum())},
                    "init_blocks": INIT, "local_blocks": LOCAL, "chunk_pages": chunk, "max_chunks": max_chunks,
-                   "splits": splits, "selection": "split" if split_select else "single"},
+                   "splits": splits, "selection": select_mode},
         "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
         "achieved_layer_hbm_gbps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "kernels_us": {"attention": round(kernel_us, 3), "attention_in_step": round(att, 3),

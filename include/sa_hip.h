@@ -215,6 +215,26 @@ int sa_hip_score_select_split(const sa_paged_kv* kv, const float* query,
                               int32_t* counts, float* scores, int32_t* status,
                               void* stream);
 
+/* The same selection as one launch that spreads long lists over the device:
+ * a workgroup scores at most 1024 consecutive blocks of a (sequence, group)
+ * list (2048 once the lists outnumber the compute units); a list of one
+ * such chunk selects on the spot, the chunks of a longer
+ * list hand their keys to the last of them to finish, which selects.  For
+ * batches of mixed lengths, where one workgroup per list leaves the compute
+ * units that drew short lists idle while others walk long ones.  A budget
+ * that takes every block skips the scoring.  workspace: at least
+ * sa_hip_score_select_chunked_workspace_bytes(kv, params) bytes, zeroed
+ * once when allocated; every call leaves its arrival counters at zero, and
+ * calls that share a workspace must not run concurrently.  Needs 16-byte
+ * aligned representatives and rep_stride % 4 == 0.  ids and counts are bit-
+ * identical to sa_hip_score_select's (selection.cpp:96-147 per group). */
+size_t sa_hip_score_select_chunked_workspace_bytes(const sa_paged_kv* kv,
+                                                   const sa_select_params* params);
+int sa_hip_score_select_chunked(const sa_paged_kv* kv, const float* query,
+                                const sa_select_params* params, int32_t* selected,
+                                int32_t* counts, void* workspace, size_t workspace_bytes,
+                                int32_t* status, void* stream);
+
 /* 1 when sa_hip_score_select_split is expected to be the faster form for
  * this geometry (fewer (sequence, group) lists than compute units), else 0. */
 int sa_hip_score_select_split_preferred(const sa_paged_kv* kv,

@@ -429,6 +429,27 @@ int sa_hip_score_select_split(const sa_paged_kv* kv, const float* query, const s
   return check_hip(sa::launch_score_select_split(l, as_stream(stream)), "score_select_split launch");
 }
 
+size_t sa_hip_score_select_chunked_workspace_bytes(const sa_paged_kv* kv, const sa_select_params* params) {
+  if (!kv || !params || kv->batch <= 0 || params->select_groups <= 0 || kv->rep_stride <= 0) return 0;
+  return sa::score_select_chunked_workspace_bytes(kv->batch, params->select_groups, kv->rep_stride);
+}
+
+int sa_hip_score_select_chunked(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
+                                int32_t* selected, int32_t* counts, void* workspace, size_t workspace_bytes,
+                                int32_t* status, void* stream) {
+  sa::SelectLaunch l;
+  if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, "score_select_chunked", &l))
+    return e;
+  if (!sa::score_select_chunked_supported(l))
+    return fail(SA_HIP_EINVAL, "score_select_chunked: representatives must be 16-byte aligned with rep_stride a "
+                               "multiple of 4");
+  const size_t need = sa::score_select_chunked_workspace_bytes(kv->batch, params->select_groups, kv->rep_stride);
+  if (!workspace || workspace_bytes < need)
+    return fail(SA_HIP_EINVAL, "score_select_chunked: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  return check_hip(sa::launch_score_select_chunked(l, workspace, as_stream(stream)), "score_select_chunked launch");
+}
+
 int sa_hip_score_select_split_preferred(const sa_paged_kv* kv, const sa_select_params* params) {
   if (!kv || !params || params->select_groups <= 0) return 0;
   // measured on MI355X: spreading the scoring pays while the lists alone

@@ -49,26 +49,6 @@ __device__ inline f32x4_t load_nt4(const float* p) {
 // invalidate the whole L2 of the XCD, and with it the x rows every other
 // workgroup is reading).  The writer waits for its stores to complete before
 // the arrival counter is incremented.
-__device__ inline void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline float load_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// The last of `arrivals` workgroups to reach the counter gets true and
-// resets it; every thread calls it after its handed-over stores.
-__device__ inline bool last_arrival(int32_t* ctr, int arrivals, int* s_last) {
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const bool last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == arrivals - 1;
-    if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_last = last;
-  }
-  __syncthreads();
-  return *s_last;
-}
-
 __device__ inline float block_sum(float v, float* red) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);

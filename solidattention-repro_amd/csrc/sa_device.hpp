@@ -28,6 +28,33 @@ __device__ inline void flag_status(int32_t* status, int32_t bits) {
   if (status) atomicOr(status, bits);
 }
 
+// ---- values handed between workgroups -------------------------------------
+// A workgroup that hands values to another (possibly on another XCD, whose
+// L2 is not shared) stores them with agent-scope atomic stores and the
+// receiver reads them with agent-scope atomic loads.  An agent-scope fence
+// (__threadfence) would write back and invalidate the whole L2 of the XCD.
+template <class T>
+__device__ inline void store_agent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ inline T load_agent(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The last of `arrivals` workgroups to reach the counter gets true and
+// resets it to zero; every thread calls it after its handed-over stores.
+__device__ inline bool last_arrival(int32_t* ctr, int arrivals, int* s_last) {
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == arrivals - 1;
+    if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = last;
+  }
+  __syncthreads();
+  return *s_last;
+}
+
 // ---- FP16 ------------------------------------------------------------------
 // v_cvt_f32_f16 is exact for every FP16 input (subnormals included), so it
 // equals the reference's bit-level decode (attention_reference.cpp:30-53).

@@ -77,6 +77,12 @@ struct SelectLaunch {
 hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream);
 // scoring over chunks of 256 blocks into s.scores, then selection from them
 hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream);
+// lists split into chunks of 512 blocks, one launch: workspace of
+// score_select_chunked_workspace_bytes(), its arrival counters zeroed once
+// (each launch leaves them at zero); needs 16-byte representative loads
+size_t score_select_chunked_workspace_bytes(int64_t batch, int32_t select_groups, int32_t rep_stride);
+bool score_select_chunked_supported(const SelectLaunch& s);
+hipError_t launch_score_select_chunked(const SelectLaunch& s, void* workspace, hipStream_t stream);
 
 // ---- query producer / output consumer (producer.hip) -----------------------
 struct LinearLaunch {

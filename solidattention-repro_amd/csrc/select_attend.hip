@@ -243,17 +243,19 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
       s_count = 0;
     }
   } else {
-    if (tid < G * D) q_s[tid] = q_entry;
-    __syncthreads();
-    if (kPrefetch) {
-      sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr, pre, have_pre);
-    } else {
-      sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr);
-    }
-    __syncthreads();
-    st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
     const sel::Budget bs =
         sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
+    if (!bs.take_all) {  // (a budget that takes every block needs no scores)
+      if (tid < G * D) q_s[tid] = q_entry;
+      __syncthreads();
+      if (kPrefetch) {
+        sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr, pre, have_pre);
+      } else {
+        sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr);
+      }
+      __syncthreads();
+    }
+    st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
     if (bs.bad) {
       if (tid == 0) {
         flag_status(p.v.status, kStatusBadBudget);
@@ -496,7 +498,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   int32_t early_page = -1;
   if (wave == kWaves - 1 && lane < F)
     early_page = static_cast<int32_t>(lookup_page(p.v, b, lane < e_init ? lane : n - e_local + (lane - e_init)));
-  if (n_ok) {
+  if (n_ok && !bs.take_all) {  // (a budget that takes every block needs no scores)
     sel::ScoreArgs a{};
     a.query = p.query;
     a.reps = p.reps;

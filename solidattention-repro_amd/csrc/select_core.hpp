@@ -334,10 +334,11 @@ __device__ inline void score_vec(const ScoreArgs& a, const float* q_t, int blk0,
 // keys/scores of blocks [0, n), NB per lane, by the kThreads threads with
 // index tid; the loads of a lane's last group may cover blocks
 // n..rep_stride-1 (inside the row, discarded).
+// Blocks [lo, n) (lo a multiple of NB).
 template <int GR, int NB, int kThreads>
 __device__ inline void score_blocks_vec(const ScoreArgs& a, const float* q_t, int n, uint32_t* keys, float* scores,
-                                        int tid) {
-  for (int blk0 = NB * tid; blk0 < n; blk0 += NB * kThreads) {
+                                        int tid, int lo = 0) {
+  for (int blk0 = lo + NB * tid; blk0 < n; blk0 += NB * kThreads) {
     float sc[NB];
     score_vec<GR, NB>(a, q_t, blk0, sc);
 #pragma unroll

@@ -89,6 +89,8 @@ EXPORTS = {
     "sa_hip_pages_to_host_async": (C.c_int, [_P, _I64, _I64, _P, _I32, _P, _P, _P, _P]),
     "sa_hip_score_select_split": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _P, _P]),
     "sa_hip_score_select_split_preferred": (C.c_int, [_KV, C.POINTER(SelectParamsStruct)]),
+    "sa_hip_score_select_chunked_workspace_bytes": (_SZ, [_KV, C.POINTER(SelectParamsStruct)]),
+    "sa_hip_score_select_chunked": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _SZ, _P, _P]),
     "sa_hip_sparse_decode_attention_chunked": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _I32,
                                                          _P, _P]),
     "sa_hip_contiguous_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
@@ -262,6 +264,36 @@ def score_select_split(kv: PagedKV, query, select_groups, budget, init, local, s
     check(lib().sa_hip_score_select_split(C.byref(s), _ptr(query), C.byref(params), _ptr(selected), _ptr(counts),
                                           _ptr(scores), _ptr(status), _stream(stream)), "score_select_split")
     return selected, counts, scores
+
+
+def score_select_chunked_workspace(kv: PagedKV, select_groups, budget, init, local, sel_stride=None):
+    """A zeroed workspace for score_select_chunked (reusable across calls that
+    do not overlap)."""
+    import torch
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride or budget, 0, None)
+    s = kv.struct()
+    nbytes = int(lib().sa_hip_score_select_chunked_workspace_bytes(C.byref(s), C.byref(params)))
+    return torch.zeros(max(nbytes // 4, 1), dtype=torch.int32, device="cuda"), nbytes
+
+
+def score_select_chunked(kv: PagedKV, query, select_groups, budget, init, local, workspace, selected=None,
+                         counts=None, status=None, sel_stride=None, stream=None, budgets=None):
+    """score_select as one launch that splits long lists over workgroups of at
+    most 1024 or 2048 blocks (workspace from score_select_chunked_workspace)."""
+    import torch
+    sel_stride = sel_stride or budget
+    dev = query.device
+    if selected is None:
+        selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
+    s = kv.struct()
+    check(lib().sa_hip_score_select_chunked(C.byref(s), _ptr(query), C.byref(params), _ptr(selected),
+                                            _ptr(counts), _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                            _ptr(status), _stream(stream)), "score_select_chunked")
+    return selected, counts
 
 
 def score_select_split_preferred(kv: PagedKV, select_groups, budget, init, local, sel_stride=None) -> bool:

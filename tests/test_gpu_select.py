@@ -12,36 +12,51 @@ from paged_case import D, make_case
 pytestmark = pytest.mark.gpu
 
 
-def gpu_select(hip, case, select_groups, budget, init, local, sel_stride=None, split=False):
+MODES = ("single", "split", "chunked")
+
+
+def gpu_select(hip, case, select_groups, budget, init, local, sel_stride=None, split=False, mode=None):
+    """mode: "single" (one workgroup per list), "split" (scores in a first
+    launch) or "chunked" (lists in chunks of blocks, one launch; run twice
+    on one workspace, which the first call must leave reusable)."""
+    mode = mode or ("split" if split else "single")
     kv = device_kv(case)
     sel_stride = sel_stride or budget
     scores = torch.zeros((case.batch, select_groups, case.rep_stride), dtype=torch.float32, device="cuda")
     st = status_tensor()
-    if split:
+    if mode == "split":
         sel, cnt, _ = hip.score_select_split(kv, to_dev(case.query), select_groups, budget, init, local,
                                              scores=scores, status=st, sel_stride=sel_stride)
+    elif mode == "chunked":
+        ws, _ = hip.score_select_chunked_workspace(kv, select_groups, budget, init, local, sel_stride)
+        for _ in range(2):
+            sel, cnt = hip.score_select_chunked(kv, to_dev(case.query), select_groups, budget, init, local, ws,
+                                                status=st, sel_stride=sel_stride)
+        scores = None
     else:
         sel, cnt = hip.score_select(kv, to_dev(case.query), select_groups, budget, init, local, scores=scores,
                                     status=st, sel_stride=sel_stride)
     torch.cuda.synchronize()
     assert int(st.item()) == 0
-    return sel.cpu().numpy(), cnt.cpu().numpy(), scores.cpu().numpy()
+    return sel.cpu().numpy(), cnt.cpu().numpy(), None if scores is None else scores.cpu().numpy()
 
 
-def check(hip, case, select_groups, budget, init, local):
-    """Both forms, one workgroup per list and the split scoring, against the
-    oracle: same ids, same score bits."""
+def check(hip, case, select_groups, budget, init, local, modes=MODES):
+    """Every form (one workgroup per list, the split scoring, the chunked
+    lists) against the oracle: same ids, and same score bits where the form
+    returns scores."""
     esel, ecnt, esc = O.paged_score_select(case.query, case.reps, case.sealed, case.batch, case.hq, case.hkv, D,
                                            case.rep_heads, case.rep_stride, select_groups, budget, init, local,
                                            want_scores=True)
-    for split in (False, True):
-        sel, cnt, sc = gpu_select(hip, case, select_groups, budget, init, local, split=split)
-        assert np.array_equal(cnt, ecnt), split
+    for mode in modes:
+        sel, cnt, sc = gpu_select(hip, case, select_groups, budget, init, local, mode=mode)
+        assert np.array_equal(cnt, ecnt), mode
         for b in range(case.batch):
             n = int(case.sealed[b])
             for g in range(select_groups):
-                assert sel[b, g, : cnt[b, g]].tolist() == esel[b, g, : ecnt[b, g]].tolist(), (split, b, g)
-                assert np.array_equal(sc[b, g, :n].view(np.uint32), esc[b, g, :n].view(np.uint32)), (split, b, g)
+                assert sel[b, g, : cnt[b, g]].tolist() == esel[b, g, : ecnt[b, g]].tolist(), (mode, b, g)
+                if sc is not None:
+                    assert np.array_equal(sc[b, g, :n].view(np.uint32), esc[b, g, :n].view(np.uint32)), (mode, b, g)
 
 
 @pytest.mark.parametrize("group,hkv", [(2, 8), (4, 8), (1, 8), (8, 2)])
@@ -51,11 +66,53 @@ def test_group_selection_bit_exact(hip, group, hkv):
 
 
 def test_unpadded_rep_stride_scalar_path(hip):
-    """rep_stride not a multiple of 4: the one-block-per-lane scoring path."""
+    """rep_stride not a multiple of 4: the one-block-per-lane scoring path;
+    the chunked form (16-byte loads only) refuses the layout."""
     case = make_case(109, 3, 16, 8, [32 * 129, 32 * 77 + 3, 32 * 7], table_stride=131, rep_stride=131)
     assert case.rep_stride % 4 != 0
-    check(hip, case, 8, 32, 2, 4)
-    check(hip, case, 1, 32, 2, 4)
+    check(hip, case, 8, 32, 2, 4, modes=("single", "split"))
+    check(hip, case, 1, 32, 2, 4, modes=("single", "split"))
+    kv = device_kv(case)
+    ws, _ = hip.score_select_chunked_workspace(kv, 8, 32, 2, 4)
+    with pytest.raises(RuntimeError):
+        hip.score_select_chunked(kv, to_dev(case.query), 8, 32, 2, 4, ws)
+
+
+def test_chunked_mixed_lengths_and_budgets(hip):
+    """Lists of 1 to 3 chunks of 1024 blocks (up to 2400 blocks) in one batch with
+    per-sequence budgets, one of which takes every block (no scoring) and one
+    of which is out of range (flagged, nothing selected): ids and counts
+    equal the oracle's per sequence, over three calls on one workspace."""
+    lengths = [32 * 2400 + 5, 32 * 511, 32 * 513, 32 * 1024, 32 * 40 + 7, 32 * 1700]
+    case = make_case(150, len(lengths), 16, 8, lengths, planted=8)
+    kv = device_kv(case)
+    budgets = np.array([64, 64, 513, 16, 16, 300], np.int32)  # 513 >= 513 blocks: every block
+    bd = to_dev(budgets)
+    q = to_dev(case.query)
+    ws, _ = hip.score_select_chunked_workspace(kv, 8, 600, 4, 8)
+    expect = [O.paged_score_select(case.query[b:b + 1], case.reps[b:b + 1], case.sealed[b:b + 1], 1, 16, 8, D, 8,
+                                   case.rep_stride, 8, int(budgets[b]), 4, 8) for b in range(case.batch)]
+    assert (expect[2][1] == 513).all()  # the budget takes every block
+    for it in range(3):
+        print(f"case: chunked mixed lengths, call {it}", flush=True)
+        st = status_tensor()
+        sel, cnt = hip.score_select_chunked(kv, q, 8, 600, 4, 8, ws, status=st, sel_stride=600, budgets=bd)
+        torch.cuda.synchronize()
+        assert int(st.item()) == 0
+        c, s_ = cnt.cpu().numpy(), sel.cpu().numpy()
+        for b in range(case.batch):
+            esel, ecnt = expect[b]
+            assert np.array_equal(c[b], ecnt[0]), (it, b)
+            for g in range(8):
+                assert s_[b, g, : c[b, g]].tolist() == esel[0, g, : ecnt[0, g]].tolist(), (it, b, g)
+    # a budget below init + local is flagged and selects nothing for that sequence
+    bad = budgets.copy()
+    bad[3] = 5
+    st = status_tensor()
+    _, cnt = hip.score_select_chunked(kv, q, 8, 600, 4, 8, ws, status=st, sel_stride=600, budgets=to_dev(bad))
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_BAD_BUDGET
+    assert (cnt.cpu().numpy()[3] == 0).all()
 
 
 def test_shared_selection_per_query_head_reps(hip):
@@ -138,7 +195,7 @@ def test_split_capacity_flag(hip):
         assert s[1, g, : c[1, g]].tolist() == esel[0, g, : ecnt[0, g]].tolist()
 
 
-@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("split", [False, True, "chunked"])
 def test_selection_at_the_8192_block_limit(hip, split):
     """8192 sealed blocks (256K tokens) is the selection's limit: selected
     bit-exact with the oracle; 8193 blocks are flagged (capacity) and select
@@ -155,7 +212,11 @@ def test_selection_at_the_8192_block_limit(hip, split):
     st = status_tensor()
     scores = torch.zeros((1, hkv, rep_stride), dtype=torch.float32, device="cuda")
     print(f"case: {n} blocks split={split}", flush=True)
-    fn = hip.score_select_split if split else hip.score_select
+    if split == "chunked":
+        ws, _ = hip.score_select_chunked_workspace(kv, hkv, budget, 4, 8)
+        fn = lambda *a, scores=None, **k: hip.score_select_chunked(*a, ws, **k)  # noqa: E731
+    else:
+        fn = hip.score_select_split if split else hip.score_select
     res = fn(kv, to_dev(q), hkv, budget, 4, 8, scores=scores, status=st)
     sel, cnt = res[0], res[1]
     torch.cuda.synchronize()
@@ -164,7 +225,8 @@ def test_selection_at_the_8192_block_limit(hip, split):
                                            budget, 4, 8, want_scores=True)
     assert np.array_equal(cnt.cpu().numpy(), ecnt)
     assert np.array_equal(sel.cpu().numpy(), esel)
-    assert np.array_equal(scores.cpu().numpy()[..., :n].view(np.uint32), esc[..., :n].view(np.uint32))
+    if split != "chunked":
+        assert np.array_equal(scores.cpu().numpy()[..., :n].view(np.uint32), esc[..., :n].view(np.uint32))
     kv.sealed.fill_(n + 1)
     kv.seq_len.fill_((n + 1) * 32)
     st.zero_()
