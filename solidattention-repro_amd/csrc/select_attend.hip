@@ -17,10 +17,10 @@
 // and the same attention output within fp32 rounding (the waves visit the
 // pages in another order).
 //
-// Wave roles after scoring: wave 0 runs the radix select and the compaction
-// alone (no workgroup barrier) while waves 1..7 attend the last local blocks,
-// which are selected whatever the scores; then all 8 waves attend the rest
-// of the selected blocks and the tail, round robin starting at wave 0.
+// Wave roles after scoring: wave 0 selects alone (no workgroup barrier) while
+// waves 1..7 attend the forced blocks (init and local, selected whatever the
+// scores); then every wave attends its planned share of the other selected
+// blocks and the tail (the planned walk, below).
 //
 // Sequence counters: the 8 workgroups of a sequence all read seq_len,
 // sealed and generation; the last of them to arrive (a per-sequence arrival
@@ -174,6 +174,195 @@ __device__ inline void commit_sequence(const Params& p, int b, int64_t len, int 
   p.arrive[b] = 0;
 }
 
+// ---- the planned page walk (both fused kernels) ------------------------------
+// After the scoring every wave walks its own positions of one list:
+//   * positions [0, F): the forced blocks (init, then local: selected
+//     whatever the scores; at most kEarly), whose pages the last wave looked
+//     up while it scored; waves 1..7 take them round robin while wave 0
+//     selects;
+//   * positions [F, F + late): the other selected blocks, then the tail
+//     pages, listed by wave 0 after its selection and split into contiguous
+//     ranges so that every wave's total count of positions is balanced
+//     (wave 0's selection counting as kSelectPages positions).
+// A wave that reaches the late positions before the list is out waits for it
+// (an LDS flag that wave 0 sets on every path).  No wave idles at a barrier
+// between the selection and the walk, and the plan depends only on the list:
+// every run attends the same pages in the same order on the same waves, so
+// the outputs are reproducible bit for bit.
+constexpr int kEarly = 64;      // forced blocks looked up before the selection
+constexpr int kTailPages = 64;  // tail pages listed by wave 0 (more are looked up when reached)
+// Wave 0's selection takes about as long as two pages of the walk (measured
+// at 16K-32K contexts), so its planned share is two positions smaller.
+constexpr int kSelectPages = 2;
+
+// Page of logical block blk of sequence b, or -1 (flagged) if there is none.
+__device__ inline int64_t lookup_page(const attn::PoolView& v, int b, int64_t blk) {
+  if (v.contig_tokens > 0) return blk;
+  if (blk < 0 || blk >= v.table_stride) {
+    flag_status(v.status, kStatusBadBlock);
+    return -1;
+  }
+  const int64_t page = v.table[static_cast<int64_t>(b) * v.table_stride + blk];
+  if (page < 0 || page >= v.num_pages) {
+    flag_status(v.status, kStatusBadPage);
+    return -1;
+  }
+  return page;
+}
+
+// LDS state of the planned walk (the late pages live in the caller's id array).
+struct ClaimSmem {
+  int late_ready;   // 1 once wave 0 has listed the late positions
+  int late_n;       // late positions: selected blocks, then tail pages
+  int late_mid;     // of which selected blocks
+  int tail_listed;  // tail pages with their page in the list (the rest looked up when reached)
+  int32_t early[kEarly];
+};
+
+__device__ inline void wait_late(ClaimSmem& cs) {
+  while (__hip_atomic_load(&cs.late_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+    __builtin_amdgcn_s_sleep(1);
+}
+
+// The forced blocks listed early: [0, e_init) and [n - e_local, n).
+struct Forced {
+  int e_init;
+  int e_local;
+  int F;
+};
+
+__device__ inline Forced forced_blocks(const sel::Budget& bs, int n) {
+  int init_f = 0, local_f = 0;  // every block is forced when the budget takes all
+  if (!bs.bad) {
+    init_f = bs.take_all ? n : bs.init_n;
+    local_f = bs.take_all ? 0 : n - (bs.local_first > bs.init_n ? bs.local_first : bs.init_n);
+  }
+  Forced f;
+  f.e_init = init_f < kEarly ? init_f : kEarly;
+  f.e_local = local_f < kEarly - f.e_init ? local_f : kEarly - f.e_init;
+  f.F = f.e_init + f.e_local;
+  return f;
+}
+
+// Lane `lane` of the looking-up wave: the page of forced position `lane`.
+__device__ inline int32_t early_page(const Params& p, int b, int n, const Forced& f, int lane) {
+  if (lane >= f.F) return -1;
+  return static_cast<int32_t>(lookup_page(p.v, b, lane < f.e_init ? lane : n - f.e_local + (lane - f.e_init)));
+}
+
+// Wave 0, after its selection (count ids ascending in late[]): the late
+// positions in place over the ids (position j reads id e_init + j >= j, all
+// lanes read before any writes), at most late_cap entries, then the flag.
+__device__ inline void list_late(const Params& p, int b, ClaimSmem& cl, int32_t* late, int late_cap, int count,
+                                 const Forced& f, int wn, int tail_pages, int lane) {
+  const int mid = count - f.F > 0 ? count - f.F : 0;
+  int tail_listed = tail_pages < kTailPages ? tail_pages : kTailPages;
+  if (mid + tail_listed > late_cap) tail_listed = late_cap - mid;
+  const int listed = mid + tail_listed;
+  for (int j0 = 0; j0 < listed; j0 += kWave) {
+    const int j = j0 + lane;
+    int64_t page = -1;
+    if (j < mid) {
+      page = lookup_page(p.v, b, late[f.e_init + j]);
+    } else if (j < listed) {
+      page = lookup_page(p.v, b, static_cast<int64_t>(wn) + (j - mid));
+    }
+    __builtin_amdgcn_wave_barrier();  // every lane has read its id before any lane writes
+    if (j < listed) late[j] = static_cast<int32_t>(page);
+  }
+  if (lane == 0) {
+    cl.late_mid = mid;
+    cl.late_n = mid + tail_pages;
+    cl.tail_listed = tail_listed;
+  }
+  // the wave's stores (an appended token among them) and LDS writes are
+  // complete before any wave can reach the late positions
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  if (lane == 0) __hip_atomic_store(&cl.late_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Page source of the walk: this wave's planned positions (see above); all
+// values wave-uniform.
+struct PlanPages {
+  ClaimSmem& cs;
+  const int32_t* late;
+  const attn::PoolView& v;
+  int b;
+  int wave;
+  int F;        // forced positions listed early
+  int n;        // sealed blocks
+  int64_t len;  // tokens (after this step's append)
+  int e_next;   // next forced position of this wave (F when done)
+  int l_next = 0;
+  int l_end = 0;
+  bool ready = false;
+
+  __device__ PlanPages(ClaimSmem& cs_, const int32_t* late_, const attn::PoolView& v_, int b_, int wave_, int F_,
+                       int n_, int64_t len_)
+      : cs(cs_), late(late_), v(v_), b(b_), wave(wave_), F(F_), n(n_), len(len_) {
+    e_next = wave == 0 ? F : wave - 1;
+  }
+
+  // Forced positions of wave w (>= 1): w - 1, w - 1 + 7, ... below F.
+  __device__ static int forced_count(int w, int F) {
+    if (w == 0 || w - 1 >= F) return 0;
+    return (F - (w - 1) + kWaves - 2) / (kWaves - 1);
+  }
+
+  // This wave's contiguous range of the late positions: every wave's total
+  // (forced + late) is T / 8 or T / 8 + 1 with T = positions + kSelectPages,
+  // wave 0 counting its selection as kSelectPages positions; the waves in
+  // order, wave 7 taking any remainder.
+  __device__ inline void plan_late(int late_n) {
+    const int total = F + late_n + kSelectPages;
+    int begin = 0;
+    for (int w = 0; w <= wave; ++w) {
+      const int target = total / kWaves + (w < total % kWaves ? 1 : 0);
+      const int want = target - (w == 0 ? kSelectPages : forced_count(w, F));
+      const int take = want > 0 ? want : 0;
+      if (w == wave) {
+        l_next = begin < late_n ? begin : late_n;
+        const int end = begin + take;
+        l_end = wave == kWaves - 1 ? late_n : (end < late_n ? end : late_n);
+      }
+      begin += take;
+    }
+  }
+
+  __device__ inline attn::PageRef next(bool wait) {
+    while (e_next < F) {
+      const int c = e_next;
+      e_next += kWaves - 1;
+      const int32_t page = __builtin_amdgcn_readfirstlane(cs.early[c]);
+      if (page >= 0) return attn::PageRef{page, kPageTokens};
+    }
+    if (!ready) {
+      if (!wait && __hip_atomic_load(&cs.late_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+        return attn::PageRef{0, -1};
+      wait_late(cs);
+      ready = true;
+      plan_late(__builtin_amdgcn_readfirstlane(cs.late_n));
+    }
+    const int mid = __builtin_amdgcn_readfirstlane(cs.late_mid);
+    const int tail_listed = __builtin_amdgcn_readfirstlane(cs.tail_listed);
+    while (l_next < l_end) {
+      const int j = l_next++;
+      if (j < mid) {
+        const int32_t page = __builtin_amdgcn_readfirstlane(late[j]);
+        if (page >= 0) return attn::PageRef{page, kPageTokens};
+        continue;
+      }
+      const int k = j - mid;
+      const int64_t left = len - static_cast<int64_t>(n + k) * kPageTokens;
+      const int valid = left < kPageTokens ? static_cast<int>(left) : kPageTokens;
+      const int64_t page = k < tail_listed ? static_cast<int64_t>(__builtin_amdgcn_readfirstlane(late[j]))
+                                           : lookup_page(v, b, static_cast<int64_t>(n) + k);
+      if (page >= 0 && valid > 0) return attn::PageRef{page, valid};
+    }
+    return attn::PageRef{0, 0};
+  }
+};
+
 // G = query heads per KV head; GR = query heads sharing one representative
 // row (G for per-KV-head representatives, 1 for per-query-head ones);
 // APPEND: decode step (append + seal first); F16: raw FP16 K/V input.
@@ -186,10 +375,10 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   const int lane = tid % kWave;
 
   __shared__ float q_s[G * D];
-  __shared__ uint32_t keys[kMaxSelectBlocks];  // block keys, then the selected ids
+  __shared__ uint32_t keys[kMaxSelectBlocks];  // block keys, then the selected ids, then the late pages
   __shared__ uint32_t hist[256];
   __shared__ attn::CombineSmem<G, kWaves> cs;
-  __shared__ int s_count;
+  __shared__ ClaimSmem cl;
 
   const int64_t out_row = static_cast<int64_t>(b) * p.v.kv_heads + g;
   // the group's query rows, loaded at entry (their latency overlaps the append)
@@ -233,74 +422,57 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   attn::WaveState<G> st;
   const attn::LaneGeom lg = attn::lane_geom(p.v, g, lane);
 
-  // ---- 2. score + select ------------------------------------------------------
-  int pre_pages = 0;  // local blocks [n - pre_pages, n) attended by waves 1.. during the selection
-  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) {
-    st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
-    if (tid == 0) {
-      flag_status(p.v.status, kStatusCapacity);
-      p.counts[out_row] = 0;
-      s_count = 0;
+  // ---- 2. score; the forced blocks' pages looked up meanwhile ----------------
+  const bool n_ok = n >= 0 && n <= p.rep_stride && n <= kMaxSelectBlocks;
+  const sel::Budget bs =
+      n_ok ? sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride)
+           : sel::Budget{0, 0, 0, false, true};
+  const Forced fb = forced_blocks(bs, n);
+  const int32_t early = wave == kWaves - 1 ? early_page(p, b, n, fb, lane) : -1;
+  if (n_ok && !bs.take_all) {  // (a budget that takes every block needs no scores)
+    if (tid < G * D) q_s[tid] = q_entry;
+    __syncthreads();
+    if (kPrefetch) {
+      sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr, pre, have_pre);
+    } else {
+      sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr);
     }
-  } else {
-    const sel::Budget bs =
-        sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
-    if (!bs.take_all) {  // (a budget that takes every block needs no scores)
-      if (tid < G * D) q_s[tid] = q_entry;
-      __syncthreads();
-      if (kPrefetch) {
-        sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr, pre, have_pre);
-      } else {
-        sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr);
-      }
-      __syncthreads();
-    }
-    st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D, p.qscale, lg.col);
-    if (bs.bad) {
-      if (tid == 0) {
-        flag_status(p.v.status, kStatusBadBudget);
+  }
+  if (wave == kWaves - 1) cl.early[lane] = early;
+  if (tid == 0) cl.late_ready = 0;
+  st.init(q_group, p.qscale, lg.col);
+  // the walk's view of the sequence (a length below the sealed blocks is
+  // flagged and walked as no tail)
+  int wn = n;
+  int64_t wlen = len;
+  if (wn < 0 || wlen < static_cast<int64_t>(wn) * kPageTokens) {
+    if (tid == 0) flag_status(p.v.status, kStatusBadLength);
+    if (wn < 0) wn = 0;
+    wlen = static_cast<int64_t>(wn) * kPageTokens;
+  }
+  const int tail_pages = static_cast<int>((wlen - static_cast<int64_t>(wn) * kPageTokens + kPageTokens - 1) /
+                                          kPageTokens);
+  __syncthreads();  // keys, the early pages and the flag visible
+
+  // ---- 3. select (wave 0) and walk (every wave, planned positions) -------------
+  int32_t* late = reinterpret_cast<int32_t*>(keys);  // the selected ids, then the late pages
+  if (wave == 0) {
+    int count = 0;
+    if (!n_ok || bs.bad) {
+      if (lane == 0) {
+        flag_status(p.v.status, n_ok ? kStatusBadBudget : kStatusCapacity);
         p.counts[out_row] = 0;
-        s_count = 0;
       }
     } else {
-      const int local_n = p.local_blocks < n ? p.local_blocks : n;
-      pre_pages = local_n < kWaves - 1 ? local_n : kWaves - 1;
-      if (wave == 0) {
-        const int count = sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride,
-                                               p.sel_stride, reinterpret_cast<int32_t*>(keys));
-        if (lane == 0) {
-          p.counts[out_row] = count;
-          s_count = count;
-        }
-      } else if (wave <= pre_pages) {
-        // forced local block n - wave: selected whatever the scores
-        const int64_t logical = n - wave;
-        const int64_t page = table_page(p.v, b, logical);
-        if (page < 0) {
-          flag_status(p.v.status, logical >= p.v.table_stride ? kStatusBadBlock : kStatusBadPage);
-        } else {
-          st.attend(p.v, attn::PageRef{page, kPageTokens}, lg);
-        }
-      }
+      count = sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride, p.sel_stride, late);
+      if (lane == 0) p.counts[out_row] = count;
     }
+    list_late(p, b, cl, late, kMaxSelectBlocks, count, fb, wn, tail_pages, lane);
   }
-  __syncthreads();
-
-  // ---- 3. attend the other selected blocks and the tail ---------------------------
-  attn::PageList L{reinterpret_cast<const int32_t*>(keys), 0, 0, 0, 0};
-  L.len = len;
-  L.sealed = n;
-  L.n_sel = s_count - pre_pages;  // the last pre_pages ids are n - pre_pages .. n - 1, already attended
-  if (L.sealed < 0 || L.len < static_cast<int64_t>(L.sealed) * kPageTokens) {
-    flag_status(p.v.status, kStatusBadLength);
-    if (L.sealed < 0) L.sealed = 0;
-    L.len = static_cast<int64_t>(L.sealed) * kPageTokens;
-  }
-  const int64_t tail_tokens = L.len - static_cast<int64_t>(L.sealed) * kPageTokens;
-  L.total = L.n_sel + static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
-  for (int i = wave; i < L.total; i += kWaves) {
-    const attn::PageRef pr = attn::resolve_page(p.v, b, i, L);
-    if (pr.valid <= 0) continue;
+  PlanPages src(cl, late, p.v, b, wave, fb.F, wn, wlen);
+  for (;;) {
+    const attn::PageRef pr = src.next(true);
+    if (pr.valid <= 0) break;
     st.attend(p.v, pr, lg);
   }
 
@@ -322,108 +494,11 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
 // One 8-wave workgroup per (sequence, KV head), one per CU (the eight 16 KiB
 // page slots).  After append + seal, all 512 threads score two blocks per lane
 // (8-byte representative loads); the keys borrow the page slots of waves 0
-// and 1.  Then every wave walks pages with the staged walk of attn_core.hpp
-// (pages HBM -> LDS by DMA, q.K on v_mfma_f32_16x16x32_f16), claiming list
-// positions one at a time from an LDS counter:
-//   * positions [0, F): the forced blocks (init, then local: selected
-//     whatever the scores; at most kEarly), whose pages the last wave looked
-//     up while it scored;
-//   * positions [F, F + late): the other selected blocks, then the tail
-//     pages, listed by wave 0 after its selection.
-// Waves 1..7 start on the forced blocks while wave 0 selects; a wave that
-// claims a late position before the list is out waits for it (an LDS flag
-// that wave 0 sets on every path).  No wave idles at a barrier between the
-// selection and the walk, and the waves end within about a page of each
-// other.
-constexpr int kEarly = 64;      // forced blocks looked up before the selection
-constexpr int kTailPages = 64;  // tail pages listed by wave 0 (more are looked up when claimed)
-
-// Page of logical block blk of sequence b, or -1 (flagged) if there is none.
-__device__ inline int64_t lookup_page(const attn::PoolView& v, int b, int64_t blk) {
-  if (v.contig_tokens > 0) return blk;
-  if (blk < 0 || blk >= v.table_stride) {
-    flag_status(v.status, kStatusBadBlock);
-    return -1;
-  }
-  const int64_t page = v.table[static_cast<int64_t>(b) * v.table_stride + blk];
-  if (page < 0 || page >= v.num_pages) {
-    flag_status(v.status, kStatusBadPage);
-    return -1;
-  }
-  return page;
-}
-
-// LDS state of the claimed walk.
-struct ClaimSmem {
-  int next;        // next position to claim
-  int late_ready;  // 1 once wave 0 has listed the late positions
-  int late_n;      // late positions: selected blocks, then tail pages
-  int late_mid;    // of which selected blocks
-  int32_t early[kEarly];
-  int32_t late[kStagedIds + kTailPages];  // the selected ids, then (in place) the late pages
-};
-
-__device__ inline void wait_late(ClaimSmem& cs) {
-  while (__hip_atomic_load(&cs.late_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
-    __builtin_amdgcn_s_sleep(1);
-}
-
-// Page source of the staged walk: claims positions (see above); all values
-// wave-uniform.
-struct ClaimPages {
-  ClaimSmem& cs;
-  const attn::PoolView& v;
-  int b;
-  int lane;
-  int F;        // forced positions listed early
-  int n;        // sealed blocks
-  int64_t len;  // tokens (after this step's append)
-  int pending = -1;
-  bool ready = false;
-
-  __device__ inline attn::PageRef next(bool wait) {
-    for (;;) {
-      int c;
-      if (pending >= 0) {
-        c = pending;
-        pending = -1;
-      } else {
-        int x = 0;
-        if (lane == 0) x = __hip_atomic_fetch_add(&cs.next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        c = __builtin_amdgcn_readfirstlane(x);
-      }
-      if (c < F) {
-        const int32_t page = __builtin_amdgcn_readfirstlane(cs.early[c]);
-        if (page >= 0) return attn::PageRef{page, kPageTokens};
-        continue;
-      }
-      if (!ready) {
-        if (!wait) {
-          pending = c;
-          return attn::PageRef{0, -1};
-        }
-        wait_late(cs);
-        ready = true;
-      }
-      const int j = c - F;
-      const int late_n = __builtin_amdgcn_readfirstlane(cs.late_n);
-      if (j >= late_n) return attn::PageRef{0, 0};
-      const int mid = __builtin_amdgcn_readfirstlane(cs.late_mid);
-      if (j < mid) {
-        const int32_t page = __builtin_amdgcn_readfirstlane(cs.late[j]);
-        if (page >= 0) return attn::PageRef{page, kPageTokens};
-        continue;
-      }
-      const int k = j - mid;
-      const int64_t left = len - static_cast<int64_t>(n + k) * kPageTokens;
-      const int valid = left < kPageTokens ? static_cast<int>(left) : kPageTokens;
-      const int64_t page = k < kTailPages ? static_cast<int64_t>(__builtin_amdgcn_readfirstlane(cs.late[j]))
-                                          : lookup_page(v, b, static_cast<int64_t>(n) + k);
-      if (page >= 0 && valid > 0) return attn::PageRef{page, valid};
-    }
-  }
-};
-
+// and 1.  Then every wave walks its planned positions (the planned walk
+// above) with the staged walk of attn_core.hpp (pages HBM -> LDS by DMA, q.K
+// on v_mfma_f32_16x16x32_f16), one page in flight while the previous one is
+// computed.  A step that seals nothing stores its token at the start of the
+// walk phase (wave 0, before it lists the tail).
 template <int GR, bool APPEND, bool F16, bool ONLINE = false>
 __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p) {
   constexpr int G = 4;
@@ -443,6 +518,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   __shared__ __align__(16) float q_t[G * D];
   __shared__ uint32_t hist[256];
   __shared__ ClaimSmem cl;
+  __shared__ int32_t late_ids[kStagedIds + kTailPages];  // the selected ids, then (in place) the late pages
   uint32_t* keys = reinterpret_cast<uint32_t*>(smem);
   uint4* stage = reinterpret_cast<uint4*>(smem) + wave * attn::kStageVecs;
   float* pbuf = reinterpret_cast<float*>(smem + kStageBytes) + wave * kPbufFloats;
@@ -486,18 +562,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   const sel::Budget bs =
       n_ok ? sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride)
            : sel::Budget{0, 0, 0, false, true};
-  // forced blocks: [0, init_f) and [n - local_f, n); every block if all are taken
-  int init_f = 0, local_f = 0;
-  if (!bs.bad) {
-    init_f = bs.take_all ? n : bs.init_n;
-    local_f = bs.take_all ? 0 : n - (bs.local_first > bs.init_n ? bs.local_first : bs.init_n);
-  }
-  const int e_init = init_f < kEarly ? init_f : kEarly;
-  const int e_local = local_f < kEarly - e_init ? local_f : kEarly - e_init;
-  const int F = e_init + e_local;
-  int32_t early_page = -1;
-  if (wave == kWaves - 1 && lane < F)
-    early_page = static_cast<int32_t>(lookup_page(p.v, b, lane < e_init ? lane : n - e_local + (lane - e_init)));
+  const Forced fb = forced_blocks(bs, n);
+  const int32_t early = wave == kWaves - 1 ? early_page(p, b, n, fb, lane) : -1;
   if (n_ok && !bs.take_all) {  // (a budget that takes every block needs no scores)
     sel::ScoreArgs a{};
     a.query = p.query;
@@ -521,11 +587,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
     p.online.ring[((static_cast<int64_t>(b) * p.online.query_heads + h) * p.online.ring_tokens + slot) * D +
                   tid % D] = q_entry;
   }
-  if (wave == kWaves - 1) cl.early[lane] = early_page;
-  if (tid == 0) {
-    cl.next = 0;
-    cl.late_ready = 0;
-  }
+  if (wave == kWaves - 1) cl.early[lane] = early;
+  if (tid == 0) cl.late_ready = 0;
   if (deferred && tail_page >= 0) {
     commit.appended = true;
     len += 1;
@@ -541,9 +604,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   }
   const int64_t tail_tokens = wlen - static_cast<int64_t>(wn) * kPageTokens;
   const int tail_pages = static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens);
-  __syncthreads();  // keys, the early pages and the claim counter visible
+  __syncthreads();  // keys, the early pages and the flag visible
 
-  // ---- 3. select (wave 0) and walk (every wave, claimed positions) -------------
+  // ---- 3. select (wave 0) and walk (every wave, planned positions) -------------
   if (wave == 0) {
     if (deferred) {
       if (tail_page >= 0) store_token_quad(p, tail_page, len - 1, g, lane, token);
@@ -556,36 +619,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
         p.counts[out_row] = 0;
       }
     } else {
-      count = sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride, p.sel_stride, cl.late);
+      count = sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride, p.sel_stride, late_ids);
       if (lane == 0) p.counts[out_row] = count;
     }
-    // late positions: the selected blocks not listed early, then the tail
-    // pages; in place over the ids (position j reads id e_init + j >= j)
-    const int mid = count - F > 0 ? count - F : 0;
-    const int listed = mid + (tail_pages < kTailPages ? tail_pages : kTailPages);
-    for (int j0 = 0; j0 < listed; j0 += kWave) {
-      const int j = j0 + lane;
-      int64_t page = -1;
-      if (j < mid) {
-        page = lookup_page(p.v, b, cl.late[e_init + j]);
-      } else if (j < listed) {
-        page = lookup_page(p.v, b, static_cast<int64_t>(wn) + (j - mid));
-      }
-      __builtin_amdgcn_wave_barrier();  // every lane has read its id before any lane writes
-      if (j < listed) cl.late[j] = static_cast<int32_t>(page);
-    }
-    if (lane == 0) {
-      cl.late_mid = mid;
-      cl.late_n = mid + tail_pages;
-    }
-    // the appended token has reached memory before a wave can claim the tail
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    if (lane == 0) __hip_atomic_store(&cl.late_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    list_late(p, b, cl, late_ids, kStagedIds + kTailPages, count, fb, wn, tail_pages, lane);
   }
   const bool waits = wave != 0 && wave * kSlotBytes < n * 4;  // the keys reach into this wave's page slot
   if (waits) wait_late(cl);
-  ClaimPages src{cl, p.v, b, lane, F, wn, wlen};
-  src.ready = wave == 0 || waits;
+  PlanPages src(cl, late_ids, p.v, b, wave, fb.F, wn, wlen);
   st.attend_staged(p.v, src, lg, lane, g, stage, pbuf, q_group, p.qscale);
   __syncthreads();  // every wave is done with its slot before the combine reuses the area
 
