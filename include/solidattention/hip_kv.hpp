@@ -72,7 +72,7 @@ class DeviceArray {
   T* get() const { return p_; }
   std::size_t size() const { return n_; }
   void upload(const std::vector<T>& v) {
-    if (v.size() > n_) throw std::runtime_error("upload: host vector larger than device array");
+    if (v.size() != n_) throw std::runtime_error("upload: host vector size differs from the device array's");
     hip_check(hipMemcpy(p_, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D");
   }
   std::vector<T> download() const {
@@ -106,6 +106,9 @@ class PagedKvPool {
   std::size_t batch() const { return batch_; }
   std::size_t query_heads() const { return query_heads_; }
   std::size_t kv_heads() const { return kv_heads_; }
+  std::size_t table_stride() const { return table_stride_; }
+  std::size_t rep_heads() const { return rep_heads_; }
+  std::size_t rep_stride() const { return rep_stride_; }
 
   sa_paged_kv view() const {
     sa_paged_kv v{};

@@ -261,7 +261,7 @@ void check_decode_step() {
   for (std::size_t i = 0; i < table.size(); ++i) table[i] = static_cast<int32_t>((i * 37 + 11) % pages);
   std::vector<int32_t> seq_len = {32 * 9 + 30, 32 * 12, 32 * 5 + 7, 32 * 16 + 1};
   std::vector<int32_t> sealed(batch, 0), gen(batch, 0);
-  const std::size_t rep_stride = (stride + 3) / 4 * 4;
+  const std::size_t rep_stride = pool.rep_stride();  // rows padded to whole 128-byte lines
   std::vector<float> reps(batch * hkv * d * rep_stride, 0.0f);
   sao_paged_seal(host_pool.data(), 32, table.data(), stride, seq_len.data(), sealed.data(), gen.data(),
                  reps.data(), hkv, rep_stride, batch, hq, hkv, d, 0);
