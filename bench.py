@@ -339,10 +339,10 @@ def main():
     log(f"copy reference: gather_pages_kernel {copy_ref['gbps']:.0f} GB/s over {copy_ref['bytes']} bytes")
     grp = hq // hkv
     if grp == 4:  # the LDS-staged one-launch kernel (4 query heads per KV head)
-        kernel_name = {1: "decode_kernel_staged<4,true,false>", 2: "decode_kernel_staged<4,false,false>",
+        kernel_name = {1: "decode_kernel_staged<4,true,false,false>", 2: "decode_kernel_staged<4,false,false,false>",
                        3: "sparse_decode_attention_kernel<4>"}[launches]
     else:
-        kernel_name = {1: f"decode_kernel<{grp},{grp},true,false>", 2: f"decode_kernel<{grp},{grp},false,false>",
+        kernel_name = {1: f"decode_kernel<{grp},{grp},true,false,false>", 2: f"decode_kernel<{grp},{grp},false,false,false>",
                        3: f"sparse_decode_attention_kernel<{grp}>"}[launches]
     traffic = measured_traffic(args.config, kernel_name)
 
