@@ -312,6 +312,7 @@ def main():
         kernel_us = sel_us if launches == 2 else att_us
 
     copy_ref = copy_reference(sa, torch, L[0].kv, args.seed)
+    read_ref = read_reference(sa, np, torch, L[-1], hkv)
 
     # algorithmic bytes of one launch: selected KV + tail KV + q + out + ids,
     # plus the fp32 representatives of every sealed block (select+attend) and
@@ -337,6 +338,7 @@ def main():
             f"eager append {app_us:.2f} / select {sel_us:.2f} / attention {att_us:.2f} us; "
             f"layer {us_per_layer:.2f} us")
     log(f"copy reference: gather_pages_kernel {copy_ref['gbps']:.0f} GB/s over {copy_ref['bytes']} bytes")
+    log(f"read reference: read_step_bytes_kernel {read_ref['gbps']:.0f} GB/s over {read_ref['bytes']} bytes")
     grp = hq // hkv
     if grp == 4:  # the LDS-staged one-launch kernel (4 query heads per KV head)
         kernel_name = {1: "decode_kernel_staged<4,true,false,false>", 2: "decode_kernel_staged<4,false,false,false>",
@@ -387,11 +389,43 @@ def main():
                      "launch_us": round(kernel_us, 3),
                      "launch_timing": ("graph-replayed timed region / (steps x layers)" if launches == 1 and graph
                                        else "events around each launch in the eager timed steps"),
-                     "copy_reference": copy_ref},
+                     "copy_reference": copy_ref, "read_reference": read_ref,
+                     "frac_of_read_reference": round(achieved / read_ref["gbps"], 4)},
         "parity": parity,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def read_reference(sa, np, torch, ly, hkv, reps=5):
+    """A measured bandwidth reference on the decode step's own access
+    pattern: read_step_bytes_kernel reads, for every (sequence, KV head) of
+    the layer's last step, the representatives of the sealed blocks, the K/V
+    slices of the selected pages and the tail, with no arithmetic but an XOR
+    of the words read, timed with HIP events over `reps` launches on the
+    bench stream.  Its rate is what the memory system gives this pattern of
+    reads; the decode step's rate over it says how much the kernel's own
+    structure costs."""
+    kv = ly.kv
+    out = sa.read_step_bytes(kv, ly.selected, ly.counts, hkv)  # warm
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        sa.read_step_bytes(kv, ly.selected, ly.counts, hkv, out=out)
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = 1000.0 * start.elapsed_time(end) / reps
+    seq_len = kv.seq_len.cpu().numpy().astype(np.int64)
+    sealed = kv.sealed.cpu().numpy().astype(np.int64)
+    counts = np.minimum(ly.counts.cpu().numpy().astype(np.int64), ly.selected.shape[-1])
+    kv_tok_bytes = 2 * D * 2  # K+V of one KV head, FP16
+    nbytes = int(sealed.sum() * kv.rep_heads * D * 4 + counts.sum() * PAGE * kv_tok_bytes +
+                 (seq_len - sealed * PAGE).sum() * hkv * kv_tok_bytes)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": "read_step_bytes_kernel",
+            "what": "the layer's representatives, selected page slices and tails read with no arithmetic",
+            "bytes": nbytes, "us": round(us, 2), "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
 def copy_reference(sa, torch, kv, seed, pages=4096, reps=5):

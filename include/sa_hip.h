@@ -443,6 +443,24 @@ int sa_hip_gather_pages(const uint16_t* pool, int64_t page_bytes,
                         int32_t count, uint16_t* out, int32_t* status,
                         void* stream);
 
+/* ---- measurement: the decode step's bytes, read with no arithmetic ------ */
+
+/* No counterpart in the reference: a measurement aid for the attention
+ * kernels.  For every (sequence b, KV head h) it reads exactly the bytes a
+ * decode step reads for that pair: the fp32 representative rows of the
+ * sealed blocks (rep heads h, h + kv_heads, ...), the K/V slices of head h in
+ * the pages of list b * select_groups + h / (kv_heads / select_groups) of
+ * `selected` (first counts[...] entries, at most sel_stride), and the K/V of
+ * the unsealed tail [32 * sealed, seq_len).  out[b * kv_heads + h] is the XOR
+ * of every 32-bit word read (device, batch * kv_heads).  Needs 16-byte
+ * aligned reps with rep_stride a multiple of 4; ids outside the sealed range
+ * and pages outside [0, num_pages) are skipped and flagged in status
+ * (optional). */
+int sa_hip_read_step_bytes(const sa_paged_kv* kv, const int32_t* selected,
+                           const int32_t* counts, int32_t select_groups,
+                           int32_t sel_stride, uint32_t* out, int32_t* status,
+                           void* stream);
+
 /* ---- R10: history prediction and miss correction ------------------------ */
 
 /* Host-only set logic of compare_prediction (pipeline_main.cpp:686-717):

@@ -786,6 +786,40 @@ int sa_hip_seal(const sa_paged_kv* kv, int32_t local_tokens, int32_t* status, vo
   return lifecycle_common(kv, nullptr, nullptr, nullptr, nullptr, local_tokens, 0, status, stream, "seal");
 }
 
+// ---- read reference ------------------------------------------------------------
+
+int sa_hip_read_step_bytes(const sa_paged_kv* kv, const int32_t* selected, const int32_t* counts,
+                           int32_t select_groups, int32_t sel_stride, uint32_t* out, int32_t* status,
+                           void* stream) {
+  if (int e = check_geometry(kv, "read_step_bytes")) return e;
+  if (int e = check_reps(kv, "read_step_bytes")) return e;
+  if (!selected || !counts || !out) return fail(SA_HIP_EINVAL, "read_step_bytes: null selected/counts/out");
+  if (!aligned16(kv->reps) || kv->rep_stride % 4 != 0)
+    return fail(SA_HIP_EINVAL, "read_step_bytes: reps must be 16-byte aligned with rep_stride a multiple of 4");
+  if (select_groups <= 0 || kv->kv_heads % select_groups != 0)
+    return fail(SA_HIP_EINVAL, "read_step_bytes: select_groups must divide kv_heads");
+  if (sel_stride <= 0) return fail(SA_HIP_EINVAL, "read_step_bytes: sel_stride must be positive");
+  sa::ReadStepLaunch l{};
+  l.pool = kv->pool;
+  l.table = kv->block_table;
+  l.seq_len = kv->seq_len;
+  l.sealed = kv->sealed;
+  l.reps = kv->reps;
+  l.selected = selected;
+  l.counts = counts;
+  l.out = out;
+  l.status = status;
+  l.num_pages = kv->num_pages;
+  l.batch = kv->batch;
+  l.table_stride = kv->table_stride;
+  l.kv_heads = kv->kv_heads;
+  l.rep_heads = kv->rep_heads;
+  l.rep_stride = kv->rep_stride;
+  l.select_groups = select_groups;
+  l.sel_stride = sel_stride;
+  return check_hip(sa::launch_read_step_bytes(l, as_stream(stream)), "read_step_bytes launch");
+}
+
 // ---- gather --------------------------------------------------------------------
 
 int sa_hip_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* pages,

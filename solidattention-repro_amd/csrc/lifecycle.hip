@@ -154,6 +154,121 @@ __global__ __launch_bounds__(kThreads) void gather_pages_kernel(const uint4* poo
     dst[e] = src[e];
 }
 
+// A read-only pass over the bytes one decode step reads for each (sequence,
+// KV head): the fp32 representative rows of its sealed blocks, the K/V
+// slices of its selected pages and the K/V of its unsealed tail.  Nothing is
+// computed but an XOR of every 32-bit word read (one value per (sequence, KV
+// head), so that no load is dead).  It times the memory system on the decode
+// step's own access pattern, the reference point for the attention kernels'
+// bandwidth.  Workgroup (h, b) as in the decode-step kernels; 8 waves.
+constexpr int kReadThreads = 512;
+constexpr int kReadWaves = kReadThreads / kWave;
+
+__global__ __launch_bounds__(kReadThreads) void read_step_bytes_kernel(const ReadStepLaunch p) {
+  __shared__ uint32_t red[kReadWaves];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  uint32_t x = 0;
+  const int64_t sealed = p.sealed[b];
+  const int64_t len = p.seq_len[b];
+  if (sealed < 0 || sealed > p.table_stride || len < sealed * kPageTokens ||
+      len > static_cast<int64_t>(p.table_stride) * kPageTokens) {
+    if (tid == 0) flag_status(p.status, kStatusBadLength);
+    return;
+  }
+
+  // representative rows: rep heads h, h + kv_heads, ...; wave w takes rows
+  // d = w + 8 u, 16 loads in flight per lane
+  const int64_t quads = sealed / 4;
+  for (int r = h; r < p.rep_heads; r += p.kv_heads) {
+    const float* rows = p.reps + (static_cast<int64_t>(b) * p.rep_heads + r) * D * p.rep_stride;
+    for (int64_t j = lane; j < quads; j += kWave) {
+      u32x4_t v[D / kReadWaves];
+#pragma unroll
+      for (int u = 0; u < D / kReadWaves; ++u)
+        v[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(rows + static_cast<int64_t>(wave + kReadWaves * u) * p.rep_stride) + j);
+#pragma unroll
+      for (int u = 0; u < D / kReadWaves; ++u) x ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    const int rem = static_cast<int>(sealed % 4);
+    if (tid < D * rem) {
+      const int d = tid / rem, w = tid % rem;
+      x ^= __float_as_uint(rows[static_cast<int64_t>(d) * p.rep_stride + 4 * quads + w]);
+    }
+  }
+
+  // selected pages: wave w takes list entries w + 8 i; its lanes resolve 64
+  // entries at a time (id, then page), then every lane reads 16 of the
+  // page's 1024 16-byte pieces of head h (64 segments of 256 bytes: token
+  // t = segment / 2, K or V = segment % 2)
+  const int per_sel = p.kv_heads / p.select_groups;
+  const int64_t list = static_cast<int64_t>(b) * p.select_groups + h / per_sel;
+  const int count = min(p.counts[list], p.sel_stride);
+  const int32_t* ids = p.selected + list * p.sel_stride;
+  const int32_t* table = p.table + static_cast<int64_t>(b) * p.table_stride;
+  const int64_t tok_vecs = 2 * p.kv_heads * D * 2 / 16;  // 16-byte pieces per token row
+  const int64_t page_vecs = kPageTokens * tok_vecs;
+  const u32x4_t* pool = reinterpret_cast<const u32x4_t*>(p.pool);
+  for (int first = wave; first < count; first += kReadWaves * kWave) {
+    const int mine = first + kReadWaves * lane;
+    int64_t page = -1;
+    if (mine < count) {
+      const int blk = ids[mine];
+      if (blk < 0 || blk >= sealed) {
+        flag_status(p.status, kStatusBadBlock);
+      } else {
+        page = table[blk];
+        if (page < 0 || page >= p.num_pages) {
+          flag_status(p.status, kStatusBadPage);
+          page = -1;
+        }
+      }
+    }
+    const int n = min(kWave, (count - first + kReadWaves - 1) / kReadWaves);
+    for (int i = 0; i < n; ++i) {
+      const int64_t pg = __shfl(page, i, kWave);
+      if (pg < 0) continue;
+      const u32x4_t* base = pool + pg * page_vecs + h * (D * 2 / 16);
+      u32x4_t v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int piece = j * kWave + lane;
+        const int seg = piece / 16;
+        v[j] = __builtin_nontemporal_load(base + (seg / 2) * tok_vecs + (seg % 2) * (tok_vecs / 2) + piece % 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x ^= v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
+    }
+  }
+
+  // the unsealed tail: 32 pieces (K then V of head h) per token
+  const int64_t tail = len - sealed * kPageTokens;
+  for (int64_t i = tid; i < tail * 32; i += kReadThreads) {
+    const int64_t t = sealed * kPageTokens + i / 32;
+    const int q = static_cast<int>(i % 32);
+    const int64_t page = table[t / kPageTokens];
+    if (page < 0 || page >= p.num_pages) {
+      flag_status(p.status, kStatusBadPage);
+      continue;
+    }
+    const u32x4_t v = pool[page * page_vecs + (t % kPageTokens) * tok_vecs + (q / 16) * (tok_vecs / 2) +
+                           h * (D * 2 / 16) + q % 16];
+    x ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) x ^= __shfl_xor(x, off, kWave);
+  if (lane == 0) red[wave] = x;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kReadWaves; ++w) t ^= red[w];
+    p.out[static_cast<int64_t>(b) * p.kv_heads + h] = t;
+  }
+}
+
 // Pages whose ids travel in the kernel arguments (no device-side list):
 // page i of the launch goes to out + i * page_vecs; out may be pinned host
 // memory (seal writeback staging), written through its device mapping.
@@ -292,6 +407,11 @@ hipError_t launch_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t
   hipLaunchKernelGGL(gather_pages_kernel, grid, dim3(kThreads), 0, stream,
                      reinterpret_cast<const uint4*>(pool), vecs, num_pages, pages,
                      reinterpret_cast<uint4*>(out), status);
+  return hipGetLastError();
+}
+
+hipError_t launch_read_step_bytes(const ReadStepLaunch& l, hipStream_t stream) {
+  hipLaunchKernelGGL(read_step_bytes_kernel, dim3(l.kv_heads, l.batch), dim3(kReadThreads), 0, stream, l);
   return hipGetLastError();
 }
 

@@ -233,6 +233,30 @@ struct LifecycleLaunch {
 
 hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream);
 
+// The decode step's bytes for each (sequence, KV head) read with no
+// arithmetic: representatives of the sealed blocks, the selected pages' K/V
+// slices and the tail; out[b * kv_heads + h] is the XOR of the 32-bit words.
+struct ReadStepLaunch {
+  const uint16_t* pool;
+  const int32_t* table;
+  const int32_t* seq_len;
+  const int32_t* sealed;
+  const float* reps;
+  const int32_t* selected;
+  const int32_t* counts;
+  uint32_t* out;
+  int32_t* status;
+  int64_t num_pages;
+  int32_t batch;
+  int32_t table_stride;
+  int32_t kv_heads;
+  int32_t rep_heads;
+  int32_t rep_stride;
+  int32_t select_groups;
+  int32_t sel_stride;
+};
+hipError_t launch_read_step_bytes(const ReadStepLaunch& l, hipStream_t stream);
+
 hipError_t launch_gather_pages(const uint16_t* pool, int64_t page_bytes, int64_t num_pages,
                                const int32_t* pages, int32_t count, uint16_t* out,
                                int32_t* status, hipStream_t stream);

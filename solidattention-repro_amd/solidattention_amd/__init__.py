@@ -115,6 +115,7 @@ EXPORTS = {
     "sa_hip_append_seal_f16": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_seal": (C.c_int, [_KV, _I32, _P, _P]),
     "sa_hip_gather_pages": (C.c_int, [_P, _I64, _I64, _P, _I32, _P, _P, _P]),
+    "sa_hip_read_step_bytes": (C.c_int, [_KV, _P, _P, _I32, _I32, _P, _P, _P]),
     "sa_hip_local_causal_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
     "sa_hip_local_causal_representatives": (C.c_int, [_P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
                                                       _I32, _P, _P, _SZ, _P]),
@@ -721,6 +722,21 @@ def local_causal_representatives(prompt_queries, kv16, tokens, query_heads, kv_h
 def gather_pages(pool, page_bytes, num_pages, pages, out, status=None, stream=None):
     check(lib().sa_hip_gather_pages(_ptr(pool), page_bytes, num_pages, _ptr(pages), pages.numel(), _ptr(out),
                                     _ptr(status), _stream(stream)), "gather_pages")
+    return out
+
+
+def read_step_bytes(kv: PagedKV, selected, counts, select_groups, out=None, status=None, stream=None):
+    """The decode step's bytes for each (sequence, KV head) read with no
+    arithmetic (representatives of the sealed blocks, the selected pages'
+    K/V slices, the tail): a bandwidth reference for the attention kernels.
+    Returns the XOR of the 32-bit words read, int32 [batch, kv_heads]."""
+    import torch
+    if out is None:
+        out = torch.zeros((kv.batch, kv.kv_heads), dtype=torch.int32, device=kv.pool.device)
+    st = kv.struct()
+    check(lib().sa_hip_read_step_bytes(C.byref(st), _ptr(selected), _ptr(counts), select_groups,
+                                       selected.shape[-1], _ptr(out), _ptr(status), _stream(stream)),
+          "read_step_bytes")
     return out
 
 
