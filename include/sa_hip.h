@@ -176,7 +176,10 @@ int sa_hip_attention_merge(const sa_paged_kv* kv, const void* workspace,
 /* Attention over a contiguous token-major K/V-interleaved buffer of
  * `tokens` tokens (the AttentionProblem layout, backend.hpp:18-31); the
  * device kernel of AcceleratorBackend::attention (cuda_backend.cpp:70-158)
- * without its 128/256-token limits. */
+ * without its 128/256-token limits.  head_dim: 128 (the paged attention
+ * kernel) or any other multiple of 8 up to 512 (attention_reference.cpp
+ * :55-96 takes any head_dim), with 1, 2, 4 or 8 query heads per KV head;
+ * the workspace size depends on head_dim. */
 size_t sa_hip_contiguous_workspace_bytes(int64_t tokens, int32_t query_heads,
                                          int32_t kv_heads, int32_t head_dim);
 int sa_hip_attention_contiguous(const uint16_t* kv, const float* query,

@@ -1,0 +1,287 @@
+// attention_any.hip — attention of one query token over a contiguous
+// token-major K/V buffer for head dimensions other than 128 (gfx950): any
+// multiple of 8 up to 512, 1, 2, 4 or 8 query heads per KV head.  Semantics
+// of the reference's attention_reference (cpp/src/attention_reference.cpp
+// :55-96): per query head h of KV head g = h / group, logits q_h . K_t *
+// scale over every token, softmax, and the weighted sum of V_t; the buffer
+// is [tokens][K: kv_heads x head_dim][V: kv_heads x head_dim] FP16
+// (backend.hpp:18-31).  The head_dim = 128 path is the paged attention
+// kernel in contiguous mode (attention.hip); this one serves the others.
+//
+// Grid (kv_heads, splits): a workgroup takes one KV head's query heads over
+// one contiguous token range.  Its 4 waves take 64-token tiles in turn:
+//   * scores: lane = token; the lane reads its token's K row in 16-byte
+//     pieces (eight in flight) against the query heads held in LDS;
+//   * online softmax per head over the tile (log2 domain, wave reductions);
+//   * P.V: lanes over d (two values of d per 4-byte load, 256 d per
+//     instruction), four tokens' loads in flight, the tile's probabilities
+//     read back from LDS.
+// The waves' states combine in LDS; with several splits each workgroup
+// writes (max, denominator, accumulator) per head and a merge kernel adds
+// the splits in split order (deterministic).
+#include <algorithm>
+
+#include "sa_device.hpp"
+#include "sa_internal.hpp"
+
+namespace sa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxD = kAnyMaxHeadDim;
+constexpr int kPairs = kMaxD / (2 * kWave);  // 4-byte V loads per lane per token
+constexpr int kTile = kWave;                // tokens per wave tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct AnyParams {
+  const uint16_t* kv;
+  const float* query;
+  float* out;
+  float* part;  // [kv_heads][splits][group][head_dim + 2]: max, denominator, accumulator
+  int64_t tokens;
+  int64_t chunk;  // tokens per split
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t splits;
+  float scale;
+};
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void attention_any_kernel(const AnyParams p) {
+  __shared__ float q_s[G * kMaxD];
+  __shared__ float p_s[kWaves][G][kTile];
+  __shared__ float w_ml[kWaves][G][2];
+  __shared__ float w_acc[kWaves][G][kMaxD];
+  const int g = blockIdx.x;
+  const int s = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int D = p.head_dim;
+  const int64_t t_begin = static_cast<int64_t>(s) * p.chunk;
+  const int64_t t_end = std::min<int64_t>(p.tokens, t_begin + p.chunk);
+  const int64_t tok_elems = 2LL * p.kv_heads * D;
+  const uint16_t* kbase = p.kv + static_cast<int64_t>(g) * D;
+  const uint16_t* vbase = p.kv + static_cast<int64_t>(p.kv_heads + g) * D;
+  const float* q = p.query + static_cast<int64_t>(g) * G * D;
+  for (int i = tid; i < G * D; i += kThreads) q_s[(i / D) * kMaxD + i % D] = q[i];
+  __syncthreads();
+
+  const float sl2 = p.scale * kLog2e;
+  float m[G], l[G], acc[G][2 * kPairs];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = kNegInf;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2 * kPairs; ++j) acc[h][j] = 0.0f;
+  }
+
+  for (int64_t t0 = t_begin + static_cast<int64_t>(wave) * kTile; t0 < t_end; t0 += kWaves * kTile) {
+    // scores of the tile's tokens, lane = token
+    const int64_t t = t0 + lane;
+    const bool valid = t < t_end;
+    float sc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) sc[h] = 0.0f;
+    if (valid) {
+      const uint16_t* k = kbase + t * tok_elems;
+      for (int d0 = 0; d0 < D; d0 += 64) {
+        uint4 w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (d0 + 8 * u < D) w[u] = *reinterpret_cast<const uint4*>(k + d0 + 8 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (d0 + 8 * u >= D) break;
+          const uint32_t ww[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float kf = (e & 1) ? hi_h2f(ww[e >> 1]) : lo_h2f(ww[e >> 1]);
+#pragma unroll
+            for (int h = 0; h < G; ++h) sc[h] = __builtin_fmaf(q_s[h * kMaxD + d0 + 8 * u + e], kf, sc[h]);
+          }
+        }
+      }
+    }
+    // online softmax per head over the tile
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float x = valid ? sc[h] * sl2 : kNegInf;
+      const float mn = fmaxf(m[h], wave_max(x));
+      const float corr = __builtin_amdgcn_exp2f(m[h] - mn);  // 0 while m is -inf
+      const float pt = valid ? __builtin_amdgcn_exp2f(x - mn) : 0.0f;
+      l[h] = l[h] * corr + wave_sum(pt);
+      m[h] = mn;
+#pragma unroll
+      for (int j = 0; j < 2 * kPairs; ++j) acc[h][j] *= corr;
+      p_s[wave][h][lane] = pt;
+    }
+    __builtin_amdgcn_wave_barrier();  // the wave's LDS writes precede its reads below
+    // P.V: lane holds d = 2 (lane + 64 j) + {0, 1}
+    const int n = static_cast<int>(std::min<int64_t>(kTile, t_end - t0));
+    for (int i0 = 0; i0 < n; i0 += 4) {
+      uint32_t vw[4][kPairs];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t* v = vbase + (t0 + i0 + i) * tok_elems;
+#pragma unroll
+        for (int j = 0; j < kPairs; ++j) {
+          const int d = 2 * (lane + kWave * j);
+          vw[i][j] = 0u;
+          if (i0 + i < n && d < D) vw[i][j] = *reinterpret_cast<const uint32_t*>(v + d);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i0 + i >= n) break;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float pv = p_s[wave][h][i0 + i];
+#pragma unroll
+          for (int j = 0; j < kPairs; ++j) {
+            acc[h][2 * j] = __builtin_fmaf(pv, lo_h2f(vw[i][j]), acc[h][2 * j]);
+            acc[h][2 * j + 1] = __builtin_fmaf(pv, hi_h2f(vw[i][j]), acc[h][2 * j + 1]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the tile's reads of p_s precede the next tile's writes
+  }
+
+  // combine the waves
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    if (lane == 0) {
+      w_ml[wave][h][0] = m[h];
+      w_ml[wave][h][1] = l[h];
+    }
+#pragma unroll
+    for (int j = 0; j < kPairs; ++j) {
+      const int d = 2 * (lane + kWave * j);
+      if (d < D) {
+        w_acc[wave][h][d] = acc[h][2 * j];
+        w_acc[wave][h][d + 1] = acc[h][2 * j + 1];
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += kThreads) {
+    const int h = i / D;
+    const int d = i % D;
+    float mx = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, w_ml[w][h][0]);
+    float lw = 0.0f, aw = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = __builtin_amdgcn_exp2f(w_ml[w][h][0] - mx);  // waves without tokens: 0
+      lw += w_ml[w][h][1] * f;
+      aw += w_acc[w][h][d] * f;
+    }
+    if (p.splits == 1) {
+      p.out[(static_cast<int64_t>(g) * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
+    } else {
+      float* rec = p.part + ((static_cast<int64_t>(g) * p.splits + s) * G + h) * (D + 2);
+      if (d == 0) {
+        rec[0] = mx;
+        rec[1] = lw;
+      }
+      rec[2 + d] = aw;
+    }
+  }
+}
+
+// out[h][d] from the splits' records of head h, added in split order.
+__global__ __launch_bounds__(kThreads) void attention_any_merge_kernel(const AnyParams p, int group) {
+  const int hq = blockIdx.x;
+  const int g = hq / group;
+  const int hh = hq % group;
+  const int D = p.head_dim;
+  const int64_t rec_stride = static_cast<int64_t>(group) * (D + 2);
+  const float* first = p.part + (static_cast<int64_t>(g) * p.splits * group + hh) * (D + 2);
+  float mx = kNegInf;
+  for (int s = 0; s < p.splits; ++s) mx = fmaxf(mx, first[s * rec_stride]);
+  for (int d = threadIdx.x; d < D; d += kThreads) {
+    float lw = 0.0f, aw = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+      const float* rec = first + s * rec_stride;
+      const float f = __builtin_amdgcn_exp2f(rec[0] - mx);
+      lw += rec[1] * f;
+      aw += rec[2 + d] * f;
+    }
+    p.out[static_cast<int64_t>(hq) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
+  }
+}
+
+// Splits that give every compute unit about two workgroups, each with at
+// least 256 tokens (four tiles per wave), and no empty split.
+void any_split(int64_t tokens, int32_t kv_heads, int32_t& splits, int64_t& chunk) {
+  const int64_t want = std::max<int64_t>(1, 2LL * compute_units() / std::max(kv_heads, 1));
+  const int64_t most = std::max<int64_t>(1, tokens / 256);
+  int64_t n = std::min<int64_t>(std::min(want, most), 1024);
+  chunk = (tokens + n - 1) / n;
+  n = (tokens + chunk - 1) / chunk;
+  splits = static_cast<int32_t>(n);
+}
+
+}  // namespace
+
+bool attention_any_supported(int32_t query_heads, int32_t kv_heads, int32_t head_dim) {
+  if (kv_heads <= 0 || query_heads <= 0 || query_heads % kv_heads != 0) return false;
+  const int group = query_heads / kv_heads;
+  return (group == 1 || group == 2 || group == 4 || group == 8) && head_dim > 0 && head_dim % 8 == 0 &&
+         head_dim <= kAnyMaxHeadDim;
+}
+
+size_t attention_any_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t kv_heads, int32_t head_dim) {
+  if (tokens <= 0 || !attention_any_supported(query_heads, kv_heads, head_dim)) return 0;
+  int32_t splits = 1;
+  int64_t chunk = tokens;
+  any_split(tokens, kv_heads, splits, chunk);
+  if (splits == 1) return 0;
+  return static_cast<size_t>(kv_heads) * splits * (query_heads / kv_heads) * (head_dim + 2) * sizeof(float);
+}
+
+hipError_t launch_attention_any(const uint16_t* kv, const float* query, int64_t tokens, int32_t query_heads,
+                                int32_t kv_heads, int32_t head_dim, float scale, float* out, void* workspace,
+                                hipStream_t stream) {
+  AnyParams p{};
+  p.kv = kv;
+  p.query = query;
+  p.out = out;
+  p.part = static_cast<float*>(workspace);
+  p.tokens = tokens;
+  p.kv_heads = kv_heads;
+  p.head_dim = head_dim;
+  p.scale = scale;
+  any_split(tokens, kv_heads, p.splits, p.chunk);
+  const int group = query_heads / kv_heads;
+  const dim3 grid(kv_heads, p.splits);
+  switch (group) {
+    case 1: hipLaunchKernelGGL(attention_any_kernel<1>, grid, dim3(kThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(attention_any_kernel<2>, grid, dim3(kThreads), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(attention_any_kernel<4>, grid, dim3(kThreads), 0, stream, p); break;
+    default: hipLaunchKernelGGL(attention_any_kernel<8>, grid, dim3(kThreads), 0, stream, p); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  hipLaunchKernelGGL(attention_any_merge_kernel, dim3(query_heads), dim3(kThreads), 0, stream, p, group);
+  return hipGetLastError();
+}
+
+}  // namespace sa

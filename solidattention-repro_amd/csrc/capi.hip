@@ -314,6 +314,7 @@ static int32_t contiguous_splits(int64_t tokens, int32_t query_heads, int32_t kv
 size_t sa_hip_contiguous_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t kv_heads,
                                          int32_t head_dim) {
   if (tokens <= 0 || kv_heads <= 0) return 0;
+  if (head_dim != sa::kHeadDim) return sa::attention_any_workspace_bytes(tokens, query_heads, kv_heads, head_dim);
   return sa_hip_attention_workspace_bytes(1, query_heads, kv_heads, head_dim,
                                           contiguous_splits(tokens, query_heads, kv_heads));
 }
@@ -325,6 +326,20 @@ int sa_hip_attention_contiguous(const uint16_t* kv, const float* query, int64_t 
   if (tokens <= 0) return fail(SA_HIP_EINVAL, "attention_contiguous: tokens must be positive");
   if (!aligned16(kv) || !aligned16(query))
     return fail(SA_HIP_EINVAL, "attention_contiguous: kv and query must be 16-byte aligned");
+  if (head_dim != sa::kHeadDim) {
+    if (!sa::attention_any_supported(query_heads, kv_heads, head_dim))
+      return fail(SA_HIP_EINVAL,
+                  "attention_contiguous: head_dim %d with %d/%d heads unsupported (head_dim a multiple of 8 up "
+                  "to %d; 1, 2, 4 or 8 query heads per KV head)",
+                  head_dim, query_heads, kv_heads, sa::kAnyMaxHeadDim);
+    const size_t need = sa::attention_any_workspace_bytes(tokens, query_heads, kv_heads, head_dim);
+    if (workspace_bytes < need || (need && !workspace))
+      return fail(SA_HIP_EINVAL, "attention_contiguous: workspace of %zu bytes needed, %zu given", need,
+                  workspace_bytes);
+    return check_hip(sa::launch_attention_any(kv, query, tokens, query_heads, kv_heads, head_dim, scale, out,
+                                              workspace, as_stream(stream)),
+                     "attention_contiguous launch");
+  }
   sa_paged_kv view{};
   view.pool = const_cast<uint16_t*>(kv);
   view.block_table = reinterpret_cast<int32_t*>(1);  // unused in contiguous mode

@@ -233,6 +233,15 @@ struct LifecycleLaunch {
 
 hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream);
 
+// Contiguous attention for head dimensions other than 128 (attention_any.hip):
+// multiples of 8 up to kAnyMaxHeadDim, 1/2/4/8 query heads per KV head.
+constexpr int kAnyMaxHeadDim = 512;
+bool attention_any_supported(int32_t query_heads, int32_t kv_heads, int32_t head_dim);
+size_t attention_any_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t kv_heads, int32_t head_dim);
+hipError_t launch_attention_any(const uint16_t* kv, const float* query, int64_t tokens, int32_t query_heads,
+                                int32_t kv_heads, int32_t head_dim, float scale, float* out, void* workspace,
+                                hipStream_t stream);
+
 // The decode step's bytes for each (sequence, KV head) read with no
 // arithmetic: representatives of the sealed blocks, the selected pages' K/V
 // slices and the tail; out[b * kv_heads + h] is the XOR of the 32-bit words.

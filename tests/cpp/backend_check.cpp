@@ -83,12 +83,12 @@ void check_c0(sa::AcceleratorBackend& backend) {
 
 // C1: 128-token fixture through every attention variant with the
 // reference's acceptance bars (attention_main.cpp:265-270).
-void check_c1(sa::AcceleratorBackend& backend, std::size_t tokens, const char* tag) {
-  const std::size_t hq = 16, hkv = 8, d = 128;
+void check_c1(sa::AcceleratorBackend& backend, std::size_t tokens, const char* tag, std::size_t d = 128) {
+  const std::size_t hq = 16, hkv = 8;
   std::vector<std::uint16_t> kv(tokens * 2 * hkv * d);
   std::vector<float> q(hq * d);
   sao_fixture_c1(tokens, hq, hkv, d, kv.data(), q.data());
-  const float scale = 0.08838834764831845f;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(d));
   std::vector<float> ref(hq * d);
   if (sao_attention_reference(kv.data(), q.data(), tokens, hq, hkv, d, scale, ref.data()) != 0)
     throw std::runtime_error("oracle attention failed");
@@ -340,6 +340,9 @@ int main() {
     check_c0(*backend);
     check_c1(*backend, 128, "c1");
     check_c1(*backend, 4096, "c1_4096_tokens");
+    // the reference's attention takes any head_dim (attention_reference.cpp:55-96)
+    check_c1(*backend, 1000, "c1_head_dim_64", 64);
+    check_c1(*backend, 3000, "c1_head_dim_256", 256);
     check_c2(*backend);
     check_lifecycle();
     check_decode_step();

@@ -76,6 +76,24 @@ def test_compare_prediction_cardinality_error():
         sa.compare_prediction([0, 0, 2, 15], [0, 1, 2, 15])
 
 
+def test_contiguous_attention_head_dims():
+    """head_dim 128 takes the paged kernel's workspace; other multiples of 8
+    up to 512 the any-head_dim kernel's (records of head_dim + 2 floats per
+    split and query head, none for a single split); the rest are refused
+    before any launch."""
+    import solidattention_amd as sa
+    L = sa.lib()
+    assert L.sa_hip_contiguous_workspace_bytes(100, 16, 8, 64) == 0  # one split below 512 tokens
+    n = L.sa_hip_contiguous_workspace_bytes(40000, 16, 8, 64)  # 256 CUs off the GPU: 64 splits
+    assert n == 8 * 64 * 2 * 66 * 4
+    assert L.sa_hip_contiguous_workspace_bytes(40000, 16, 8, 100) == 0
+    p = C.c_void_p(16)
+    for d, hq, hkv, what in ((100, 16, 8, b"head_dim 100"), (1024, 16, 8, b"head_dim 1024"),
+                             (64, 24, 8, b"24/8")):
+        rc = L.sa_hip_attention_contiguous(p, p, 100, hq, hkv, d, C.c_float(1.0), p, None, 0, None)
+        assert rc == -1 and what in L.sa_hip_last_error()
+
+
 def test_invalid_arguments_fail_before_any_launch():
     """Argument validation returns SA_HIP_EINVAL with a message and launches
     nothing (safe without a GPU)."""

@@ -29,6 +29,9 @@ def test_cpp_backend_check(hip):
     assert m["c2_packed_kv_exact"] is True
     assert m["lifecycle_sealed_blocks"] == 448
     assert m["c1_attention_max_abs_error"] <= 2e-5
+    for d in (64, 256):  # any head_dim through make_hip_backend()
+        assert m[f"c1_head_dim_{d}_attention_max_abs_error"] <= 2e-5
+        assert m[f"c1_head_dim_{d}_consumed_abs_error"] <= 1e-4
 
 
 EXE_STORE = os.path.join(ROOT, "tests", "cpp", "store_check")
