@@ -3,11 +3,12 @@
 
 Qwen3-0.6B attention shape (hidden 1024, 16 query / 8 KV heads, head_dim
 128), batch 64 sequences of 16384 tokens, budget 64 blocks (4 + 8 + 52),
-fp32 weights.  One layer step = three launches: the q/k/v producer (RMSNorm
-of the hidden rows folded into the projections, head RMS norm and RoPE at
-each sequence's position in the same launch) -> the one-launch decode step
-(append k/v, seal, score + select, attend) -> the o-projection with the
-residual add.  Every layer's output is the next layer's input; inputs and
+fp32 weights.  One layer step = three calls, five launches: the q/k/v
+producer (K-slice partial projections with the RMSNorm of the hidden rows
+folded in, then the slices' sum with head RMS norm and RoPE at each
+sequence's position) -> the one-launch decode step (append k/v, seal,
+score + select, attend) -> the o-projection (partials, then their sum with
+the residual add).  Every layer's output is the next layer's input; inputs and
 weights are resident in HBM.
 
 Reported: µs per layer (HIP graph of one step over all layers), the
@@ -66,10 +67,10 @@ def run(args):
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
     status = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws, _ = sa.decode_step_workspace(L[0].kv, 1)
-    # zeroed once: the projections' arrival counters start at zero
-    qkv_ws = torch.zeros(sa.lib().sa_hip_qkv_workspace_bytes(batch, hidden, hq, hkv) // 4, dtype=torch.float32,
+    # the projections' K-slice partial tiles
+    qkv_ws = torch.empty(sa.lib().sa_hip_qkv_workspace_bytes(batch, hidden, hq, hkv) // 4, dtype=torch.float32,
                          device="cuda")
-    lin_ws = torch.zeros(sa.lib().sa_hip_linear_workspace_bytes(batch, hq * D, hidden) // 4, dtype=torch.float32,
+    lin_ws = torch.empty(sa.lib().sa_hip_linear_workspace_bytes(batch, hq * D, hidden) // 4, dtype=torch.float32,
                          device="cuda")
     q = torch.empty((batch, hq, D), dtype=torch.float32, device="cuda")
     k = torch.empty((batch, hkv, D), dtype=torch.float32, device="cuda")

@@ -529,30 +529,30 @@ int sa_hip_rms_norm(const float* x, const float* w, float* out, int32_t rows, in
                     void* stream);
 /* y[r][o] = sum_i x[r][i] * w[o][i] (+ residual[r][o] when non-null): the
  * reference's cublasSgemm(CUBLAS_OP_T) on its row-major [out][in] weights,
- * one launch.  in a multiple of 256, out of 64; x, w, residual, y and the
- * workspace 16-byte aligned; workspace of sa_hip_linear_workspace_bytes(rows,
- * in, out) bytes: arrival counters, then the K-slice partial sums (added in
- * a fixed order: deterministic).  The caller zeroes the workspace ONCE before
- * its first call; every call leaves the counters at zero.  Calls sharing a
- * workspace must not run concurrently. */
+ * two launches on `stream` (K-slice partial tiles, then their sum in slice
+ * order: deterministic).  in a multiple of 256, out of 64; x, w, residual, y
+ * and the workspace 16-byte aligned; workspace of
+ * sa_hip_linear_workspace_bytes(rows, in, out) bytes holding the partial
+ * tiles (no initialisation needed).  Calls sharing a workspace must not run
+ * concurrently. */
 size_t sa_hip_linear_workspace_bytes(int32_t rows, int32_t in, int32_t out);
 int sa_hip_linear(const float* x, const float* w, const float* residual, float* y, int32_t rows, int32_t in,
                   int32_t out, void* workspace, size_t workspace_bytes, void* stream);
-/* The query producer of one layer for a batch of decode tokens, one launch:
+/* The query producer of one layer for a batch of decode tokens, two launches:
  * from the normalised hidden x [rows][hidden], q = head_rms(x wq^T) then
  * RoPE, k = head_rms(x wk^T) then RoPE, v = x wv^T, with head_dim 128, the
  * rotation at positions[rows] (device int32), frequencies theta^(-2i/128)
  * correctly rounded to fp32 and the reference's NeoX pairing (d, d + 64).
  * Outputs [rows][heads][128] fp32, ready for sa_hip_decode_step (q) and its
- * k/v.  hidden % 256 == 0; workspace of sa_hip_qkv_workspace_bytes bytes,
- * zeroed ONCE before the first call (arrival counters, left at zero). */
+ * k/v.  hidden % 256 == 0; workspace of sa_hip_qkv_workspace_bytes bytes
+ * (the K-slice partial tiles; no initialisation needed). */
 size_t sa_hip_qkv_workspace_bytes(int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads);
 int sa_hip_qkv_project(const float* x, const float* wq, const float* wk, const float* wv, const float* q_norm,
                        const float* k_norm, const int32_t* positions, int32_t rows, int32_t hidden,
                        int32_t q_heads, int32_t kv_heads, float theta, float eps, float* q, float* k, float* v,
                        void* workspace, size_t workspace_bytes, void* stream);
 /* sa_hip_rms_norm(hidden_rows, input_norm, input_eps) followed by
- * sa_hip_qkv_project, as ONE launch: the RMS scale of each row is applied to
+ * sa_hip_qkv_project, in the same two launches: the RMS scale of each row is applied to
  * its projected sums (x * w_norm is projected, then scaled by
  * 1 / sqrt(mean(x^2) + eps)), equal to the two calls within fp32 rounding.
  * Replaces the reference's rms_norm + q/k/v projections

@@ -902,9 +902,7 @@ static int linear_shape_ok(int32_t rows, int32_t in, int32_t out, const char* op
 
 size_t sa_hip_linear_workspace_bytes(int32_t rows, int32_t in, int32_t out) {
   if (rows <= 0 || in <= 0 || out <= 0) return 0;
-  const int ks = sa::linear_ksplit(rows, in, out);
-  return sa::linear_counter_bytes(rows, out) +
-         (ks > 1 ? static_cast<size_t>(ks) * rows * out * sizeof(float) : 0);
+  return sa::split_part_bytes(rows, in, out, false);
 }
 
 int sa_hip_linear(const float* x, const float* w, const float* residual, float* y, int32_t rows, int32_t in,
@@ -924,7 +922,7 @@ int sa_hip_linear(const float* x, const float* w, const float* residual, float* 
 size_t sa_hip_qkv_workspace_bytes(int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads) {
   if (rows <= 0 || hidden <= 0 || q_heads <= 0 || kv_heads <= 0) return 0;
   const int64_t out = static_cast<int64_t>(q_heads + 2 * kv_heads) * sa::kHeadDim;
-  return sa::qkv_counter_bytes(rows, q_heads, kv_heads) + static_cast<size_t>(rows) * out * sizeof(float);
+  return sa::split_part_bytes(rows, hidden, out, true);
 }
 
 static int qkv_common(const float* x, const float* gain, float in_eps, const float* wq, const float* wk,

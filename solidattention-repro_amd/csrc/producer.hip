@@ -6,20 +6,21 @@
 // :576-584, :640-645; cpp/src/qwen_chain_main.cpp:365-399) for a batch of
 // decode tokens (one row per sequence).
 //
-// Projection (proj_kernel): y[r][o] = sum_i x[r][i] w[o][i].  At decode the
-// rows are few (the batch) and the weights are the traffic.  A workgroup of
-// 4 waves owns 16 output columns and up to 64 rows over a K range (all of K,
-// or 1/ks of it), taken in 128-k chunks that all 256 threads stage in LDS
-// with row-contiguous loads (two chunks ahead); wave t then runs the
-// v_mfma_f32_16x16x4f32 steps of rows 16 t .. 16 t + 15 against the 16
-// columns (any order of the k sum is a valid fp32 sum, and the order is
-// fixed: deterministic).  Epilogues run in the same launch:
-//   * linear: with ks > 1 the K slices write partial tiles; the last slice to
-//     arrive (an arrival counter per column slab, left at zero) adds them in
-//     slice order plus the residual;
-//   * q/k/v: the optional input RMSNorm folds into a per-row scale (every
-//     workgroup sees whole rows: ks is 1), v columns are written directly,
-//     and the last of a q/k head's 8 slabs to arrive applies head RMS + RoPE.
+// Projections: y[r][o] = sum_i x[r][i] w[o][i].  At decode the rows are few
+// (the batch) and the weights are the traffic.  Two launches:
+//   * proj_split_kernel<C, KS>: a workgroup of 4 waves takes 64 rows x C
+//     columns (64 or 32) over one K slice of KS = 256 (one workgroup per
+//     compute unit at 1024 -> 4096 and 2048 -> 1024).  It issues all its
+//     loads at once in 32-k units, stores each
+//     unit to its LDS region as it arrives and runs that unit's
+//     v_mfma_f32_16x16x4f32 steps (wave t: rows 16 t .. + 15) while later
+//     units are in flight; the partial tile goes to the workspace.  With
+//     the input RMSNorm folded in, x is multiplied by the norm weight as it
+//     is staged and the slice's sum of squares of x per row is kept.
+//   * the reduce launch adds the slices in slice order (any order of the k
+//     sum is a valid fp32 sum; this one is fixed: deterministic) and applies
+//     the epilogue: the residual (linear), or the row's RMSNorm scale, then
+//     head RMS norm + RoPE for q/k heads (qkv).
 #include <algorithm>
 
 #include "sa_device.hpp"
@@ -31,24 +32,14 @@ namespace {
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;  // 4
-constexpr int kCols = 16;                 // output columns per workgroup
 constexpr int kMTile = 16;
 constexpr int kMTiles = 4;
 constexpr int kRowsPerWg = kMTile * kMTiles;  // 64
-constexpr int kChunk = 64;                // k per pipeline stage and wave
-constexpr int kKPerWgUnit = kWaves * kChunk;  // 256: K per workgroup is a multiple
 
 __device__ inline f32x4_t load_nt4(const float* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
 }
 
-// Values handed from one workgroup to another (possibly on another XCD) go
-// through agent-scope atomic stores and loads: coherent single accesses, with
-// no L2 writeback or invalidate (an agent-scope fence would write back and
-// invalidate the whole L2 of the XCD, and with it the x rows every other
-// workgroup is reading).  The writer waits for its stores to complete before
-// the arrival counter is incremented.
 __device__ inline float block_sum(float v, float* red) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
@@ -88,26 +79,151 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* x, cons
   }
 }
 
-struct ProjParams {
+// ---- split-K projections ------------------------------------------------------
+// A workgroup takes 64 rows x C columns over one K slice of KS.  All its
+// loads (x times the input gain, and w: up to 32 float4 per thread) are
+// issued at once, in 32-k units; each unit goes to
+// its own LDS region as it arrives and its matrix steps run while the later
+// units are still in flight.  A second launch adds the slices in slice order
+// and applies the epilogue.  Against whole-K columns of 16 this cuts what a
+// compute unit pulls from L2 (x is read once per slice and column block, not
+// once per 16 columns) and gives each LDS read of x C / 16 matrix steps.
+constexpr int kUnitK = 32;
+constexpr int kSplitMaxSlices = 8;
+
+struct SplitParams {
   const float* x;          // [rows][in]
-  const float* w[3];       // [out][in]; weight j covers output columns [w_end[j-1], w_end[j])
+  const float* w[3];       // [out][in]; weight j covers columns [w_end[j-1], w_end[j])
   int32_t w_end[3];
-  const float* gain;       // q/k/v: optional input RMSNorm weight [in]
-  float in_eps;
-  const float* residual;   // linear: optional [rows][out]
-  float* y;                // linear: [rows][out]
-  float* part;             // linear: [ks][rows][out] slice tiles (ks > 1); q/k/v: [rows][out] before the head epilogue
-  int32_t* counters;       // arrival counters, zero between launches
+  const float* gain;       // optional input RMSNorm weight [in]: x * gain is projected
+  float* part;             // [slices][rows_pad][out]
+  float* ss;               // [slices][rows_pad]: partial sums of squares of x (gain only)
   int32_t rows;
+  int32_t rows_pad;
   int32_t in;
   int32_t out;
-  int32_t ks;
-  // q/k/v epilogue
+};
+
+template <int C, int KS, bool GAIN>
+__global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams p) {
+  constexpr int kNU = KS / kUnitK;                        // units
+  constexpr int kXU = kRowsPerWg * kUnitK / 4 / kThreads;  // 2 float4 of x per thread and unit
+  constexpr int kWU = C * kUnitK / 4 / kThreads;          // C / 32 float4 of w
+  constexpr int kCT = C / 16;                             // column tiles
+  constexpr int kStr = KS + 4;                            // padded LDS row (floats)
+  static_assert(kXU * kNU + kWU * kNU <= 32, "the whole tile in registers");
+  __shared__ __align__(16) float xs[kRowsPerWg * kStr];
+  __shared__ __align__(16) float ws[C * kStr];
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int cb = blockIdx.x;
+  const int z = blockIdx.y;
+  const int mb = blockIdx.z;
+  const int n0 = cb * C;
+  const int m0 = mb * kRowsPerWg;
+  int wi = 0;
+  if (n0 >= p.w_end[0]) wi = n0 >= p.w_end[1] ? 2 : 1;
+  const int col0 = wi == 0 ? 0 : p.w_end[wi - 1];
+  const float* wbase = p.w[wi] + static_cast<int64_t>(n0 - col0) * p.in;
+  const int k0 = z * KS;
+  const int c4 = tid % 8;  // float4 e of a thread covers k 4 c4 .. + 3 of its unit; row / column e / 8
+
+  f32x4_t xr[kNU][kXU], wr[kNU][kWU], g4[kNU];
+#pragma unroll
+  for (int u = 0; u < kNU; ++u) {
+    const int kc = k0 + u * kUnitK + 4 * c4;
+#pragma unroll
+    for (int i = 0; i < kXU; ++i) {
+      const int m = m0 + (i * kThreads + tid) / 8;
+      const int mm = m < p.rows ? m : p.rows - 1;  // rows past the batch read row rows-1, never used
+      xr[u][i] = *reinterpret_cast<const f32x4_t*>(p.x + static_cast<int64_t>(mm) * p.in + kc);
+    }
+#pragma unroll
+    for (int i = 0; i < kWU; ++i)
+      wr[u][i] = load_nt4(wbase + static_cast<int64_t>((i * kThreads + tid) / 8) * p.in + kc);
+    if (GAIN) g4[u] = *reinterpret_cast<const f32x4_t*>(p.gain + kc);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4_t acc[kCT];
+#pragma unroll
+  for (int t = 0; t < kCT; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float ss[kXU];
+#pragma unroll
+  for (int i = 0; i < kXU; ++i) ss[i] = 0.0f;
+  // wave: rows 16 wave .. + 15 against the C columns; step s of a unit covers
+  // k = 16 s + [0, 16), lane l supplying k = 16 s + 4 (l / 16) + e to matrix step 4 s + e
+  const float* xa = &xs[(wave * kMTile + lane % 16) * kStr + 4 * (lane / 16)];
+  const float* wb = &ws[(lane % 16) * kStr + 4 * (lane / 16)];
+#pragma unroll
+  for (int u = 0; u < kNU; ++u) {
+#pragma unroll
+    for (int i = 0; i < kXU; ++i) {
+      f32x4_t v = xr[u][i];
+      if (GAIN) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss[i] = __builtin_fmaf(v[e], v[e], ss[i]);
+        v = v * g4[u];
+      }
+      *reinterpret_cast<f32x4_t*>(&xs[((i * kThreads + tid) / 8) * kStr + u * kUnitK + 4 * c4]) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < kWU; ++i)
+      *reinterpret_cast<f32x4_t*>(&ws[((i * kThreads + tid) / 8) * kStr + u * kUnitK + 4 * c4]) = wr[u][i];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kUnitK / 16; ++s) {
+      const int k = u * kUnitK + 16 * s;
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(xa + k);
+      f32x4_t b[kCT];
+#pragma unroll
+      for (int t = 0; t < kCT; ++t) b[t] = *reinterpret_cast<const f32x4_t*>(wb + t * 16 * kStr + k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int t = 0; t < kCT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[t][e], acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // D layout: lane holds rows 16 wave + 4 (lane / 16) + i, column 16 t + lane % 16
+  float* part = p.part + static_cast<int64_t>(z) * p.rows_pad * p.out;
+#pragma unroll
+  for (int t = 0; t < kCT; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = m0 + wave * kMTile + 4 * (lane / 16) + i;
+      part[static_cast<int64_t>(row) * p.out + n0 + 16 * t + lane % 16] = acc[t][i];
+    }
+  }
+  if (GAIN && cb == 0) {
+    // the slice's sum of squares of x per row: row (i * 256 + tid) / 8 is
+    // held by 8 consecutive threads
+#pragma unroll
+    for (int i = 0; i < kXU; ++i) {
+      float v = ss[i];
+#pragma unroll
+      for (int off = 4; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+      if (c4 == 0) p.ss[static_cast<int64_t>(z) * p.rows_pad + m0 + (i * kThreads + tid) / 8] = v;
+    }
+  }
+}
+
+struct QkvReduceParams {
+  const float* part;       // [slices][rows_pad][out]
+  const float* ss;         // [slices][rows_pad] or null (no input RMSNorm)
+  int32_t slices;
+  int32_t rows;
+  int32_t rows_pad;
+  int32_t in;
+  int32_t out;
+  float in_eps;
   const float* q_norm;
   const float* k_norm;
   const int32_t* positions;
-  float* q;                // [rows][q_heads][128]
-  float* k;                // [rows][kv_heads][128]
+  float* q;
+  float* k;
   float* v;
   int32_t q_heads;
   int32_t kv_heads;
@@ -115,339 +231,113 @@ struct ProjParams {
   float inv_freq[64];
 };
 
-// One thread's share of a 128-k chunk: x [64 rows][128] is 2048 float4 (8 per
-// thread), w [16 columns][128] is 512 float4 (2 per thread); thread e of a
-// float4 index reads row e / 32, float4 e % 32 of that row, so a wave's load
-// covers two whole 512-byte row segments.
-constexpr int kKC = 128;
-constexpr int kLdsStride = kKC + 4;  // padded LDS rows (floats)
-constexpr int kXVecs = kRowsPerWg * kKC / 4 / kThreads;  // 8
-constexpr int kWVecs = kCols * kKC / 4 / kThreads;       // 2
-
-struct ChunkRegs {
-  f32x4_t x[kXVecs];
-  f32x4_t w[kWVecs];
-  f32x4_t g;
-};
-
-template <bool GAIN>
-__device__ inline void chunk_load(ChunkRegs& r, const ProjParams& p, const float* wbase, int m0, int kc) {
+// Workgroup (head, 8-row block): the slices of the head's 128 columns added
+// in slice order, times the row's input RMSNorm scale; q and k heads then
+// take the head RMS norm and RoPE (NeoX pairs d, d + 64).  Thread t: row
+// t / 32, d = 4 (t % 32) .. + 3; d and d + 64 sit 16 threads apart.
+__device__ inline void qkv_reduce_rows(const QkvReduceParams& p, int hh, int rb) {
   const int tid = threadIdx.x;
-  const int c4 = tid % 32;
-#pragma unroll
-  for (int i = 0; i < kWVecs; ++i) {
-    const int col = (i * kThreads + tid) / 32;
-    r.w[i] = load_nt4(wbase + static_cast<int64_t>(col) * p.in + kc + 4 * c4);
+  const int j = tid % 32;
+  const int row = rb * 8 + tid / 32;
+  const int rr = row < p.rows ? row : p.rows - 1;  // rows past the batch compute row rows-1, not stored
+  const int64_t col = static_cast<int64_t>(hh) * kHeadDim + 4 * j;
+  f32x4_t v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int z = 0; z < p.slices; ++z)
+    v += *reinterpret_cast<const f32x4_t*>(p.part + (static_cast<int64_t>(z) * p.rows_pad + rr) * p.out + col);
+  if (p.ss) {
+    float tot = 0.0f;
+    for (int z = 0; z < p.slices; ++z) tot += p.ss[static_cast<int64_t>(z) * p.rows_pad + rr];
+    v *= 1.0f / __builtin_sqrtf(tot / static_cast<float>(p.in) + p.in_eps);
   }
-#pragma unroll
-  for (int i = 0; i < kXVecs; ++i) {
-    const int m = m0 + (i * kThreads + tid) / 32;
-    const int mm = m < p.rows ? m : p.rows - 1;  // rows past the batch read row rows-1, never stored
-    r.x[i] = *reinterpret_cast<const f32x4_t*>(p.x + static_cast<int64_t>(mm) * p.in + kc + 4 * c4);
+  if (hh >= p.q_heads + p.kv_heads) {
+    if (row < p.rows)
+      *reinterpret_cast<f32x4_t*>(p.v + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads - p.kv_heads)) *
+                                            kHeadDim + 4 * j) = v;
+    return;
   }
-  if (GAIN) r.g = *reinterpret_cast<const f32x4_t*>(p.gain + kc + 4 * c4);
-}
-
-template <bool GAIN>
-__device__ inline void chunk_store(const ChunkRegs& r, float* xs, float* ws, float (&ss)[kXVecs]) {
-  const int tid = threadIdx.x;
-  const int c4 = tid % 32;
-#pragma unroll
-  for (int i = 0; i < kWVecs; ++i) {
-    const int col = (i * kThreads + tid) / 32;
-    *reinterpret_cast<f32x4_t*>(ws + col * kLdsStride + 4 * c4) = r.w[i];
-  }
-#pragma unroll
-  for (int i = 0; i < kXVecs; ++i) {
-    const int row = (i * kThreads + tid) / 32;
-    f32x4_t v = r.x[i];
-    if (GAIN) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ss[i] = __builtin_fmaf(v[e], v[e], ss[i]);
-      v = v * r.g;
-    }
-    *reinterpret_cast<f32x4_t*>(xs + row * kLdsStride + 4 * c4) = v;
-  }
-}
-
-// Wave t: rows 16 t .. 16 t + 15 of the chunk against its 16 columns; step s
-// covers k = 16 s + [0, 16), lane l supplying k = 16 s + 4 (l / 16) + e to
-// MFMA 4 s + e.
-__device__ inline void chunk_mfma(const float* xs, const float* ws, int wave, int lane, f32x4_t& acc) {
-  const float* xa = xs + (wave * kMTile + lane % 16) * kLdsStride + 4 * (lane / 16);
-  const float* wb = ws + (lane % 16) * kLdsStride + 4 * (lane / 16);
-#pragma unroll
-  for (int s = 0; s < kKC / 16; ++s) {
-    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(xa + 16 * s);
-    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(wb + 16 * s);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
-  }
-}
-
-// The head RMS norm then RoPE (NeoX pairs d, d + 64) of rows [m0, m0 + 64) of
-// q/k head hh (hh < q_heads: q) from the pre-epilogue values in part.  Wave w
-// takes rows m0 + w + 4 i, i < 16, lane l holding d = l and l + 64; the 16
-// rows are independent, so their loads, reductions, sincos and stores are
-// issued together (fully unrolled, no early exit).
-__device__ inline void qk_head_epilogue(const ProjParams& p, int m0, int hh) {
-  constexpr int kRowsPerWave = kRowsPerWg / kWaves;
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
   const bool is_q = hh < p.q_heads;
-  const float* norm = is_q ? p.q_norm : p.k_norm;
-  const float n_lo = norm[lane], n_hi = norm[lane + 64];
-  const float f = p.inv_freq[lane];
-  float a[kRowsPerWave], b[kRowsPerWave], ss[kRowsPerWave], angle[kRowsPerWave];
+  float sq = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
 #pragma unroll
-  for (int i = 0; i < kRowsPerWave; ++i) {
-    const int row = m0 + wave + kWaves * i;
-    const int rr = row < p.rows ? row : m0;
-    const float* src = p.part + static_cast<int64_t>(rr) * p.out + hh * kHeadDim;
-    a[i] = load_agent(src + lane);
-    b[i] = load_agent(src + lane + 64);
-    angle[i] = static_cast<float>(p.positions[rr]) * f;
-  }
+  for (int off = 16; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
+  const float inv = 1.0f / __builtin_sqrtf(sq / static_cast<float>(kHeadDim) + p.eps);
+  const f32x4_t n4 = *reinterpret_cast<const f32x4_t*>((is_q ? p.q_norm : p.k_norm) + 4 * j);
+  f32x4_t x, y, o;
 #pragma unroll
-  for (int i = 0; i < kRowsPerWave; ++i) ss[i] = a[i] * a[i] + b[i] * b[i];
+  for (int e = 0; e < 4; ++e) x[e] = v[e] * inv * n4[e];
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
+  for (int e = 0; e < 4; ++e) y[e] = __shfl_xor(x[e], 16, kWave);  // the pair partner, d +- 64
+  const float pos = static_cast<float>(p.positions[rr]);
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave; ++i) ss[i] += __shfl_xor(ss[i], off, kWave);
-  }
-#pragma unroll
-  for (int i = 0; i < kRowsPerWave; ++i) {
-    const int row = m0 + wave + kWaves * i;
-    const float inv = 1.0f / __builtin_sqrtf(ss[i] / static_cast<float>(kHeadDim) + p.eps);
-    const float x0 = a[i] * inv * n_lo;
-    const float x1 = b[i] * inv * n_hi;
+  for (int e = 0; e < 4; ++e) {
     float sn, cs;
-    sincosf(angle[i], &sn, &cs);
-    if (row < p.rows) {
-      float* dst = is_q ? p.q + (static_cast<int64_t>(row) * p.q_heads + hh) * kHeadDim
-                        : p.k + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads)) * kHeadDim;
-      dst[lane] = x0 * cs - x1 * sn;
-      dst[lane + 64] = x1 * cs + x0 * sn;
-    }
+    sincosf(pos * p.inv_freq[(4 * j + e) % 64], &sn, &cs);
+    o[e] = j < 16 ? x[e] * cs - y[e] * sn : x[e] * cs + y[e] * sn;
+  }
+  if (row < p.rows) {
+    float* dst = is_q ? p.q + (static_cast<int64_t>(row) * p.q_heads + hh) * kHeadDim
+                      : p.k + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads)) * kHeadDim;
+    *reinterpret_cast<f32x4_t*>(dst + 4 * j) = o;
   }
 }
 
-// QKV: q/k/v producer (ks 1); else the linear (ks K slices).  Chunks of the
-// workgroup's K range are staged in LDS two ahead (registers, then one of two
-// LDS buffers); the chunk order starts at the slab's index so that the
-// workgroups, which read the same x, do not all read the same addresses at
-// the same time.
-template <bool QKV, bool GAIN>
-__global__ __launch_bounds__(kThreads) void proj_kernel(const ProjParams p) {
-  __shared__ __align__(16) float xs[2][kRowsPerWg * kLdsStride];
-  __shared__ __align__(16) float ws[2][kCols * kLdsStride];
-  __shared__ float ss_s[kRowsPerWg];
-  __shared__ int s_last;
-  const int tid = threadIdx.x;
-  const int wave = tid / kWave;
-  const int lane = tid % kWave;
-  const int slab = blockIdx.x;
-  const int z = blockIdx.y;
-  const int mb = blockIdx.z;
-  const int n0 = slab * kCols;
-  const int m0 = mb * kRowsPerWg;
-  const int kslice = p.in / p.ks;
-  const int chunks = kslice / kKC;  // even, >= 2
-  const int rot = slab % chunks;
+__global__ __launch_bounds__(kThreads) void qkv_reduce_kernel(const QkvReduceParams p) {
+  for (int rb = blockIdx.y; rb * 8 < p.rows; rb += gridDim.y) qkv_reduce_rows(p, blockIdx.x, rb);
+}
 
-  int wi = 0;
-  if (n0 >= p.w_end[0]) wi = n0 >= p.w_end[1] ? 2 : 1;
-  const int col0 = wi == 0 ? 0 : p.w_end[wi - 1];
-  const float* wbase = p.w[wi] + static_cast<int64_t>(n0 - col0) * p.in;
-  auto kc_of = [&](int c) { return z * kslice + ((c + rot) % chunks) * kKC; };
-
-  f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float ss[kXVecs];
-#pragma unroll
-  for (int i = 0; i < kXVecs; ++i) ss[i] = 0.0f;
-  if (chunks % 4 == 0) {
-    // four chunks in flight (registers r0..r3), two in LDS: at the top of
-    // an iteration chunk c is in LDS buffer 0 and r1, r2, r3 hold c + 1 ..
-    // c + 3; the loads of the steady state are unconditional
-    ChunkRegs r0, r1, r2, r3;
-    chunk_load<GAIN>(r0, p, wbase, m0, kc_of(0));
-    chunk_load<GAIN>(r1, p, wbase, m0, kc_of(1));
-    chunk_load<GAIN>(r2, p, wbase, m0, kc_of(2));
-    chunk_load<GAIN>(r3, p, wbase, m0, kc_of(3));
-    chunk_store<GAIN>(r0, xs[0], ws[0], ss);
-    __syncthreads();
-    int c = 0;
-    for (; c + 7 < chunks; c += 4) {
-      chunk_load<GAIN>(r0, p, wbase, m0, kc_of(c + 4));
-      __builtin_amdgcn_sched_barrier(0);
-      chunk_mfma(xs[0], ws[0], wave, lane, acc);
-      chunk_store<GAIN>(r1, xs[1], ws[1], ss);
-      __syncthreads();
-      chunk_load<GAIN>(r1, p, wbase, m0, kc_of(c + 5));
-      __builtin_amdgcn_sched_barrier(0);
-      chunk_mfma(xs[1], ws[1], wave, lane, acc);
-      chunk_store<GAIN>(r2, xs[0], ws[0], ss);
-      __syncthreads();
-      chunk_load<GAIN>(r2, p, wbase, m0, kc_of(c + 6));
-      __builtin_amdgcn_sched_barrier(0);
-      chunk_mfma(xs[0], ws[0], wave, lane, acc);
-      chunk_store<GAIN>(r3, xs[1], ws[1], ss);
-      __syncthreads();
-      chunk_load<GAIN>(r3, p, wbase, m0, kc_of(c + 7));
-      __builtin_amdgcn_sched_barrier(0);
-      chunk_mfma(xs[1], ws[1], wave, lane, acc);
-      chunk_store<GAIN>(r0, xs[0], ws[0], ss);
-      __syncthreads();
-    }
-    // the last four chunks
-    chunk_mfma(xs[0], ws[0], wave, lane, acc);
-    chunk_store<GAIN>(r1, xs[1], ws[1], ss);
-    __syncthreads();
-    chunk_mfma(xs[1], ws[1], wave, lane, acc);
-    chunk_store<GAIN>(r2, xs[0], ws[0], ss);
-    __syncthreads();
-    chunk_mfma(xs[0], ws[0], wave, lane, acc);
-    chunk_store<GAIN>(r3, xs[1], ws[1], ss);
-    __syncthreads();
-    chunk_mfma(xs[1], ws[1], wave, lane, acc);
-  } else {
-  ChunkRegs r0, r1;
-  chunk_load<GAIN>(r0, p, wbase, m0, kc_of(0));
-  chunk_load<GAIN>(r1, p, wbase, m0, kc_of(1));
-  chunk_store<GAIN>(r0, xs[0], ws[0], ss);
-  __syncthreads();
-  // iteration c: chunk c in LDS buffer 0, chunk c + 1 in registers r1.  The
-  // loads of the steady state are unconditional: a load under a branch makes
-  // the compiler wait for it at the next use of the other buffer, which would
-  // expose the whole latency once per chunk.
-  // (the scheduling barriers keep each chunk's loads ahead of the matrix
-  // work instead of sunk next to their LDS stores)
-  int c = 0;
-  for (; c + 3 < chunks; c += 2) {
-    chunk_load<GAIN>(r0, p, wbase, m0, kc_of(c + 2));
-    __builtin_amdgcn_sched_barrier(0);
-    chunk_mfma(xs[0], ws[0], wave, lane, acc);
-    chunk_store<GAIN>(r1, xs[1], ws[1], ss);
-    __syncthreads();
-    chunk_load<GAIN>(r1, p, wbase, m0, kc_of(c + 3));
-    __builtin_amdgcn_sched_barrier(0);
-    chunk_mfma(xs[1], ws[1], wave, lane, acc);
-    chunk_store<GAIN>(r0, xs[0], ws[0], ss);
-    __syncthreads();
+// y[row][c..c+3] = the slices added in slice order (+ residual).
+__global__ __launch_bounds__(kWave) void linear_reduce_kernel(const float* part, int slices, int rows,
+                                                              int rows_pad, int out, const float* residual,
+                                                              float* y) {
+  const int c = (blockIdx.x * kWave + threadIdx.x) * 4;
+  if (c >= out) return;
+  for (int row = blockIdx.y; row < rows; row += gridDim.y) {
+    f32x4_t v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int z = 0; z < slices; ++z)
+      v += *reinterpret_cast<const f32x4_t*>(part + (static_cast<int64_t>(z) * rows_pad + row) * out + c);
+    const int64_t o = static_cast<int64_t>(row) * out + c;
+    if (residual) v += *reinterpret_cast<const f32x4_t*>(residual + o);
+    *reinterpret_cast<f32x4_t*>(y + o) = v;
   }
-  // the last two chunks
-  chunk_mfma(xs[0], ws[0], wave, lane, acc);
-  chunk_store<GAIN>(r1, xs[1], ws[1], ss);
-  __syncthreads();
-  chunk_mfma(xs[1], ws[1], wave, lane, acc);
-  }
-
-  // D layout: lane holds rows 16 wave + 4 (lane / 16) + i, column lane % 16
-  float inv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-  if (GAIN) {
-    // ss[i] of row (i * 256 + tid) / 32: the 32 threads of a row are half a wave
-#pragma unroll
-    for (int i = 0; i < kXVecs; ++i) {
-      float v = ss[i];
-#pragma unroll
-      for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-      if (tid % 32 == 0) ss_s[(i * kThreads + tid) / 32] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float tot = ss_s[wave * kMTile + 4 * (lane / 16) + i];
-      inv[i] = 1.0f / __builtin_sqrtf(tot / static_cast<float>(p.in) + p.in_eps);
-    }
-  }
-  const int col = n0 + lane % 16;
-
-  if (QKV) {
-    const bool is_v = n0 >= p.w_end[1];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = m0 + wave * kMTile + 4 * (lane / 16) + i;
-      if (row >= p.rows) continue;
-      const float val = acc[i] * inv[i];
-      if (is_v) {
-        p.v[static_cast<int64_t>(row) * p.kv_heads * kHeadDim + (col - p.w_end[1])] = val;
-      } else {
-        store_agent(p.part + static_cast<int64_t>(row) * p.out + col, val);
-      }
-    }
-    if (is_v) return;
-    // the last of the head's 8 slabs applies head RMS + RoPE
-    const int hh = n0 / kHeadDim;
-    if (!last_arrival(p.counters + mb * (p.q_heads + p.kv_heads) + hh, kHeadDim / kCols, &s_last)) return;
-    qk_head_epilogue(p, m0, hh);
-    return;
-  }
-
-  // linear
-  const int64_t slice = static_cast<int64_t>(p.rows) * p.out;
-  if (p.ks == 1) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = m0 + wave * kMTile + 4 * (lane / 16) + i;
-      if (row >= p.rows) continue;
-      const int64_t o = static_cast<int64_t>(row) * p.out + col;
-      p.y[o] = p.residual ? acc[i] + p.residual[o] : acc[i];
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = m0 + wave * kMTile + 4 * (lane / 16) + i;
-    if (row < p.rows) store_agent(p.part + z * slice + static_cast<int64_t>(row) * p.out + col, acc[i]);
-  }
-  if (!last_arrival(p.counters + mb * (p.out / kCols) + slab, p.ks, &s_last)) return;
-  // the slices in slice order, then the residual: thread e sums row e / 4,
-  // columns 4 (e % 4) .. + 3
-  const int row = m0 + tid / 4;
-  if (row >= p.rows) return;
-  const int64_t o = static_cast<int64_t>(row) * p.out + n0 + 4 * (tid % 4);
-  // the slices' values loaded together (up to 8 at a time), then added in order
-  float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int z0 = 0; z0 < p.ks; z0 += 8) {
-    float v[8][4];
-#pragma unroll
-    for (int zz = 0; zz < 8; ++zz) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[zz][j] = z0 + zz < p.ks ? load_agent(p.part + (z0 + zz) * slice + o + j) : 0.0f;
-    }
-#pragma unroll
-    for (int zz = 0; zz < 8; ++zz) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (z0 + zz < p.ks) sum[j] += v[zz][j];
-    }
-  }
-  f32x4_t v4{sum[0], sum[1], sum[2], sum[3]};
-  if (p.residual) v4 += *reinterpret_cast<const f32x4_t*>(p.residual + o);
-  *reinterpret_cast<f32x4_t*>(p.y + o) = v4;
 }
 
 }  // namespace
 
-int linear_ksplit(int64_t rows, int64_t in, int64_t out) {
-  // K slices so that the workgroups (16 columns x 64 rows each) about fill
-  // the compute units, each slice a multiple of 256 k (4 waves x 64)
-  const int64_t mblocks = (rows + kRowsPerWg - 1) / kRowsPerWg;
-  const int64_t blocks = (out / kCols) * mblocks;
-  int64_t ks = 1;
-  while (blocks * ks * 2 <= compute_units() && (in / (ks * 2)) % kKPerWgUnit == 0) ks *= 2;
-  return static_cast<int>(ks);
+// Tile of a split projection: 64 columns x 256 k when that gives every
+// compute unit a workgroup with at most 8 K slices (1024 -> 4096: 256
+// workgroups, 4 slices), else 32 columns x 256 k (2048 -> 1024: 256
+// workgroups, 8 slices); the slices are in / 256.
+SplitShape split_shape(int64_t rows, int64_t in, int64_t out) {
+  const int64_t rb = (rows + kRowsPerWg - 1) / kRowsPerWg;
+  SplitShape sh{64, static_cast<int32_t>(in / 256)};
+  if (sh.slices > kSplitMaxSlices || (out / 64) * sh.slices * rb < compute_units()) {
+    sh.cols = 32;
+    sh.slices = static_cast<int32_t>(in / 256);
+  }
+  return sh;
 }
 
-size_t linear_counter_bytes(int64_t rows, int64_t out) {
-  const int64_t mblocks = (rows + kRowsPerWg - 1) / kRowsPerWg;
-  return static_cast<size_t>((mblocks * (out / kCols) * 4 + 255) / 256 * 256);
+size_t split_part_bytes(int64_t rows, int64_t in, int64_t out, bool with_ss) {
+  const SplitShape sh = split_shape(rows, in, out);
+  const int64_t rows_pad = (rows + kRowsPerWg - 1) / kRowsPerWg * kRowsPerWg;
+  const size_t part = static_cast<size_t>(sh.slices) * rows_pad * out * sizeof(float);
+  return part + (with_ss ? static_cast<size_t>(sh.slices) * rows_pad * sizeof(float) : 0);
 }
 
-size_t qkv_counter_bytes(int64_t rows, int q_heads, int kv_heads) {
-  const int64_t mblocks = (rows + kRowsPerWg - 1) / kRowsPerWg;
-  return static_cast<size_t>((mblocks * (q_heads + kv_heads) * 4 + 255) / 256 * 256);
+namespace {
+
+hipError_t launch_split(const SplitParams& p, const SplitShape& sh, int rb, hipStream_t stream) {
+  const dim3 grid(p.out / sh.cols, sh.slices, rb);
+  if (sh.cols == 64) {
+    if (p.gain) hipLaunchKernelGGL((proj_split_kernel<64, 256, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((proj_split_kernel<64, 256, false>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    if (p.gain) hipLaunchKernelGGL((proj_split_kernel<32, 256, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((proj_split_kernel<32, 256, false>), grid, dim3(kThreads), 0, stream, p);
+  }
+  return hipGetLastError();
 }
+
+}  // namespace
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, int rows, int width, float eps,
                            hipStream_t stream) {
@@ -456,28 +346,31 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* out, int rows,
 }
 
 hipError_t launch_linear(const LinearLaunch& l, hipStream_t stream) {
-  const int ks = linear_ksplit(l.rows, l.in, l.out);
-  ProjParams p{};
+  const SplitShape sh = split_shape(l.rows, l.in, l.out);
+  const int rb = (l.rows + kRowsPerWg - 1) / kRowsPerWg;
+  SplitParams p{};
   p.x = l.x;
   p.w[0] = p.w[1] = p.w[2] = l.w;
   p.w_end[0] = p.w_end[1] = p.w_end[2] = l.out;
-  p.residual = l.residual;
-  p.y = l.y;
-  p.counters = reinterpret_cast<int32_t*>(l.workspace);
-  p.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(l.workspace) + linear_counter_bytes(l.rows, l.out));
+  p.part = l.workspace;
   p.rows = l.rows;
+  p.rows_pad = rb * kRowsPerWg;
   p.in = l.in;
   p.out = l.out;
-  p.ks = ks;
-  const dim3 grid(l.out / kCols, ks, (l.rows + kRowsPerWg - 1) / kRowsPerWg);
-  hipLaunchKernelGGL((proj_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
+  hipError_t e = launch_split(p, sh, rb, stream);
+  if (e != hipSuccess) return e;
+  const dim3 grid((l.out / 4 + kWave - 1) / kWave, std::min(l.rows, 65535));
+  hipLaunchKernelGGL(linear_reduce_kernel, grid, dim3(kWave), 0, stream, p.part, sh.slices, l.rows, p.rows_pad,
+                     l.out, l.residual, l.y);
   return hipGetLastError();
 }
 
 hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream) {
   const int qw = q.q_heads * kHeadDim, kw = q.kv_heads * kHeadDim;
   const int out = qw + 2 * kw;
-  ProjParams p{};
+  const SplitShape sh = split_shape(q.rows, q.hidden, out);
+  const int rb = (q.rows + kRowsPerWg - 1) / kRowsPerWg;
+  SplitParams p{};
   p.x = q.x;
   p.w[0] = q.wq;
   p.w[1] = q.wk;
@@ -486,30 +379,35 @@ hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream) {
   p.w_end[1] = qw + kw;
   p.w_end[2] = out;
   p.gain = q.gain;
-  p.in_eps = q.in_eps;
-  p.counters = reinterpret_cast<int32_t*>(q.workspace);
-  p.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(q.workspace) +
-                                    qkv_counter_bytes(q.rows, q.q_heads, q.kv_heads));
+  p.part = q.workspace;
   p.rows = q.rows;
+  p.rows_pad = rb * kRowsPerWg;
+  p.ss = q.workspace + static_cast<int64_t>(sh.slices) * p.rows_pad * out;
   p.in = q.hidden;
   p.out = out;
-  p.ks = 1;
-  p.q_norm = q.q_norm;
-  p.k_norm = q.k_norm;
-  p.positions = q.positions;
-  p.q = q.q;
-  p.k = q.k;
-  p.v = q.v;
-  p.q_heads = q.q_heads;
-  p.kv_heads = q.kv_heads;
-  p.eps = q.eps;
-  for (int i = 0; i < 64; ++i) p.inv_freq[i] = q.inv_freq[i];
-  const dim3 grid(out / kCols, 1, (q.rows + kRowsPerWg - 1) / kRowsPerWg);
-  if (q.gain) {
-    hipLaunchKernelGGL((proj_kernel<true, true>), grid, dim3(kThreads), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((proj_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
-  }
+  hipError_t e = launch_split(p, sh, rb, stream);
+  if (e != hipSuccess) return e;
+  QkvReduceParams r{};
+  r.part = p.part;
+  r.ss = q.gain ? p.ss : nullptr;
+  r.slices = sh.slices;
+  r.rows = q.rows;
+  r.rows_pad = p.rows_pad;
+  r.in = q.hidden;
+  r.out = out;
+  r.in_eps = q.in_eps;
+  r.q_norm = q.q_norm;
+  r.k_norm = q.k_norm;
+  r.positions = q.positions;
+  r.q = q.q;
+  r.k = q.k;
+  r.v = q.v;
+  r.q_heads = q.q_heads;
+  r.kv_heads = q.kv_heads;
+  r.eps = q.eps;
+  for (int i = 0; i < 64; ++i) r.inv_freq[i] = q.inv_freq[i];
+  const dim3 grid(q.q_heads + 2 * q.kv_heads, std::min((q.rows + 7) / 8, 65535));
+  hipLaunchKernelGGL(qkv_reduce_kernel, grid, dim3(kThreads), 0, stream, r);
   return hipGetLastError();
 }
 

@@ -90,7 +90,7 @@ struct LinearLaunch {
   const float* w;         // [out][in]
   const float* residual;  // [rows][out] or null
   float* y;               // [rows][out]
-  float* workspace;       // linear_counter_bytes, then (ks > 1) ks * rows * out floats; zero once
+  float* workspace;       // split_part_bytes(rows, in, out, false): the slices' partial tiles
   int32_t rows, in, out;
 };
 struct QkvLaunch {
@@ -111,10 +111,14 @@ struct QkvLaunch {
   float eps;
   float inv_freq[64];
 };
-int linear_ksplit(int64_t rows, int64_t in, int64_t out);
-// arrival counters at the front of the projection workspaces (256-byte padded)
-size_t linear_counter_bytes(int64_t rows, int64_t out);
-size_t qkv_counter_bytes(int64_t rows, int q_heads, int kv_heads);
+// Split-K projections: columns per workgroup and K slices; the workspace is
+// the slices' partial tiles (plus per-slice sums of squares of x for q/k/v).
+struct SplitShape {
+  int32_t cols;
+  int32_t slices;
+};
+SplitShape split_shape(int64_t rows, int64_t in, int64_t out);
+size_t split_part_bytes(int64_t rows, int64_t in, int64_t out, bool with_ss);
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, int rows, int width, float eps,
                            hipStream_t stream);
 hipError_t launch_linear(const LinearLaunch& l, hipStream_t stream);

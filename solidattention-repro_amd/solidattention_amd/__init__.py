@@ -322,8 +322,8 @@ def linear(x, w, residual=None, out=None, workspace=None, stream=None):
     if out is None:
         out = torch.empty((rows, n_out), dtype=torch.float32, device=x.device)
     nbytes = lib().sa_hip_linear_workspace_bytes(rows, n_in, n_out)
-    if workspace is None:  # zeroed once: its arrival counters start at zero
-        workspace = torch.zeros(max(nbytes // 4, 1), dtype=torch.float32, device=x.device)
+    if workspace is None:  # the K-slice partial tiles (no initialisation needed)
+        workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=x.device)
     check(lib().sa_hip_linear(_ptr(x), _ptr(w), _ptr(residual), _ptr(out), rows, n_in, n_out, _ptr(workspace),
                               workspace.numel() * 4, _stream(stream)), "linear")
     return out
@@ -342,8 +342,8 @@ def qkv_project(x, wq, wk, wv, q_norm, k_norm, positions, q_heads, kv_heads, the
     k = k if k is not None else torch.empty((rows, kv_heads, HEAD_DIM), dtype=torch.float32, device=dev)
     v = v if v is not None else torch.empty((rows, kv_heads, HEAD_DIM), dtype=torch.float32, device=dev)
     nbytes = lib().sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads)
-    if workspace is None:  # zeroed once: its arrival counters start at zero
-        workspace = torch.zeros(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
+    if workspace is None:  # the K-slice partial tiles (no initialisation needed)
+        workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
     if input_norm is None:
         check(lib().sa_hip_qkv_project(_ptr(x), _ptr(wq), _ptr(wk), _ptr(wv), _ptr(q_norm), _ptr(k_norm),
                                        _ptr(positions), rows, hidden, q_heads, kv_heads, C.c_float(theta),

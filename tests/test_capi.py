@@ -185,13 +185,17 @@ def test_producer_argument_checks():
     L = sa.lib()
     f = C.c_void_p(4096)
     need = L.sa_hip_linear_workspace_bytes(4, 1024, 2048)
-    assert need > 0 and need % 256 == 0  # arrival counters (+ K-slice partial sums)
+    # the K-slice partial tiles: 64-row tiles, 64 columns x 256 k when that
+    # gives the 256 compute units (off the GPU) a workgroup each, else 32
+    assert need == 4 * 64 * 2048 * 4  # 1024 -> 2048: 32 x 4 workgroups of 64 columns -> 32 columns
+    assert L.sa_hip_linear_workspace_bytes(64, 2048, 1024) == 8 * 64 * 1024 * 4
     assert L.sa_hip_linear(f, f, None, f, 4, 1000, 2048, f, need, None) == -1
     assert L.sa_hip_linear(f, f, None, f, 4, 1024, 2000, f, need, None) == -1
     assert L.sa_hip_linear(f, f, None, f, 4, 1024, 2048, f, need - 4, None) == -1
     assert L.sa_hip_linear(f, f, None, f, 4, 1024, 2048, None, need, None) == -1
     assert L.sa_hip_linear(f, f, None, f, 0, 1024, 2048, f, need, None) == -1
     qn = L.sa_hip_qkv_workspace_bytes(4, 1024, 16, 8)
+    assert qn == 4 * 64 * 4096 * 4 + 4 * 64 * 4  # 4 slices of partial tiles + sums of squares
     args = [f, f, f, f, f, f, f, 4, 1024, 16, 8]
     assert L.sa_hip_qkv_project(*args, C.c_float(1.0), C.c_float(1e-6), f, f, f, f, qn, None) == -1
     assert b"theta" in L.sa_hip_last_error()
