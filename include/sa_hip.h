@@ -426,7 +426,8 @@ size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads,
  * reference's std::exp(float)): the same table, polynomial and fused
  * multiply-adds in double, equal to it on every float, so the chosen tokens,
  * representatives and received masses are the reference's bit for bit.
- * Limits: head_dim 128, block_tokens 32, local_window <= 256. */
+ * Limits: head_dim 128, block_tokens 32, local_window <= 256, kv_heads <=
+ * 65536; prompt_queries and kv 16-byte aligned. */
 int sa_hip_local_causal_representatives(
     const float* prompt_queries, const uint16_t* kv, int64_t tokens,
     int32_t query_heads, int32_t kv_heads, int32_t head_dim,

@@ -707,7 +707,9 @@ int sa_hip_local_causal_representatives(const float* prompt_queries, const uint1
     return fail(SA_HIP_EINVAL, "local_causal_representatives: no output given");
   if (reps && rep_stride < tokens / block_tokens)
     return fail(SA_HIP_EINVAL, "local_causal_representatives: rep_stride %d below the block count", rep_stride);
-  if (!aligned16(kv)) return fail(SA_HIP_EINVAL, "local_causal_representatives: kv must be 16-byte aligned");
+  if (kv_heads > 65536) return fail(SA_HIP_EINVAL, "local_causal_representatives: kv_heads %d above 65536", kv_heads);
+  if (!aligned16(kv) || !aligned16(prompt_queries))
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: prompt_queries and kv must be 16-byte aligned");
   const size_t need = sa_hip_local_causal_workspace_bytes(tokens, query_heads, local_window);
   if (!workspace || workspace_bytes < need)
     return fail(SA_HIP_EINVAL, "local_causal_representatives: workspace of %zu bytes needed, %zu given", need,

@@ -30,16 +30,17 @@ __constant__ uint64_t kExpfTab[32] = {
 // the nearest integer by adding and subtracting 1.5 * 2^52 (k sits in the low
 // bits of the shifted double); r = fma(32/ln2, x, -k); 2^(k/32) from the
 // table; 2^(r/32) ~ 1 + c2 r + c1 r^2 + c0 r^3 as fma(fma(c0, r, c1), r^2,
-// fma(c2, r, 1)); the double result rounded to float.
+// fma(c2, r, 1)); the double result rounded to float.  The special inputs
+// (NaN, overflow, underflow) are selected after the main path, which runs for
+// every x (its table index k mod 32 is always in range), so a caller's
+// several exponentials issue their table reads together instead of one
+// branch at a time.
 __device__ inline float expf_glibc(float x) {
   constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32;
   constexpr double kShift = 0x1.8p+52;
   constexpr double kC0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
   constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0);
   constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-  if (x != x) return x + x;
-  if (x > 0x1.62e42ep6f) return __builtin_huge_valf();  // above log(2^128)
-  if (x < -0x1.9fe368p6f) return 0.0f;                  // below log(2^-150)
   const double xd = static_cast<double>(x);
   const double z = kInvLn2N * xd;
   const double kd_shifted = z + kShift;
@@ -52,7 +53,10 @@ __device__ inline float expf_glibc(float x) {
   double y = __builtin_fma(kC2, r, 1.0);
   y = __builtin_fma(p, r2, y);
   y = y * s;
-  return static_cast<float>(y);
+  float out = static_cast<float>(y);
+  out = x < -0x1.9fe368p6f ? 0.0f : out;                  // below log(2^-150)
+  out = x > 0x1.62e42ep6f ? __builtin_huge_valf() : out;  // above log(2^128)
+  return x != x ? x + x : out;
 }
 
 }  // namespace

@@ -34,7 +34,7 @@ namespace {
 constexpr int D = kHeadDim;
 constexpr int kMaxKeysPerLane = 4;  // window <= 4 x 64
 
-// Workgroup of the window kernel: 256 threads, at most 64 queries (32 KB of
+// Workgroup of the window kernel: 256 threads, at most 64 queries (33 KB of
 // staged queries).
 template <int WL>
 constexpr int window_threads() { return WL >= 4 ? 256 : 64 * WL; }
@@ -84,22 +84,69 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
   const int64_t q = q0 + qi;
   const int64_t token_elems = 2LL * p.hkv * D;
 
-  __shared__ float q_s[kQueriesPerGroup][D];
+  // query rows padded by 16 bytes: the 64 / WL queries of a wave read the
+  // same column at once, which unpadded 512-byte rows put in one bank group
+  __shared__ __align__(16) float q_s[kQueriesPerGroup][D + 4];
   __shared__ uint4 k_s[kMaxRows][kRowVecs + 1];
   __shared__ __align__(16) float e_s[kQueriesPerGroup][kMaxKeysPerLane * WL];
-  for (int e = tid; e < kQueriesPerGroup * D; e += kWindowThreads) {
-    const int64_t qq = q0 + e / D;
-    q_s[e / D][e % D] = qq < p.tokens ? p.pq[(static_cast<int64_t>(h) * p.tokens + qq) * D + e % D] : 0.0f;
-  }
+  // staging: per pass each thread issues a batch of query loads and a batch
+  // of key loads (4 pieces of 16 bytes each) before its first LDS store, so
+  // a pass costs one memory round trip.  Offsets are 32-bit from
+  // per-workgroup bases; pieces past the end are read from a clamped
+  // address (queries past the last token are never used, and a clamped key
+  // piece rewrites its own value).
+  constexpr int kQVecs = kQueriesPerGroup * D / 4;
+  constexpr int kBatch = 4;
+  constexpr int kQPasses = (kQVecs + kBatch * kWindowThreads - 1) / (kBatch * kWindowThreads);
+  const int q_rows = p.tokens - q0 < kQueriesPerGroup ? static_cast<int>(p.tokens - q0) : kQueriesPerGroup;
+  const int q_last_vec = q_rows * (D / 4) - 1;
+  const u32x4_t* qbase = reinterpret_cast<const u32x4_t*>(p.pq + (static_cast<int64_t>(h) * p.tokens + q0) * D);
   // key rows [row0, row0 + rows): every window of the workgroup's queries
   const int64_t row0 = q0 + 1 > p.window ? q0 + 1 - p.window : 0;
-  if (STAGE) {
-    const int64_t q_last = q0 + kQueriesPerGroup - 1 < p.tokens - 1 ? q0 + kQueriesPerGroup - 1 : p.tokens - 1;
-    const int rows = static_cast<int>(q_last - row0 + 1);
-    for (int e = tid; e < rows * kRowVecs; e += kWindowThreads) {
-      const int r = e / kRowVecs;
-      const int c = e % kRowVecs;
-      k_s[r][c] = reinterpret_cast<const uint4*>(p.kv + (row0 + r) * token_elems + g * D)[c];
+  const int64_t q_last = q0 + kQueriesPerGroup - 1 < p.tokens - 1 ? q0 + kQueriesPerGroup - 1 : p.tokens - 1;
+  const int rows = static_cast<int>(q_last - row0 + 1);
+  const int k_pieces = STAGE ? rows * kRowVecs : 0;
+  const u32x4_t* kbase = reinterpret_cast<const u32x4_t*>(p.kv + row0 * token_elems + g * D);
+  const int row_vecs = static_cast<int>(token_elems / 8);  // 16-byte pieces per token row of the pool
+  for (int pass = 0;; ++pass) {
+    const bool do_q = pass < kQPasses;                      // uniform
+    const bool do_k = pass * kBatch * kWindowThreads < k_pieces;  // uniform
+    if (!do_q && !do_k) break;
+    const int e0 = tid + pass * kBatch * kWindowThreads;
+    u32x4_t qv[kBatch];  // the float bits
+    u32x4_t kv[kBatch];
+    if (do_q) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + i * kWindowThreads;
+        qv[i] = qbase[e < q_last_vec ? e : q_last_vec];
+      }
+    }
+    if (do_k) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + i * kWindowThreads;
+        const int r = e / kRowVecs < rows ? e / kRowVecs : rows - 1;
+        kv[i] = kbase[r * row_vecs + e % kRowVecs];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (do_q) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        // a piece past the tile rewrites the last query's slot with the
+        // value its owner writes (or the slot of a query past the last token)
+        const int e = e0 + i * kWindowThreads < kQVecs ? e0 + i * kWindowThreads : kQVecs - 1;
+        *reinterpret_cast<u32x4_t*>(&q_s[e / (D / 4)][(e % (D / 4)) * 4]) = qv[i];
+      }
+    }
+    if (do_k) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + i * kWindowThreads;
+        const int r = e / kRowVecs < rows ? e / kRowVecs : rows - 1;
+        *reinterpret_cast<u32x4_t*>(&k_s[r][e % kRowVecs]) = kv[i];
+      }
     }
   }
   __syncthreads();
@@ -150,7 +197,10 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
 
   float e[kMaxKeysPerLane];
 #pragma unroll
-  for (int j = 0; j < kMaxKeysPerLane; ++j) e[j] = (wl + j * WL < count) ? expf_glibc(logit[j] - maximum) : 0.0f;
+  for (int j = 0; j < kMaxKeysPerLane; ++j) {
+    const float ej = expf_glibc(logit[j] - maximum);  // every key: the table reads go out together
+    e[j] = wl + j * WL < count ? ej : 0.0f;
+  }
 
   // denominator summed in window order, w = 0 .. count-1: the query's lanes
   // put their exponentials in LDS (the query's lanes are in one wave, whose
@@ -179,6 +229,17 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
   }
 }
 
+// Probability rows staged per token column: 32 columns plus one of padding,
+// so that lane j reading (row j + i, column j) hits bank 34 j mod 64.
+constexpr int kStageCols = kPageTokens + 1;
+static_assert(D == 2 * kWave, "block_topk_kernel: a lane per pair of dimensions");
+
+// Dynamic LDS of block_topk_kernel: the probabilities of the queries whose
+// windows reach a block (32 + W - 1 rows), one column per token of the block.
+size_t block_topk_lds_bytes(int window) {
+  return static_cast<size_t>(kPageTokens + window - 1) * kStageCols * sizeof(float);
+}
+
 // One wave per (block, head): received mass, stable rank, top-k, representative.
 __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   const int b = blockIdx.x;
@@ -186,34 +247,69 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   const int lane = threadIdx.x;
   const int g = h / (p.hq / p.hkv);
   const int64_t blocks = p.tokens / kPageTokens;
+  const int64_t t0 = static_cast<int64_t>(b) * kPageTokens;
   __shared__ int order[kPageTokens];
+  extern __shared__ float stage_s[];  // [rows][kStageCols]
 
-  // received mass: the probabilities of the queries t .. t+W-1 in query
-  // order, loaded 16 at a time before the sequential sum
+  // stage (row r, column j) = the probability query q = t0 + r gives token
+  // t0 + j, for the queries t0 .. t0 + 31 + W - 1: each row's 32 columns are
+  // contiguous in the query's window row, so a load instruction covers two
+  // rows; entries outside a query's window are loaded from a clamped column
+  // and never read
+  const int64_t q_last = t0 + kPageTokens - 1 + p.window - 1 < p.tokens - 1 ? t0 + kPageTokens - 1 + p.window - 1
+                                                                             : p.tokens - 1;
+  const int pieces = static_cast<int>(q_last - t0 + 1) * kPageTokens;
+  const float* prob_b = p.prob + (static_cast<int64_t>(h) * p.tokens + t0) * p.window;  // row of query t0
+  // the window of query t0 + r starts at t0 + r + 1 - W (at 0 for the first
+  // W - 1 queries): token t0 + j sits in column j - r + W - 1 (t0 + j)
+  const int first_full = static_cast<int>(t0 + 1 >= p.window ? 0 : p.window - 1 - t0);  // first row whose start > 0
+  constexpr int kBatch = 16;
+  for (int e0 = lane; e0 < pieces; e0 += kBatch * kWave) {
+    float v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;
+      const int r = e / kPageTokens;
+      const int j = e % kPageTokens;
+      int col = r >= first_full ? j - r + p.window - 1 : static_cast<int>(t0) + j;
+      col = col < 0 ? 0 : (col >= p.window ? p.window - 1 : col);
+      v[i] = prob_b[r * p.window + col];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch ahead of the stores
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;  // a clamped piece rewrites its value
+      stage_s[(e / kPageTokens) * kStageCols + e % kPageTokens] = v[i];
+    }
+  }
+  __syncthreads();
+
+  // received mass of token t = t0 + lane: the probabilities of the queries
+  // t .. min(t + W - 1, tokens - 1) summed in query order
   float r = 0.0f;
   if (lane < kPageTokens) {
-    const int64_t t = static_cast<int64_t>(b) * kPageTokens + lane;
-    const int64_t q_end = t + p.window - 1 < p.tokens - 1 ? t + p.window - 1 : p.tokens - 1;
-    constexpr int kBatch = 16;
-    for (int64_t q0 = t; q0 <= q_end; q0 += kBatch) {
-      float v[kBatch];
+    const int64_t t = t0 + lane;
+    const int n = static_cast<int>((t + p.window - 1 < p.tokens - 1 ? t + p.window - 1 : p.tokens - 1) - t + 1);
+    const float* col = stage_s + lane * kStageCols + lane;
+    constexpr int kReads = 8;  // LDS reads issued together, then added in order
+    for (int i0 = 0; i0 < n; i0 += kReads) {
+      float c[kReads];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const int64_t q = q0 + i;
-        const int64_t start = q + 1 > p.window ? q + 1 - p.window : 0;
-        v[i] = q <= q_end ? p.prob[(static_cast<int64_t>(h) * p.tokens + q) * p.window + (t - start)] : 0.0f;
-      }
+      for (int i = 0; i < kReads; ++i) c[i] = col[(i0 + i < n ? i0 + i : n - 1) * kStageCols];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i)
-        if (q0 + i <= q_end) r = r + v[i];
+      for (int i = 0; i < kReads; ++i)
+        if (i0 + i < n) r = r + c[i];
     }
     p.received[static_cast<int64_t>(h) * p.tokens + t] = r;
   }
-  // stable descending rank: greater ones first, equal ones in token order
+  // stable descending rank: greater ones first, equal (or unordered) ones in
+  // token order; lane j's mass broadcast by readlane, the tests combined
+  // without branches
   int rank = 0;
+#pragma unroll
   for (int j = 0; j < kPageTokens; ++j) {
-    const float rj = __shfl(r, j, kWave);
-    rank += (rj > r || (!(r > rj) && !(rj > r) && j < lane)) ? 1 : 0;
+    const float rj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), j));
+    rank += static_cast<int>((rj > r) | (!(r > rj) & !(rj > r) & (j < lane)));
   }
   if (lane < kPageTokens && rank < p.topk) {
     order[rank] = lane;
@@ -221,19 +317,44 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   }
   __syncthreads();
 
+  // representative: lane d-pair (2 lane, 2 lane + 1); the chosen keys' words
+  // loaded 8 at a time, summed in rank order
   const int64_t token_elems = 2LL * p.hkv * D;
-  const uint16_t* kblock = p.kv + static_cast<int64_t>(b) * kPageTokens * token_elems + g * D;
-  for (int d = lane; d < D; d += kWave) {
-    float sum = 0.0f;
-    for (int rk = 0; rk < p.topk; ++rk) sum = sum + h2f(kblock[order[rk] * token_elems + d]);
-    const float v = sum / static_cast<float>(p.topk);
-    if (p.values) p.values[(static_cast<int64_t>(h) * blocks + b) * D + d] = v;
-    if (p.reps) p.reps[(static_cast<int64_t>(h) * D + d) * p.rep_stride + b] = v;
+  const uint32_t* kblock =
+      reinterpret_cast<const uint32_t*>(p.kv + t0 * token_elems + g * D) + lane;  // word lane of each key row
+  float sum0 = 0.0f;
+  float sum1 = 0.0f;
+  constexpr int kKeys = 8;
+  for (int rk0 = 0; rk0 < p.topk; rk0 += kKeys) {
+    uint32_t w[kKeys];
+#pragma unroll
+    for (int i = 0; i < kKeys; ++i) {
+      const int rk = rk0 + i < p.topk ? rk0 + i : p.topk - 1;
+      w[i] = kblock[order[rk] * (token_elems / 2)];
+    }
+#pragma unroll
+    for (int i = 0; i < kKeys; ++i) {
+      if (rk0 + i < p.topk) {
+        sum0 = sum0 + lo_h2f(w[i]);
+        sum1 = sum1 + hi_h2f(w[i]);
+      }
+    }
+  }
+  const float k = static_cast<float>(p.topk);
+  const float v0 = sum0 / k;
+  const float v1 = sum1 / k;
+  const int d = 2 * lane;
+  if (p.values) {
+    float* out = p.values + (static_cast<int64_t>(h) * blocks + b) * D + d;
+    out[0] = v0;
+    out[1] = v1;
+  }
+  if (p.reps) {
+    p.reps[(static_cast<int64_t>(h) * D + d) * p.rep_stride + b] = v0;
+    p.reps[(static_cast<int64_t>(h) * D + d + 1) * p.rep_stride + b] = v1;
   }
 }
 
-// Windows up to 128 keys stage their key rows in LDS (at most 135 padded
-// rows, 37 KB); longer ones read them from memory.
 template <int WL>
 void launch_window(const Params& p, hipStream_t stream) {
   constexpr int kQueriesPerGroup = window_threads<WL>() / WL;
@@ -278,7 +399,7 @@ hipError_t launch_local_causal_representatives(const RepresentativeLaunch& r, hi
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 grid(static_cast<unsigned>(r.tokens / kPageTokens), r.query_heads);
-  hipLaunchKernelGGL(block_topk_kernel, grid, dim3(kWave), 0, stream, p);
+  hipLaunchKernelGGL(block_topk_kernel, grid, dim3(kWave), block_topk_lds_bytes(r.window), stream, p);
   return hipGetLastError();
 }
 

@@ -133,12 +133,13 @@ def test_local_causal_argument_checks():
     fake = C.c_void_p(4096)
     assert L.sa_hip_local_causal_workspace_bytes(64, 4, 32) == 64 * 4 * 33 * 4
 
-    def call(tokens=64, hq=4, hkv=2, d=128, block=32, window=32, topk=4, values=fake, wsb=1 << 30):
-        return L.sa_hip_local_causal_representatives(fake, fake, tokens, hq, hkv, d, block, window, topk, values,
+    def call(tokens=64, hq=4, hkv=2, d=128, block=32, window=32, topk=4, values=fake, wsb=1 << 30, pq=fake, kv=fake):
+        return L.sa_hip_local_causal_representatives(pq, kv, tokens, hq, hkv, d, block, window, topk, values,
                                                      None, None, 0, None, fake, wsb, None)
 
     bad = [dict(tokens=65), dict(window=0), dict(window=257), dict(topk=0), dict(topk=33), dict(hq=3),
-           dict(d=64), dict(block=16), dict(values=None), dict(wsb=16)]
+           dict(d=64), dict(block=16), dict(values=None), dict(wsb=16), dict(pq=C.c_void_p(4100)),
+           dict(kv=C.c_void_p(4104)), dict(hq=65536 * 2, hkv=65536 * 2, tokens=32)]
     for kw in bad:
         assert call(**kw) == -1, kw
         assert L.sa_hip_last_error()
