@@ -205,7 +205,9 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
   // denominator summed in window order, w = 0 .. count-1: the query's lanes
   // put their exponentials in LDS (the query's lanes are in one wave, whose
   // LDS operations execute in order) and every lane reads them back four at
-  // a time
+  // a time.  The slots past count hold +0, and adding +0 leaves the running
+  // sum (which starts at +0) unchanged, so every lane adds all 4 WL slots
+  // with no per-slot test.
 #pragma unroll
   for (int j = 0; j < kMaxKeysPerLane; ++j) e_s[qi][wl + j * WL] = e[j];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -213,34 +215,47 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float denominator = 0.0f;
   const float4* e4 = reinterpret_cast<const float4*>(e_s[qi]);
-  for (int w = 0; w < count; w += 4) {
-    const float4 v = e4[w / 4];
+#pragma unroll 8
+  for (int w4 = 0; w4 < kMaxKeysPerLane * WL / 4; ++w4) {
+    const float4 v = e4[w4];
     denominator = denominator + v.x;
-    if (w + 1 < count) denominator = denominator + v.y;
-    if (w + 2 < count) denominator = denominator + v.z;
-    if (w + 3 < count) denominator = denominator + v.w;
+    denominator = denominator + v.y;
+    denominator = denominator + v.z;
+    denominator = denominator + v.w;
   }
 
   float* row = p.prob + (static_cast<int64_t>(h) * p.tokens + q) * p.window;
 #pragma unroll
   for (int j = 0; j < kMaxKeysPerLane; ++j) {
     const int w = wl + j * WL;
-    if (w < count) row[w] = e[j] / denominator;
+    const float pr = e[j] / denominator;
+    if (w < count) row[w] = pr;
   }
 }
 
-// Probability rows staged per token column: 32 columns plus one of padding,
-// so that lane j reading (row j + i, column j) hits bank 34 j mod 64.
+// block_topk_kernel stages, per block, the probabilities of the queries whose
+// windows reach it (32 + W - 1 rows) in LDS, in one of two layouts:
+//   * per token column (any W): row r holds the 32 probabilities query
+//     t0 + r gives the block's tokens, plus one column of padding, so that
+//     lane j reading (row j + i, column j) hits bank 34 j mod 64;
+//   * whole rows (W a power of two, 4..64, 16-byte aligned probabilities):
+//     the block's query rows are one contiguous span of the workspace, copied
+//     in 16-byte pieces into rows of W + 4 floats.
 constexpr int kStageCols = kPageTokens + 1;
+constexpr int kMaxWholeRowWindow = 64;
 static_assert(D == 2 * kWave, "block_topk_kernel: a lane per pair of dimensions");
 
-// Dynamic LDS of block_topk_kernel: the probabilities of the queries whose
-// windows reach a block (32 + W - 1 rows), one column per token of the block.
-size_t block_topk_lds_bytes(int window) {
-  return static_cast<size_t>(kPageTokens + window - 1) * kStageCols * sizeof(float);
+bool block_topk_whole_rows(int window, const float* prob) {
+  return window >= 4 && window <= kMaxWholeRowWindow && (window & (window - 1)) == 0 &&
+         reinterpret_cast<uintptr_t>(prob) % 16 == 0;
+}
+
+size_t block_topk_lds_bytes(int window, bool whole_rows) {
+  return static_cast<size_t>(kPageTokens + window - 1) * (whole_rows ? window + 4 : kStageCols) * sizeof(float);
 }
 
 // One wave per (block, head): received mass, stable rank, top-k, representative.
+template <bool WHOLE_ROWS>
 __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   const int b = blockIdx.x;
   const int h = blockIdx.y;
@@ -248,38 +263,57 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   const int g = h / (p.hq / p.hkv);
   const int64_t blocks = p.tokens / kPageTokens;
   const int64_t t0 = static_cast<int64_t>(b) * kPageTokens;
+  const int W = p.window;
   __shared__ int order[kPageTokens];
-  extern __shared__ float stage_s[];  // [rows][kStageCols]
+  extern __shared__ float stage_s[];
 
-  // stage (row r, column j) = the probability query q = t0 + r gives token
-  // t0 + j, for the queries t0 .. t0 + 31 + W - 1: each row's 32 columns are
-  // contiguous in the query's window row, so a load instruction covers two
-  // rows; entries outside a query's window are loaded from a clamped column
-  // and never read
-  const int64_t q_last = t0 + kPageTokens - 1 + p.window - 1 < p.tokens - 1 ? t0 + kPageTokens - 1 + p.window - 1
-                                                                             : p.tokens - 1;
-  const int pieces = static_cast<int>(q_last - t0 + 1) * kPageTokens;
-  const float* prob_b = p.prob + (static_cast<int64_t>(h) * p.tokens + t0) * p.window;  // row of query t0
-  // the window of query t0 + r starts at t0 + r + 1 - W (at 0 for the first
-  // W - 1 queries): token t0 + j sits in column j - r + W - 1 (t0 + j)
-  const int first_full = static_cast<int>(t0 + 1 >= p.window ? 0 : p.window - 1 - t0);  // first row whose start > 0
-  constexpr int kBatch = 16;
-  for (int e0 = lane; e0 < pieces; e0 += kBatch * kWave) {
-    float v[kBatch];
+  // the queries t0 .. q_last, whose rows start at prob_b; the window of query
+  // t0 + r starts at t0 + r + 1 - W (at 0 for the first W - 1 queries)
+  const int64_t q_last = t0 + kPageTokens - 1 + W - 1 < p.tokens - 1 ? t0 + kPageTokens - 1 + W - 1 : p.tokens - 1;
+  const int rows = static_cast<int>(q_last - t0 + 1);
+  const float* prob_b = p.prob + (static_cast<int64_t>(h) * p.tokens + t0) * W;
+  if (WHOLE_ROWS) {
+    // rows x W floats from prob_b, W / 4 pieces per row (a power of two)
+    const int pieces = rows * (W / 4);
+    const int shift = __builtin_ctz(W / 4);
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(prob_b);
+    constexpr int kBatch = 8;
+    for (int e0 = lane; e0 < pieces; e0 += kBatch * kWave) {
+      u32x4_t v[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;
-      const int r = e / kPageTokens;
-      const int j = e % kPageTokens;
-      int col = r >= first_full ? j - r + p.window - 1 : static_cast<int>(t0) + j;
-      col = col < 0 ? 0 : (col >= p.window ? p.window - 1 : col);
-      v[i] = prob_b[r * p.window + col];
+      for (int i = 0; i < kBatch; ++i) v[i] = src[e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1];
+      __builtin_amdgcn_sched_barrier(0);  // every load of the batch ahead of the stores
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;  // a clamped piece rewrites its value
+        *reinterpret_cast<u32x4_t*>(stage_s + (e >> shift) * (W + 4) + (e & (W / 4 - 1)) * 4) = v[i];
+      }
     }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the batch ahead of the stores
+  } else {
+    // (row r, column j) = the probability query t0 + r gives token t0 + j:
+    // each row's 32 columns are contiguous in the query's window row, so a
+    // load instruction covers two rows; entries outside a query's window are
+    // loaded from a clamped column and never read
+    const int pieces = rows * kPageTokens;
+    const int first_full = static_cast<int>(t0 + 1 >= W ? 0 : W - 1 - t0);  // first row whose start > 0
+    constexpr int kBatch = 16;
+    for (int e0 = lane; e0 < pieces; e0 += kBatch * kWave) {
+      float v[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;  // a clamped piece rewrites its value
-      stage_s[(e / kPageTokens) * kStageCols + e % kPageTokens] = v[i];
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;
+        const int r = e / kPageTokens;
+        const int j = e % kPageTokens;
+        int col = r >= first_full ? j - r + W - 1 : static_cast<int>(t0) + j;
+        col = col < 0 ? 0 : (col >= W ? W - 1 : col);
+        v[i] = prob_b[r * W + col];
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every load of the batch ahead of the stores
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;  // a clamped piece rewrites its value
+        stage_s[(e / kPageTokens) * kStageCols + e % kPageTokens] = v[i];
+      }
     }
   }
   __syncthreads();
@@ -289,13 +323,20 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   float r = 0.0f;
   if (lane < kPageTokens) {
     const int64_t t = t0 + lane;
-    const int n = static_cast<int>((t + p.window - 1 < p.tokens - 1 ? t + p.window - 1 : p.tokens - 1) - t + 1);
-    const float* col = stage_s + lane * kStageCols + lane;
+    const int n = static_cast<int>((t + W - 1 < p.tokens - 1 ? t + W - 1 : p.tokens - 1) - t + 1);
+    // stage index of query t + i's probability of token t
+    auto at = [&](int i) {
+      if (WHOLE_ROWS) {
+        const int64_t start = t + i + 1 > W ? t + i + 1 - W : 0;
+        return (lane + i) * (W + 4) + static_cast<int>(t - start);
+      }
+      return (lane + i) * kStageCols + lane;
+    };
     constexpr int kReads = 8;  // LDS reads issued together, then added in order
     for (int i0 = 0; i0 < n; i0 += kReads) {
       float c[kReads];
 #pragma unroll
-      for (int i = 0; i < kReads; ++i) c[i] = col[(i0 + i < n ? i0 + i : n - 1) * kStageCols];
+      for (int i = 0; i < kReads; ++i) c[i] = stage_s[at(i0 + i < n ? i0 + i : n - 1)];
 #pragma unroll
       for (int i = 0; i < kReads; ++i)
         if (i0 + i < n) r = r + c[i];
@@ -399,7 +440,11 @@ hipError_t launch_local_causal_representatives(const RepresentativeLaunch& r, hi
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 grid(static_cast<unsigned>(r.tokens / kPageTokens), r.query_heads);
-  hipLaunchKernelGGL(block_topk_kernel, grid, dim3(kWave), block_topk_lds_bytes(r.window), stream, p);
+  if (block_topk_whole_rows(r.window, p.prob)) {
+    hipLaunchKernelGGL(block_topk_kernel<true>, grid, dim3(kWave), block_topk_lds_bytes(r.window, true), stream, p);
+  } else {
+    hipLaunchKernelGGL(block_topk_kernel<false>, grid, dim3(kWave), block_topk_lds_bytes(r.window, false), stream, p);
+  }
   return hipGetLastError();
 }
 
