@@ -64,6 +64,25 @@ struct Params {
   float scale;
 };
 
+// Workgroup -> (tile x, query head y) of a grid (nx tiles, hq heads).
+// Workgroups are dispatched in order x fastest and handed to the 8 XCDs
+// round robin; when their count is a multiple of 8, dispatch number i is
+// given the (i mod 8)-th eighth of the order (KV group, tile, query head in
+// the group), so that each XCD's L2 sees consecutive tiles, whose key rows
+// and probability rows overlap, and the query heads that share a KV head,
+// next to each other.
+__device__ inline void xcd_tile(int hq, int hkv, int& x, int& y) {
+  const int nx = static_cast<int>(gridDim.x);
+  const int group = hq / hkv;
+  const int id = static_cast<int>(blockIdx.x) + static_cast<int>(blockIdx.y) * nx;
+  const int total = nx * hq;
+  const int v = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
+  const int per_kv = nx * group;
+  const int rem = v % per_kv;
+  x = rem / group;
+  y = (v / per_kv) * group + rem % group;
+}
+
 // Lanes per query: WL (a power of two, 1..64); queries per wave 64 / WL.
 // STAGE: the keys of the workgroup's windows are staged in LDS (rows padded
 // by 16 bytes so the lanes of a query, reading consecutive rows, hit
@@ -75,12 +94,13 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
   constexpr int kQueriesPerGroup = kWindowThreads / WL;
   constexpr int kRowVecs = D / 8;                              // 16 uint4 per key row
   constexpr int kMaxRows = STAGE ? kQueriesPerGroup + kMaxKeysPerLane * WL - 1 : 1;
-  const int h = blockIdx.y;
+  int tile, h;
+  xcd_tile(p.hq, p.hkv, tile, h);
   const int tid = threadIdx.x;
   const int qi = tid / WL;          // query within the workgroup
   const int wl = tid % WL;          // window lane within the query
   const int g = h / (p.hq / p.hkv);
-  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kQueriesPerGroup;
+  const int64_t q0 = static_cast<int64_t>(tile) * kQueriesPerGroup;
   const int64_t q = q0 + qi;
   const int64_t token_elems = 2LL * p.hkv * D;
 
@@ -240,7 +260,9 @@ __global__ __launch_bounds__(window_threads<WL>()) void window_softmax_kernel(co
 //     lane j reading (row j + i, column j) hits bank 34 j mod 64;
 //   * whole rows (W a power of two, 4..64, 16-byte aligned probabilities):
 //     the block's query rows are one contiguous span of the workspace, copied
-//     in 16-byte pieces into rows of W + 4 floats.
+//     in 16-byte pieces (stored as two 8-byte halves) into rows of W + 2
+//     floats, so that lane j reading (row j + i, column W - 1 - i) hits bank
+//     pair (W + 2) j mod 64, distinct for the 32 lanes.
 constexpr int kStageCols = kPageTokens + 1;
 constexpr int kMaxWholeRowWindow = 64;
 static_assert(D == 2 * kWave, "block_topk_kernel: a lane per pair of dimensions");
@@ -251,14 +273,14 @@ bool block_topk_whole_rows(int window, const float* prob) {
 }
 
 size_t block_topk_lds_bytes(int window, bool whole_rows) {
-  return static_cast<size_t>(kPageTokens + window - 1) * (whole_rows ? window + 4 : kStageCols) * sizeof(float);
+  return static_cast<size_t>(kPageTokens + window - 1) * (whole_rows ? window + 2 : kStageCols) * sizeof(float);
 }
 
 // One wave per (block, head): received mass, stable rank, top-k, representative.
 template <bool WHOLE_ROWS>
 __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
-  const int b = blockIdx.x;
-  const int h = blockIdx.y;
+  int b, h;
+  xcd_tile(p.hq, p.hkv, b, h);
   const int lane = threadIdx.x;
   const int g = h / (p.hq / p.hkv);
   const int64_t blocks = p.tokens / kPageTokens;
@@ -286,7 +308,10 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;  // a clamped piece rewrites its value
-        *reinterpret_cast<u32x4_t*>(stage_s + (e >> shift) * (W + 4) + (e & (W / 4 - 1)) * 4) = v[i];
+        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+        u32x2_t* dst = reinterpret_cast<u32x2_t*>(stage_s + (e >> shift) * (W + 2) + (e & (W / 4 - 1)) * 4);
+        dst[0] = u32x2_t{v[i].x, v[i].y};
+        dst[1] = u32x2_t{v[i].z, v[i].w};
       }
     }
   } else {
@@ -328,7 +353,7 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
     auto at = [&](int i) {
       if (WHOLE_ROWS) {
         const int64_t start = t + i + 1 > W ? t + i + 1 - W : 0;
-        return (lane + i) * (W + 4) + static_cast<int>(t - start);
+        return (lane + i) * (W + 2) + static_cast<int>(t - start);
       }
       return (lane + i) * kStageCols + lane;
     };
