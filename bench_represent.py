@@ -11,8 +11,9 @@ the selection reads.
 Reported: µs per layer and prompt tokens per second; achieved GB/s and
 GFLOP/s of the call (algorithmic bytes: queries, keys, the probabilities
 written and read back once, the outputs; flops: one multiply and one add per
-(query, key, dim) of every window); the oracle's single-thread time on a
-512-token sample (the reference publishes 51.5 ms for 512 tokens on an
+(query, key, dim) of every window); the reference builder's single-thread
+time on a 512-token sample (oracle/_ref, built from the reference's sources;
+the oracle's restatement where that is absent; the reference publishes 51.5 ms for 512 tokens on an
 i9-14900HX, docs/cpp-versions/C2.1-infllm-selection-uring.md:58); and a
 parity check of the last layer against the oracle's builder with the same
 exponential (bit-exact) and of a 512-token prefix against the reference's
@@ -128,9 +129,14 @@ def check(sa, np, torch, pq, kv, reps, offs, HQ, HKV, T, W, K, blocks, rep_strid
 
 
 def cpu_baseline(np, HQ, HKV, W, K):
-    """The oracle's restatement of the reference builder (glibc expf), one
-    thread, on a 512-token prompt (the reference's C2.1 size)."""
+    """The reference's build_local_causal_representatives (selection.cpp:12-94)
+    on the host, one thread, on a 512-token prompt (the reference's C2.1
+    size), scaled linearly to 16384 tokens.  kind "reference": the
+    reference's own function compiled from its sources (oracle/_ref); kind
+    "port": the oracle's C restatement (libm expf) where oracle/_ref is
+    absent."""
     import oracle as O
+    use_ref = O.ref_available()
     rng = np.random.default_rng(5)
     T = 512
     pq = rng.standard_normal(HQ * T * D).astype(np.float32)
@@ -138,13 +144,16 @@ def cpu_baseline(np, HQ, HKV, W, K):
     t0 = time.perf_counter()
     loops = 0
     while True:
-        O.local_causal_representatives(pq, kv, T, HQ, HKV, D, 32, W, K)
+        O.local_causal_representatives(pq, kv, T, HQ, HKV, D, 32, W, K, use_ref=use_ref)
         loops += 1
         el = time.perf_counter() - t0
         if el > 10.0 or loops >= 200:
             break
     per_512 = el / loops
-    return {"value": round(per_512 * 1e6 * (16384 / 512), 1), "unit": "us/layer", "cores": 1, "kind": "port",
-            "sample": f"512-token prompt x {loops} repeats (oracle C restatement, glibc expf, 1 thread), "
+    what = ("the reference's builder, oracle/_ref built from its sources" if use_ref
+            else "the oracle's C restatement, libm expf")
+    return {"value": round(per_512 * 1e6 * (16384 / 512), 1), "unit": "us/layer", "cores": 1,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"512-token prompt x {loops} repeats ({what}, 1 thread), "
                       f"{per_512 * 1e3:.2f} ms each, scaled linearly to 16384 tokens",
             "nproc": os.cpu_count()}
