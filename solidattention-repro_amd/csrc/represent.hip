@@ -33,6 +33,7 @@ namespace {
 
 constexpr int D = kHeadDim;
 constexpr int kMaxKeysPerLane = 4;  // window <= 4 x 64
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 // Workgroup of the window kernel: 256 threads, at most 64 queries (33 KB of
 // staged queries).
@@ -308,7 +309,6 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;  // a clamped piece rewrites its value
-        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
         u32x2_t* dst = reinterpret_cast<u32x2_t*>(stage_s + (e >> shift) * (W + 2) + (e & (W / 4 - 1)) * 4);
         dst[0] = u32x2_t{v[i].x, v[i].y};
         dst[1] = u32x2_t{v[i].z, v[i].w};
