@@ -77,6 +77,32 @@ def test_gpu_builder_vs_oracle(hip, window, topk, hq, hkv, tokens):
     check_vs_oracle(hip, pq, kv, tokens, hq, hkv, window, topk)
 
 
+@pytest.mark.parametrize("window", [32, 64])
+def test_gpu_builder_unaligned_workspace(hip, window):
+    """A workspace 4 bytes off a 16-byte boundary: the block kernel stages
+    the probabilities per token column instead of as whole rows (its 16-byte
+    copies need an aligned workspace); results bit-exact as with an aligned
+    one."""
+    rng = np.random.default_rng(700 + window)
+    tokens, hq, hkv, topk = 320, 8, 4, 4
+    pq = rng.standard_normal(hq * tokens * 128).astype(np.float32)
+    kv = rng.standard_normal(tokens * 2 * hkv * 128).astype(np.float16).view(np.uint16)
+    nbytes = hip.lib().sa_hip_local_causal_workspace_bytes(tokens, hq, window)
+    base = torch.empty(nbytes // 4 + 4, dtype=torch.float32, device="cuda")
+    ws = base[1:1 + nbytes // 4]
+    assert ws.data_ptr() % 16 == 4
+    dq = torch.from_numpy(pq).cuda()
+    dkv = torch.from_numpy(kv.view(np.int16)).cuda().view(torch.uint16)
+    received = torch.empty((hq, tokens), dtype=torch.float32, device="cuda")
+    vals, offs = hip.local_causal_representatives(dq, dkv, tokens, hq, hkv, window, topk, received=received,
+                                                  workspace=ws)
+    torch.cuda.synchronize()
+    evals, eoffs, erec = O.local_causal_representatives_restated(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
+    assert np.array_equal(received.cpu().numpy().view(np.uint32), erec.view(np.uint32))
+    assert np.array_equal(offs.cpu().numpy().astype(np.int64), eoffs.astype(np.int64))
+    assert np.array_equal(vals.cpu().numpy().view(np.uint32), evals.view(np.uint32))
+
+
 def test_gpu_builder_outliers_and_ties(hip):
     """+-60000 keys (saturated softmax rows) and repeated tokens (equal mass:
     the stable rank keeps token order)."""
