@@ -228,55 +228,102 @@ struct QkvReduceParams {
   int32_t q_heads;
   int32_t kv_heads;
   float eps;
-  float inv_freq[64];
+  alignas(16) float inv_freq[64];  // 16-byte aligned: a lane reads its 4 frequencies in one load
 };
 
 // Workgroup (head, 8-row block): the slices of the head's 128 columns added
 // in slice order, times the row's input RMSNorm scale; q and k heads then
 // take the head RMS norm and RoPE (NeoX pairs d, d + 64).  Thread t: row
 // t / 32, d = 4 (t % 32) .. + 3; d and d + 64 sit 16 threads apart.
+// The K-slice partials at offset off of each slice (slice_stride floats
+// apart), added in slice order from zero; each batch of 8 slices' loads is
+// issued before its adds.
+__device__ inline f32x4_t sum_slices4(const float* part, int slices, int64_t slice_stride, int64_t off) {
+  constexpr int kBatch = 8;
+  f32x4_t v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int z0 = 0; z0 < slices; z0 += kBatch) {
+    f32x4_t s[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int z = z0 + i < slices ? z0 + i : slices - 1;
+      s[i] = *reinterpret_cast<const f32x4_t*>(part + z * slice_stride + off);
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (z0 + i < slices) v += s[i];
+  }
+  return v;
+}
+
+// sum_slices4 together with the same slices' scalars (sum of squares) at
+// soff of each sslice_stride-float slice, both batches in flight at once.
+__device__ inline f32x4_t sum_slices4_ss(const float* part, int slices, int64_t slice_stride, int64_t off,
+                                         const float* ss, int64_t ss_stride, int64_t soff, float& tot) {
+  constexpr int kBatch = 8;
+  f32x4_t v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  tot = 0.0f;
+  for (int z0 = 0; z0 < slices; z0 += kBatch) {
+    f32x4_t s[kBatch];
+    float q[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int z = z0 + i < slices ? z0 + i : slices - 1;
+      s[i] = *reinterpret_cast<const f32x4_t*>(part + z * slice_stride + off);
+      q[i] = ss[z * ss_stride + soff];
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (z0 + i < slices) {
+        v += s[i];
+        tot += q[i];
+      }
+    }
+  }
+  return v;
+}
+
 __device__ inline void qkv_reduce_rows(const QkvReduceParams& p, int hh, int rb) {
   const int tid = threadIdx.x;
   const int j = tid % 32;
   const int row = rb * 8 + tid / 32;
   const int rr = row < p.rows ? row : p.rows - 1;  // rows past the batch compute row rows-1, not stored
   const int64_t col = static_cast<int64_t>(hh) * kHeadDim + 4 * j;
-  f32x4_t v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int z = 0; z < p.slices; ++z)
-    v += *reinterpret_cast<const f32x4_t*>(p.part + (static_cast<int64_t>(z) * p.rows_pad + rr) * p.out + col);
-  if (p.ss) {
-    float tot = 0.0f;
-    for (int z = 0; z < p.slices; ++z) tot += p.ss[static_cast<int64_t>(z) * p.rows_pad + rr];
-    v *= 1.0f / __builtin_sqrtf(tot / static_cast<float>(p.in) + p.in_eps);
-  }
-  if (hh >= p.q_heads + p.kv_heads) {
-    if (row < p.rows)
-      *reinterpret_cast<f32x4_t*>(p.v + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads - p.kv_heads)) *
-                                            kHeadDim + 4 * j) = v;
-    return;
-  }
+  const bool is_v = hh >= p.q_heads + p.kv_heads;
   const bool is_q = hh < p.q_heads;
+  // every load of the row issued up front: the position, the head norm
+  // weights, the RoPE frequencies of d and d + 64 (the same 4), the slices
+  const float pos = static_cast<float>(p.positions[rr]);
+  const f32x4_t n4 = *reinterpret_cast<const f32x4_t*>((is_q ? p.q_norm : p.k_norm) + 4 * j);
+  const f32x4_t fr = *reinterpret_cast<const f32x4_t*>(p.inv_freq + 4 * (j % 16));
+  // (without an input RMSNorm the sums of squares are read from the
+  // partials instead, unconditionally, and not used)
+  float tot;
+  f32x4_t v = sum_slices4_ss(p.part, p.slices, static_cast<int64_t>(p.rows_pad) * p.out,
+                             static_cast<int64_t>(rr) * p.out + col, p.ss ? p.ss : p.part, p.rows_pad, rr, tot);
+  if (p.ss) v *= 1.0f / __builtin_sqrtf(tot / static_cast<float>(p.in) + p.in_eps);
+  // q and k heads: head RMS norm, then RoPE (v heads take v as it is; the
+  // head is uniform over the workgroup, so the selects below cost nothing
+  // but keep the loads above ahead of the slice sums)
   float sq = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
 #pragma unroll
   for (int off = 16; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
   const float inv = 1.0f / __builtin_sqrtf(sq / static_cast<float>(kHeadDim) + p.eps);
-  const f32x4_t n4 = *reinterpret_cast<const f32x4_t*>((is_q ? p.q_norm : p.k_norm) + 4 * j);
   f32x4_t x, y, o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) x[e] = v[e] * inv * n4[e];
 #pragma unroll
   for (int e = 0; e < 4; ++e) y[e] = __shfl_xor(x[e], 16, kWave);  // the pair partner, d +- 64
-  const float pos = static_cast<float>(p.positions[rr]);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     float sn, cs;
-    sincosf(pos * p.inv_freq[(4 * j + e) % 64], &sn, &cs);
+    sincosf(pos * fr[e], &sn, &cs);
     o[e] = j < 16 ? x[e] * cs - y[e] * sn : x[e] * cs + y[e] * sn;
   }
   if (row < p.rows) {
-    float* dst = is_q ? p.q + (static_cast<int64_t>(row) * p.q_heads + hh) * kHeadDim
-                      : p.k + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads)) * kHeadDim;
-    *reinterpret_cast<f32x4_t*>(dst + 4 * j) = o;
+    float* dst = is_v ? p.v + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads - p.kv_heads)) * kHeadDim
+                 : is_q ? p.q + (static_cast<int64_t>(row) * p.q_heads + hh) * kHeadDim
+                        : p.k + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads)) * kHeadDim;
+    *reinterpret_cast<f32x4_t*>(dst + 4 * j) = is_v ? v : o;
   }
 }
 
@@ -291,11 +338,10 @@ __global__ __launch_bounds__(kWave) void linear_reduce_kernel(const float* part,
   const int c = (blockIdx.x * kWave + threadIdx.x) * 4;
   if (c >= out) return;
   for (int row = blockIdx.y; row < rows; row += gridDim.y) {
-    f32x4_t v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int z = 0; z < slices; ++z)
-      v += *reinterpret_cast<const f32x4_t*>(part + (static_cast<int64_t>(z) * rows_pad + row) * out + c);
     const int64_t o = static_cast<int64_t>(row) * out + c;
-    if (residual) v += *reinterpret_cast<const f32x4_t*>(residual + o);
+    const f32x4_t r = residual ? *reinterpret_cast<const f32x4_t*>(residual + o) : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4_t v = sum_slices4(part, slices, static_cast<int64_t>(rows_pad) * out, o);
+    if (residual) v += r;
     *reinterpret_cast<f32x4_t*>(y + o) = v;
   }
 }
