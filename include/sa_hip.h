@@ -545,7 +545,8 @@ int sa_hip_linear(const float* x, const float* w, const float* residual, float* 
  * rotation at positions[rows] (device int32), frequencies theta^(-2i/128)
  * correctly rounded to fp32 and the reference's NeoX pairing (d, d + 64).
  * Outputs [rows][heads][128] fp32, ready for sa_hip_decode_step (q) and its
- * k/v.  hidden % 256 == 0; workspace of sa_hip_qkv_workspace_bytes bytes
+ * k/v.  hidden % 256 == 0; x, the weights, the norms, q/k/v and the
+ * workspace 16-byte aligned; workspace of sa_hip_qkv_workspace_bytes bytes
  * (the K-slice partial tiles; no initialisation needed). */
 size_t sa_hip_qkv_workspace_bytes(int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads);
 int sa_hip_qkv_project(const float* x, const float* wq, const float* wk, const float* wv, const float* q_norm,

@@ -938,8 +938,10 @@ static int qkv_common(const float* x, const float* gain, float in_eps, const flo
   if (!x || !wq || !wk || !wv || !q_norm || !k_norm || !positions || !q || !k || !v || !workspace)
     return fail(SA_HIP_EINVAL, "%s: null argument", op);
   if (!aligned16(x) || !aligned16(wq) || !aligned16(wk) || !aligned16(wv) || (gain && !aligned16(gain)) ||
-      !aligned16(v) || !aligned16(workspace))
-    return fail(SA_HIP_EINVAL, "%s: x, the weights, v and the workspace must be 16-byte aligned", op);
+      !aligned16(q_norm) || !aligned16(k_norm) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+      !aligned16(workspace))
+    return fail(SA_HIP_EINVAL, "%s: x, the weights, the norms, q/k/v and the workspace must be 16-byte aligned",
+                op);
   if (!(theta > 1.0f)) return fail(SA_HIP_EINVAL, "%s: rope theta must exceed 1", op);
   if (workspace_bytes < sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads))
     return fail(SA_HIP_EINVAL, "%s: workspace of %zu bytes < %zu", op, workspace_bytes,

@@ -201,6 +201,11 @@ def test_producer_argument_checks():
     assert L.sa_hip_qkv_project(*args, C.c_float(1.0), C.c_float(1e-6), f, f, f, f, qn, None) == -1
     assert b"theta" in L.sa_hip_last_error()
     assert L.sa_hip_qkv_project(*args, C.c_float(1e6), C.c_float(1e-6), f, f, f, f, qn - 4, None) == -1
+    # q and k are written with 16-byte stores: an unaligned one is refused
+    odd = C.c_void_p(4100)
+    assert L.sa_hip_qkv_project(*args, C.c_float(1e6), C.c_float(1e-6), odd, f, f, f, qn, None) == -1
+    assert L.sa_hip_qkv_project(*args, C.c_float(1e6), C.c_float(1e-6), f, odd, f, f, qn, None) == -1
+    assert b"aligned" in L.sa_hip_last_error()
     assert L.sa_hip_rms_norm(f, f, f, 4, 1022, C.c_float(1e-6), None) == -1
 
 
