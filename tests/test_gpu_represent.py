@@ -68,7 +68,10 @@ def test_gpu_builder_vs_reference_golden(hip, name):
 
 @pytest.mark.parametrize("window,topk,hq,hkv,tokens", [
     (1, 1, 4, 4, 64), (2, 3, 8, 4, 96), (5, 4, 8, 2, 160), (32, 4, 16, 8, 512), (64, 8, 8, 8, 256),
-    (100, 16, 4, 1, 320), (256, 32, 8, 2, 544), (33, 32, 2, 2, 64)])
+    (100, 16, 4, 1, 320), (256, 32, 8, 2, 544), (33, 32, 2, 2, 64),
+    # whole-row staging in the block kernel (windows 4..64, powers of two),
+    # including prompts shorter than a block's 32 + W - 1 query rows
+    (4, 2, 8, 4, 128), (8, 3, 4, 2, 96), (16, 5, 8, 8, 224), (64, 4, 4, 2, 64), (32, 32, 2, 1, 32)])
 def test_gpu_builder_vs_oracle(hip, window, topk, hq, hkv, tokens):
     print(f"case: window={window} topk={topk} hq={hq} hkv={hkv} tokens={tokens}", flush=True)
     rng = np.random.default_rng(window * 7 + tokens)
