@@ -80,6 +80,9 @@ def parse():
                          "(stress workload: chunked; decode workload: the library's preference)")
     ap.add_argument("--chunk", type=int, default=None,
                     help="stress workload: pages per attention chunk (0 = split schedule instead)")
+    ap.add_argument("--chunk-grid-order", action="store_true",
+                    help="stress workload: chunked attention in grid order (a workspace without room for the "
+                         "longest-first schedule)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
                     help="also run one plain page copy of PAGES pages (HBM counter calibration)")
     return ap.parse_args()

@@ -117,7 +117,9 @@ def run(args):
     else:
         max_chunks = 0
         splits = args.splits or sa.default_splits(B, HKV, int(blocks.mean()), HQ)
-    ws_bytes = sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, splits)
+    ws_bytes = max(sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, splits),
+                   sa.lib().sa_hip_attention_chunked_workspace_bytes(B, HQ, HKV, D, max_chunks)
+                   if chunk > 0 and not getattr(args, "chunk_grid_order", False) else 0)
     workspace = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
     # mixed lengths: the chunked selection (long lists spread over workgroups)

@@ -146,12 +146,22 @@ int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query,
  * beyond max_chunks * chunk_pages.  The partial records (max_chunks per
  * (sequence, KV head), workspace as sa_hip_attention_workspace_bytes(...,
  * max_chunks)) are merged with log-sum-exp.  Same result as
- * sa_hip_sparse_decode_attention within fp32 rounding. */
+ * sa_hip_sparse_decode_attention within fp32 rounding.  With a workspace of
+ * sa_hip_attention_chunked_workspace_bytes (batch x kv_heads <= 4096) the
+ * workgroups first run longest list first (below). */
 int sa_hip_sparse_decode_attention_chunked(
     const sa_paged_kv* kv, const float* query, const int32_t* selected,
     const int32_t* counts, int32_t select_groups, int32_t sel_stride,
     float scale, float* out, void* workspace, size_t workspace_bytes,
     int32_t chunk_pages, int32_t max_chunks, int32_t* status, void* stream);
+/* Workspace that also holds the chunk schedule: with at least this many
+ * bytes (and batch x kv_heads <= 4096), sa_hip_sparse_decode_attention_chunked
+ * first orders its workgroups by list length, longest first with each list's
+ * chunks consecutive (one extra single-workgroup launch), so that short lists
+ * fill the end of the launch; the results equal those of the grid order.  No
+ * reference counterpart: a scheduling aid for mixed-length batches. */
+size_t sa_hip_attention_chunked_workspace_bytes(int32_t batch, int32_t query_heads, int32_t kv_heads,
+                                                int32_t head_dim, int32_t max_chunks);
 
 /* Split-phase attention, for schedules that attend the blocks already
  * resident while missing blocks are still being copied in (the overlap the

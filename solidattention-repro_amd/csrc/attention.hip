@@ -60,6 +60,9 @@ struct Params {
   int32_t direct;        // write the normalised output instead of a partial record
   int32_t chunk_pages;   // > 0: workgroup z attends list positions [z*chunk, (z+1)*chunk)
   float qscale;          // softmax scale * log2(e)
+  // chunked, lists longest first: workgroup w (dispatch order) attends
+  // chunk sched[slots + w] of list sched[w] = b * kv_heads + g (-1: none)
+  const int32_t* sched;
 };
 
 // The page list of (sequence b, KV head g): selected sealed blocks, then the
@@ -92,9 +95,18 @@ template <int G>
 __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_attention_kernel(const Params p) {
   constexpr int kWavesPerGroup = waves_per_group<G>();
   constexpr int kThreads = kWavesPerGroup * kWave;
-  const int g = blockIdx.x;
-  const int b = blockIdx.y;
-  const int z = blockIdx.z;
+  int g = blockIdx.x;
+  int b = blockIdx.y;
+  int z = blockIdx.z;
+  if (p.sched) {
+    const int64_t w = blockIdx.x + static_cast<int64_t>(gridDim.x) * (blockIdx.y + static_cast<int64_t>(gridDim.y) *
+                                                                                     blockIdx.z);
+    const int32_t l = p.sched[w];
+    if (l < 0) return;
+    b = l / p.v.kv_heads;
+    g = l % p.v.kv_heads;
+    z = p.sched[static_cast<int64_t>(gridDim.x) * gridDim.y * gridDim.z + w];
+  }
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
 
@@ -223,8 +235,132 @@ __global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const Par
 }
 
 // mode 0: attention (+ merge when split); 1: partial records only; 2: merge only.
+// ---- chunked attention: lists longest first ---------------------------------
+// The chunks of a mixed-length batch run as independent workgroups; in grid
+// order (chunk index slowest) the last ones dispatched are the late chunks of
+// the longest lists, which leave most compute units idle at the end.  This
+// kernel orders the workgroups by list length, longest first, with a list's
+// chunks consecutive (a counting sort on the page total, one workgroup):
+// short lists fill the end.  Results do not depend on the order: each chunk
+// attends the same pages and the merge adds the chunks in chunk order.
+constexpr int kSchedMaxLists = 4096;
+constexpr int kSchedBins = 4096;
+constexpr int kSchedThreads = 1024;
+constexpr int kSchedPer = kSchedMaxLists / kSchedThreads;
+
+// Exclusive prefix sum over the workgroup's threads (in thread order).
+__device__ inline int sched_scan(int v, int* wave_sums) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int t = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += t;
+  }
+  if (lane == kWave - 1) wave_sums[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < kSchedThreads / kWave ? wave_sums[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int t = __shfl_up(w, off, kWave);
+      if (lane >= off) w += t;
+    }
+    if (lane < kSchedThreads / kWave) wave_sums[lane] = w;  // inclusive over waves
+  }
+  __syncthreads();
+  const int before = wave > 0 ? wave_sums[wave - 1] : 0;
+  __syncthreads();  // wave_sums reusable
+  return before + incl - v;
+}
+
+__global__ __launch_bounds__(kSchedThreads) void chunk_schedule_kernel(const Params p, int batch, int32_t* sched) {
+  const int n = batch * p.v.kv_heads;  // <= kSchedMaxLists
+  const int64_t slots = static_cast<int64_t>(n) * p.splits;
+  const int tid = threadIdx.x;
+  __shared__ int hist[kSchedBins];
+  __shared__ int sorted[kSchedMaxLists];
+  __shared__ int nch[kSchedMaxLists];
+  __shared__ int wave_sums[kSchedThreads / kWave];
+  for (int i = tid; i < kSchedBins; i += kSchedThreads) hist[i] = 0;
+  __syncthreads();
+  // each list's page total and chunk count (chunk 0 always runs: it writes
+  // the record the merge reads; the last chunk takes any remainder)
+  int bin[kSchedPer];
+#pragma unroll
+  for (int k = 0; k < kSchedPer; ++k) {
+    const int l = tid + k * kSchedThreads;
+    bin[k] = -1;
+    if (l < n) {
+      const PageList L = page_list(p, l / p.v.kv_heads, l % p.v.kv_heads);
+      const int64_t total = L.total;
+      nch[l] = total <= 0 ? 1 : static_cast<int>(min<int64_t>(p.splits, (total + p.chunk_pages - 1) / p.chunk_pages));
+      const int64_t key = total < 0 ? 0 : (total > kSchedBins - 1 ? kSchedBins - 1 : total);
+      bin[k] = kSchedBins - 1 - static_cast<int>(key);  // longest in bin 0
+      atomicAdd(&hist[bin[k]], 1);
+    }
+  }
+  __syncthreads();
+  // bins -> first sorted position (4 bins per thread)
+  constexpr int kBinsPer = kSchedBins / kSchedThreads;
+  int hs[kBinsPer];
+  int hsum = 0;
+#pragma unroll
+  for (int i = 0; i < kBinsPer; ++i) {
+    hs[i] = hist[tid * kBinsPer + i];
+    hsum += hs[i];
+  }
+  int off = sched_scan(hsum, wave_sums);
+#pragma unroll
+  for (int i = 0; i < kBinsPer; ++i) {
+    hist[tid * kBinsPer + i] = off;
+    off += hs[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kSchedPer; ++k) {
+    const int l = tid + k * kSchedThreads;
+    if (l < n) sorted[atomicAdd(&hist[bin[k]], 1)] = l;  // order within a bin does not matter
+  }
+  __syncthreads();
+  // first workgroup of each sorted list (kSchedPer consecutive lists per thread)
+  int c[kSchedPer];
+  int csum = 0;
+#pragma unroll
+  for (int k = 0; k < kSchedPer; ++k) {
+    const int i = tid * kSchedPer + k;
+    c[k] = i < n ? nch[sorted[i]] : 0;
+    csum += c[k];
+  }
+  int w = sched_scan(csum, wave_sums);
+#pragma unroll
+  for (int k = 0; k < kSchedPer; ++k) {
+    const int i = tid * kSchedPer + k;
+    if (i < n) {
+      const int l = sorted[i];
+      for (int zz = 0; zz < c[k]; ++zz) {
+        sched[w + zz] = l;
+        sched[slots + w + zz] = zz;
+      }
+    }
+    w += c[k];
+  }
+  // the workgroups past the last chunk have nothing to attend
+  __shared__ int s_used;
+  if (tid == kSchedThreads - 1) s_used = w;  // every list's chunks
+  __syncthreads();
+  for (int64_t e = s_used + tid; e < slots; e += kSchedThreads) sched[e] = -1;
+}
+
 template <int G>
 hipError_t launch_g(const Params& p, int batch, int mode, hipStream_t stream) {
+  if (p.sched) {
+    hipLaunchKernelGGL(chunk_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, stream, p, batch,
+                       const_cast<int32_t*>(p.sched));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   if (mode != 2) {
     const dim3 grid(p.v.kv_heads, batch, p.splits);
     hipLaunchKernelGGL(sparse_decode_attention_kernel<G>, grid, dim3(waves_per_group<G>() * kWave), 0, stream, p);
@@ -273,6 +409,11 @@ hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t strea
   }
   p.chunk_pages = a.chunk_pages;
   p.qscale = a.scale * kLog2e;
+  // chunked with room for the schedule: lists longest first
+  p.sched = a.mode == 0 && a.chunk_pages > 0 && a.sched &&
+                    static_cast<int64_t>(a.batch) * a.kv_heads <= kSchedMaxLists
+                ? a.sched
+                : nullptr;
   const int group = a.query_heads / a.kv_heads;
   switch (group) {
     case 1: return launch_g<1>(p, a.batch, a.mode, stream);

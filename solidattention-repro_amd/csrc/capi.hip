@@ -145,6 +145,13 @@ size_t sa_hip_attention_workspace_bytes(int32_t batch, int32_t query_heads, int3
   return static_cast<size_t>(batch) * kv_heads * splits * group * sa::part_stride(head_dim) * sizeof(float);
 }
 
+size_t sa_hip_attention_chunked_workspace_bytes(int32_t batch, int32_t query_heads, int32_t kv_heads,
+                                                int32_t head_dim, int32_t max_chunks) {
+  const size_t records = sa_hip_attention_workspace_bytes(batch, query_heads, kv_heads, head_dim, max_chunks);
+  if (!records) return 0;
+  return records + 2 * static_cast<size_t>(batch) * kv_heads * max_chunks * sizeof(int32_t);
+}
+
 int32_t sa_hip_attention_splits_for(int32_t batch, int32_t query_heads, int32_t kv_heads,
                                     int32_t pages_per_group_hint) {
   // Workgroups per (sequence, KV head) so that every CU holds as many as can
@@ -173,7 +180,8 @@ int32_t sa_hip_attention_default_splits(int32_t batch, int32_t kv_heads, int32_t
 static int attention_common(const sa_paged_kv* kv, const float* query, const int32_t* selected,
                             const int32_t* counts, int32_t select_groups, int32_t sel_stride, float scale,
                             float* out, void* workspace, size_t workspace_bytes, int32_t splits,
-                            int32_t* status, void* stream, int64_t contig_tokens, int32_t chunk_pages = 0) {
+                            int32_t* status, void* stream, int64_t contig_tokens, int32_t chunk_pages = 0,
+                            int32_t* sched = nullptr) {
   sa::AttnLaunch a{};
   a.pool = kv->pool;
   a.table = kv->block_table;
@@ -196,6 +204,7 @@ static int attention_common(const sa_paged_kv* kv, const float* query, const int
   a.splits = splits;
   a.scale = scale;
   a.chunk_pages = chunk_pages;
+  a.sched = sched;
   const size_t need =
       sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
   if (workspace_bytes < need || (need && !workspace))
@@ -234,8 +243,16 @@ int sa_hip_sparse_decode_attention_chunked(const sa_paged_kv* kv, const float* q
   if (chunk_pages < 1) return fail(SA_HIP_EINVAL, "attention_chunked: chunk_pages must be positive");
   if (max_chunks < 2 || max_chunks > 65535)
     return fail(SA_HIP_EINVAL, "attention_chunked: max_chunks must lie in [2, 65535]");
+  // with room for it after the records, the chunks run longest list first
+  const size_t records =
+      sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, max_chunks);
+  int32_t* sched = nullptr;
+  if (workspace && workspace_bytes >= sa_hip_attention_chunked_workspace_bytes(kv->batch, kv->query_heads,
+                                                                                 kv->kv_heads, kv->head_dim,
+                                                                                 max_chunks))
+    sched = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + records);
   return attention_common(kv, query, selected, counts, select_groups, sel_stride, scale, out, workspace,
-                          workspace_bytes, max_chunks, status, stream, 0, chunk_pages);
+                          workspace_bytes, max_chunks, status, stream, 0, chunk_pages, sched);
 }
 
 int sa_hip_sparse_decode_attention_partial(const sa_paged_kv* kv, const float* query, const int32_t* selected,

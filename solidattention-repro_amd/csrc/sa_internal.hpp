@@ -49,6 +49,7 @@ struct AttnLaunch {
   int32_t part_total;
   int32_t include_tail;
   int32_t chunk_pages;     // > 0 (mode 0): split by chunks of pages, `splits` chunks
+  int32_t* sched;          // chunked: 2 x batch x kv_heads x splits int32 for the longest-first order, or null
 };
 
 hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t stream);

@@ -91,6 +91,7 @@ EXPORTS = {
     "sa_hip_score_select_split_preferred": (C.c_int, [_KV, C.POINTER(SelectParamsStruct)]),
     "sa_hip_score_select_chunked_workspace_bytes": (_SZ, [_KV, C.POINTER(SelectParamsStruct)]),
     "sa_hip_score_select_chunked": (C.c_int, [_KV, _P, C.POINTER(SelectParamsStruct), _P, _P, _P, _SZ, _P, _P]),
+    "sa_hip_attention_chunked_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
     "sa_hip_sparse_decode_attention_chunked": (C.c_int, [_KV, _P, _P, _P, _I32, _I32, _F, _P, _P, _SZ, _I32, _I32,
                                                          _P, _P]),
     "sa_hip_contiguous_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
@@ -633,14 +634,19 @@ def sparse_decode_attention(kv: PagedKV, query, selected, counts, scale, out=Non
 def sparse_decode_attention_chunked(kv: PagedKV, query, selected, counts, scale, chunk_pages, max_chunks, out=None,
                                     workspace=None, status=None, stream=None):
     """Attention with every page list cut into chunks of chunk_pages pages
-    (one workgroup each, merged): for mixed lengths and budgets."""
+    (one workgroup each, merged): for mixed lengths and budgets.  The default
+    workspace has room for the longest-first schedule; one of
+    sa_hip_attention_workspace_bytes(..., max_chunks) bytes keeps the grid
+    order (same results)."""
     import torch
     select_groups, sel_stride = selected.shape[1], selected.shape[2]
     if out is None:
         out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=query.device)
-    nbytes = lib().sa_hip_attention_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim, max_chunks)
-    if workspace is None:
+    if workspace is None:  # room for the partial records and the longest-first schedule
+        nbytes = lib().sa_hip_attention_chunked_workspace_bytes(kv.batch, kv.query_heads, kv.kv_heads, kv.head_dim,
+                                                                max_chunks)
         workspace = torch.zeros(nbytes // 4, dtype=torch.float32, device=query.device)
+    nbytes = workspace.numel() * workspace.element_size()
     s = kv.struct()
     check(lib().sa_hip_sparse_decode_attention_chunked(
         C.byref(s), _ptr(query), _ptr(selected), _ptr(counts), select_groups, sel_stride, C.c_float(scale),

@@ -66,6 +66,39 @@ def test_chunked_pages(hip, chunk, max_chunks, hq):
     assert_close_2e3(got, expect)
 
 
+@pytest.mark.parametrize("hq,chunk,max_chunks", [(16, 4, 12), (32, 8, 7), (64, 3, 40), (16, 1, 200)])
+def test_chunked_longest_first_equals_grid_order(hip, hq, chunk, max_chunks):
+    """The longest-first schedule (a workspace of
+    sa_hip_attention_chunked_workspace_bytes) attends the same chunks and
+    merges them in the same order as the grid order (a workspace of
+    sa_hip_attention_workspace_bytes): equal bit for bit, over lists of very
+    different lengths, empty lists and lists longer than max_chunks chunks."""
+    print(f"case: chunk schedule hq={hq} chunk={chunk} max_chunks={max_chunks}", flush=True)
+    lengths = [32 * 200 + 9, 20, 32 * 3 + 5, 32 * 77 + 1, 31, 32 * 150, 32 * 12 + 17]
+    case = make_case(26 + hq, len(lengths), hq, 8, lengths, planted=2)
+    sel, cnt = O.paged_score_select(case.query, case.reps, case.sealed, case.batch, hq, 8, D, case.rep_heads,
+                                    case.rep_stride, 8, 180, 1, 2)
+    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, sel, cnt, 8,
+                                      case.query, case.batch, hq, 8, D, SCALE)
+    kv = device_kv(case)
+    L = hip.lib()
+    small = L.sa_hip_attention_workspace_bytes(kv.batch, hq, 8, 128, max_chunks)
+    big = L.sa_hip_attention_chunked_workspace_bytes(kv.batch, hq, 8, 128, max_chunks)
+    assert big > small
+    outs = []
+    for nbytes in (small, big, big):
+        ws = torch.zeros(nbytes // 4, dtype=torch.float32, device="cuda")
+        st = status_tensor()
+        out = hip.sparse_decode_attention_chunked(kv, to_dev(case.query), to_dev(sel), to_dev(cnt), SCALE, chunk,
+                                                  max_chunks, workspace=ws, status=st)
+        torch.cuda.synchronize()
+        assert int(st.item()) == 0
+        outs.append(out.cpu().numpy())
+    assert_close_2e3(outs[0], expect)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[1].view(np.uint32), outs[2].view(np.uint32))  # the schedule rebuilt each call
+
+
 def test_chunked_equals_split_within_rounding(hip):
     """The chunked and the split schedules sum the same terms in another
     order: equal within fp32 rounding."""
