@@ -184,10 +184,11 @@ class SparseDecoder {
         step_workspace_((step_workspace_bytes_ + 3) / 4),
         chunk_pages_(chunk_pages),
         max_chunks_(chunks_for(params.sel_stride, chunk_pages)),
-        chunk_workspace_bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),
-                                                                static_cast<int32_t>(pool.query_heads()),
-                                                                static_cast<int32_t>(pool.kv_heads()), 128,
-                                                                max_chunks_)),
+        // the partial records and the longest-list-first schedule
+        chunk_workspace_bytes_(sa_hip_attention_chunked_workspace_bytes(static_cast<int32_t>(pool.batch()),
+                                                                        static_cast<int32_t>(pool.query_heads()),
+                                                                        static_cast<int32_t>(pool.kv_heads()), 128,
+                                                                        max_chunks_)),
         chunk_workspace_((chunk_workspace_bytes_ + 3) / 4) {}
 
   // Score every sealed block against the query [batch][query_heads][128]
