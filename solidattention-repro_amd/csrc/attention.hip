@@ -26,6 +26,7 @@
 // ~3% of the same kernel with its arithmetic removed (timing probe); the
 // register kernel with splits of 2 + merge ran ~13% slower on the same box.
 #include "attn_core.hpp"
+#include "schedule.hpp"
 
 namespace sa {
 namespace {
@@ -243,114 +244,16 @@ __global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const Par
 // chunks consecutive (a counting sort on the page total, one workgroup):
 // short lists fill the end.  Results do not depend on the order: each chunk
 // attends the same pages and the merge adds the chunks in chunk order.
-constexpr int kSchedMaxLists = 4096;
-constexpr int kSchedBins = 4096;
-constexpr int kSchedThreads = 1024;
-constexpr int kSchedPer = kSchedMaxLists / kSchedThreads;
-
-// Exclusive prefix sum over the workgroup's threads (in thread order).
-__device__ inline int sched_scan(int v, int* wave_sums) {
-  const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int t = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += t;
-  }
-  if (lane == kWave - 1) wave_sums[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    int w = lane < kSchedThreads / kWave ? wave_sums[lane] : 0;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int t = __shfl_up(w, off, kWave);
-      if (lane >= off) w += t;
-    }
-    if (lane < kSchedThreads / kWave) wave_sums[lane] = w;  // inclusive over waves
-  }
-  __syncthreads();
-  const int before = wave > 0 ? wave_sums[wave - 1] : 0;
-  __syncthreads();  // wave_sums reusable
-  return before + incl - v;
-}
-
 __global__ __launch_bounds__(kSchedThreads) void chunk_schedule_kernel(const Params p, int batch, int32_t* sched) {
   const int n = batch * p.v.kv_heads;  // <= kSchedMaxLists
-  const int64_t slots = static_cast<int64_t>(n) * p.splits;
-  const int tid = threadIdx.x;
-  __shared__ int hist[kSchedBins];
-  __shared__ int sorted[kSchedMaxLists];
-  __shared__ int nch[kSchedMaxLists];
-  __shared__ int wave_sums[kSchedThreads / kWave];
-  for (int i = tid; i < kSchedBins; i += kSchedThreads) hist[i] = 0;
-  __syncthreads();
-  // each list's page total and chunk count (chunk 0 always runs: it writes
-  // the record the merge reads; the last chunk takes any remainder)
-  int bin[kSchedPer];
-#pragma unroll
-  for (int k = 0; k < kSchedPer; ++k) {
-    const int l = tid + k * kSchedThreads;
-    bin[k] = -1;
-    if (l < n) {
-      const PageList L = page_list(p, l / p.v.kv_heads, l % p.v.kv_heads);
-      const int64_t total = L.total;
-      nch[l] = total <= 0 ? 1 : static_cast<int>(min<int64_t>(p.splits, (total + p.chunk_pages - 1) / p.chunk_pages));
-      const int64_t key = total < 0 ? 0 : (total > kSchedBins - 1 ? kSchedBins - 1 : total);
-      bin[k] = kSchedBins - 1 - static_cast<int>(key);  // longest in bin 0
-      atomicAdd(&hist[bin[k]], 1);
-    }
-  }
-  __syncthreads();
-  // bins -> first sorted position (4 bins per thread)
-  constexpr int kBinsPer = kSchedBins / kSchedThreads;
-  int hs[kBinsPer];
-  int hsum = 0;
-#pragma unroll
-  for (int i = 0; i < kBinsPer; ++i) {
-    hs[i] = hist[tid * kBinsPer + i];
-    hsum += hs[i];
-  }
-  int off = sched_scan(hsum, wave_sums);
-#pragma unroll
-  for (int i = 0; i < kBinsPer; ++i) {
-    hist[tid * kBinsPer + i] = off;
-    off += hs[i];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kSchedPer; ++k) {
-    const int l = tid + k * kSchedThreads;
-    if (l < n) sorted[atomicAdd(&hist[bin[k]], 1)] = l;  // order within a bin does not matter
-  }
-  __syncthreads();
-  // first workgroup of each sorted list (kSchedPer consecutive lists per thread)
-  int c[kSchedPer];
-  int csum = 0;
-#pragma unroll
-  for (int k = 0; k < kSchedPer; ++k) {
-    const int i = tid * kSchedPer + k;
-    c[k] = i < n ? nch[sorted[i]] : 0;
-    csum += c[k];
-  }
-  int w = sched_scan(csum, wave_sums);
-#pragma unroll
-  for (int k = 0; k < kSchedPer; ++k) {
-    const int i = tid * kSchedPer + k;
-    if (i < n) {
-      const int l = sorted[i];
-      for (int zz = 0; zz < c[k]; ++zz) {
-        sched[w + zz] = l;
-        sched[slots + w + zz] = zz;
-      }
-    }
-    w += c[k];
-  }
-  // the workgroups past the last chunk have nothing to attend
-  __shared__ int s_used;
-  if (tid == kSchedThreads - 1) s_used = w;  // every list's chunks
-  __syncthreads();
-  for (int64_t e = s_used + tid; e < slots; e += kSchedThreads) sched[e] = -1;
+  build_list_schedule(n, static_cast<int64_t>(n) * p.splits, sched, [&](int l, int& key, int& chunks) {
+    // each list's page total and chunk count (chunk 0 always runs: it writes
+    // the record the merge reads; the last chunk takes any remainder)
+    const PageList L = page_list(p, l / p.v.kv_heads, l % p.v.kv_heads);
+    const int64_t total = L.total;
+    chunks = total <= 0 ? 1 : static_cast<int>(min<int64_t>(p.splits, (total + p.chunk_pages - 1) / p.chunk_pages));
+    key = static_cast<int>(total < 0 ? 0 : (total > kSchedBins - 1 ? kSchedBins - 1 : total));
+  });
 }
 
 template <int G>

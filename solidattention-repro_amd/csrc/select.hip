@@ -8,6 +8,7 @@
 // (rounds of resident workgroups) x (blocks per lane): 8 waves (two
 // workgroups per CU) at B=64 / 16K, 16 waves (one per CU, one block per
 // lane) at B=32 / 32K.  This file is compiled with -ffp-contract=off.
+#include "schedule.hpp"
 #include "select_core.hpp"
 
 namespace sa {
@@ -34,6 +35,9 @@ struct Params {
   int32_t init_blocks;
   int32_t local_blocks;
   int32_t sel_stride;
+  // chunked selection, lists longest first (schedule.hpp): workgroup w takes
+  // chunk sched[slots + w] of list sched[w] = b * select_groups + sg (-1: none)
+  const int32_t* sched;
 };
 
 // QUAD: four blocks per lane with 16-byte representative loads (reps 16-byte
@@ -160,9 +164,18 @@ __global__ __launch_bounds__(kThreads) void score_select_chunked_kernel(const Pa
                                                                         int32_t* ws_arrive, int32_t key_stride) {
   constexpr int kWaves = kThreads / kWave;
   constexpr int kChunk = NB * kThreads;
-  const int sg = blockIdx.x;
-  const int b = blockIdx.y;
-  const int z = blockIdx.z;
+  int sg = blockIdx.x;
+  int b = blockIdx.y;
+  int z = blockIdx.z;
+  if (p.sched) {
+    const int64_t w = blockIdx.x + static_cast<int64_t>(gridDim.x) * (blockIdx.y + static_cast<int64_t>(gridDim.y) *
+                                                                                     blockIdx.z);
+    const int32_t l = p.sched[w];
+    if (l < 0) return;
+    b = l / p.select_groups;
+    sg = l % p.select_groups;
+    z = p.sched[static_cast<int64_t>(gridDim.x) * gridDim.y * gridDim.z + w];
+  }
   const int tid = threadIdx.x;
 
   extern __shared__ __align__(16) float dyn_smem[];
@@ -350,35 +363,65 @@ hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Smallest chunk of any width (256 threads x 2 blocks): bounds the schedule.
+constexpr int kMinSelectChunk = 512;
+
 size_t score_select_chunked_workspace_bytes(int64_t batch, int32_t select_groups, int32_t rep_stride) {
   const int64_t lists = batch * select_groups;
   const int64_t key_stride = (rep_stride < kMaxSelectBlocks ? rep_stride : kMaxSelectBlocks);
-  return static_cast<size_t>((lists * 4 + 255) / 256 * 256 + lists * key_stride * 4);
+  const int64_t sched = 2 * lists * ((key_stride + kMinSelectChunk - 1) / kMinSelectChunk);
+  return static_cast<size_t>((lists * 4 + 255) / 256 * 256 + lists * key_stride * 4 + sched * 4);
 }
 
 bool score_select_chunked_supported(const SelectLaunch& s) { return sel::vec_layout<4>(s.reps, s.rep_stride); }
 
+// The chunked selection's workgroups, lists longest first (schedule.hpp):
+// the length key is the list's block count when it is scored; a list whose
+// budget takes every block (or is invalid) does no scoring and sorts last.
+__global__ __launch_bounds__(kSchedThreads) void select_schedule_kernel(const Params p, int batch, int chunk,
+                                                                         int max_chunks, int32_t* sched) {
+  const int lists = batch * p.select_groups;
+  build_list_schedule(lists, static_cast<int64_t>(lists) * max_chunks, sched, [&](int l, int& key, int& chunks) {
+    const int b = l / p.select_groups;
+    const int n = p.sealed[b];
+    key = 0;
+    chunks = 1;
+    if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) return;
+    const Budget bs = budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
+    if (bs.bad || bs.take_all) return;
+    key = n;
+    chunks = (n + chunk - 1) / chunk;
+  });
+}
+
 template <int GR, int kThreads, int NB>
 void launch_chunked(const Params& p, int batch, int32_t* arrive, uint32_t* keys, int32_t key_stride,
-                    hipStream_t stream) {
+                    int32_t* sched, hipStream_t stream) {
   constexpr int kChunk = NB * kThreads;
-  const dim3 grid(p.select_groups, batch, (key_stride + kChunk - 1) / kChunk);
-  hipLaunchKernelGGL((score_select_chunked_kernel<GR, kThreads, NB>), grid, dim3(kThreads), select_smem_bytes(p),
-                     stream, p, keys, arrive, key_stride);
+  const int max_chunks = (key_stride + kChunk - 1) / kChunk;
+  const dim3 grid(p.select_groups, batch, max_chunks);
+  Params q = p;
+  if (sched && static_cast<int64_t>(batch) * p.select_groups <= kSchedMaxLists) {
+    hipLaunchKernelGGL(select_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, stream, p, batch, kChunk,
+                       max_chunks, sched);
+    q.sched = sched;
+  }
+  hipLaunchKernelGGL((score_select_chunked_kernel<GR, kThreads, NB>), grid, dim3(kThreads), select_smem_bytes(q),
+                     stream, q, keys, arrive, key_stride);
 }
 
 template <int GR, int NB>
 void launch_chunked_width(const Params& p, int batch, bool many_lists, int32_t* arrive, uint32_t* keys,
-                          int32_t key_stride, hipStream_t stream) {
+                          int32_t key_stride, int32_t* sched, hipStream_t stream) {
   // with a list per compute unit or more, 16-wave workgroups (chunks of 2048
   // blocks) pull the most per list; with fewer lists, 4-wave workgroups
   // (chunks of 1024) spread each list over more compute units.  Measured on
   // the mixed B=128 workload (1024 lists of 61-2038 blocks): 512 threads
   // 80.9 us, 256 threads 82.8 us, 128 threads 91.8 us.
   if (many_lists) {
-    launch_chunked<GR, 512, NB>(p, batch, arrive, keys, key_stride, stream);
+    launch_chunked<GR, 512, NB>(p, batch, arrive, keys, key_stride, sched, stream);
   } else {
-    launch_chunked<GR, 256, NB>(p, batch, arrive, keys, key_stride, stream);
+    launch_chunked<GR, 256, NB>(p, batch, arrive, keys, key_stride, sched, stream);
   }
 }
 
@@ -389,12 +432,13 @@ hipError_t launch_score_select_chunked(const SelectLaunch& s, void* workspace, h
   const int32_t key_stride = s.rep_stride < kMaxSelectBlocks ? s.rep_stride : kMaxSelectBlocks;
   int32_t* arrive = static_cast<int32_t*>(workspace);
   uint32_t* keys = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + (lists * 4 + 255) / 256 * 256);
+  int32_t* sched = reinterpret_cast<int32_t*>(keys + lists * key_stride);  // rewritten by every call
   const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
   switch (gr) {
-    case 1: launch_chunked_width<1, 4>(p, s.batch, many, arrive, keys, key_stride, stream); break;
-    case 2: launch_chunked_width<2, 4>(p, s.batch, many, arrive, keys, key_stride, stream); break;
-    case 4: launch_chunked_width<4, 4>(p, s.batch, many, arrive, keys, key_stride, stream); break;
-    case 8: launch_chunked_width<8, 2>(p, s.batch, many, arrive, keys, key_stride, stream); break;
+    case 1: launch_chunked_width<1, 4>(p, s.batch, many, arrive, keys, key_stride, sched, stream); break;
+    case 2: launch_chunked_width<2, 4>(p, s.batch, many, arrive, keys, key_stride, sched, stream); break;
+    case 4: launch_chunked_width<4, 4>(p, s.batch, many, arrive, keys, key_stride, sched, stream); break;
+    case 8: launch_chunked_width<8, 2>(p, s.batch, many, arrive, keys, key_stride, sched, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
