@@ -273,48 +273,65 @@ bool block_topk_whole_rows(int window, const float* prob) {
          reinterpret_cast<uintptr_t>(prob) % 16 == 0;
 }
 
+// Blocks per workgroup of block_topk_kernel with whole rows.
+constexpr int kWholeRowBlocks = 4;
+
 size_t block_topk_lds_bytes(int window, bool whole_rows) {
-  return static_cast<size_t>(kPageTokens + window - 1) * (whole_rows ? window + 2 : kStageCols) * sizeof(float);
+  const int blocks = whole_rows ? kWholeRowBlocks : 1;
+  return static_cast<size_t>(blocks * kPageTokens + window - 1) * (whole_rows ? window + 2 : kStageCols) *
+         sizeof(float);
 }
 
 // One wave per (block, head): received mass, stable rank, top-k, representative.
-template <bool WHOLE_ROWS>
-__global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
-  int b, h;
-  xcd_tile(p.hq, p.hkv, b, h);
-  const int lane = threadIdx.x;
+// BPW blocks per workgroup, one wave each: with whole rows the BPW blocks'
+// query rows overlap (32 BPW + W - 1 rows for BPW blocks, against 32 + W - 1
+// each), so the waves stage them once together and more blocks fit in LDS at
+// once; the per-column layout holds one block's columns (BPW = 1).
+template <bool WHOLE_ROWS, int BPW>
+__global__ __launch_bounds__(BPW * kWave) void block_topk_kernel(const Params p) {
+  constexpr int kThreads = BPW * kWave;
+  int tile, h;
+  xcd_tile(p.hq, p.hkv, tile, h);
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
   const int g = h / (p.hq / p.hkv);
   const int64_t blocks = p.tokens / kPageTokens;
+  const int b = tile * BPW + wave;
+  const bool valid = b < blocks;  // a wave past the last block only joins the staging and the barriers
+  const int64_t tt = static_cast<int64_t>(tile) * BPW * kPageTokens;  // first token of the tile
   const int64_t t0 = static_cast<int64_t>(b) * kPageTokens;
   const int W = p.window;
-  __shared__ int order[kPageTokens];
+  __shared__ int order[BPW][kPageTokens];
   extern __shared__ float stage_s[];
 
-  // the queries t0 .. q_last, whose rows start at prob_b; the window of query
-  // t0 + r starts at t0 + r + 1 - W (at 0 for the first W - 1 queries)
-  const int64_t q_last = t0 + kPageTokens - 1 + W - 1 < p.tokens - 1 ? t0 + kPageTokens - 1 + W - 1 : p.tokens - 1;
-  const int rows = static_cast<int>(q_last - t0 + 1);
-  const float* prob_b = p.prob + (static_cast<int64_t>(h) * p.tokens + t0) * W;
+  // the queries tt .. q_last, whose rows start at prob_b; the window of query
+  // tt + r starts at tt + r + 1 - W (at 0 for the first W - 1 queries)
+  const int64_t q_last = tt + BPW * kPageTokens - 1 + W - 1 < p.tokens - 1 ? tt + BPW * kPageTokens - 1 + W - 1
+                                                                           : p.tokens - 1;
+  const int rows = static_cast<int>(q_last - tt + 1);
+  const float* prob_b = p.prob + (static_cast<int64_t>(h) * p.tokens + tt) * W;
   if (WHOLE_ROWS) {
     // rows x W floats from prob_b, W / 4 pieces per row (a power of two)
     const int pieces = rows * (W / 4);
     const int shift = __builtin_ctz(W / 4);
     const u32x4_t* src = reinterpret_cast<const u32x4_t*>(prob_b);
     constexpr int kBatch = 8;
-    for (int e0 = lane; e0 < pieces; e0 += kBatch * kWave) {
+    for (int e0 = tid; e0 < pieces; e0 += kBatch * kThreads) {
       u32x4_t v[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) v[i] = src[e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1];
+      for (int i = 0; i < kBatch; ++i) v[i] = src[e0 + i * kThreads < pieces ? e0 + i * kThreads : pieces - 1];
       __builtin_amdgcn_sched_barrier(0);  // every load of the batch ahead of the stores
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
-        const int e = e0 + i * kWave < pieces ? e0 + i * kWave : pieces - 1;  // a clamped piece rewrites its value
+        const int e = e0 + i * kThreads < pieces ? e0 + i * kThreads : pieces - 1;  // a clamped piece rewrites its value
         u32x2_t* dst = reinterpret_cast<u32x2_t*>(stage_s + (e >> shift) * (W + 2) + (e & (W / 4 - 1)) * 4);
         dst[0] = u32x2_t{v[i].x, v[i].y};
         dst[1] = u32x2_t{v[i].z, v[i].w};
       }
     }
   } else {
+    static_assert(WHOLE_ROWS || BPW == 1, "the per-column layout holds one block");
     // (row r, column j) = the probability query t0 + r gives token t0 + j:
     // each row's 32 columns are contiguous in the query's window row, so a
     // load instruction covers two rows; entries outside a query's window are
@@ -346,16 +363,17 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
   // received mass of token t = t0 + lane: the probabilities of the queries
   // t .. min(t + W - 1, tokens - 1) summed in query order
   float r = 0.0f;
-  if (lane < kPageTokens) {
+  if (valid && lane < kPageTokens) {
     const int64_t t = t0 + lane;
     const int n = static_cast<int>((t + W - 1 < p.tokens - 1 ? t + W - 1 : p.tokens - 1) - t + 1);
+    const int row_t = static_cast<int>(t - tt);  // the stage row of query t
     // stage index of query t + i's probability of token t
     auto at = [&](int i) {
       if (WHOLE_ROWS) {
         const int64_t start = t + i + 1 > W ? t + i + 1 - W : 0;
-        return (lane + i) * (W + 2) + static_cast<int>(t - start);
+        return (row_t + i) * (W + 2) + static_cast<int>(t - start);
       }
-      return (lane + i) * kStageCols + lane;
+      return (row_t + i) * kStageCols + lane;
     };
     constexpr int kReads = 8;  // LDS reads issued together, then added in order
     for (int i0 = 0; i0 < n; i0 += kReads) {
@@ -377,11 +395,12 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
     const float rj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), j));
     rank += static_cast<int>((rj > r) | (!(r > rj) & !(rj > r) & (j < lane)));
   }
-  if (lane < kPageTokens && rank < p.topk) {
-    order[rank] = lane;
+  if (valid && lane < kPageTokens && rank < p.topk) {
+    order[wave][rank] = lane;
     if (p.offsets) p.offsets[(static_cast<int64_t>(h) * blocks + b) * p.topk + rank] = lane;
   }
   __syncthreads();
+  if (!valid) return;
 
   // representative: lane d-pair (2 lane, 2 lane + 1); the chosen keys' words
   // loaded 8 at a time, summed in rank order
@@ -396,7 +415,7 @@ __global__ __launch_bounds__(kWave) void block_topk_kernel(const Params p) {
 #pragma unroll
     for (int i = 0; i < kKeys; ++i) {
       const int rk = rk0 + i < p.topk ? rk0 + i : p.topk - 1;
-      w[i] = kblock[order[rk] * (token_elems / 2)];
+      w[i] = kblock[order[wave][rk] * (token_elems / 2)];
     }
 #pragma unroll
     for (int i = 0; i < kKeys; ++i) {
@@ -464,11 +483,15 @@ hipError_t launch_local_causal_representatives(const RepresentativeLaunch& r, hi
   else launch_window<64>(p, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const dim3 grid(static_cast<unsigned>(r.tokens / kPageTokens), r.query_heads);
+  const int64_t blocks = r.tokens / kPageTokens;
   if (block_topk_whole_rows(r.window, p.prob)) {
-    hipLaunchKernelGGL(block_topk_kernel<true>, grid, dim3(kWave), block_topk_lds_bytes(r.window, true), stream, p);
+    const dim3 grid(static_cast<unsigned>((blocks + kWholeRowBlocks - 1) / kWholeRowBlocks), r.query_heads);
+    hipLaunchKernelGGL((block_topk_kernel<true, kWholeRowBlocks>), grid, dim3(kWholeRowBlocks * kWave),
+                       block_topk_lds_bytes(r.window, true), stream, p);
   } else {
-    hipLaunchKernelGGL(block_topk_kernel<false>, grid, dim3(kWave), block_topk_lds_bytes(r.window, false), stream, p);
+    const dim3 grid(static_cast<unsigned>(blocks), r.query_heads);
+    hipLaunchKernelGGL((block_topk_kernel<false, 1>), grid, dim3(kWave), block_topk_lds_bytes(r.window, false), stream,
+                       p);
   }
   return hipGetLastError();
 }
