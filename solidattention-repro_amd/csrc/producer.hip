@@ -156,8 +156,8 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
   // k = 16 s + [0, 16), lane l supplying k = 16 s + 4 (l / 16) + e to matrix step 4 s + e
   const float* xa = &xs[(wave * kMTile + lane % 16) * kStr + 4 * (lane / 16)];
   const float* wb = &ws[(lane % 16) * kStr + 4 * (lane / 16)];
-#pragma unroll
-  for (int u = 0; u < kNU; ++u) {
+  // unit u's x (times the gain) and w into its own LDS region
+  auto stage = [&](int u) {
 #pragma unroll
     for (int i = 0; i < kXU; ++i) {
       f32x4_t v = xr[u][i];
@@ -171,20 +171,62 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
 #pragma unroll
     for (int i = 0; i < kWU; ++i)
       *reinterpret_cast<f32x4_t*>(&ws[((i * kThreads + tid) / 8) * kStr + u * kUnitK + 4 * c4]) = wr[u][i];
-    __syncthreads();
+  };
+  auto mfma_step = [&](const f32x4_t& a, const f32x4_t* b) {
 #pragma unroll
-    for (int s = 0; s < kUnitK / 16; ++s) {
-      const int k = u * kUnitK + 16 * s;
-      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(xa + k);
-      f32x4_t b[kCT];
+    for (int e = 0; e < 4; ++e) {
 #pragma unroll
-      for (int t = 0; t < kCT; ++t) b[t] = *reinterpret_cast<const f32x4_t*>(wb + t * 16 * kStr + k);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int t = 0; t < kCT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[t][e], acc[t], 0, 0, 0);
-      }
+      for (int t = 0; t < kCT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[t][e], acc[t], 0, 0, 0);
     }
+  };
+  // Two steps per unit.  The operands of each step are read from LDS one step
+  // ahead, and unit u + 1 is staged among the matrix steps of unit u's first
+  // step, so its barrier passes between unit u's two steps and no LDS
+  // latency or barrier wait sits between matrix steps.
+  static_assert(kUnitK == 32, "two 16-k steps per unit");
+  constexpr int kSteps = 4 * kCT;       // matrix steps per step
+  constexpr int kReads = 1 + kCT;       // LDS reads of one step's operands
+  constexpr int kWrites = kXU + kWU;    // LDS writes of one unit
+  stage(0);
+  __syncthreads();
+  f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(xa), b0[kCT];
+#pragma unroll
+  for (int t = 0; t < kCT; ++t) b0[t] = *reinterpret_cast<const f32x4_t*>(wb + t * 16 * kStr);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < kNU; ++u) {
+    const int k1 = u * kUnitK + 16;
+    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(xa + k1);
+    f32x4_t b1[kCT];
+#pragma unroll
+    for (int t = 0; t < kCT; ++t) b1[t] = *reinterpret_cast<const f32x4_t*>(wb + t * 16 * kStr + k1);
+    mfma_step(a0, b0);
+    if (u + 1 < kNU) stage(u + 1);
+    // reads of step 1, then the writes of unit u + 1, spread over step 0's matrix steps
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+    for (int r = 0; r < kWrites; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, (kSteps - 2) / kWrites > 0 ? (kSteps - 2) / kWrites : 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (u + 1 < kNU) {
+      __syncthreads();
+      const int k2 = (u + 1) * kUnitK;
+      a0 = *reinterpret_cast<const f32x4_t*>(xa + k2);
+#pragma unroll
+      for (int t = 0; t < kCT; ++t) b0[t] = *reinterpret_cast<const f32x4_t*>(wb + t * 16 * kStr + k2);
+    }
+    mfma_step(a1, b1);
+    // reads of unit u + 1's step 0 spread over step 1's matrix steps
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+#pragma unroll
+    for (int r = 0; r < kReads; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, (kSteps - 1) / kReads > 0 ? (kSteps - 1) / kReads : 1, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // D layout: lane holds rows 16 wave + 4 (lane / 16) + i, column 16 t + lane % 16
