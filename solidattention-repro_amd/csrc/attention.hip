@@ -216,19 +216,41 @@ __global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const Par
     const int64_t total = page_list(p, b, g).total;
     records = static_cast<int>(min<int64_t>(p.part_total, max<int64_t>(1, (total + p.chunk_pages - 1) / p.chunk_pages)));
   }
+  // The records' loads are issued kMergeBatch at a time (indices past the
+  // last record read the last one and are not used); the maximum over all
+  // records comes first, then the weighted sums are added in chunk order.
+  constexpr int kMergeBatch = 8;
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
     const int h = o / D;
     const int d = o % D;
+    const float* rh = base + h * part_stride(D);
+    const int64_t rstride = static_cast<int64_t>(G) * part_stride(D);
     float mx = kNegInf;
-    for (int zz = 0; zz < records; ++zz) mx = fmaxf(mx, base[(zz * G + h) * part_stride(D)]);
+    for (int z0 = 0; z0 < records; z0 += kMergeBatch) {
+      float m[kMergeBatch];
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) m[j] = rh[min(z0 + j, records - 1) * rstride];
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) mx = fmaxf(mx, m[j]);
+    }
     float lw = 0.0f, aw = 0.0f;
     if (mx != kNegInf) {
-      for (int zz = 0; zz < records; ++zz) {
-        const float* rec = base + (zz * G + h) * part_stride(D);
-        if (rec[0] == kNegInf) continue;
-        const float f = __builtin_amdgcn_exp2f(rec[0] - mx);
-        lw = __builtin_fmaf(rec[1], f, lw);
-        aw = __builtin_fmaf(rec[kPartPad + d], f, aw);
+      for (int z0 = 0; z0 < records; z0 += kMergeBatch) {
+        float m[kMergeBatch], l[kMergeBatch], a[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+          const float* rec = rh + min(z0 + j, records - 1) * rstride;
+          m[j] = rec[0];
+          l[j] = rec[1];
+          a[j] = rec[kPartPad + d];
+        }
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+          if (z0 + j >= records || m[j] == kNegInf) continue;
+          const float f = __builtin_amdgcn_exp2f(m[j] - mx);
+          lw = __builtin_fmaf(l[j], f, lw);
+          aw = __builtin_fmaf(a[j], f, aw);
+        }
       }
     }
     p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
