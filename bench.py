@@ -116,7 +116,10 @@ class Layer:
         # planted high-score blocks: keys = 0.5 * mean(q of the group) + 0.5 * noise
         if planted:
             full = ctx // PAGE
-            blocks = torch.randint(0, full, (batch, hkv, planted), generator=g).cuda()
+            # distinct blocks per (sequence, head): a block drawn twice would be
+            # written twice by one index assignment, and which write lands is
+            # not defined on the GPU
+            blocks = torch.rand((batch, hkv, full), generator=g).argsort(dim=-1)[..., :planted].cuda()
             grp = hq // hkv
             qmean = q0.view(batch, hkv, grp, D).mean(dim=2)  # [B, Hkv, D]
             pool16 = kv.pool.view(torch.float16)  # [pages, 32, 2, Hkv, D]
