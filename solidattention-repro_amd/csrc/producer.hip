@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = m0 + wave * kMTile + 4 * (lane / 16) + i;
-      part[static_cast<int64_t>(row) * p.out + n0 + 16 * t + lane % 16] = acc[t][i];
+      __builtin_nontemporal_store(acc[t][i], &part[static_cast<int64_t>(row) * p.out + n0 + 16 * t + lane % 16]);
     }
   }
   if (GAIN && cb == 0) {
