@@ -184,6 +184,8 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
   // step, so its barrier passes between unit u's two steps and no LDS
   // latency or barrier wait sits between matrix steps.
   static_assert(kUnitK == 32, "two 16-k steps per unit");
+  // instruction classes of __builtin_amdgcn_sched_group_barrier
+  constexpr int kSgMfma = 0x008, kSgDsRead = 0x100, kSgDsWrite = 0x200;
   constexpr int kSteps = 4 * kCT;       // matrix steps per step
   constexpr int kReads = 1 + kCT;       // LDS reads of one step's operands
   constexpr int kWrites = kXU + kWU;    // LDS writes of one unit
@@ -203,12 +205,12 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
     mfma_step(a0, b0);
     if (u + 1 < kNU) stage(u + 1);
     // reads of step 1, then the writes of unit u + 1, spread over step 0's matrix steps
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgDsRead, kReads, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
 #pragma unroll
     for (int r = 0; r < kWrites; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, (kSteps - 2) / kWrites > 0 ? (kSteps - 2) / kWrites : 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, (kSteps - 2) / kWrites > 0 ? (kSteps - 2) / kWrites : 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (u + 1 < kNU) {
@@ -220,11 +222,11 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
     }
     mfma_step(a1, b1);
     // reads of unit u + 1's step 0 spread over step 1's matrix steps
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 1);
 #pragma unroll
     for (int r = 0; r < kReads; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, (kSteps - 1) / kReads > 0 ? (kSteps - 1) / kReads : 1, 1);
+      __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, (kSteps - 1) / kReads > 0 ? (kSteps - 1) / kReads : 1, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
