@@ -130,7 +130,12 @@ class Layer:
             vals = (0.5 * qmean[:, :, None, None, :] + 0.5 * noise).to(torch.float16)
             pool16[pages.reshape(-1), :, 0, heads.reshape(-1), :] = vals.reshape(-1, PAGE, D)
         kv.seq_len.fill_(ctx)
+        # the prefill's bulk seal: every whole page gets its representative
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         sa.seal(kv, 0)
+        e1.record()
+        self.seal_events = (e0, e1)
         self.kv, self.q, self.knew, self.vnew = kv, q, knew, vnew
         self.budget, self.init, self.local = budget, init, local
         self.selected = torch.full((batch, hkv, budget), -1, dtype=torch.int32, device="cuda")
@@ -317,6 +322,10 @@ def main():
     else:
         kernel_us = sel_us if launches == 2 else att_us
 
+    seal_us = 1000.0 * sum(ly.seal_events[0].elapsed_time(ly.seal_events[1]) for ly in L) / layers
+    seal_bytes = batch * (ctx // PAGE) * (PAGE * hkv * D * 2 + hkv * D * 4)
+    log(f"prefill bulk seal: {seal_us:.1f} us per layer ({seal_bytes / (seal_us * 1e-6) / 1e9:.0f} GB/s over the "
+        f"keys read and representatives written)")
     copy_ref = copy_reference(sa, torch, L[0].kv, args.seed)
     read_ref = read_reference(sa, np, torch, L[-1], hkv)
 
@@ -383,6 +392,8 @@ def main():
         "launch": "hip graph per decode step" if graph else "eager",
         "eager_us_per_layer": round(eager_ms * 1000.0 / args.steps / layers, 3),
         "achieved_layer_hbm_gbps": round(layer_gbps, 1),
+        "prefill_seal": {"us_per_layer": round(seal_us, 1), "bytes_per_layer": seal_bytes,
+                         "gbps": round(seal_bytes / (seal_us * 1e-6) / 1e9, 1)},
         "kernels_us": ({"decode_step": round(kernel_us, 3), "decode_step_eager": round(app_us, 3)}
                        if launches == 1 else
                        {"select_attend": round(kernel_us, 3), "select_attend_in_step": round(sel_us, 3),

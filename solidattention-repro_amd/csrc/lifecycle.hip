@@ -138,6 +138,108 @@ __global__ __launch_bounds__(kThreads) void append_seal_kernel(const Params p) {
   }
 }
 
+// ---- bulk seal (no append): a prefill's whole pages sealed at once ----------
+// The tail rule of append_seal_kernel seals blocks sealed, sealed + 1, ...
+// while seq_len >= (block + 1) * 32 + local_tokens, and stops at the first
+// block without a representative slot or a page (a capacity error).  The
+// bulk form computes the same block range up front: the last block to seal
+// from seq_len, the stopping block by a scan of the table.  Workgroup
+// (chunk, KV head, sequence) sums kSealBlocks consecutive blocks of one KV
+// head; a second launch of one wave per sequence commits sealed and
+// generation, so that no workgroup reads a counter another has moved.
+constexpr int kSealBlocks = 16;
+constexpr int kSealPieces = D / 8;  // 16-byte pieces of one head's key row
+static_assert(kSealBlocks * kSealPieces == kThreads, "one thread per (block, piece)");
+
+// Blocks sealed once the tail rule has run to its end, ignoring capacity.
+__device__ inline int64_t seal_target(int64_t len, int64_t local, int64_t s0) {
+  if (len < local) return s0;
+  const int64_t t = (len - local) / kPageTokens;
+  return t > s0 ? t : s0;
+}
+
+// The first block of [from, to) that cannot be sealed (no representative
+// slot or no page), or `to`; strided over `threads` threads, the caller
+// takes the minimum.
+__device__ inline int64_t first_unsealable(const Params& p, int b, int64_t from, int64_t to, int tid, int threads) {
+  for (int64_t s = from + tid; s < to; s += threads)
+    if (s >= p.rep_stride || table_page(p, b, s) < 0) return s;
+  return to;
+}
+
+__global__ __launch_bounds__(kThreads) void seal_blocks_kernel(const Params p) {
+  const int g = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int64_t s0 = p.sealed[b];
+  const int64_t target = seal_target(p.seq_len[b], p.local_tokens, s0);
+  const int64_t first = s0 + static_cast<int64_t>(blockIdx.x) * kSealBlocks;
+  if (first >= target) return;
+  __shared__ int32_t s_stop;
+  __shared__ float tile[D][kSealBlocks + 1];
+  // blocks past a capacity error stay unsealed, as in the tail rule
+  const int64_t end = target < first + kSealBlocks ? target : first + kSealBlocks;
+  if (tid == 0) s_stop = static_cast<int32_t>(end - first);
+  __syncthreads();
+  const int64_t bad = first_unsealable(p, b, s0, end, tid, kThreads);
+  if (bad < end) atomicMin(&s_stop, static_cast<int32_t>(bad > first ? bad - first : 0));
+  __syncthreads();
+  const int n = s_stop;
+  if (n <= 0) return;
+
+  // thread = (block j, 16-byte piece q of head g's key row); 32 loads in
+  // flight, then the 32 keys summed in token order
+  const int j = tid / kSealPieces, q = tid % kSealPieces;
+  if (j < n) {
+    const int64_t page = table_page(p, b, first + j);
+    const uint16_t* src = p.pool + page * p.page_elems + g * D + q * 8;
+    uint4 w[kPageTokens];
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) w[t] = load_stream16(src + static_cast<int64_t>(t) * p.token_elems);
+    float sum[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum[i] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) {
+      const uint32_t h[4] = {w[t].x, w[t].y, w[t].z, w[t].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sum[2 * i] = sum[2 * i] + lo_h2f(h[i]);
+        sum[2 * i + 1] = sum[2 * i + 1] + hi_h2f(h[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tile[q * 8 + i][j] = sum[i] / static_cast<float>(kPageTokens);
+  }
+  __syncthreads();
+  // rows d of the representative: kSealBlocks consecutive floats each
+  for (int e = tid; e < D * kSealBlocks; e += kThreads) {
+    const int d = e / kSealBlocks, jj = e % kSealBlocks;
+    if (jj >= n) continue;
+    const float rep = tile[d][jj];
+    for (int r = 0; r < p.group; ++r)
+      p.reps[((static_cast<int64_t>(b) * p.rep_heads + g * p.group + r) * D + d) * p.rep_stride + first + jj] = rep;
+  }
+}
+
+// One wave per sequence: the counters after the bulk seal.
+__global__ __launch_bounds__(kWave) void seal_commit_kernel(const Params p) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int64_t s0 = p.sealed[b];
+  const int64_t target = seal_target(p.seq_len[b], p.local_tokens, s0);
+  int64_t stop = first_unsealable(p, b, s0, target, lane, kWave);
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const int64_t o = __shfl_xor(stop, off, kWave);
+    stop = o < stop ? o : stop;
+  }
+  if (lane == 0) {
+    if (stop < target) flag_status(p.status, kStatusCapacity);
+    p.sealed[b] = static_cast<int32_t>(stop);
+    if (p.generation) p.generation[b] += static_cast<int32_t>(stop - s0);
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void gather_pages_kernel(const uint4* pool, int64_t page_vecs,
                                                                 int64_t num_pages, const int32_t* pages,
                                                                 uint4* out, int32_t* status) {
@@ -392,6 +494,13 @@ hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream) {
     p.query = l.query;
     p.online = online::Args{l.ring, l.ring_tokens, l.window, l.topk, l.query_heads, l.seal_scale};
     hipLaunchKernelGGL(append_seal_kernel<true>, dim3(l.batch), dim3(kThreads), 0, stream, p);
+  } else if (!l.append) {
+    // bulk seal: every block of a sequence's range in its own workgroup
+    const int64_t blocks = l.table_stride < l.rep_stride ? l.table_stride : l.rep_stride;
+    const dim3 grid(static_cast<unsigned>((blocks + kSealBlocks - 1) / kSealBlocks), l.kv_heads, l.batch);
+    hipLaunchKernelGGL(seal_blocks_kernel, grid, dim3(kThreads), 0, stream, p);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL(seal_commit_kernel, dim3(l.batch), dim3(kWave), 0, stream, p);
   } else {
     hipLaunchKernelGGL(append_seal_kernel<false>, dim3(l.batch), dim3(kThreads), 0, stream, p);
   }

@@ -69,6 +69,76 @@ def test_seal_after_prefill_per_query_head_reps(hip):
     assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
 
 
+@pytest.mark.parametrize("rep_heads,local_tokens", [(8, 0), (8, 32), (16, 0)])
+def test_bulk_seal_from_partial_state(hip, rep_heads, local_tokens):
+    """The bulk seal (one workgroup per 16 blocks and KV head) from sealed
+    counts part-way through the range, over chunk boundaries (0, 1, 15, 16,
+    17, 33, 100 blocks to seal): representatives, sealed and generation
+    bit-exact against the oracle's tail rule."""
+    lengths = [32 * 100 + 7, 32 * 17, 32 * 16 + 31, 31, 32 * 33, 32 * 61 + 1, 32 * 2]
+    case = make_case(214 + local_tokens + rep_heads, len(lengths), 16, 8, lengths, rep_heads=rep_heads,
+                     local_tokens=local_tokens)
+    start = np.array([0, 0, 1, 0, 3, 44, 1], np.int32)
+    start = np.minimum(start, case.sealed)
+    reps0 = np.random.default_rng(5).standard_normal(case.reps.shape).astype(np.float32)
+    kv = device_kv(case)
+    kv.sealed.copy_(to_dev(start))
+    kv.generation.copy_(to_dev(start * 3))
+    kv.reps.copy_(to_dev(reps0))
+    st = status_tensor()
+    hip.seal(kv, local_tokens, status=st)
+    # oracle: the same start, the tail rule block by block
+    sealed = start.copy()
+    gen = start * 3
+    reps = reps0.copy()
+    O.paged_seal(case.pool, PAGE, case.table, case.seq_len, sealed, gen, reps, rep_heads, case.rep_stride,
+                 case.batch, 16, 8, D, local_tokens)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    assert np.array_equal(kv.sealed.cpu().numpy(), sealed)
+    assert np.array_equal(kv.generation.cpu().numpy(), gen)
+    assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), reps.view(np.uint32))
+
+
+@pytest.mark.parametrize("hole", ["page", "rep_stride"])
+def test_bulk_seal_stops_at_capacity(hip, hole):
+    """A block without a page (table entry -1) or past the representative
+    capacity stops the bulk seal there, as the tail rule stops: the blocks
+    before it are sealed bit-exact, nothing after it is written, the
+    capacity bit is set and the counters stop at the hole."""
+    lengths = np.array([32 * 60, 32 * 40], np.int32)
+    if hole == "page":
+        stop = 37
+        case = make_case(215, 2, 16, 8, lengths)
+        short = lengths.copy()
+        short[0] = stop * PAGE
+    else:
+        # 62 pages per sequence, representative slots for 36 blocks only
+        stop = 36
+        short = np.array([32 * stop, 32 * stop], np.int32)
+        case = make_case(215, 2, 16, 8, short, table_stride=62, rep_stride=stop)
+    table = case.table.copy()
+    if hole == "page":
+        table[0, stop] = -1
+    kv = device_kv(case)
+    kv.block_table.copy_(to_dev(table))
+    kv.seq_len.copy_(to_dev(lengths))
+    kv.sealed.zero_()
+    kv.generation.zero_()
+    kv.reps.zero_()
+    st = status_tensor()
+    hip.seal(kv, 0, status=st)
+    sealed = np.zeros(2, np.int32)
+    gen = np.zeros(2, np.int32)
+    reps = np.zeros_like(case.reps)
+    O.paged_seal(case.pool, PAGE, case.table, short, sealed, gen, reps, 8, case.rep_stride, 2, 16, 8, D, 0)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    assert np.array_equal(kv.sealed.cpu().numpy(), sealed)
+    assert np.array_equal(kv.generation.cpu().numpy(), gen)
+    assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), reps.view(np.uint32))
+
+
 def test_capacity_is_flagged(hip):
     case = make_case(212, 1, 16, 8, [32 * 4 - 1], table_stride=4)
     kv = device_kv(case)
