@@ -110,6 +110,25 @@ __device__ inline float row16_sum(float v) {
   return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave: shifts by 1, 2, 4, 8
+// within each 16-lane row, then row 0's last lane into rows 1 and 3 and lane
+// 31 into rows 2 and 3 (row_bcast).  Lanes whose source lies outside the
+// row, and rows the row mask leaves out, add 0.
+template <int Ctrl, int RowMask>
+__device__ inline uint32_t dpp_or_zero(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), Ctrl, RowMask, 0xF, false));
+}
+
+__device__ inline uint32_t wave_prefix_sum(uint32_t v) {
+  v += dpp_or_zero<0x111, 0xF>(v);  // row_shr:1
+  v += dpp_or_zero<0x112, 0xF>(v);  // row_shr:2
+  v += dpp_or_zero<0x114, 0xF>(v);  // row_shr:4
+  v += dpp_or_zero<0x118, 0xF>(v);  // row_shr:8
+  v += dpp_or_zero<0x142, 0xA>(v);  // row_bcast:15
+  v += dpp_or_zero<0x143, 0xC>(v);  // row_bcast:31
+  return v;
+}
+
 __device__ inline float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }

@@ -148,6 +148,68 @@ __global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params 
   }
 }
 
+// ---- split scoring of a group with several representative rows -----------
+// A selection group whose query heads read several representative rows (the
+// reference's shared mode: one block set over every query head, a row per KV
+// head) spreads the rows over the waves: workgroup (group, sequence, chunk of
+// 64 NB blocks), wave w computes the per-head dots of rows w, w + 8, ... for
+// the chunk (NB blocks per lane, row_dots(): each dot the sequential fp32 sum
+// over d), the dots meet in LDS, and one lane per block adds dot / heads in
+// head order.  The same operations in the same order as score_vec(), so the
+// scores are bit-identical; each lane holds one row's chains instead of every
+// row's, and the launch has rows x more lanes in flight.
+constexpr int kRowWaves = 8;
+constexpr int kRowThreads = kRowWaves * kWave;
+
+template <int GR, int NB, int KB>
+__global__ __launch_bounds__(kRowThreads) void score_rows_kernel(const Params p) {
+  constexpr int kBlocks = kWave * NB;
+  const int sg = blockIdx.x;
+  const int b = blockIdx.y;
+  const int first = blockIdx.z * kBlocks;
+  const int n = p.sealed[b];
+  // invalid lengths are flagged by the selection kernel
+  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks || first >= n) return;
+  __shared__ __align__(16) float q_t[kMaxSelectHeads * D];
+  __shared__ float dots[kMaxSelectHeads][kBlocks + 1];
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  ScoreArgs a{};
+  a.query = p.query;
+  a.reps = p.reps;
+  a.b = b;
+  a.h_first = sg * p.heads_per_sel;
+  a.heads_per_sel = p.heads_per_sel;
+  a.query_heads = p.query_heads;
+  a.group = p.group;
+  a.rep_heads = p.rep_heads;
+  a.rep_stride = p.rep_stride;
+  load_query_t<kRowThreads>(a, q_t);
+  __syncthreads();
+  const int blk0 = first + lane * NB;
+  if (blk0 < n) {
+    // blk0 + NB <= rep_stride: rep_stride is a multiple of NB
+    for (int h0 = wave * GR; h0 < p.heads_per_sel; h0 += kRowWaves * GR) {
+      float dot[GR][NB];
+      row_dots<GR, NB, KB>(a, q_t, blk0, h0, dot);
+#pragma unroll
+      for (int j = 0; j < GR; ++j) {
+#pragma unroll
+        for (int c = 0; c < NB; ++c) dots[h0 + j][lane * NB + c] = dot[j][c];
+      }
+    }
+  }
+  __syncthreads();
+  const float heads_f = static_cast<float>(p.heads_per_sel);
+  float* row = p.scores + (static_cast<int64_t>(b) * p.select_groups + sg) * p.rep_stride;
+  for (int t = tid; t < kBlocks; t += kRowThreads) {
+    if (first + t >= n) break;
+    float score = 0.0f;
+    for (int h = 0; h < p.heads_per_sel; ++h) score = score + dots[h][t] / heads_f;
+    row[first + t] = score;
+  }
+}
+
 // ---- chunked selection: long lists spread over workgroups, one launch -------
 // One workgroup scores kThreads x NB consecutive blocks of a list (NB per
 // lane, 4 NB-byte representative loads, the score_select_kernel arithmetic;
@@ -250,27 +312,32 @@ __global__ __launch_bounds__(kThreads) void score_select_chunked_kernel(const Pa
   if (tid == 0) p.counts[out_row] = count;
 }
 
-template <int kThreads>
-__global__ __launch_bounds__(kThreads) void select_scores_kernel(const Params p) {
-  constexpr int kWaves = kThreads / kWave;
+// The selection of the split form: one workgroup per list, the list's
+// scores held in registers (kRegsKeys contiguous blocks per thread, the
+// workgroup sized by the launch to the representative row, at most 1024
+// threads: 8192 blocks), radix_threshold_regs() and compact_ids_regs().  The
+// same ids as score_select_kernel.
+constexpr int kRegsThreads = 1024;
+constexpr int kRegsKeys = 8;
+static_assert(kRegsThreads * kRegsKeys >= kMaxSelectBlocks, "every selectable block in registers");
+
+template <int kThreads, int NC>
+__global__ __launch_bounds__(kThreads) void select_scores_regs_kernel(const Params p) {
   const int sg = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  __shared__ uint32_t keys[kMaxSelectBlocks];
-  __shared__ SelectSmem<kWaves> sm;
+  __shared__ __align__(16) RegsSelectSmem<kThreads> sm;
   const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
   int32_t* out_ids = p.selected + out_row * p.sel_stride;
+  clear_regs_select<kThreads>(sm);
   const int n = p.sealed[b];
-  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks) {
+  if (n < 0 || n > p.rep_stride || n > static_cast<int>(blockDim.x) * NC) {
     if (tid == 0) {
       flag_status(p.status, kStatusCapacity);
       p.counts[out_row] = 0;
     }
     return;
   }
-  const float* row = p.scores + out_row * p.rep_stride;
-  for (int blk = tid; blk < n; blk += kThreads) keys[blk] = order_key(row[blk]);
-  __syncthreads();
   const Budget bs = budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
   if (bs.bad) {
     if (tid == 0) {
@@ -279,9 +346,30 @@ __global__ __launch_bounds__(kThreads) void select_scores_kernel(const Params p)
     }
     return;
   }
+  const float* row = p.scores + out_row * p.rep_stride;
+  const int base = NC * tid;
+  uint32_t kr[NC];
+  if (base + NC <= n && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+#pragma unroll
+    for (int i = 0; i < NC; i += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(row + base + i);
+      kr[i] = order_key(v.x);
+      kr[i + 1] = order_key(v.y);
+      kr[i + 2] = order_key(v.z);
+      kr[i + 3] = order_key(v.w);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) kr[i] = base + i < n ? order_key(row[base + i]) : 0u;
+  }
+  const bool dynamic = bs.k > 0 && !bs.take_all;
+  bool cand[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) cand[i] = dynamic && base + i >= bs.init_n && base + i < bs.local_first;
+  __syncthreads();  // histograms zeroed
   uint32_t threshold = 0xffffffffu, equal_take = 0;
-  if (bs.k > 0) radix_threshold<kThreads>(keys, bs, sm, threshold, equal_take);
-  const int count = compact_ids<kThreads>(keys, n, bs, threshold, equal_take, out_ids, p.sel_stride, nullptr, sm);
+  if (dynamic) radix_threshold_regs<kThreads, NC>(kr, cand, bs.k, sm, threshold, equal_take);
+  const int count = compact_ids_regs<kThreads, NC>(kr, cand, n, bs, threshold, equal_take, out_ids, p.sel_stride, sm);
   if (tid == 0) p.counts[out_row] = count;
 }
 
@@ -444,21 +532,53 @@ hipError_t launch_score_select_chunked(const SelectLaunch& s, void* workspace, h
   return hipGetLastError();
 }
 
+// Two blocks per lane (8-byte loads) where the layout allows: measured at
+// the long-context shared selection (8 lists x 4096 blocks x 8 rows), two
+// blocks per lane with 8-row load batches 23.1 us, one block per lane with
+// 16-row batches 23.1-23.8 us, four blocks per lane 29 us (half the
+// workgroups), 32- and 64-row batches 24-36 us (fewer resident waves).
+template <int GR>
+void launch_rows(const Params& p, int batch, hipStream_t stream) {
+  if (vec_layout<2>(p.reps, p.rep_stride)) {
+    const dim3 grid(p.select_groups, batch, (p.rep_stride + 2 * kWave - 1) / (2 * kWave));
+    hipLaunchKernelGGL((score_rows_kernel<GR, 2, 8>), grid, dim3(kRowThreads), 0, stream, p);
+  } else {
+    const dim3 grid(p.select_groups, batch, (p.rep_stride + kWave - 1) / kWave);
+    hipLaunchKernelGGL((score_rows_kernel<GR, 1, 16>), grid, dim3(kRowThreads), 0, stream, p);
+  }
+}
+
 hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream) {
   const Params p = make_params(s);
   const int chunks = (s.rep_stride + kChunkBlocks - 1) / kChunkBlocks;
   const dim3 grid(s.select_groups, s.batch, chunks);
   const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
-  switch (gr) {
-    case 1: hipLaunchKernelGGL(score_chunk_kernel<1>, grid, dim3(kChunkBlocks), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL(score_chunk_kernel<2>, grid, dim3(kChunkBlocks), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL(score_chunk_kernel<4>, grid, dim3(kChunkBlocks), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL(score_chunk_kernel<8>, grid, dim3(kChunkBlocks), 0, stream, p); break;
-    default: return hipErrorInvalidValue;
+  // a group over four or more representative rows: a wave per row
+  if (p.heads_per_sel / gr >= kRowWaves / 2) {
+    switch (gr) {
+      case 1: launch_rows<1>(p, s.batch, stream); break;
+      case 2: launch_rows<2>(p, s.batch, stream); break;
+      case 4: launch_rows<4>(p, s.batch, stream); break;
+      case 8: launch_rows<8>(p, s.batch, stream); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (gr) {
+      case 1: hipLaunchKernelGGL(score_chunk_kernel<1>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+      case 2: hipLaunchKernelGGL(score_chunk_kernel<2>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+      case 4: hipLaunchKernelGGL(score_chunk_kernel<4>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+      case 8: hipLaunchKernelGGL(score_chunk_kernel<8>, grid, dim3(kChunkBlocks), 0, stream, p); break;
+      default: return hipErrorInvalidValue;
+    }
   }
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(select_scores_kernel<512>, dim3(s.select_groups, s.batch), dim3(512), 0, stream, p);
+  const hipError_t e0 = hipGetLastError();
+  if (e0 != hipSuccess) return e0;
+  // enough whole waves for every block of the row (the blocks past 8192 are
+  // refused by the kernel)
+  const int keys = s.rep_stride < kMaxSelectBlocks ? s.rep_stride : kMaxSelectBlocks;
+  const int waves = (keys + kRegsKeys * kWave - 1) / (kRegsKeys * kWave);
+  hipLaunchKernelGGL((select_scores_regs_kernel<kRegsThreads, kRegsKeys>), dim3(s.select_groups, s.batch),
+                     dim3(waves * kWave), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -266,19 +266,19 @@ struct RepVec {
   typedef float type __attribute__((ext_vector_type(NB)));
 };
 
-template <int NB>
-__device__ inline void load_vecs(const float* r, int64_t stride, int d0, typename RepVec<NB>::type (&rv)[kVecBatch]) {
+template <int NB, int KB = kVecBatch>
+__device__ inline void load_vecs(const float* r, int64_t stride, int d0, typename RepVec<NB>::type (&rv)[KB]) {
   typedef typename RepVec<NB>::type vec_t;
 #pragma unroll
-  for (int k = 0; k < kVecBatch; ++k)
+  for (int k = 0; k < KB; ++k)
     rv[k] = __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(r + static_cast<int64_t>(d0 + k) * stride));
 }
 
-template <int GR, int NB>
+template <int GR, int NB, int KB = kVecBatch>
 __device__ inline void dot_vecs(const float* q_t, int qoff, int hps, int h0, int d0,
-                                const typename RepVec<NB>::type (&rv)[kVecBatch], float (&dot)[GR][NB]) {
+                                const typename RepVec<NB>::type (&rv)[KB], float (&dot)[GR][NB]) {
 #pragma unroll
-  for (int k = 0; k < kVecBatch; ++k) {
+  for (int k = 0; k < KB; ++k) {
     float qv[GR];
     read_q_t<GR>(q_t + qoff + (d0 + k) * hps + h0, qv);
 #pragma unroll
@@ -328,6 +328,42 @@ __device__ inline void score_vec(const ScoreArgs& a, const float* q_t, int blk0,
 #pragma unroll
       for (int c = 0; c < NB; ++c) score[c] = score[c] + dot[j][c] / heads_f;
     }
+  }
+}
+
+// The GR per-head dots of one representative row (the row of query heads
+// h_first + h0 .. + GR - 1 within the group) for blocks blk0 .. blk0 + NB - 1:
+// the inner loop of score_vec() for one h0, the same operations in the same
+// order, so that summing dot[j][c] / heads in head order gives score_vec()'s
+// scores bit for bit.
+// KB rows per load batch, two batches in flight: the batches follow each
+// other on the lane's own latency, so deep batches keep the chain short.
+template <int GR, int NB, int KB>
+__device__ inline void row_dots(const ScoreArgs& a, const float* q_t, int blk0, int h0, float (&dot)[GR][NB]) {
+  static_assert(D % (2 * KB) == 0, "whole double batches per representative row");
+  typedef typename RepVec<NB>::type vec_t;
+  int qoff = 0;
+  asm volatile("" : "+s"(qoff));
+  int hps = a.heads_per_sel;
+  asm volatile("" : "+s"(hps));
+  int64_t stride = a.rep_stride;
+  asm volatile("" : "+s"(stride));
+  const int h = a.h_first + h0;
+  const int rh = a.rep_heads == a.query_heads ? h : h / a.group;
+  const float* r = a.reps + (static_cast<int64_t>(a.b) * a.rep_heads + rh) * D * stride + blk0;
+#pragma unroll
+  for (int j = 0; j < GR; ++j) {
+#pragma unroll
+    for (int c = 0; c < NB; ++c) dot[j][c] = 0.0f;
+  }
+  vec_t ra[KB], rb[KB];
+  load_vecs<NB, KB>(r, stride, 0, ra);
+#pragma unroll
+  for (int d0 = 0; d0 < D; d0 += 2 * KB) {
+    load_vecs<NB, KB>(r, stride, d0 + KB, rb);
+    dot_vecs<GR, NB, KB>(q_t, qoff, hps, h0, d0, ra, dot);
+    if (d0 + 2 * KB < D) load_vecs<NB, KB>(r, stride, d0 + 2 * KB, ra);
+    dot_vecs<GR, NB, KB>(q_t, qoff, hps, h0, d0 + KB, rb, dot);
   }
 }
 
@@ -730,6 +766,136 @@ __device__ inline int select_ids_wave_regs(const uint32_t* keys, int n, const Bu
     written += __popcll(m_take);
   }
   return written < sel_stride ? written : sel_stride;
+}
+
+// ---- workgroup selection with the keys in registers (n <= kThreads NC) -------
+// For one list per workgroup with the workgroup to itself (the split
+// selection's second launch), of any whole number of waves up to kThreads
+// (blockDim.x).  Thread t holds the keys of blocks NC t .. NC t + NC - 1
+// (contiguous, so that the ascending compaction is one scan).
+//
+// Threshold: the same 4 passes of 8 bits as radix_threshold(), with the
+// histogram of each pass spread over kRadixCopies copies (lane l adds into
+// copy l % 16, copies 4 banks apart): scores from a narrow range share their
+// top digits, and 64 lanes adding into one LDS word serialise.  Each pass has
+// its own histogram set (zeroed once), so a pass costs two barriers; wave 0
+// sums the copies and scans the digits.
+constexpr int kRadixCopies = 16;
+constexpr int kRadixPad = 260;  // words per copy: 256 bins, 16-byte rows, 4 banks apart
+
+template <int kThreads>
+struct RegsSelectSmem {
+  uint32_t hist[4][kRadixCopies * kRadixPad];
+  uint32_t prefix[4];
+  uint32_t remaining[4];
+  uint32_t wave_sum[kThreads / kWave];
+};
+
+template <int kThreads>
+__device__ inline void clear_regs_select(RegsSelectSmem<kThreads>& sm) {
+  uint4* h = reinterpret_cast<uint4*>(&sm.hist[0][0]);
+  for (int e = threadIdx.x; e < 4 * kRadixCopies * kRadixPad / 4; e += blockDim.x) h[e] = make_uint4(0, 0, 0, 0);
+}
+
+// k-th largest key among the candidates (cand[i]) and how many keys equal
+// to it are taken; k > 0.  clear_regs_select() and a barrier must precede.
+template <int kThreads, int NC>
+__device__ inline void radix_threshold_regs(const uint32_t (&kr)[NC], const bool (&cand)[NC], int k,
+                                            RegsSelectSmem<kThreads>& sm, uint32_t& threshold,
+                                            uint32_t& equal_take) {
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  uint32_t prefix = 0, mask = 0, remaining = static_cast<uint32_t>(k);
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    uint32_t* h = sm.hist[pass] + (lane % kRadixCopies) * kRadixPad;
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      if (cand[i] && (kr[i] & mask) == prefix) atomicAdd(&h[(kr[i] >> shift) & 255u], 1u);
+    __syncthreads();
+    if (tid < kWave) {
+      // lane covers digits 255-4*lane .. 252-4*lane (descending)
+      uint32_t c[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int cp = 0; cp < kRadixCopies; ++cp) {
+        const uint4 v = *reinterpret_cast<const uint4*>(sm.hist[pass] + cp * kRadixPad + 252 - 4 * lane);
+        c[3] += v.x;
+        c[2] += v.y;
+        c[1] += v.z;
+        c[0] += v.w;
+      }
+      const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+      uint32_t before = wave_prefix_sum(mine) - mine;  // candidates in higher digits
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (before < remaining && before + c[q] >= remaining) {
+          sm.prefix[pass] = prefix | (static_cast<uint32_t>(255 - 4 * lane - q) << shift);
+          sm.remaining[pass] = remaining - before;
+        }
+        before += c[q];
+      }
+    }
+    __syncthreads();
+    prefix = sm.prefix[pass];
+    remaining = sm.remaining[pass];
+    mask |= 255u << shift;
+  }
+  threshold = prefix;
+  equal_take = remaining;
+}
+
+// Ascending compaction of the selected ids of blocks [0, n) (thread t holds
+// blocks NC t ..): forced blocks, candidates above the threshold, and the
+// lowest-id candidates equal to it up to equal_take.  One scan of the
+// per-thread (sure, equal) counts.  Returns the count (clamped to
+// sel_stride).
+template <int kThreads, int NC>
+__device__ inline int compact_ids_regs(const uint32_t (&kr)[NC], const bool (&cand)[NC], int n, const Budget& bs,
+                                       uint32_t threshold, uint32_t equal_take, int32_t* out_ids, int sel_stride,
+                                       RegsSelectSmem<kThreads>& sm) {
+  const int waves = static_cast<int>(blockDim.x) / kWave;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int base = NC * tid;
+  bool sure[NC], eq[NC];
+  uint32_t sure_c = 0, eq_c = 0;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int blk = base + i;
+    const bool forced = blk < n && (bs.take_all || blk < bs.init_n || blk >= bs.local_first);
+    eq[i] = cand[i] && kr[i] == threshold;
+    sure[i] = forced || (cand[i] && kr[i] > threshold);
+    sure_c += sure[i];
+    eq_c += eq[i];
+  }
+  // (sure, equal) counts packed in 16-bit halves: each at most 8192
+  const uint32_t packed = (sure_c << 16) | eq_c;
+  const uint32_t incl = wave_prefix_sum(packed);
+  if (lane == kWave - 1) sm.wave_sum[wave] = incl;
+  __syncthreads();
+  uint32_t before = incl - packed, total = 0;
+  for (int w = 0; w < waves; ++w) {
+    const uint32_t s = sm.wave_sum[w];
+    if (w < wave) before += s;
+    total += s;
+  }
+  const int take_eq = static_cast<int>(equal_take);
+  int eq_seen = static_cast<int>(before & 0xffffu);
+  int pos = static_cast<int>(before >> 16) + (eq_seen < take_eq ? eq_seen : take_eq);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    bool take = sure[i];
+    if (eq[i]) take = eq_seen++ < take_eq;
+    if (take) {
+      if (pos < sel_stride) out_ids[pos] = base + i;
+      ++pos;
+    }
+  }
+  const int tot_eq = static_cast<int>(total & 0xffffu);
+  const int count = static_cast<int>(total >> 16) + (tot_eq < take_eq ? tot_eq : take_eq);
+  return count < sel_stride ? count : sel_stride;
 }
 
 // Single-wave selection of one list: forced blocks plus the k best

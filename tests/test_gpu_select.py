@@ -234,3 +234,22 @@ def test_selection_at_the_8192_block_limit(hip, split):
     torch.cuda.synchronize()
     assert int(st.item()) & hip.STATUS_CAPACITY
     assert (res[1].cpu().numpy() == 0).all()
+
+
+@pytest.mark.parametrize("lengths", [[32 * 4096, 32 * 4095 + 7], [32 * 64, 32 * 65 + 1, 32 * 1]])
+def test_shared_selection_long_context_rows(hip, lengths):
+    """The reference's shared mode at the long-context shape (32 query heads
+    over 8 representative rows, 4096 blocks, budget 128 = 4 + 8 + 116) and
+    at lengths around one 64-block chunk: the split scoring spreads the rows
+    over waves; ids and score bits equal the oracle's."""
+    case = make_case(135, len(lengths), 32, 8, lengths, planted=16)
+    check(hip, case, 1, 128, 4, 8, modes=("single", "split"))
+
+
+@pytest.mark.parametrize("group", [4, 8])
+def test_group_selection_per_query_head_reps_rows(hip, group):
+    """Per-KV-group selection over per-query-head representatives (the
+    online seal's layout): each group reads `group` rows, which the split
+    scoring spreads over waves."""
+    case = make_case(136 + group, 3, group * 4, 4, [32 * 700 + 3, 32 * 129, 32 * 2], rep_heads=group * 4)
+    check(hip, case, 4, 32, 2, 4)
