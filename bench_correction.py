@@ -1,336 +1,66 @@
 """Long-context miss-correction workload (bench.py --workload correction).
 
-Qwen3-8B attention shape (32 query / 8 KV heads, head_dim 128), batch 8,
-context 131072 tokens (4096 blocks per sequence), budget 128 blocks
-(4 init + 8 local + 116 dynamic), one block set per sequence (the
-reference's shared selection, selection_main.cpp:178-181).  The whole KV of a
-layer (4 GiB) lives in pinned host memory, standing in for the SSD tier's
-registered buffers; HBM holds every block representative plus 130 page slots
-per sequence (128 selected blocks + the tail).  Queries drift as a random
-walk calibrated so that the previous step's selection covers ~75% of the
-next one (the reference's history prediction, pipeline_main.cpp:760-850).
+Runs the self-checking C++ driver tests/cpp/correction_check (built by
+__graft_entry__.build()), whose per-layer loop is the reference's P1
+history-correction loop (cpp/src/pipeline_main.cpp:752-924) over the C++ API
+of include/solidattention/hip_kv.hpp: Qwen3-8B attention shape, batch 8,
+131072 tokens (4096 blocks per sequence), budget 128 blocks (4 init + 8 local
++ 116 dynamic), one block set per sequence (the reference's shared
+selection), the layer's whole KV in pinned host memory and 130 page slots
+per sequence in HBM.  Each KV head has 16 planted blocks (4 runs of 4) that
+move one block position per step, so the previous step's selection covers
+99 / 128 = 0.7734 of the next one by construction.
 
-Per step and layer:
-  1. append + seal (the new token lands in the resident tail page);
-  2. GPU score + select;
-  3. ids to the host; compare_prediction against the resident set
-     (pipeline_main.cpp:686-717) gives misses and replacement slots;
-  4. the block table is updated; misses are copied from pinned memory into
-     the replaced slots with hipMemcpyAsync on a copy stream;
-  5. overlapped schedule: the compute stream attends the hit blocks (and
-     tail) while the copies run, waits on the copy event on the device,
-     attends the misses, and merges (split-phase attention);
-     serial schedule (the reference's correct_and_wait): host barrier on the
-     copies, then one attention over the selection.
-Fills are either one hipMemcpyAsync per page or one kernel reading the pinned
-store through its device mapping.  Reported per layer: the device critical
-path from the first fill issued to the attention output (copy-stream and
-compute-stream events on one clock), the fill bandwidth, and the host wall
-time of this Python driver (dominated by its own bookkeeping).
-Acceptance, after the timed steps (the reference's serial-vs-pipelined check,
-pipeline_main.cpp:1090-1123, and its corrected-set check, :704-715): for
-`accept_steps` more steps every layer runs the overlapped schedule and, on the
-same resident state, the serial one (one attention over the whole selection);
-the two outputs agree within 2e-3 (the merge order differs, so not bit for
-bit).  Then, for every sequence of every layer: the selection equals the
-oracle's (bit-exact ids), the resident set equals the selection, every slot's
-bytes equal its host-store block, and the attention matches the oracle on the
-resident pages within 2e-3.  run() returns the result line; any failed check
-raises SystemExit (a non-zero exit status) after the line is printed.
+Four schedules run on the same recorded steps (each replayed from the same
+state, so each sees the same misses): serial (the reference's host barrier
+on the fills, then one attention), serial_split (host barrier, then the
+split arithmetic: hits, misses, merge), overlapped (hits attended while the
+copy stream fills the misses, device-side wait, misses, merge) with one
+hipMemcpyAsync per page, and overlapped_gather (the fills as one kernel over
+the pinned store's device mapping).  Reported per layer: the host wall time
+of the whole loop (host leg included), the host leg alone (compare_prediction,
+table and list updates), the selection, the device critical path and the
+fill bandwidth.  The driver's checks (exit status 2 on a failure): the same
+misses in every schedule, the closed-form planted selection at every step,
+overlapped == serial_split bit for bit (the reference's exact bar,
+pipeline_main.cpp:1123), serial within 2e-3 of serial_split, and against the
+oracle after the last step: selection ids, resident set, slot bytes and
+attention (2e-3).
 """
 from __future__ import annotations
 
 import json
+import os
+import subprocess
 import sys
-import time
 
-PAGE = 32
-D = 128
+ROOT = os.path.dirname(os.path.abspath(__file__))
+EXE = os.path.join(ROOT, "tests", "cpp", "correction_check")
 
 
 def log(msg):
     print(f"[correction] {msg}", file=sys.stderr, flush=True)
 
 
-def run(args):
-    import numpy as np
-    import torch
-
-    import solidattention_amd as sa
-
-    B, HQ, HKV, CTX = 8, 32, 8, 131072
-    BUDGET, INIT, LOCAL = 128, 4, 8
-    NBLK = CTX // PAGE                     # 4096 sealed blocks
-    TS = NBLK + 2                          # logical blocks incl. the tail page(s)
-    SLOTS = BUDGET + 2                     # resident pages per sequence
-    EPS = 0.36                             # query random-walk step (~75% coverage)
-    layers = args.layers or 2
-    steps, warmup = args.steps, args.warmup
-    accept_steps = max(1, int(getattr(args, "accept_steps", 2) or 2))
-    total_steps = warmup + 3 * steps + accept_steps + 1
-    assert total_steps < PAGE, "the tail page must not seal during the run"
-    torch.cuda.set_device(0)
-    dev = torch.device("cuda")
-    page_elems = PAGE * 2 * HKV * D
-    page_bytes = page_elems * 2
-    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
-    compute = torch.cuda.current_stream()
-    copy_stream = torch.cuda.Stream()
-    status = torch.zeros(1, dtype=torch.int32, device=dev)
-    TOTAL_SPLITS = 4  # 2 for the hit phase, 2 for the miss phase
-
-    Ls = []
-    t0 = time.time()
-    for layer in range(layers):
-        seed = args.seed + 104729 * layer
-        # full KV on the device once, to fill the host store and compute every representative
-        full = sa.PagedKV(B, HQ, HKV, TS, num_pages=B * TS)
-        full.block_table.copy_(torch.arange(B * TS, dtype=torch.int32, device=dev).view(B, TS))
-        sa.fill_synthetic_f16(full.pool.view(-1), seed, 0)
-        full.seq_len.fill_(CTX)
-        sa.seal(full, 0, status=status)
-        store = torch.empty((B * TS, page_elems), dtype=torch.int16, pin_memory=True)
-        store.copy_(full.pool.view(torch.int16).view(B * TS, page_elems))
-        torch.cuda.synchronize()
-        # resident slot pool: pages b*SLOTS + slot; slot BUDGET is the tail page
-        kv = sa.PagedKV(B, HQ, HKV, TS, num_pages=B * SLOTS, rep_stride=full.rep_stride)
-        kv.reps = full.reps
-        kv.seq_len.fill_(CTX)
-        kv.sealed.fill_(NBLK)
-        table = np.full((B, TS), -1, np.int32)
-        table[:, NBLK] = np.arange(B, dtype=np.int32) * SLOTS + BUDGET
-        tail_rows = torch.stack([full.pool.view(torch.int16).view(B * TS, page_elems)[b * TS + NBLK] for b in range(B)])
-        kv.pool.view(torch.int16).view(B * SLOTS, page_elems)[torch.arange(B, device=dev) * SLOTS + BUDGET] = tail_rows
-        del full
-        q0 = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
-        sa.fill_synthetic_f32(q0.view(-1), seed + 1, 0)
-        noise = torch.empty((total_steps, B, HQ, D), dtype=torch.float32, device=dev)
-        sa.fill_synthetic_f32(noise.view(-1), seed + 2, 0)
-        q = q0.unsqueeze(0) + EPS * torch.cumsum(noise, dim=0)
-        knew = torch.empty((total_steps, B, HKV, D), dtype=torch.float32, device=dev)
-        vnew = torch.empty_like(knew)
-        sa.fill_synthetic_f32(knew.view(-1), seed + 3, 0)
-        sa.fill_synthetic_f32(vnew.view(-1), seed + 4, 0)
-        sel = torch.full((B, 1, BUDGET), -1, dtype=torch.int32, device=dev)
-        cnt = torch.zeros((B, 1), dtype=torch.int32, device=dev)
-        # initial residency: the selection of q0, copied in full
-        sa.score_select(kv, q0, 1, BUDGET, INIT, LOCAL, selected=sel, counts=cnt, status=status)
-        ids = sel.cpu().numpy()[:, 0, :]
-        resident = [ids[b].tolist() for b in range(B)]
-        for b in range(B):
-            for slot, blk in enumerate(resident[b]):
-                table[b, blk] = b * SLOTS + slot
-        kv.block_table.copy_(torch.from_numpy(table))
-        for b in range(B):
-            kv.pool.view(torch.int16).view(B * SLOTS, page_elems)[b * SLOTS: b * SLOTS + BUDGET] = \
-                store[torch.tensor([b * TS + x for x in resident[b]])].to(dev)
-        ly = dict(kv=kv, store=store, q=q, knew=knew, vnew=vnew, sel=sel, cnt=cnt, table=table, resident=resident)
-        ly["hit"] = torch.full((B, 1, BUDGET), -1, dtype=torch.int32, device=dev)
-        ly["miss"] = torch.full((B, 1, BUDGET), -1, dtype=torch.int32, device=dev)
-        ly["hitc"] = torch.zeros((B, 1), dtype=torch.int32, device=dev)
-        ly["missc"] = torch.zeros((B, 1), dtype=torch.int32, device=dev)
-        ly["ws"] = torch.zeros(sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, TOTAL_SPLITS) // 4,
-                               dtype=torch.float32, device=dev)
-        ly["out"] = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
-        ly["out_serial"] = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
-        ly["ws_serial"] = torch.zeros(sa.lib().sa_hip_attention_workspace_bytes(B, HQ, HKV, D, 2) // 4,
-                                      dtype=torch.float32, device=dev)
-        ly["scores"] = torch.zeros((B, 1, kv.rep_stride), dtype=torch.float32, device=dev)
-        ly["done"] = torch.cuda.Event()
-        ly["done"].record(copy_stream)
-        Ls.append(ly)
-    torch.cuda.synchronize()
-    log(f"setup {time.time() - t0:.1f}s: {layers} layers, host store {layers * B * TS * page_bytes / 2**30:.1f} GiB pinned")
-
-    # 8 lists (one shared selection per sequence): the split scoring form
-    split_select = sa.score_select_split_preferred(Ls[0]["kv"], 1, BUDGET, INIT, LOCAL)
-    select_events = []
-    host_tables = [torch.from_numpy(ly["table"]).pin_memory() for ly in Ls]
-    host_fill = [torch.zeros((2, B * BUDGET), dtype=torch.int64).pin_memory() for _ in Ls]
-    for ly in Ls:
-        ly["fill_lists"] = torch.zeros((2, B * BUDGET), dtype=torch.int64, device=dev)
-        ly["dst32"] = torch.zeros(B * BUDGET, dtype=torch.int32, device=dev)
-    host_lists = [torch.zeros((4, B, BUDGET), dtype=torch.int32).pin_memory() for _ in Ls]
-    host_counts = [torch.zeros((2, B), dtype=torch.int32).pin_memory() for _ in Ls]
-    miss_total = [0]
-    sel_total = [0]
-    copy_events = []
-    crit_events = []  # (first copy issued, attention output ready) per layer step
-
-    serial_err = []  # per acceptance layer step: max |overlapped - serial|, and whether within 2e-3
-
-    def step(s, mode, fill, accept=False):
-        for li, ly in enumerate(Ls):
-            kv = ly["kv"]
-            sa.append_seal(kv, ly["knew"][s], ly["vnew"][s], 0, status=status)
-            e_s0, e_s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e_s0.record(compute)
-            if split_select:
-                sa.score_select_split(kv, ly["q"][s], 1, BUDGET, INIT, LOCAL, selected=ly["sel"], counts=ly["cnt"],
-                                      scores=ly["scores"], status=status)
-            else:
-                sa.score_select(kv, ly["q"][s], 1, BUDGET, INIT, LOCAL, selected=ly["sel"], counts=ly["cnt"],
-                                status=status)
-            e_s1.record(compute)
-            select_events.append((e_s0, e_s1))
-            ids = ly["sel"].cpu().numpy()[:, 0, :]  # synchronises the compute stream
-            table = ly["table"]
-            hl = host_lists[li].numpy()
-            hc = host_counts[li].numpy()
-            dst_pages, src_blocks = [], []
-            for b in range(B):
-                cur = ids[b].tolist()
-                hits, misses, slots = sa.compare_prediction(ly["resident"][b], cur)
-                miss_total[0] += len(misses)
-                sel_total[0] += len(cur)
-                for slot, blk in zip(slots, misses):
-                    table[b, ly["resident"][b][slot]] = -1
-                    table[b, blk] = b * SLOTS + slot
-                    ly["resident"][b][slot] = blk
-                    dst_pages.append(b * SLOTS + slot)
-                    src_blocks.append(b * TS + blk)
-                hit_ids = sorted(set(cur) - set(misses))
-                hl[0, b, : len(hit_ids)] = hit_ids
-                hl[1, b, : len(misses)] = sorted(misses)
-                hc[0, b], hc[1, b] = len(hit_ids), len(misses)
-            assert np.all(table[table >= 0] < B * SLOTS)
-            host_tables[li].copy_(torch.from_numpy(table))
-            kv.block_table.copy_(host_tables[li], non_blocking=True)
-            ly["hit"][:, 0, :].copy_(host_lists[li][0], non_blocking=True)
-            ly["miss"][:, 0, :].copy_(host_lists[li][1], non_blocking=True)
-            ly["hitc"][:, 0].copy_(host_counts[li][0], non_blocking=True)
-            ly["missc"][:, 0].copy_(host_counts[li][1], non_blocking=True)
-            # the replaced slots were last read by the previous step, which
-            # has completed; the hit phase reads other slots, so the copies
-            # start at once
-            c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            if fill == "gather":
-                # the fill kernel reads its page lists from device memory,
-                # uploaded on the copy stream itself
-                hd = host_fill[li]
-                hd[0, : len(dst_pages)] = torch.tensor(dst_pages, dtype=torch.int64)
-                hd[1, : len(src_blocks)] = torch.tensor(src_blocks, dtype=torch.int64)
-                with torch.cuda.stream(copy_stream):
-                    ly["fill_lists"].copy_(hd, non_blocking=True)
-                    ly["dst32"].copy_(ly["fill_lists"][0].to(torch.int32))
-            c0.record(copy_stream)
-            if fill == "gather":
-                sa.fill_pages_gather_async(kv.pool, page_bytes, kv.num_pages, ly["dst32"], ly["store"].data_ptr(),
-                                           B * TS, ly["fill_lists"][1], len(dst_pages), copy_stream, ly["done"],
-                                           status=status)
-            else:
-                sa.fill_pages_async(kv.pool, page_bytes, dst_pages, ly["store"].data_ptr(), src_blocks, copy_stream,
-                                    ly["done"])
-            c1.record(copy_stream)
-            copy_events.append((c0, c1, len(dst_pages)))
-            if mode == "overlapped":
-                sa.sparse_decode_attention_partial(kv, ly["q"][s], ly["hit"], ly["hitc"], scale, True, ly["ws"], 0, 2,
-                                                   TOTAL_SPLITS, status=status)
-                sa.stream_wait_event(compute, ly["done"])
-                sa.sparse_decode_attention_partial(kv, ly["q"][s], ly["miss"], ly["missc"], scale, False, ly["ws"], 2,
-                                                   2, TOTAL_SPLITS, status=status)
-                sa.attention_merge(kv, ly["ws"], TOTAL_SPLITS, ly["out"])
-                if accept:
-                    # the serial schedule's attention on the same resident state
-                    sa.sparse_decode_attention(kv, ly["q"][s], ly["sel"], ly["cnt"], scale, out=ly["out_serial"],
-                                               splits=2, workspace=ly["ws_serial"], status=status)
-            else:
-                copy_stream.synchronize()  # the reference's host barrier (pipeline_main.cpp:322-323)
-                sa.sparse_decode_attention(kv, ly["q"][s], ly["sel"], ly["cnt"], scale, out=ly["out"], splits=2,
-                                           workspace=ly["ws"], status=status)
-            e_end = torch.cuda.Event(enable_timing=True)
-            e_end.record(compute)
-            crit_events.append((c0, e_end))
-            if accept:
-                a = ly["out"].double()
-                b_ = ly["out_serial"].double()
-                err = (a - b_).abs()
-                ok = bool(((err <= 2e-3) | (err <= 2e-3 * b_.abs())).all().item())
-                serial_err.append((float(err.max().item()), ok))
-        torch.cuda.synchronize()
-
-    for s in range(warmup):
-        step(s, "overlapped", "gather")
-    miss_total[0] = sel_total[0] = 0
-    copy_events.clear()
-    results = {}
-    s = warmup
-    schedules = (("serial", "memcpy"), ("overlapped", "memcpy"), ("overlapped", "gather"))
-    for mode, fill in schedules:
-        m0, t_all = miss_total[0], 0.0
-        n_copy_ms, n_copy_pages = 0.0, 0
-        ev0 = len(copy_events)
-        cr0 = len(crit_events)
-        for _ in range(steps):
-            t = time.perf_counter()
-            step(s, mode, fill)
-            t_all += time.perf_counter() - t
-            s += 1
-        for c0, c1, n in copy_events[ev0:]:
-            n_copy_ms += c0.elapsed_time(c1)
-            n_copy_pages += n
-        crit_ms = sum(a.elapsed_time(b) for a, b in crit_events[cr0:])
-        results[f"{mode}_{fill}"] = {"device_critical_us_per_layer": round(crit_ms * 1000 / steps / layers, 1),
-                                     "host_wall_us_per_layer": round(t_all / steps / layers * 1e6, 1),
-                         "misses_per_layer": round((miss_total[0] - m0) / steps / layers, 1),
-                         "h2d_gbps": round(n_copy_pages * page_bytes / max(n_copy_ms, 1e-9) / 1e6, 1),
-                         "h2d_us_per_layer": round(n_copy_ms * 1000 / steps / layers, 1)}
-    for _ in range(accept_steps):
-        step(s, "overlapped", "gather", accept=True)
-        s += 1
-    if int(status.item()) != 0:
-        raise SystemExit(f"device status flagged {int(status.item())}")
-    coverage = 1.0 - miss_total[0] / max(sel_total[0], 1)
-
-    # checks on every sequence of every layer after the last step
-    import oracle as O
-    sets_ok = bytes_ok = sel_ok = att_ok = True
-    att_err = 0.0
-    for ly in Ls:
-        kv = ly["kv"]
-        ids = ly["sel"].cpu().numpy()[:, 0, :]
-        sets_ok &= all(sorted(ly["resident"][b]) == ids[b].tolist() for b in range(B))
-        pool = kv.pool.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B * SLOTS, page_elems)
-        store = ly["store"].numpy().view(np.uint16)
-        bytes_ok &= all(np.array_equal(pool[b * SLOTS + slot], store[b * TS + blk])
-                        for b in range(B) for slot, blk in enumerate(ly["resident"][b]))
-        table = kv.block_table.cpu().numpy()
-        seq_len = kv.seq_len.cpu().numpy()
-        sealed = kv.sealed.cpu().numpy()
-        cnt = ly["cnt"].cpu().numpy()
-        sel = ly["sel"].cpu().numpy()
-        qh = ly["q"][s - 1].cpu().numpy()
-        # the selection of the last step against the oracle's (bit-exact ids)
-        esel, ecnt = O.paged_score_select(qh, kv.reps.cpu().numpy(), sealed, B, HQ, HKV, D, kv.rep_heads,
-                                          kv.rep_stride, 1, BUDGET, INIT, LOCAL)
-        sel_ok &= bool(np.array_equal(cnt, ecnt)) and all(
-            sel[b, 0, : ecnt[b, 0]].tolist() == esel[b, 0, : ecnt[b, 0]].tolist() for b in range(B))
-        expect = O.paged_sparse_attention(pool.reshape(-1), PAGE, table, seq_len, sealed, sel, cnt, 1, qh, B, HQ, HKV,
-                                          D, scale)
-        got = ly["out"].cpu().numpy()
-        err = np.abs(got.astype(np.float64) - expect)
-        att_ok &= bool(((err <= 2e-3) | (err <= 2e-3 * np.abs(expect))).all())
-        att_err = max(att_err, float(err.max()))
-    checks = {"sequences": B * layers,
-              "selection_equals_oracle": bool(sel_ok),
-              "resident_set_equals_selection": bool(sets_ok), "slot_bytes_equal_store": bool(bytes_ok),
-              "attention_within_2e-3": bool(att_ok), "attention_max_abs_err": att_err,
-              "serial_equals_pipelined_within_2e-3": all(ok for _, ok in serial_err),
-              "serial_pipelined_max_abs_err": max(e for e, _ in serial_err),
-              "accept_layer_steps": len(serial_err)}
-    line = {
-        "workload": "long-context miss correction, Qwen3-8B shape, B=8, 131072 tokens, budget 128 blocks",
-        "layers": layers, "steps": steps, "warmup": warmup,
-        "history_coverage": round(coverage, 4),
-        "selection": {"form": "split" if split_select else "single",
-                      "us_per_layer": round(1000.0 * float(np.mean([a.elapsed_time(b) for a, b in select_events])),
-                                            1)},
-        "schedules": results,
-        "page_bytes": page_bytes,
-        "checks": checks,
-    }
+def run(args, batch=None, context=None, timeout=1100):
+    """Run the driver; returns its JSON line (printed on stdout).  Raises
+    SystemExit on a failed check or an error, after printing the line."""
+    if not os.path.exists(EXE):
+        raise SystemExit("tests/cpp/correction_check is not built: run __graft_entry__.build()")
+    cmd = [EXE, "--layers", str(args.layers or 2), "--steps", str(args.steps), "--warmup", str(args.warmup),
+           "--seed", str(args.seed)]
+    if batch:
+        cmd += ["--batch", str(batch)]
+    if context:
+        cmd += ["--context", str(context)]
+    log(" ".join(cmd[1:]))
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=sys.stderr, text=True, timeout=timeout)
+    lines = [x for x in r.stdout.splitlines() if x.startswith("{")]
+    if not lines:
+        raise SystemExit(f"correction_check printed no result (exit {r.returncode})")
+    line = json.loads(lines[-1])
     print(json.dumps(line), flush=True)
-    failed = [k for k, v in checks.items() if v is False]
-    if failed:
-        raise SystemExit(f"correction workload checks failed: {failed}")
+    if r.returncode != 0:
+        failed = [k for k, v in line.get("checks", {}).items() if v is False]
+        raise SystemExit(f"correction_check exit {r.returncode}; failed checks: {failed}")
     return line

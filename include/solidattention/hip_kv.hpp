@@ -18,6 +18,9 @@
 //                              fused kernel applies
 //   MissCorrector              CudaPipeline::correct_and_wait without the
 //                              host barrier (pipeline_main.cpp:305-331)
+//   SplitAttention             attention of the resident blocks while the
+//                              misses are copied, then of the misses, merged
+//                              (the overlap of pipeline_main.cpp:811-848)
 //   compare_prediction         pipeline_main.cpp:686-717
 // Errors are std::runtime_error("operation: message"), as the reference's
 // cuda_check does (cuda_backend.cpp:16-21).
@@ -339,8 +342,22 @@ class MissCorrector {
                                   src_blocks.data(), static_cast<int32_t>(dst_pages.size()), copy_, done_),
           "fill_pages_async");
   }
+  // The same fills as one kernel on the copy stream reading the pinned
+  // store through its device mapping (pinned_src from hipHostMalloc, holding
+  // src_total pages); dst_pages_dev / src_blocks_dev are device arrays,
+  // e.g. uploaded on copy_stream() just before.
+  void fill_gather(std::uint16_t* pool, std::size_t page_bytes, int64_t num_pages, const int32_t* dst_pages_dev,
+                   const void* pinned_src, int64_t src_total, const int64_t* src_blocks_dev, int32_t count,
+                   int32_t* status = nullptr) {
+    check(sa_hip_fill_pages_gather_async(pool, static_cast<int64_t>(page_bytes), num_pages, dst_pages_dev,
+                                         pinned_src, src_total, src_blocks_dev, count, status, copy_, done_),
+          "fill_pages_gather_async");
+  }
   // Make `compute` wait (on the device) for the last fill.
   void order(hipStream_t compute) { check(sa_hip_stream_wait_event(compute, done_), "stream_wait_event"); }
+  // Host barrier on the fills (the reference's correct_and_wait,
+  // pipeline_main.cpp:322-323).
+  void wait() { hip_check(hipStreamSynchronize(copy_), "hipStreamSynchronize copy"); }
   // Make the next fills wait for the work queued so far on `s` (earlier
   // writers or readers of the destination pages, e.g. a prefetch the compute
   // stream was ordered after).
@@ -355,6 +372,44 @@ class MissCorrector {
   hipStream_t copy_{};
   hipEvent_t done_{};
   hipEvent_t after_{};
+};
+
+// Split-phase attention over several id lists of one step (for example the
+// blocks already resident, then the blocks a copy stream fills meanwhile),
+// merged with log-sum-exp into one output: the same result as one
+// SparseDecoder::attend over the union, within fp32 rounding.  Each partial
+// call writes `splits` records from split_base of total_splits; the tail is
+// included by exactly one call.  Calls sharing the object must not run
+// concurrently.
+class SplitAttention {
+ public:
+  SplitAttention(const PagedKvPool& pool, int total_splits)
+      : total_(total_splits),
+        bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),
+                                                static_cast<int32_t>(pool.query_heads()),
+                                                static_cast<int32_t>(pool.kv_heads()), 128, total_splits)),
+        workspace_((bytes_ + 3) / 4) {
+    if (total_splits < 2) throw std::runtime_error("SplitAttention: total_splits must be >= 2");
+  }
+  void partial(const PagedKvPool& pool, const float* query, const int32_t* ids, const int32_t* counts,
+               int select_groups, int sel_stride, float scale, bool include_tail, int split_base, int splits,
+               hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_sparse_decode_attention_partial(&kv, query, ids, counts, select_groups, sel_stride, scale,
+                                                 include_tail ? 1 : 0, workspace_.get(), bytes_, split_base, splits,
+                                                 total_, status, stream),
+          "sparse_decode_attention_partial");
+  }
+  // out [batch][query_heads][128] fp32 (device).
+  void merge(const PagedKvPool& pool, float* out, hipStream_t stream = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_attention_merge(&kv, workspace_.get(), bytes_, total_, out, stream), "attention_merge");
+  }
+
+ private:
+  int total_;
+  std::size_t bytes_;
+  DeviceArray<float> workspace_;
 };
 
 }  // namespace solidattention::hip
