@@ -41,6 +41,12 @@ CONFIGS = {
     "qwen3-0.6b-b64-16k": (28, 64, 16, 8, 16384, 64, 4, 8, 8, "Qwen3-0.6B"),
     "qwen3-8b-b32-32k": (36, 32, 32, 8, 32768, 64, 4, 8, 8, "Qwen3-8B"),
 }
+# key channels scaled up in every key (pool, planted blocks, appended tokens):
+# (channels, factor), the post-RoPE key outliers of the Qwen3-8B shape
+KEY_OUTLIERS = {"qwen3-8b-b32-32k": (4, 8.0)}
+# the generator of fill_synthetic_*: an Irwin-Hall(4) sum of four 16-bit
+# uniforms, centred and scaled to unit variance (bounded at +-3.46)
+GENERATOR = "Irwin-Hall(4) approximately normal, mean 0, variance 1, bounded at +-3.46"
 
 
 def log(msg):
@@ -129,6 +135,14 @@ class Layer:
             heads = torch.arange(hkv, device="cuda").view(1, hkv, 1).expand(batch, hkv, planted)
             vals = (0.5 * qmean[:, :, None, None, :] + 0.5 * noise).to(torch.float16)
             pool16[pages.reshape(-1), :, 0, heads.reshape(-1), :] = vals.reshape(-1, PAGE, D)
+        outliers = KEY_OUTLIERS.get(getattr(args, "config", None))
+        if outliers:
+            # every key of the pool and every appended key: the first
+            # `channels` channels scaled (exact in FP16: a power of two)
+            ch, factor = outliers
+            pool16 = kv.pool.view(torch.float16).view(-1, PAGE, 2, hkv, D)
+            pool16[:, :, 0, :, :ch] *= factor
+            knew[..., :ch] *= factor
         kv.seq_len.fill_(ctx)
         # the prefill's bulk seal: every whole page gets its representative
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -361,7 +375,7 @@ def main():
     else:
         kernel_name = {1: f"decode_kernel<{grp},{grp},true,false,false>", 2: f"decode_kernel<{grp},{grp},false,false,false>",
                        3: f"sparse_decode_attention_kernel<{grp}>"}[launches]
-    traffic = measured_traffic(args.config, kernel_name)
+    traffic, traffic_run = measured_traffic(args.config, kernel_name)
 
     parity = check_parity(sa, np, torch, L[-1], args, scale, hkv, budget, init, local, last_step)
     cpu = None if args.no_cpu_baseline else cpu_baseline(np, torch, L[0], args, budget, init, local, scale)
@@ -378,9 +392,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16 KV, fp32 math",
-        "data": "synthetic (seeded N(0,1) FP16 KV and queries, one query per sequence held over the steps, "
-                f"{planted} planted high-score blocks per (sequence, KV head) against it, new K/V every step, "
-                "randomly permuted page tables)",
+        "data": f"synthetic: seeded FP16 KV and fp32 queries from the {GENERATOR} generator, one query per "
+                f"sequence held over the steps, {planted} planted high-score blocks per (sequence, KV head) "
+                "against it, new K/V every step, randomly permuted page tables"
+                + ("" if not KEY_OUTLIERS.get(args.config) else
+                   f", keys with {KEY_OUTLIERS[args.config][0]} of 128 channels scaled x"
+                   f"{KEY_OUTLIERS[args.config][1]:g} (pool and appended tokens)"),
         "config": {"workload": f"{model} attention shape decode step: append+seal, score+select, sparse GQA "
                                f"attention", "layers": layers, "batch": batch, "query_heads": hq,
                    "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
@@ -401,7 +418,7 @@ def main():
                        {"attention": round(kernel_us, 3), "attention_in_step": round(att_us, 3),
                         "score_select": round(sel_us, 3), "append_seal": round(app_us, 3)}),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_run": traffic_run,
                      "kernel": kernel_name, "algorithmic_bytes": kernel_bytes,
                      "launch_us": round(kernel_us, 3),
                      "launch_timing": ("graph-replayed timed region / (steps x layers)" if launches == 1 and graph
@@ -476,13 +493,21 @@ def copy_reference(sa, torch, kv, seed, pages=4096, reps=5):
 def measured_traffic(config, kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
     summary for this workload (FETCH_SIZE scaled by the copy-kernel
-    calibration, plus WRITE_SIZE); None when no summary matches."""
+    calibration, plus WRITE_SIZE), and that counter run's own algorithmic
+    bytes per launch and their ratio (the counter run is a short run of its
+    own, whose steps hold slightly different tails than this run's last
+    step); (None, None) when no summary matches."""
     path = os.path.join(ROOT, "profiles", f"decode_step_{config}.traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
         entry = json.load(f).get("kernels", {}).get(kernel)
-    return None if entry is None else entry.get("traffic_bytes_per_launch")
+    if entry is None:
+        return None, None
+    return entry.get("traffic_bytes_per_launch"), {
+        "algorithmic_bytes_per_launch": entry.get("algorithmic_bytes_per_launch"),
+        "traffic_over_algorithmic": entry.get("traffic_over_algorithmic"),
+        "source": os.path.relpath(path, ROOT)}
 
 
 def check_parity(sa, np, torch, ly, args, scale, hkv, budget, init, local, s):

@@ -382,7 +382,12 @@ int sa_hip_decode_step_online(const sa_paged_kv* kv, const float* k,
  * with SA_HIP_EINVAL (the fused launch, splits == 1, needs no records).
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (unordered streams, or host threads) race and give wrong results; order
- * them on one stream.  Results equal sa_hip_decode_step's. */
+ * them on one stream.  Results equal sa_hip_decode_step's.
+ * Graph capture: the first call on each device looks the array's address up
+ * (hipGetSymbolAddress) and must run outside capture; a first call on a
+ * capturing stream returns SA_HIP_EINVAL.  Later calls may be captured.  The
+ * address is kept until the process ends: resetting the device
+ * (hipDeviceReset) after a call is not supported. */
 int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k,
                                const float* v, int32_t local_tokens,
                                const float* query,

@@ -109,6 +109,14 @@ static int greater_f32(const void* keys, size_t a, size_t b) {
   return k[a] > k[b];
 }
 
+/* The builder's received-mass order: the reference's a > b for numbers; NaN,
+ * which a > b leaves unordered (std::stable_sort then has no defined
+ * result), after every number.  The GPU builders rank the same way. */
+static int greater_mass(const void* keys, size_t a, size_t b) {
+  const float* k = (const float*)keys;
+  return k[a] > k[b] || (k[a] == k[a] && k[b] != k[b]);
+}
+
 static int greater_f64(const void* keys, size_t a, size_t b) {
   const double* k = (const double*)keys;
   return k[a] > k[b];
@@ -308,7 +316,7 @@ static int build_lcr(const float* prompt_queries, const uint16_t* kv, size_t tok
     for (size_t b = 0; b < blocks; ++b) {
       for (size_t i = 0; i < block_tokens; ++i) order[i] = i;
       stable_sort_desc(order, block_tokens, received + h * tokens + b * block_tokens,
-                       greater_f32);
+                       greater_mass);
       if (offsets)
         for (size_t r = 0; r < topk; ++r) offsets[(h * blocks + b) * topk + r] = order[r];
       for (size_t d = 0; d < head_dim; ++d) {

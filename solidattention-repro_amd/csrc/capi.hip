@@ -103,8 +103,13 @@ std::mutex g_scratch_mu;
 void* g_scratch_dev[kNoallocMaxDevices];  // device address of `scratch` per device
 
 // The device address of the current device's `scratch`, looked up on the
-// first call on that device (with the device current) and kept.
-int noalloc_scratch(void** out, const char* op) {
+// first call on that device (with the device current) and kept for the life
+// of the process: a device reset (hipDeviceReset) unloads the module and
+// leaves the kept address dangling, so resetting a device the library has
+// run on is not supported.  The lookup is not a stream operation and may
+// load the module, so the first call on a device must not run under graph
+// capture: a first call on a capturing stream is refused.
+int noalloc_scratch(void** out, const char* op, hipStream_t stream) {
   int dev = -1;
   if (int e = check_hip(hipGetDevice(&dev), "decode_step_noalloc: hipGetDevice")) return e;
   if (dev < 0 || dev >= kNoallocMaxDevices)
@@ -112,6 +117,10 @@ int noalloc_scratch(void** out, const char* op) {
                 kNoallocMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_dev[dev]) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
+      return fail(SA_HIP_EINVAL, "%s: the first call on device %d must run outside graph capture (it looks up "
+                  "the static scratch); call it once eagerly before capturing", op, dev);
     void* p = nullptr;
     if (int e = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "decode_step_noalloc: hipGetSymbolAddress"))
       return e;
@@ -686,7 +695,7 @@ int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k, const floa
                 "or a smaller batch, or sa_hip_decode_step with a workspace)", op, records,
                 kNoallocScratchBytes - kNoallocCounterBytes);
   void* base = nullptr;
-  if (int e = noalloc_scratch(&base, op)) return e;
+  if (int e = noalloc_scratch(&base, op, as_stream(stream))) return e;
   // the counters are cleared before the fused launch, whatever an earlier
   // call on this GPU left in them
   return decode_step_run(kv, k, v, nullptr, nullptr, local_tokens, query, params, scale, selected, counts, out,

@@ -146,7 +146,7 @@ __device__ inline void seal_head(const Args& a, int b, int h, const uint16_t* ke
     int rank = 0;
     for (int k = 0; k < kT; ++k) {
       const float rk = received[k];
-      rank += (rk > rj || (k < j && !(rj > rk))) ? 1 : 0;
+      rank += (mass_before(rk, rj) || (k < j && mass_tied(rk, rj))) ? 1 : 0;
     }
     order[rank] = j;
   }

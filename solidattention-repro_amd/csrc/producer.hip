@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* x, cons
 // compute unit pulls from L2 (x is read once per slice and column block, not
 // once per 16 columns) and gives each LDS read of x C / 16 matrix steps.
 constexpr int kUnitK = 32;
-constexpr int kSplitMaxSlices = 8;
+constexpr int kWideTileMaxSlices = 8;  // 64-column tiles only up to this many K slices
 
 struct SplitParams {
   const float* x;          // [rows][in]
@@ -392,17 +392,17 @@ __global__ __launch_bounds__(kWave) void linear_reduce_kernel(const float* part,
 
 }  // namespace
 
-// Tile of a split projection: 64 columns x 256 k when that gives every
-// compute unit a workgroup with at most 8 K slices (1024 -> 4096: 256
-// workgroups, 4 slices), else 32 columns x 256 k (2048 -> 1024: 256
-// workgroups, 8 slices); the slices are in / 256.
+// Tile of a split projection: always in / 256 K slices of 256 k (no upper
+// bound: the reduce adds any number of slices in slice order), with 64
+// columns per workgroup when the slices number at most 8 and the 64-column
+// grid still gives every compute unit a workgroup (1024 -> 4096: 256
+// workgroups, 4 slices), else 32 columns (2048 -> 1024: 256 workgroups, 8
+// slices; 4096 -> 4096, the Qwen3-8B o-projection: 2048 workgroups, 16
+// slices).  The workspace holds slices x rows x out partial sums.
 SplitShape split_shape(int64_t rows, int64_t in, int64_t out) {
   const int64_t rb = (rows + kRowsPerWg - 1) / kRowsPerWg;
   SplitShape sh{64, static_cast<int32_t>(in / 256)};
-  if (sh.slices > kSplitMaxSlices || (out / 64) * sh.slices * rb < compute_units()) {
-    sh.cols = 32;
-    sh.slices = static_cast<int32_t>(in / 256);
-  }
+  if (sh.slices > kWideTileMaxSlices || (out / 64) * sh.slices * rb < compute_units()) sh.cols = 32;
   return sh;
 }
 

@@ -386,14 +386,14 @@ __global__ __launch_bounds__(BPW * kWave) void block_topk_kernel(const Params p)
     }
     p.received[static_cast<int64_t>(h) * p.tokens + t] = r;
   }
-  // stable descending rank: greater ones first, equal (or unordered) ones in
-  // token order; lane j's mass broadcast by readlane, the tests combined
-  // without branches
+  // stable descending rank (mass_before / mass_tied: greater ones first,
+  // equal ones in token order, NaN last); lane j's mass broadcast by
+  // readlane, the tests combined without branches
   int rank = 0;
 #pragma unroll
   for (int j = 0; j < kPageTokens; ++j) {
     const float rj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), j));
-    rank += static_cast<int>((rj > r) | (!(r > rj) & !(rj > r) & (j < lane)));
+    rank += static_cast<int>(mass_before(rj, r) | (mass_tied(rj, r) & (j < lane)));
   }
   if (valid && lane < kPageTokens && rank < p.topk) {
     order[wave][rank] = lane;

@@ -73,6 +73,16 @@ __device__ inline uint16_t f2h_rne(float x) {
 __device__ inline float lo_h2f(uint32_t w) { return h2f(static_cast<uint16_t>(w & 0xffffu)); }
 __device__ inline float hi_h2f(uint32_t w) { return h2f(static_cast<uint16_t>(w >> 16)); }
 
+// ---- the received-mass order of the InfLLM builder ---------------------------
+// Keys are ranked by received mass, greater first, equal masses in token
+// order (the reference's std::stable_sort with a > b, selection.cpp:71-76).
+// That comparator leaves NaN unordered, where std::stable_sort has no defined
+// result; here NaN ranks after every number and NaNs keep token order, so
+// that the rank of key j, #{k : before(m_k, m_j)} + #{k < j : tied(m_k, m_j)},
+// is a bijection for every input.  Numbers rank exactly as with a > b.
+__device__ inline bool mass_before(float a, float b) { return (a > b) || (a == a && b != b); }
+__device__ inline bool mass_tied(float a, float b) { return !(a > b) && !(b > a) && ((a == a) == (b == b)); }
+
 // ---- streaming loads ---------------------------------------------------------
 // Non-temporal 16-byte load: data read once per step (KV pages,
 // representatives) is streamed past the caches.  On MI355X this lifts the

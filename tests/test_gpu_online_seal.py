@@ -164,3 +164,35 @@ def test_p13c4_online_seal_28_layers(hip):
         selected += int(cnt[b, 0].item() == 1 and sel[b, 0, 0].item() == 0)
     assert selected == 28
     assert case.reps[:, :, :, 16].size == 28 * 16 * 128  # representative values of P1.3c.4
+
+
+@pytest.mark.parametrize("hq,fused", [(16, True), (64, False)])
+def test_online_seal_nan_queries_in_ring(hip, hq, fused):
+    """Non-finite prefill queries in the ring: the sealed blocks' received
+    masses go NaN for the keys in their windows and rank after every number
+    (token order among them), on the GPU as in the oracle, so the page
+    bytes, representatives, counters and ring equal the oracle's bit for
+    bit; decode queries stay finite."""
+    print(f"case: NaN ring queries hq={hq} fused={fused}", flush=True)
+    case = make_case(960 + hq, 2, hq, 8, [32 * 5 + 20, 32 * 3 + 30], table_stride=12, rep_heads=hq)
+    kv = device_kv(case)
+    rng = np.random.default_rng(17)
+    seal, ring = start_ring(hip, kv, case, rng, 32, 8, 6)
+    ring[0, 3, (32 * 5 + 5) % 32, 7] = np.nan
+    ring[1, 0, (32 * 3 + 9) % 32, :] = np.inf
+    ring[1, hq - 1, (32 * 3 + 29) % 32, 100] = np.nan
+    seal.ring.copy_(torch.from_numpy(ring))
+    assert hip.select_attend_fused(kv, 8, sel_stride=8) == fused
+    ws, _ = hip.decode_step_workspace(kv)
+    st = status_tensor()
+    for step in range(13):
+        k = rng.standard_normal((2, 8, D)).astype(np.float32)
+        v = rng.standard_normal((2, 8, D)).astype(np.float32)
+        case.query[:] = rng.standard_normal(case.query.shape).astype(np.float32)
+        hip.decode_step_online(kv, to_dev(k), to_dev(v), 0, to_dev(case.query), seal, 8, 8, 2, 2, SCALE, ws,
+                               status=st)
+        oracle_online_append_seal(case, ring, k, v, case.query, 0, 8, 6)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    assert case.sealed.tolist() == [6, 4]
+    check_state(kv, case, seal, ring)

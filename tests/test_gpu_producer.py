@@ -34,7 +34,9 @@ def test_rms_norm(hip, rows):
 
 
 @pytest.mark.parametrize("rows,n_in,n_out,res", [(1, 1024, 2048, False), (5, 1024, 1024, True), (64, 2048, 1024, True),
-                                                  (100, 1024, 4096, False), (130, 2048, 1024, True)])
+                                                  (100, 1024, 4096, False), (130, 2048, 1024, True),
+                                                  # Qwen3-8B o-projection: 16 K slices of 32-column tiles
+                                                  (32, 4096, 4096, True), (3, 4096, 1024, False)])
 def test_linear(hip, rows, n_in, n_out, res):
     print(f"case: linear rows={rows} in={n_in} out={n_out} residual={res}", flush=True)
     rng = np.random.default_rng(rows + n_out)
@@ -65,12 +67,14 @@ def oracle_qkv(x, L, positions, hq, hkv, theta=1e6, eps=1e-6):
     return (O.qk_norm_rope(q, L["qn"], positions, theta, eps), O.qk_norm_rope(k, L["kn"], positions, theta, eps), v)
 
 
-@pytest.mark.parametrize("rows,hq,hkv", [(1, 16, 8), (64, 16, 8), (33, 32, 8), (70, 16, 4)])
-def test_qkv_project(hip, rows, hq, hkv):
-    print(f"case: qkv rows={rows} hq={hq} hkv={hkv}", flush=True)
+@pytest.mark.parametrize("rows,hq,hkv,hidden", [(1, 16, 8, 1024), (64, 16, 8, 1024), (33, 32, 8, 1024),
+                                                (70, 16, 4, 1024), (32, 32, 8, 4096)])
+def test_qkv_project(hip, rows, hq, hkv, hidden):
+    """hidden 4096 is the Qwen3-8B producer: 16 K slices per projection."""
+    print(f"case: qkv rows={rows} hq={hq} hkv={hkv} hidden={hidden}", flush=True)
     rng = np.random.default_rng(100 + rows)
-    L = make_layer(rng, 1024, hq, hkv)
-    x = rng.standard_normal((rows, 1024)).astype(np.float32)
+    L = make_layer(rng, hidden, hq, hkv)
+    x = rng.standard_normal((rows, hidden)).astype(np.float32)
     pos = rng.integers(0, 131072, size=rows).astype(np.int32)
     pos[0] = 0
     q, k, v = hip.qkv_project(to_dev(x), to_dev(L["wq"]), to_dev(L["wk"]), to_dev(L["wv"]), to_dev(L["qn"]),

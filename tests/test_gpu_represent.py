@@ -148,3 +148,25 @@ def test_gpu_c21_chain(hip):
     sel, cnt = hip.score_select(kvp, torch.from_numpy(query.reshape(1, 16, 128)).cuda(), 1, 4, 1, 1)
     torch.cuda.synchronize()
     assert sel[0, 0, : int(cnt.item())].cpu().numpy().tolist() == [0, 8, 13, 15]
+
+
+def test_gpu_builder_nan_queries_rank_last(hip):
+    """Non-finite prompt queries give NaN received masses to the keys in
+    their windows; the GPU builder ranks them after every number in token
+    order, as the oracle does (the reference's a > b leaves NaN unordered):
+    offsets and representative bits equal the oracle's, NaN masses where
+    the oracle has them and equal bits elsewhere."""
+    rng = np.random.default_rng(321)
+    tokens, hq, hkv, window, topk = 160, 8, 4, 8, 12
+    pq = rng.standard_normal((hq, tokens, 128)).astype(np.float32)
+    pq[1, 37, 5] = np.nan
+    pq[6, [3, 40, 41, 130], 0] = np.inf
+    kv = rng.standard_normal(tokens * 2 * hkv * 128).astype(np.float16).view(np.uint16)
+    vals, offs, rec = gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk)
+    evals, eoffs, erec = O.local_causal_representatives_restated(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
+    assert np.isnan(erec).any()
+    assert np.array_equal(np.isnan(rec), np.isnan(erec))
+    finite = ~np.isnan(erec)
+    assert np.array_equal(rec[finite].view(np.uint32), erec[finite].view(np.uint32))
+    assert np.array_equal(offs, eoffs.astype(np.int64))
+    assert np.array_equal(vals.view(np.uint32), evals.view(np.uint32))

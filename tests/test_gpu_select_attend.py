@@ -393,3 +393,109 @@ def test_decode_steps_key_channel_outliers_four_heads(hip):
             check_state(kv, case)
     assert seals == 3  # one seal each, after 12, 2 and 23 appends
     assert int(ws.abs().sum().item()) == 0
+
+
+def test_decode_steps_qwen3_06b_shape_two_heads(hip):
+    """The Qwen3-0.6B decode step through the kernel the headline bench
+    times: 16 query / 8 KV heads (the fused G = 2 launch with the append),
+    512+ sealed blocks per sequence in permuted pages, budget 64 = 4 init +
+    8 local + 52 dynamic, 8 planted blocks per KV head; 24 decode steps with
+    seals on the way.  Ids and state bit-exact, attention within 2e-3 of the
+    oracle on every step."""
+    lengths = [32 * 512 + 20, 32 * 530 + 30, 32 * 600 + 9, 32 * 515 + 31]
+    print(f"case: G=2 cfg2 shape lengths={lengths}", flush=True)
+    case = make_case(771, 4, 16, 8, lengths, table_stride=620, planted=8)
+    kv = device_kv(case)
+    budget, init, local = 64, 4, 8
+    assert hip.select_attend_fused(kv, 8)
+    ws, _ = hip.decode_step_workspace(kv)
+    st = status_tensor()
+    rng = np.random.default_rng(63)
+    seals = 0
+    for step in range(24):
+        k = rng.standard_normal((4, 8, D)).astype(np.float32)
+        v = rng.standard_normal((4, 8, D)).astype(np.float32)
+        # the query drifts a little, so the planted blocks keep scoring high
+        case.query[:] = case.query + 0.1 * rng.standard_normal(case.query.shape).astype(np.float32)
+        before = case.sealed.copy()
+        sel, cnt, out = hip.decode_step(kv, to_dev(k), to_dev(v), 0, to_dev(case.query), 8, budget, init, local,
+                                        SCALE, ws, status=st)
+        esel, ecnt, expect = oracle_decode(case, k, v, 0, budget, init, local, budget)
+        seals += int((case.sealed - before).sum())
+        torch.cuda.synchronize()
+        assert int(st.item()) == 0, step
+        got_sel, got_cnt = sel.cpu().numpy(), cnt.cpu().numpy()
+        assert np.array_equal(got_cnt, ecnt), step
+        assert (ecnt == budget).all()
+        for b in range(4):
+            for g in range(8):
+                assert got_sel[b, g, :budget].tolist() == esel[b, g, :budget].tolist(), (step, b, g)
+        assert_close_2e3(out.cpu().numpy(), expect)
+        if step in (0, 11, 23):
+            check_state(kv, case)
+    assert seals == 4  # after 12, 2, 23 and 1 appends
+    assert int(ws.abs().sum().item()) == 0
+
+
+def test_c1_shape_shared_selection_then_attention(hip):
+    """The reference's C1/C2 single-layer case at its own shape: 1 sequence,
+    16 query / 8 KV heads, 2048 tokens (64 blocks), 4 planted blocks whose
+    keys are 0.5 x the query of their head group plus noise, one block set
+    shared by all 16 query heads with budget 16 = init 1 + local 2 + 13
+    dynamic (selection_main.cpp:178-181), then attention over the 512
+    selected tokens.  Ids bit-exact in every selection form (the planted
+    blocks among them), attention within 2e-3 of the oracle over the paged
+    pool and, after packing the 16 blocks (gather_pages, the placement of
+    read_blocks_fixed), over the 512 contiguous tokens against the oracle's
+    attention_reference on the packed bytes."""
+    case = make_case(770, 1, 16, 8, [2048], table_stride=66)
+    rng = np.random.default_rng(77)
+    planted = [9, 22, 37, 50]
+    f16 = case.pool.view(np.float16)
+    for g in range(8):
+        qmean = case.query[0, 2 * g:2 * g + 2].mean(axis=0)
+        for blk in planted:
+            noise = rng.standard_normal((PAGE, D)).astype(np.float32)
+            f16[case.table[0, blk], :, 0, g, :] = (0.5 * qmean[None, :] + 0.5 * noise).astype(np.float16)
+    case.sealed[:] = 0
+    case.generation[:] = 0
+    case.reps[:] = 0
+    O.paged_seal(case.pool, PAGE, case.table, case.seq_len, case.sealed, case.generation, case.reps, 8,
+                 case.rep_stride, 1, 16, 8, D, 0)
+    assert int(case.sealed[0]) == 64
+    budget, init, local = 16, 1, 2
+    esel, ecnt = O.paged_score_select(case.query, case.reps, case.sealed, 1, 16, 8, D, 8, case.rep_stride, 1, budget,
+                                      init, local)
+    ids = esel[0, 0, :16].tolist()
+    assert ecnt[0, 0] == 16 and set(planted) <= set(ids) and 0 in ids and {62, 63} <= set(ids)
+    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, esel, ecnt, 1,
+                                      case.query, 1, 16, 8, D, SCALE)
+    kv = device_kv(case)
+    q = to_dev(case.query)
+    st = status_tensor()
+    forms = {"single": hip.score_select(kv, q, 1, budget, init, local, status=st),
+             "split": hip.score_select_split(kv, q, 1, budget, init, local, status=st)[:2]}
+    sel_f, cnt_f, out_f = hip.select_attend(kv, q, 1, budget, init, local, SCALE, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    for name, (sel, cnt) in forms.items():
+        assert cnt.cpu().numpy().tolist() == [[16]], name
+        assert sel.cpu().numpy()[0, 0].tolist() == ids, name
+    assert sel_f.cpu().numpy()[0, 0].tolist() == ids
+    assert_close_2e3(out_f.cpu().numpy(), expect)
+    sel, cnt = forms["single"]
+    for splits in (1, 2, 4):
+        out = hip.sparse_decode_attention(kv, q, sel, cnt, SCALE, splits=splits, status=st)
+        torch.cuda.synchronize()
+        assert_close_2e3(out.cpu().numpy(), expect)
+    # the reference's C2 flow: pack the selected blocks, attend the 512 tokens
+    pages = to_dev(case.table[0, ids].astype(np.int32))
+    packed = torch.zeros((16, case.page_elems), dtype=torch.int16, device="cuda").view(torch.uint16)
+    hip.gather_pages(kv.pool, kv.page_bytes, kv.num_pages, pages, packed, status=st)
+    out_c = hip.attention_contiguous(packed.view(-1), q[0], 512, 16, 8, SCALE)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0
+    packed_np = packed.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = O.attention_reference(packed_np, case.query[0], 512, 16, 8, D, SCALE)
+    assert np.abs(out_c.cpu().numpy().astype(np.float64) - ref).max() <= 2e-5
+    assert_close_2e3(ref[None], expect)

@@ -89,10 +89,14 @@ def test_noalloc_refuses_records_beyond_scratch(hip):
     assert kv.seq_len.cpu().numpy().tolist() == [32 * 4 + 1, 32 * 3]  # nothing launched
 
 
-def test_noalloc_graph_replays(hip):
-    """Captured in a HIP graph (counter clear + fused step) and replayed 3
-    times with eager work between replays: every replay equals an eager step
-    of the workspace entry point on a copy of the state."""
+@pytest.mark.parametrize("splits", [1, 2])
+def test_noalloc_graph_replays(hip, splits):
+    """Captured in a HIP graph and replayed 3 times with eager work between
+    replays: every replay equals an eager step of the workspace entry point
+    on a copy of the state.  splits 1: the counter clear and the fused step;
+    splits 2: the separate append/seal, selection and attention launches,
+    whose split records live in the static scratch."""
+    print(f"case: graph replays splits={splits}", flush=True)
     case = make_case(806, 4, 16, 8, [32 * 60 + 30, 32 * 33, 32 * 12 + 3, 32 * 70 + 31], table_stride=80, planted=3)
     rng = np.random.default_rng(7)
     k = to_dev((rng.standard_normal((4, 8, D)) * 2).astype(np.float32))
@@ -103,18 +107,20 @@ def test_noalloc_graph_replays(hip):
     hip.decode_step_noalloc(warm, k, v, 0, q, 8, BUDGET, INIT, LOCAL, SCALE, *outputs(4, 16))
     torch.cuda.synchronize()
     kv_a, kv_b = device_kv(case), device_kv(case)
-    ws, _ = hip.decode_step_workspace(kv_a)
+    assert hip.select_attend_fused(kv_a, 8, splits) == (splits == 1)
+    ws, _ = hip.decode_step_workspace(kv_a, splits)
     sel, cnt, out = outputs(4, 16)
     st = status_tensor()
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=side):
-            hip.decode_step_noalloc(kv_b, k, v, 0, q, 8, BUDGET, INIT, LOCAL, SCALE, sel, cnt, out, status=st)
+            hip.decode_step_noalloc(kv_b, k, v, 0, q, 8, BUDGET, INIT, LOCAL, SCALE, sel, cnt, out, splits=splits,
+                                    status=st)
     torch.cuda.synchronize()
     for r in range(3):
         print(f"replay {r}", flush=True)
-        a = hip.decode_step(kv_a, k, v, 0, q, 8, BUDGET, INIT, LOCAL, SCALE, ws)
+        a = hip.decode_step(kv_a, k, v, 0, q, 8, BUDGET, INIT, LOCAL, SCALE, ws, splits=splits)
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
@@ -123,3 +129,55 @@ def test_noalloc_graph_replays(hip):
         assert_same_step(a, (sel, cnt, out))
         assert_same_state(kv_a, kv_b)
     assert int(kv_b.seq_len.cpu().numpy()[0]) == 32 * 60 + 30 + 3  # three appends, one seal on the way
+
+
+FIRST_CALL_UNDER_CAPTURE = r"""
+import sys
+sys.path.insert(0, {root!r}); sys.path.insert(0, {pkg!r}); sys.path.insert(0, {tests!r})
+import numpy as np, torch
+import solidattention_amd as sa
+from gpu_util import device_kv
+from paged_case import make_case
+case = make_case(807, 2, 16, 8, [32 * 5 + 3, 32 * 2], table_stride=8)
+kv = device_kv(case)
+z = torch.zeros((2, 8, 128), dtype=torch.float32, device="cuda")
+q = torch.from_numpy(case.query).cuda()
+sel = torch.zeros((2, 8, 16), dtype=torch.int32, device="cuda")
+cnt = torch.zeros((2, 8), dtype=torch.int32, device="cuda")
+out = torch.zeros((2, 16, 128), dtype=torch.float32, device="cuda")
+torch.cuda.synchronize()
+side = torch.cuda.Stream()
+msg = "no error"
+try:
+    with torch.cuda.stream(side):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            sa.decode_step_noalloc(kv, z, z, 0, q, 8, 16, 2, 3, 0.088, sel, cnt, out)
+except Exception as e:  # the capture ends with the refusal
+    msg = str(e)
+torch.cuda.synchronize()
+print("REFUSED" if "outside graph capture" in msg else "NOT REFUSED: " + msg, flush=True)
+# and eagerly the same call then works
+sa.decode_step_noalloc(kv, z, z, 0, q, 8, 16, 2, 3, 0.088, sel, cnt, out)
+torch.cuda.synchronize()
+print("EAGER OK", int(kv.seq_len[0].item()), flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_refused(hip):
+    """In a fresh process (no earlier call on the device), a first call made
+    under graph capture is refused with a clear error before anything is
+    launched; the same call made eagerly afterwards runs."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    script = FIRST_CALL_UNDER_CAPTURE.format(root=root, pkg=os.path.join(root, "solidattention-repro_amd"),
+                                             tests=here)
+    print("case: first noalloc call under capture, fresh process", flush=True)
+    r = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=110)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0
+    assert "REFUSED" in r.stdout and "NOT REFUSED" not in r.stdout
+    assert "EAGER OK 164" in r.stdout
