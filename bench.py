@@ -89,6 +89,8 @@ def parse():
     ap.add_argument("--chunk-grid-order", action="store_true",
                     help="stress workload: chunked attention in grid order (a workspace without room for the "
                          "longest-first schedule)")
+    ap.add_argument("--microbatches", type=int, default=1,
+                    help="layer workload: the batch in this many parts, each a chain of layers on its own stream")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
                     help="also run one plain page copy of PAGES pages (HBM counter calibration)")
     return ap.parse_args()

@@ -66,36 +66,60 @@ def run(args):
 
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
     status = torch.zeros(1, dtype=torch.int32, device="cuda")
-    ws, _ = sa.decode_step_workspace(L[0].kv, 1)
-    # the projections' K-slice partial tiles
-    qkv_ws = torch.empty(sa.lib().sa_hip_qkv_workspace_bytes(batch, hidden, hq, hkv) // 4, dtype=torch.float32,
-                         device="cuda")
-    lin_ws = torch.empty(sa.lib().sa_hip_linear_workspace_bytes(batch, hq * D, hidden) // 4, dtype=torch.float32,
-                         device="cuda")
     q = torch.empty((batch, hq, D), dtype=torch.float32, device="cuda")
     k = torch.empty((batch, hkv, D), dtype=torch.float32, device="cuda")
     v = torch.empty_like(k)
     hs = [torch.empty((batch, hidden), dtype=torch.float32, device="cuda") for _ in range(layers + 1)]
     stream = torch.cuda.current_stream()
+    # micro-batches: the batch's sequences in `mb` equal parts, each its own
+    # chain of layers on its own stream (the parts share no state, so one
+    # part's latency-bound projections run beside another's decode step)
+    mb = max(1, int(getattr(args, "microbatches", 1) or 1))
+    if batch % mb:
+        raise SystemExit(f"--microbatches {mb} does not divide the batch of {batch}")
+    part = batch // mb
+    parts = []
+    for i in range(mb):
+        a, b = i * part, (i + 1) * part
+        kvs = [ly.kv.sequences(a, b) for ly in L]
+        parts.append(dict(
+            rows=slice(a, b), kvs=kvs, stream=None if i == 0 else torch.cuda.Stream(),
+            ws=sa.decode_step_workspace(kvs[0], 1)[0],
+            # the projections' K-slice partial tiles
+            qkv_ws=torch.empty(sa.lib().sa_hip_qkv_workspace_bytes(part, hidden, hq, hkv) // 4,
+                               dtype=torch.float32, device="cuda"),
+            lin_ws=torch.empty(sa.lib().sa_hip_linear_workspace_bytes(part, hq * D, hidden) // 4,
+                               dtype=torch.float32, device="cuda")))
 
-    def layer_step(l, ev=None):
-        ly, w = L[l], W[l]
-        if ev: ev[0].record(stream)
+    def layer_step(l, pt, ev=None):
+        # part 0 runs on the current stream (the capture stream under graph
+        # capture); the others on their own streams, forked from it
+        ly, w, r = L[l], W[l], pt["rows"]
+        st = pt["stream"] or torch.cuda.current_stream()
+        kv = pt["kvs"][l]
+        if ev: ev[0].record(st)
         # RMSNorm + q/k/v + head RMS + RoPE; the new token's position is the
         # sequence's length before the append
-        sa.qkv_project(hs[l], w["wq"], w["wk"], w["wv"], w["qn"], w["kn"], ly.kv.seq_len, hq, hkv, q=q, k=k, v=v,
-                       workspace=qkv_ws, input_norm=w["inorm"], input_eps=1e-6)
-        if ev: ev[1].record(stream)
-        sa.decode_step(ly.kv, k, v, 0, q, hkv, budget, init, local, scale, ws, selected=ly.selected,
-                       counts=ly.counts, out=ly.out, splits=1, status=status)
-        if ev: ev[2].record(stream)
-        sa.linear(ly.out.view(batch, hq * D), w["wo"], hs[l], out=hs[l + 1], workspace=lin_ws)
-        if ev: ev[3].record(stream)
+        sa.qkv_project(hs[l][r], w["wq"], w["wk"], w["wv"], w["qn"], w["kn"], kv.seq_len, hq, hkv, q=q[r], k=k[r],
+                       v=v[r], workspace=pt["qkv_ws"], input_norm=w["inorm"], input_eps=1e-6, stream=st)
+        if ev: ev[1].record(st)
+        sa.decode_step(kv, k[r], v[r], 0, q[r], hkv, budget, init, local, scale, pt["ws"], selected=ly.selected[r],
+                       counts=ly.counts[r], out=ly.out[r], splits=1, status=status, stream=st)
+        if ev: ev[2].record(st)
+        sa.linear(ly.out[r].reshape(part, hq * D), w["wo"], hs[l][r], out=hs[l + 1][r], workspace=pt["lin_ws"],
+                  stream=st)
+        if ev: ev[3].record(st)
 
     def step(ev=None):
+        cur = torch.cuda.current_stream()
         hs[0].copy_(h0)
+        for pt in parts[1:]:
+            pt["stream"].wait_stream(cur)
         for l in range(layers):
-            layer_step(l, None if ev is None else ev[l])
+            for i, pt in enumerate(parts):
+                layer_step(l, pt, None if ev is None or i else ev[l])
+        for pt in parts[1:]:
+            cur.wait_stream(pt["stream"])
 
     for _ in range(args.warmup):
         step()
@@ -132,13 +156,16 @@ def run(args):
                   "shape, B=64, 16K)",
         "value": round(us_per_layer, 3), "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "higher_is_better": False, "dtype": "fp32 weights and math, fp16 KV",
-        "data": "synthetic (seeded weights and hidden rows, N(0,1) FP16 KV, planted blocks)",
+        "data": f"synthetic: seeded weights and hidden rows, FP16 KV from the {bench.GENERATOR} generator, "
+                "planted blocks",
         "config": {"workload": "RMSNorm + q/k/v projections + head RMS + RoPE (one launch) -> decode step -> "
                                "o-proj + residual", "layers": layers, "batch": batch, "hidden": hidden, "query_heads": hq,
-                   "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget},
+                   "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
+                   "microbatches": mb, "streams": mb},
         "tokens_per_s": round(batch / (us_per_layer * layers * 1e-6), 1),
         "components_us": {"qkv_project_rms": round(comp_us[0], 3), "decode_step": round(comp_us[1], 3),
-                          "o_proj": round(comp_us[2], 3)},
+                          "o_proj": round(comp_us[2], 3),
+                          "timing": "events around each call of the first micro-batch in eager steps"},
         "projections": {"qkv_bytes": qkv_bytes, "qkv_gbps": round(qkv_bytes / (comp_us[0] * 1e-6) / 1e9, 1),
                         "o_bytes": o_bytes, "o_gbps": round(o_bytes / (comp_us[2] * 1e-6) / 1e9, 1)},
         "parity": parity, "cpu_baseline": cpu,

@@ -228,6 +228,23 @@ class PagedKV:
     def page_bytes(self) -> int:
         return PAGE_TOKENS * 2 * self.kv_heads * self.head_dim * 2
 
+    def sequences(self, first, stop):
+        """A view of sequences [first, stop): the same page pool, the rows of
+        the tables, lengths, counters and representatives of those sequences
+        (no copy).  Calls on disjoint views touch disjoint state, so they may
+        run concurrently on different streams (micro-batches)."""
+        import copy
+        if not 0 <= first < stop <= self.batch:
+            raise ValueError(f"sequences [{first}, {stop}) outside the batch of {self.batch}")
+        v = copy.copy(self)
+        v.batch = stop - first
+        v.block_table = self.block_table[first:stop]
+        v.seq_len = self.seq_len[first:stop]
+        v.sealed = self.sealed[first:stop]
+        v.generation = self.generation[first:stop]
+        v.reps = self.reps[first:stop]
+        return v
+
 
 def score_select(kv: PagedKV, query, select_groups, budget, init, local, selected=None, counts=None,
                  scores=None, status=None, sel_stride=None, stream=None, budgets=None):
