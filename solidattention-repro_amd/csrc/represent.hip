@@ -393,7 +393,7 @@ __global__ __launch_bounds__(BPW * kWave) void block_topk_kernel(const Params p)
 #pragma unroll
   for (int j = 0; j < kPageTokens; ++j) {
     const float rj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), j));
-    rank += static_cast<int>(mass_before(rj, r) | (mass_tied(rj, r) & (j < lane)));
+    rank += static_cast<int>(mass_before(rj, r)) | (static_cast<int>(mass_tied(rj, r)) & static_cast<int>(j < lane));
   }
   if (valid && lane < kPageTokens && rank < p.topk) {
     order[wave][rank] = lane;

@@ -47,7 +47,6 @@ struct Params {
 // that short representative rows leave room for more resident workgroups.
 template <int GR, int kThreads, bool QUAD>
 __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) {
-  constexpr int kWaves = kThreads / kWave;
   const int sg = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
@@ -55,7 +54,8 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   extern __shared__ __align__(16) float dyn_smem[];
   float* q_s = dyn_smem;                                                   // heads_per_sel * D
   uint32_t* keys = reinterpret_cast<uint32_t*>(dyn_smem + p.heads_per_sel * D);  // min(rep_stride, 8192)
-  __shared__ SelectSmem<kWaves> sm;
+  __shared__ __align__(16) RegsSelectSmem<kThreads, 4> sm;
+  __shared__ SelectSmem<kThreads / kWave> lds;
 
   const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
   int32_t* out_ids = p.selected + out_row * p.sel_stride;
@@ -88,6 +88,7 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
   a.group = p.group;
   a.rep_heads = p.rep_heads;
   a.rep_stride = p.rep_stride;
+  clear_regs_select(sm);
   load_query_t<kThreads>(a, q_s);
   __syncthreads();
   float* scores_row = p.scores ? p.scores + out_row * p.rep_stride : nullptr;
@@ -105,9 +106,7 @@ __global__ __launch_bounds__(kThreads) void score_select_kernel(const Params p) 
     }
     return;
   }
-  uint32_t threshold = 0xffffffffu, equal_take = 0;
-  if (bs.k > 0) radix_threshold<kThreads>(keys, bs, sm, threshold, equal_take);
-  const int count = compact_ids<kThreads>(keys, n, bs, threshold, equal_take, out_ids, p.sel_stride, nullptr, sm);
+  const int count = select_from_keys(keys, n, bs, out_ids, p.sel_stride, sm, lds);
   if (tid == 0) p.counts[out_row] = count;
 }
 
@@ -224,7 +223,6 @@ __global__ __launch_bounds__(kRowThreads) void score_rows_kernel(const Params p)
 template <int GR, int kThreads, int NB>
 __global__ __launch_bounds__(kThreads) void score_select_chunked_kernel(const Params p, uint32_t* ws_keys,
                                                                         int32_t* ws_arrive, int32_t key_stride) {
-  constexpr int kWaves = kThreads / kWave;
   constexpr int kChunk = NB * kThreads;
   int sg = blockIdx.x;
   int b = blockIdx.y;
@@ -243,7 +241,8 @@ __global__ __launch_bounds__(kThreads) void score_select_chunked_kernel(const Pa
   extern __shared__ __align__(16) float dyn_smem[];
   float* q_s = dyn_smem;                                                   // heads_per_sel * D
   uint32_t* keys = reinterpret_cast<uint32_t*>(dyn_smem + p.heads_per_sel * D);  // min(rep_stride, 8192)
-  __shared__ SelectSmem<kWaves> sm;
+  __shared__ __align__(16) RegsSelectSmem<kThreads, 4> sm;
+  __shared__ SelectSmem<kThreads / kWave> lds;
   __shared__ int s_last;
 
   const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
@@ -287,6 +286,7 @@ __global__ __launch_bounds__(kThreads) void score_select_chunked_kernel(const Pa
   a.group = p.group;
   a.rep_heads = p.rep_heads;
   a.rep_stride = p.rep_stride;
+  clear_regs_select(sm);
   load_query_t<kThreads>(a, q_s);
   __syncthreads();
   score_blocks_vec<GR, NB, kThreads>(a, q_s, hi, keys, nullptr, tid, lo);
@@ -306,9 +306,7 @@ __global__ __launch_bounds__(kThreads) void score_select_chunked_kernel(const Pa
     }
   }
   __syncthreads();
-  uint32_t threshold = 0xffffffffu, equal_take = 0;
-  if (bs.k > 0) radix_threshold<kThreads>(keys, bs, sm, threshold, equal_take);
-  const int count = compact_ids<kThreads>(keys, n, bs, threshold, equal_take, out_ids, p.sel_stride, nullptr, sm);
+  const int count = select_from_keys(keys, n, bs, out_ids, p.sel_stride, sm, lds);
   if (tid == 0) p.counts[out_row] = count;
 }
 
@@ -326,10 +324,10 @@ __global__ __launch_bounds__(kThreads) void select_scores_regs_kernel(const Para
   const int sg = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  __shared__ __align__(16) RegsSelectSmem<kThreads> sm;
+  __shared__ __align__(16) RegsSelectSmem<kThreads, 16> sm;
   const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
   int32_t* out_ids = p.selected + out_row * p.sel_stride;
-  clear_regs_select<kThreads>(sm);
+  clear_regs_select(sm);
   const int n = p.sealed[b];
   if (n < 0 || n > p.rep_stride || n > static_cast<int>(blockDim.x) * NC) {
     if (tid == 0) {
@@ -368,8 +366,9 @@ __global__ __launch_bounds__(kThreads) void select_scores_regs_kernel(const Para
   for (int i = 0; i < NC; ++i) cand[i] = dynamic && base + i >= bs.init_n && base + i < bs.local_first;
   __syncthreads();  // histograms zeroed
   uint32_t threshold = 0xffffffffu, equal_take = 0;
-  if (dynamic) radix_threshold_regs<kThreads, NC>(kr, cand, bs.k, sm, threshold, equal_take);
-  const int count = compact_ids_regs<kThreads, NC>(kr, cand, n, bs, threshold, equal_take, out_ids, p.sel_stride, sm);
+  if (dynamic) radix_threshold_regs<kThreads, NC, 16>(kr, cand, bs.k, sm, threshold, equal_take);
+  const int count =
+      compact_ids_regs<kThreads, NC, 16>(kr, cand, n, bs, threshold, equal_take, out_ids, p.sel_stride, sm);
   if (tid == 0) p.counts[out_row] = count;
 }
 

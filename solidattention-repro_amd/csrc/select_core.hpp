@@ -780,28 +780,30 @@ __device__ inline int select_ids_wave_regs(const uint32_t* keys, int n, const Bu
 // top digits, and 64 lanes adding into one LDS word serialise.  Each pass has
 // its own histogram set (zeroed once), so a pass costs two barriers; wave 0
 // sums the copies and scans the digits.
-constexpr int kRadixCopies = 16;
 constexpr int kRadixPad = 260;  // words per copy: 256 bins, 16-byte rows, 4 banks apart
 
-template <int kThreads>
+// kCopies histogram copies per pass: 16 where the workgroup has the compute
+// unit to itself (66.5 KB), fewer where the LDS bounds the workgroups a CU
+// holds (4 copies: 16.6 KB, up to 16 lanes per word in one instruction).
+template <int kThreads, int kCopies = 16>
 struct RegsSelectSmem {
-  uint32_t hist[4][kRadixCopies * kRadixPad];
+  uint32_t hist[4][kCopies * kRadixPad];
   uint32_t prefix[4];
   uint32_t remaining[4];
   uint32_t wave_sum[kThreads / kWave];
 };
 
-template <int kThreads>
-__device__ inline void clear_regs_select(RegsSelectSmem<kThreads>& sm) {
+template <int kThreads, int kCopies>
+__device__ inline void clear_regs_select(RegsSelectSmem<kThreads, kCopies>& sm) {
   uint4* h = reinterpret_cast<uint4*>(&sm.hist[0][0]);
-  for (int e = threadIdx.x; e < 4 * kRadixCopies * kRadixPad / 4; e += blockDim.x) h[e] = make_uint4(0, 0, 0, 0);
+  for (int e = threadIdx.x; e < 4 * kCopies * kRadixPad / 4; e += blockDim.x) h[e] = make_uint4(0, 0, 0, 0);
 }
 
 // k-th largest key among the candidates (cand[i]) and how many keys equal
 // to it are taken; k > 0.  clear_regs_select() and a barrier must precede.
-template <int kThreads, int NC>
+template <int kThreads, int NC, int kCopies>
 __device__ inline void radix_threshold_regs(const uint32_t (&kr)[NC], const bool (&cand)[NC], int k,
-                                            RegsSelectSmem<kThreads>& sm, uint32_t& threshold,
+                                            RegsSelectSmem<kThreads, kCopies>& sm, uint32_t& threshold,
                                             uint32_t& equal_take) {
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -809,7 +811,7 @@ __device__ inline void radix_threshold_regs(const uint32_t (&kr)[NC], const bool
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    uint32_t* h = sm.hist[pass] + (lane % kRadixCopies) * kRadixPad;
+    uint32_t* h = sm.hist[pass] + (lane % kCopies) * kRadixPad;
 #pragma unroll
     for (int i = 0; i < NC; ++i)
       if (cand[i] && (kr[i] & mask) == prefix) atomicAdd(&h[(kr[i] >> shift) & 255u], 1u);
@@ -818,7 +820,7 @@ __device__ inline void radix_threshold_regs(const uint32_t (&kr)[NC], const bool
       // lane covers digits 255-4*lane .. 252-4*lane (descending)
       uint32_t c[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int cp = 0; cp < kRadixCopies; ++cp) {
+      for (int cp = 0; cp < kCopies; ++cp) {
         const uint4 v = *reinterpret_cast<const uint4*>(sm.hist[pass] + cp * kRadixPad + 252 - 4 * lane);
         c[3] += v.x;
         c[2] += v.y;
@@ -850,10 +852,10 @@ __device__ inline void radix_threshold_regs(const uint32_t (&kr)[NC], const bool
 // lowest-id candidates equal to it up to equal_take.  One scan of the
 // per-thread (sure, equal) counts.  Returns the count (clamped to
 // sel_stride).
-template <int kThreads, int NC>
+template <int kThreads, int NC, int kCopies>
 __device__ inline int compact_ids_regs(const uint32_t (&kr)[NC], const bool (&cand)[NC], int n, const Budget& bs,
                                        uint32_t threshold, uint32_t equal_take, int32_t* out_ids, int sel_stride,
-                                       RegsSelectSmem<kThreads>& sm) {
+                                       RegsSelectSmem<kThreads, kCopies>& sm) {
   const int waves = static_cast<int>(blockDim.x) / kWave;
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -896,6 +898,43 @@ __device__ inline int compact_ids_regs(const uint32_t (&kr)[NC], const bool (&ca
   const int tot_eq = static_cast<int>(total & 0xffffu);
   const int count = static_cast<int>(total >> 16) + (tot_eq < take_eq ? tot_eq : take_eq);
   return count < sel_stride ? count : sel_stride;
+}
+
+// The selection of one list whose keys are in LDS (keys[0, n), n <= kThreads
+// NC): each thread takes NC contiguous keys into registers, then
+// radix_threshold_regs() and compact_ids_regs().  The histograms must be
+// zeroed (clear_regs_select() and a barrier, once per kernel) and keys[]
+// complete (a barrier).  Returns the count.
+template <int kThreads, int NC, int kCopies>
+__device__ inline int select_from_keys_regs(const uint32_t* keys, int n, const Budget& bs, int32_t* out_ids,
+                                            int sel_stride, RegsSelectSmem<kThreads, kCopies>& sm) {
+  const int base = NC * static_cast<int>(threadIdx.x);
+  const bool dynamic = bs.k > 0 && !bs.take_all;
+  uint32_t kr[NC];
+  bool cand[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int blk = base + i;
+    kr[i] = blk < n ? keys[blk] : 0u;
+    cand[i] = dynamic && blk >= bs.init_n && blk < bs.local_first;
+  }
+  uint32_t threshold = 0xffffffffu, equal_take = 0;
+  if (dynamic) radix_threshold_regs<kThreads, NC, kCopies>(kr, cand, bs.k, sm, threshold, equal_take);
+  return compact_ids_regs<kThreads, NC, kCopies>(kr, cand, n, bs, threshold, equal_take, out_ids, sel_stride, sm);
+}
+
+// select_from_keys_regs() with NC = 4 or 8, the smaller that covers n;
+// longer lists (more than 8 keys per thread) take the LDS radix select and
+// compaction (radix_threshold, compact_ids), so that the register form
+// does not raise the kernel's register count.  The same ids either way.
+template <int kThreads, int kCopies>
+__device__ inline int select_from_keys(const uint32_t* keys, int n, const Budget& bs, int32_t* out_ids, int sel_stride,
+                                       RegsSelectSmem<kThreads, kCopies>& sm, SelectSmem<kThreads / kWave>& lds) {
+  if (n <= kThreads * 4) return select_from_keys_regs<kThreads, 4, kCopies>(keys, n, bs, out_ids, sel_stride, sm);
+  if (n <= kThreads * 8) return select_from_keys_regs<kThreads, 8, kCopies>(keys, n, bs, out_ids, sel_stride, sm);
+  uint32_t threshold = 0xffffffffu, equal_take = 0;
+  if (bs.k > 0) radix_threshold<kThreads>(keys, bs, lds, threshold, equal_take);
+  return compact_ids<kThreads>(keys, n, bs, threshold, equal_take, out_ids, sel_stride, nullptr, lds);
 }
 
 // Single-wave selection of one list: forced blocks plus the k best
