@@ -117,8 +117,11 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
-  const int cb = blockIdx.x;
-  const int z = blockIdx.y;
+  // the K slice is the fastest-varying workgroup index: workgroups are
+  // dealt to the XCDs round robin, so each XCD's L2 holds the activation
+  // columns of one or two slices instead of all of them
+  const int z = blockIdx.x;
+  const int cb = blockIdx.y;
   const int mb = blockIdx.z;
   const int n0 = cb * C;
   const int m0 = mb * kRowsPerWg;
@@ -416,7 +419,7 @@ size_t split_part_bytes(int64_t rows, int64_t in, int64_t out, bool with_ss) {
 namespace {
 
 hipError_t launch_split(const SplitParams& p, const SplitShape& sh, int rb, hipStream_t stream) {
-  const dim3 grid(p.out / sh.cols, sh.slices, rb);
+  const dim3 grid(sh.slices, p.out / sh.cols, rb);
   if (sh.cols == 64) {
     if (p.gain) hipLaunchKernelGGL((proj_split_kernel<64, 256, true>), grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL((proj_split_kernel<64, 256, false>), grid, dim3(kThreads), 0, stream, p);
