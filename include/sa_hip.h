@@ -419,7 +419,7 @@ int sa_hip_seal(const sa_paged_kv* kv, int32_t local_tokens, int32_t* status,
 
 /* Workspace for sa_hip_local_causal_representatives: the window
  * probabilities and the received mass, tokens x query_heads x
- * (local_window + 1) floats. */
+ * (min(local_window, tokens) + 1) floats (0 when that overflows). */
 size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads,
                                            int32_t local_window);
 
@@ -427,8 +427,8 @@ size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads,
  * selection.cpp:12-94) on the GPU: every query position attends its local
  * causal window of `local_window` keys (fp32 softmax over sequential fp32
  * dots, scale 1/sqrt(head_dim)); each key's received mass is summed over the
- * queries in order; per 32-token block the `topk` keys with the most mass
- * (stable: ties keep token order) are averaged in rank order.
+ * queries in order; per block of block_tokens tokens the `topk` keys with
+ * the most mass (stable: ties keep token order) are averaged in rank order.
  *   prompt_queries  [query_heads][tokens][head_dim] fp32 (device)
  *   kv              [tokens][2][kv_heads][head_dim] FP16 bits (device, the
  *                   reference's interleaved token format)
@@ -441,8 +441,12 @@ size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads,
  * reference's std::exp(float)): the same table, polynomial and fused
  * multiply-adds in double, equal to it on every float, so the chosen tokens,
  * representatives and received masses are the reference's bit for bit.
- * Limits: head_dim 128, block_tokens 32, local_window <= 256, kv_heads <=
- * 65536; prompt_queries and kv 16-byte aligned. */
+ * Any head_dim, block_tokens and local_window, as in the reference: head_dim
+ * 128 with 32-token blocks and windows up to 256 run tiled kernels (LDS-
+ * staged queries and keys, several keys per lane), other shapes a wave per
+ * query and a wave per block; the results are the same bits either way.
+ * Limits: topk <= 16384, tokens x query_heads <= 2^31, kv_heads <= 65536;
+ * prompt_queries and kv 16-byte aligned. */
 int sa_hip_local_causal_representatives(
     const float* prompt_queries, const uint16_t* kv, int64_t tokens,
     int32_t query_heads, int32_t kv_heads, int32_t head_dim,

@@ -705,9 +705,16 @@ int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k, const floa
 
 // ---- InfLLM local-causal representatives (prefill) -----------------------------
 
+// A window of at least `tokens` keys starts every query's window at token 0,
+// exactly as a window of `tokens` keys does; the probability rows are sized
+// by the smaller one.
+static int32_t effective_window(int64_t tokens, int32_t local_window) {
+  return local_window > tokens ? static_cast<int32_t>(tokens) : local_window;
+}
+
 size_t sa_hip_local_causal_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t local_window) {
   if (tokens <= 0 || query_heads <= 0 || local_window <= 0) return 0;
-  return sa::local_causal_workspace_bytes(tokens, query_heads, local_window);
+  return sa::local_causal_workspace_bytes(tokens, query_heads, effective_window(tokens, local_window));
 }
 
 int sa_hip_local_causal_representatives(const float* prompt_queries, const uint16_t* kv, int64_t tokens,
@@ -719,14 +726,9 @@ int sa_hip_local_causal_representatives(const float* prompt_queries, const uint1
   if (!prompt_queries || !kv || tokens <= 0 || kv_heads <= 0 || query_heads % kv_heads != 0 ||
       block_tokens <= 0 || tokens % block_tokens != 0 || local_window <= 0 || topk <= 0 || topk > block_tokens)
     return fail(SA_HIP_EINVAL, "local_causal_representatives: invalid local-causal representative dimensions");
-  if (head_dim != sa::kHeadDim)
-    return fail(SA_HIP_EINVAL, "local_causal_representatives: head_dim %d unsupported (built for %d)", head_dim,
-                sa::kHeadDim);
-  if (block_tokens != SA_HIP_PAGE_TOKENS)
-    return fail(SA_HIP_EINVAL, "local_causal_representatives: block_tokens must be %d", SA_HIP_PAGE_TOKENS);
-  if (local_window > sa::kMaxLocalWindow)
-    return fail(SA_HIP_EINVAL, "local_causal_representatives: local_window %d above %d", local_window,
-                sa::kMaxLocalWindow);
+  if (head_dim <= 0) return fail(SA_HIP_EINVAL, "local_causal_representatives: head_dim must be positive");
+  if (topk > sa::kMaxGeneralTopk)
+    return fail(SA_HIP_EINVAL, "local_causal_representatives: topk %d above %d", topk, sa::kMaxGeneralTopk);
   if (tokens > (int64_t{1} << 31) / query_heads)
     return fail(SA_HIP_EINVAL, "local_causal_representatives: tokens x query_heads too large");
   if (!values && !reps && !offsets)
@@ -737,6 +739,7 @@ int sa_hip_local_causal_representatives(const float* prompt_queries, const uint1
   if (!aligned16(kv) || !aligned16(prompt_queries))
     return fail(SA_HIP_EINVAL, "local_causal_representatives: prompt_queries and kv must be 16-byte aligned");
   const size_t need = sa_hip_local_causal_workspace_bytes(tokens, query_heads, local_window);
+  if (need == 0) return fail(SA_HIP_EINVAL, "local_causal_representatives: workspace size overflows");
   if (!workspace || workspace_bytes < need)
     return fail(SA_HIP_EINVAL, "local_causal_representatives: workspace of %zu bytes needed, %zu given", need,
                 workspace_bytes);
@@ -751,7 +754,9 @@ int sa_hip_local_causal_representatives(const float* prompt_queries, const uint1
   r.tokens = tokens;
   r.query_heads = query_heads;
   r.kv_heads = kv_heads;
-  r.window = local_window;
+  r.head_dim = head_dim;
+  r.block_tokens = block_tokens;
+  r.window = effective_window(tokens, local_window);
   r.topk = topk;
   r.rep_stride = rep_stride;
   // the reference's scale: 1.0f / std::sqrt(static_cast<float>(head_dim)) (selection.cpp:26)

@@ -16,6 +16,9 @@
 //      query order, as the reference accumulates it), a stable descending
 //      rank (ties keep token order), the top-k token offsets, and the
 //      representative = sum of the chosen keys in rank order / k.
+// Those two kernels are tiled for head_dim 128, 32-token blocks and windows
+// up to 256; window_softmax_any_kernel and block_topk_any_kernel (below)
+// take any head_dim, block size and window with the same arithmetic.
 //
 // The exponential is expf_glibc(): the method of glibc 2.35's expf, which is
 // what the reference's std::exp(float) runs (a 32-entry 2^(i/32) table, a
@@ -59,6 +62,8 @@ struct Params {
   int64_t tokens;
   int32_t hq;
   int32_t hkv;
+  int32_t head_dim;      // the general kernels' (the tiled ones are built for D)
+  int32_t block_tokens;  // the general kernels' (the tiled ones: 32)
   int32_t window;
   int32_t topk;
   int32_t rep_stride;
@@ -440,6 +445,148 @@ __global__ __launch_bounds__(BPW * kWave) void block_topk_kernel(const Params p)
   }
 }
 
+// ---- general shapes: any head_dim, block size and window ------------------
+//
+// window_softmax_any_kernel: one wave per (query head h, query position q),
+// four per workgroup; lane l takes the window positions w = l, l + 64, ...
+//   1. each logit (sequential fp32 dot over head_dim, no contraction, times
+//      the scale) goes to the query's probability row, and the lanes' maxima
+//      are combined;
+//   2. in chunks of kAnyChunk positions the row's logits become
+//      exponentials (a lane rereads only the entries it wrote), the chunk is
+//      staged in LDS and every lane adds it to the denominator in window
+//      order;
+//   3. each entry is divided by the denominator.
+// VEC: head_dim a multiple of 8, rows read 16 bytes at a time.
+constexpr int kAnyWaves = 4;
+constexpr int kAnyChunk = 1024;
+
+template <bool VEC>
+__global__ __launch_bounds__(kAnyWaves * kWave) void window_softmax_any_kernel(const Params p) {
+  __shared__ __align__(16) float e_s[kAnyWaves][kAnyChunk];
+  int tile, h;
+  xcd_tile(p.hq, p.hkv, tile, h);
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int64_t q = static_cast<int64_t>(tile) * kAnyWaves + wave;
+  if (q >= p.tokens) return;  // a whole wave leaves; the kernel has no workgroup barrier
+  const int dim = p.head_dim;
+  const int g = h / (p.hq / p.hkv);
+  const int64_t token_elems = 2LL * p.hkv * dim;
+  const int64_t start = q + 1 > p.window ? q + 1 - p.window : 0;
+  const int count = static_cast<int>(q - start + 1);
+  const float* qrow = p.pq + (static_cast<int64_t>(h) * p.tokens + q) * dim;
+  float* row = p.prob + (static_cast<int64_t>(h) * p.tokens + q) * p.window;
+
+  float maximum = -__builtin_huge_valf();
+  for (int w = lane; w < count; w += kWave) {
+    const uint16_t* krow = p.kv + (start + w) * token_elems + static_cast<int64_t>(g) * dim;
+    float dot = 0.0f;
+    if (VEC) {
+      for (int d = 0; d < dim; d += 8) {
+        const uint4 kk = *reinterpret_cast<const uint4*>(krow + d);
+        const float4 qa = *reinterpret_cast<const float4*>(qrow + d);
+        const float4 qb = *reinterpret_cast<const float4*>(qrow + d + 4);
+        dot = dot + mul_h(qa.x, kk.x, 0);
+        dot = dot + mul_h(qa.y, kk.x, 1);
+        dot = dot + mul_h(qa.z, kk.y, 0);
+        dot = dot + mul_h(qa.w, kk.y, 1);
+        dot = dot + mul_h(qb.x, kk.z, 0);
+        dot = dot + mul_h(qb.y, kk.z, 1);
+        dot = dot + mul_h(qb.z, kk.w, 0);
+        dot = dot + mul_h(qb.w, kk.w, 1);
+      }
+    } else {
+      for (int d = 0; d < dim; ++d) dot = dot + mul_h(qrow[d], krow[d], 0);
+    }
+    const float logit = dot * p.scale;
+    row[w] = logit;
+    if (logit > maximum) maximum = logit;
+  }
+  // max over the wave (exact in any order)
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, off, kWave));
+
+  float denominator = 0.0f;
+  float* es = e_s[wave];
+  for (int c0 = 0; c0 < count; c0 += kAnyChunk) {
+    const int n = count - c0 < kAnyChunk ? count - c0 : kAnyChunk;
+    for (int i = lane; i < n; i += kWave) {  // c0 is a multiple of 64: entry c0 + i is this lane's
+      const float e = expf_glibc(row[c0 + i] - maximum);
+      row[c0 + i] = e;
+      es[i] = e;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) denominator = denominator + es[i];
+    // every lane has read the chunk before the next one overwrites it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  for (int w = lane; w < count; w += kWave) row[w] = row[w] / denominator;
+}
+
+// block_topk_any_kernel: one wave per (query head, block) of any size.
+// Each token's received mass is summed over the queries whose window holds
+// it, in ascending query order, and written to `received`; after a
+// workgroup barrier (which makes those writes visible to the whole wave)
+// each token's stable descending rank is counted against every token of
+// the block (mass_before / mass_tied: greater first, equal ones in token
+// order, NaN last), the top-k offsets are placed in LDS by rank, and the
+// representative of each head dimension is the sum of the chosen keys in
+// rank order / topk.
+__global__ __launch_bounds__(kWave) void block_topk_any_kernel(const Params p) {
+  extern __shared__ int order_s[];  // [topk]
+  int b, h;
+  xcd_tile(p.hq, p.hkv, b, h);
+  const int lane = threadIdx.x;
+  const int dim = p.head_dim;
+  const int bt = p.block_tokens;
+  const int W = p.window;
+  const int g = h / (p.hq / p.hkv);
+  const int64_t blocks = p.tokens / bt;
+  const int64_t t0 = static_cast<int64_t>(b) * bt;
+  float* rec = p.received + static_cast<int64_t>(h) * p.tokens;
+  const float* prob_h = p.prob + static_cast<int64_t>(h) * p.tokens * W;
+  for (int i = lane; i < bt; i += kWave) {
+    const int64_t t = t0 + i;
+    const int64_t q_end = t + W - 1 < p.tokens - 1 ? t + W - 1 : p.tokens - 1;
+    float r = 0.0f;
+    for (int64_t q = t; q <= q_end; ++q) {
+      const int64_t start = q + 1 > W ? q + 1 - W : 0;
+      r = r + prob_h[q * W + (t - start)];
+    }
+    rec[t] = r;
+  }
+  __syncthreads();
+  for (int i = lane; i < bt; i += kWave) {
+    const float ri = rec[t0 + i];
+    int rank = 0;
+    for (int j = 0; j < bt; ++j) {
+      const float rj = rec[t0 + j];
+      rank += static_cast<int>(mass_before(rj, ri)) | (static_cast<int>(mass_tied(rj, ri)) & static_cast<int>(j < i));
+    }
+    if (rank < p.topk) {
+      order_s[rank] = i;
+      if (p.offsets) p.offsets[(static_cast<int64_t>(h) * blocks + b) * p.topk + rank] = i;
+    }
+  }
+  __syncthreads();
+  const int64_t token_elems = 2LL * p.hkv * dim;
+  const uint16_t* kblock = p.kv + t0 * token_elems + static_cast<int64_t>(g) * dim;
+  const float k = static_cast<float>(p.topk);
+  for (int d = lane; d < dim; d += kWave) {
+    float sum = 0.0f;
+    for (int rk = 0; rk < p.topk; ++rk) sum = sum + lo_h2f(kblock[order_s[rk] * token_elems + d]);
+    const float v = sum / k;
+    if (p.values) p.values[(static_cast<int64_t>(h) * blocks + b) * dim + d] = v;
+    if (p.reps) p.reps[(static_cast<int64_t>(h) * dim + d) * p.rep_stride + b] = v;
+  }
+}
+
 template <int WL>
 void launch_window(const Params& p, hipStream_t stream) {
   constexpr int kQueriesPerGroup = window_threads<WL>() / WL;
@@ -454,7 +601,14 @@ void launch_window(const Params& p, hipStream_t stream) {
 }  // namespace
 
 size_t local_causal_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t window) {
-  return static_cast<size_t>(tokens) * query_heads * (static_cast<size_t>(window) + 1) * sizeof(float);
+  size_t rows = 0;
+  size_t floats = 0;
+  size_t bytes = 0;
+  if (__builtin_mul_overflow(static_cast<size_t>(tokens), static_cast<size_t>(query_heads), &rows) ||
+      __builtin_mul_overflow(rows, static_cast<size_t>(window) + 1, &floats) ||
+      __builtin_mul_overflow(floats, sizeof(float), &bytes))
+    return 0;  // too large to allocate
+  return bytes;
 }
 
 hipError_t launch_local_causal_representatives(const RepresentativeLaunch& r, hipStream_t stream) {
@@ -469,10 +623,25 @@ hipError_t launch_local_causal_representatives(const RepresentativeLaunch& r, hi
   p.tokens = r.tokens;
   p.hq = r.query_heads;
   p.hkv = r.kv_heads;
+  p.head_dim = r.head_dim;
+  p.block_tokens = r.block_tokens;
   p.window = r.window;
   p.topk = r.topk;
   p.rep_stride = r.rep_stride;
   p.scale = r.scale;
+  if (r.head_dim != D || r.block_tokens != kPageTokens || r.window > kMaxTiledLocalWindow) {
+    const int64_t blocks = r.tokens / r.block_tokens;
+    const bool vec = r.head_dim % 8 == 0 && reinterpret_cast<uintptr_t>(r.prompt_queries) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(r.kv) % 16 == 0;
+    const dim3 grid(static_cast<unsigned>((r.tokens + kAnyWaves - 1) / kAnyWaves), r.query_heads);
+    if (vec) hipLaunchKernelGGL((window_softmax_any_kernel<true>), grid, dim3(kAnyWaves * kWave), 0, stream, p);
+    else hipLaunchKernelGGL((window_softmax_any_kernel<false>), grid, dim3(kAnyWaves * kWave), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(block_topk_any_kernel, dim3(static_cast<unsigned>(blocks), r.query_heads), dim3(kWave),
+                       static_cast<size_t>(r.topk) * sizeof(int), stream, p);
+    return hipGetLastError();
+  }
   const int w = r.window;  // lanes per query: the power of two >= w / 4
   if (w <= 4) launch_window<1>(p, stream);
   else if (w <= 8) launch_window<2>(p, stream);

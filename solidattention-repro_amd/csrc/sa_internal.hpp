@@ -183,23 +183,29 @@ hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream)
 
 // InfLLM local-causal block representatives of a prefill (contiguous KV).
 struct RepresentativeLaunch {
-  const float* prompt_queries;  // [query_heads][tokens][128]
-  const uint16_t* kv;           // [tokens][2][kv_heads][128]
+  const float* prompt_queries;  // [query_heads][tokens][head_dim]
+  const uint16_t* kv;           // [tokens][2][kv_heads][head_dim]
   float* workspace;             // local_causal_workspace_bytes()
   float* received;              // [query_heads][tokens] or null (kept in the workspace)
-  float* values;                // [query_heads][blocks][128] or null
-  float* reps;                  // [query_heads][128][rep_stride] or null
+  float* values;                // [query_heads][blocks][head_dim] or null
+  float* reps;                  // [query_heads][head_dim][rep_stride] or null
   int32_t* offsets;             // [query_heads][blocks][topk] or null
   int64_t tokens;
   int32_t query_heads;
   int32_t kv_heads;
+  int32_t head_dim;
+  int32_t block_tokens;
   int32_t window;
   int32_t topk;
   int32_t rep_stride;
   float scale;
 };
 
-constexpr int kMaxLocalWindow = 256;
+// The tiled builder kernels take head_dim 128, 32-token blocks and windows
+// up to 256; other shapes run the general kernels, whose one limit is topk
+// (the chosen offsets of a block are ranked in LDS).
+constexpr int kMaxTiledLocalWindow = 256;
+constexpr int kMaxGeneralTopk = 16384;
 size_t local_causal_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t window);
 hipError_t launch_local_causal_representatives(const RepresentativeLaunch& r, hipStream_t stream);
 

@@ -722,18 +722,20 @@ def seal(kv: PagedKV, local_tokens, status=None, stream=None):
 
 
 def local_causal_representatives(prompt_queries, kv16, tokens, query_heads, kv_heads, window, topk, values=True,
-                                 offsets=True, reps=None, rep_stride=0, received=None, workspace=None, stream=None):
+                                 offsets=True, reps=None, rep_stride=0, received=None, workspace=None, stream=None,
+                                 head_dim=HEAD_DIM, block_tokens=PAGE_TOKENS):
     """InfLLM local-causal block representatives of a prefill (the
     reference's build_local_causal_representatives).  prompt_queries: fp32
-    [query_heads, tokens, 128]; kv16: uint16 [tokens, 2, kv_heads, 128].
-    Returns (values [hq, blocks, 128] or None, offsets int32 [hq, blocks,
-    topk] or None); reps (optional) is filled in the d-major layout.
-    workspace: a device tensor of at least
-    sa_hip_local_causal_workspace_bytes (allocated here when None)."""
+    [query_heads, tokens, head_dim]; kv16: uint16 [tokens, 2, kv_heads,
+    head_dim].  Returns (values [hq, blocks, head_dim] or None, offsets int32
+    [hq, blocks, topk] or None), blocks = tokens // block_tokens; reps
+    (optional) is filled in the d-major layout.  workspace: a device tensor
+    of at least sa_hip_local_causal_workspace_bytes (allocated here when
+    None)."""
     import torch
     dev = prompt_queries.device
-    blocks = tokens // PAGE_TOKENS
-    vals = torch.empty((query_heads, blocks, HEAD_DIM), dtype=torch.float32, device=dev) if values else None
+    blocks = tokens // block_tokens
+    vals = torch.empty((query_heads, blocks, head_dim), dtype=torch.float32, device=dev) if values else None
     offs = torch.empty((query_heads, blocks, topk), dtype=torch.int32, device=dev) if offsets else None
     nbytes = lib().sa_hip_local_causal_workspace_bytes(tokens, query_heads, window)
     if workspace is None:
@@ -742,7 +744,7 @@ def local_causal_representatives(prompt_queries, kv16, tokens, query_heads, kv_h
         ws = workspace
         nbytes = ws.numel() * ws.element_size()
     check(lib().sa_hip_local_causal_representatives(
-        _ptr(prompt_queries), _ptr(kv16), tokens, query_heads, kv_heads, HEAD_DIM, PAGE_TOKENS, window, topk,
+        _ptr(prompt_queries), _ptr(kv16), tokens, query_heads, kv_heads, head_dim, block_tokens, window, topk,
         _ptr(vals), _ptr(offs), _ptr(reps), rep_stride, _ptr(received), _ptr(ws), nbytes, _stream(stream)),
         "local_causal_representatives")
     return vals, offs

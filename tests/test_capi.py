@@ -127,19 +127,25 @@ def test_loads_next_to_torch_hip_runtime():
 
 def test_local_causal_argument_checks():
     """Invalid builder arguments are refused before any launch (the
-    reference's checks, selection.cpp:18-23, plus this build's limits)."""
+    reference's checks, selection.cpp:18-23, plus this build's limits:
+    topk <= 16384, aligned buffers, a large enough workspace).  Any
+    head_dim, block size and window pass the checks."""
     import solidattention_amd as sa
     L = sa.lib()
     fake = C.c_void_p(4096)
     assert L.sa_hip_local_causal_workspace_bytes(64, 4, 32) == 64 * 4 * 33 * 4
+    # a window past the prompt is the whole prompt: rows of `tokens` floats
+    assert L.sa_hip_local_causal_workspace_bytes(64, 4, 1000) == 64 * 4 * 65 * 4
+    assert L.sa_hip_local_causal_workspace_bytes(1 << 40, 1 << 30, 1 << 30) == 0  # overflows
 
     def call(tokens=64, hq=4, hkv=2, d=128, block=32, window=32, topk=4, values=fake, wsb=1 << 30, pq=fake, kv=fake):
         return L.sa_hip_local_causal_representatives(pq, kv, tokens, hq, hkv, d, block, window, topk, values,
                                                      None, None, 0, None, fake, wsb, None)
 
-    bad = [dict(tokens=65), dict(window=0), dict(window=257), dict(topk=0), dict(topk=33), dict(hq=3),
-           dict(d=64), dict(block=16), dict(values=None), dict(wsb=16), dict(pq=C.c_void_p(4100)),
-           dict(kv=C.c_void_p(4104)), dict(hq=65536 * 2, hkv=65536 * 2, tokens=32)]
+    bad = [dict(tokens=65), dict(window=0), dict(topk=0), dict(topk=33), dict(hq=3), dict(d=0), dict(block=0),
+           dict(block=24), dict(values=None), dict(wsb=16), dict(pq=C.c_void_p(4100)),
+           dict(kv=C.c_void_p(4104)), dict(hq=65536 * 2, hkv=65536 * 2, tokens=32),
+           dict(tokens=32768, block=32768, topk=16385)]
     for kw in bad:
         assert call(**kw) == -1, kw
         assert L.sa_hip_last_error()

@@ -30,28 +30,32 @@ pytestmark = pytest.mark.gpu
 GOLD = np.load(os.path.join(HERE, "reference_outputs.npz"), allow_pickle=False)
 
 
-def gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk, want_reps=False):
+def gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk, want_reps=False, d=128, block=32):
     dq = torch.from_numpy(np.ascontiguousarray(pq)).cuda()
     dkv = torch.from_numpy(np.ascontiguousarray(kv).view(np.int16)).cuda().view(torch.uint16)
     received = torch.empty((hq, tokens), dtype=torch.float32, device="cuda")
-    blocks = tokens // 32
+    blocks = tokens // block
     rep_stride = (blocks + 3) // 4 * 4
-    reps = torch.zeros((hq, 128, rep_stride), dtype=torch.float32, device="cuda") if want_reps else None
+    reps = torch.zeros((hq, d, rep_stride), dtype=torch.float32, device="cuda") if want_reps else None
     vals, offs = hip.local_causal_representatives(dq, dkv, tokens, hq, hkv, window, topk, reps=reps,
-                                                  rep_stride=rep_stride if want_reps else 0, received=received)
+                                                  rep_stride=rep_stride if want_reps else 0, received=received,
+                                                  head_dim=d, block_tokens=block)
     torch.cuda.synchronize()
     out = (vals.cpu().numpy(), offs.cpu().numpy().astype(np.int64), received.cpu().numpy())
     return out + ((reps.cpu().numpy()[:, :, :blocks],) if want_reps else ())
 
 
-def check_vs_oracle(hip, pq, kv, tokens, hq, hkv, window, topk):
-    vals, offs, rec = gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk)
-    evals, eoffs, erec = O.local_causal_representatives_restated(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
+def check_vs_oracle(hip, pq, kv, tokens, hq, hkv, window, topk, d=128, block=32, want_reps=False):
+    got = gpu_build(hip, pq, kv, tokens, hq, hkv, window, topk, want_reps=want_reps, d=d, block=block)
+    vals, offs, rec = got[:3]
+    evals, eoffs, erec = O.local_causal_representatives_restated(pq, kv, tokens, hq, hkv, d, block, window, topk)
     assert np.array_equal(rec.view(np.uint32), erec.view(np.uint32)), "received mass differs"
     assert np.array_equal(offs, eoffs.astype(np.int64)), "chosen offsets differ"
     assert np.array_equal(vals.view(np.uint32), evals.view(np.uint32)), "representative bits differ"
+    if want_reps:  # the d-major copy holds the same bits
+        assert np.array_equal(got[3].transpose(0, 2, 1).view(np.uint32), vals.view(np.uint32))
     # the reference's arithmetic: libm's expf
-    lvals, loffs = O.local_causal_representatives(pq, kv, tokens, hq, hkv, 128, 32, window, topk)
+    lvals, loffs = O.local_causal_representatives(pq, kv, tokens, hq, hkv, d, block, window, topk)
     assert np.array_equal(offs, loffs.astype(np.int64)), "chosen offsets differ from the libm builder"
     assert np.array_equal(vals.view(np.uint32), lvals.view(np.uint32)), "representative bits differ from libm"
 
@@ -78,6 +82,50 @@ def test_gpu_builder_vs_oracle(hip, window, topk, hq, hkv, tokens):
     pq = rng.standard_normal(hq * tokens * 128).astype(np.float32)
     kv = rng.standard_normal(tokens * 2 * hkv * 128).astype(np.float16).view(np.uint16)
     check_vs_oracle(hip, pq, kv, tokens, hq, hkv, window, topk)
+
+
+@pytest.mark.parametrize("d,block,window,topk,hq,hkv,tokens", [
+    (128, 32, 257, 4, 4, 2, 640),     # the first window past the tiled kernels
+    (128, 32, 1100, 8, 2, 1, 1280),   # windows over one 1024-entry denominator chunk
+    (128, 32, 5000, 4, 2, 2, 512),    # a window longer than the prompt
+    (64, 16, 48, 5, 8, 4, 160),       # head_dim 64, 16-token blocks
+    (36, 8, 20, 3, 4, 2, 96),         # head_dim not a multiple of 8 (2-byte key reads)
+    (256, 64, 100, 10, 4, 1, 256),    # head_dim 256, 64-token blocks
+    (128, 100, 64, 7, 2, 1, 300),     # blocks of 100 tokens (more than a wave's lanes)
+    (8, 1, 3, 1, 2, 2, 40),           # one-token blocks
+    (128, 32, 300, 32, 2, 2, 96)])    # topk = block_tokens
+def test_gpu_builder_general_shapes(hip, d, block, window, topk, hq, hkv, tokens):
+    """The reference's builder takes any head_dim, block size and window
+    (selection.cpp:12-23); shapes outside the tiled kernels' (head_dim 128,
+    32-token blocks, window <= 256) run the general kernels: received-mass
+    bits, offsets and representative bits equal the oracle's."""
+    print(f"case: d={d} block={block} window={window} topk={topk} hq={hq} hkv={hkv} tokens={tokens}", flush=True)
+    rng = np.random.default_rng(d * 131 + block * 7 + window)
+    pq = rng.standard_normal(hq * tokens * d).astype(np.float32)
+    kv = rng.standard_normal(tokens * 2 * hkv * d).astype(np.float16).view(np.uint16)
+    check_vs_oracle(hip, pq, kv, tokens, hq, hkv, window, topk, d=d, block=block, want_reps=True)
+
+
+def test_gpu_builder_general_shapes_ties_and_nan(hip):
+    """The general kernels' rank on repeated tokens (equal mass keeps token
+    order) and NaN masses (ranked last), at head_dim 64 with 48-token blocks
+    and a 300-token window."""
+    rng = np.random.default_rng(5)
+    d, block, tokens, hq, hkv, window, topk = 64, 48, 384, 4, 2, 300, 9
+    pq = rng.standard_normal((hq, tokens, d)).astype(np.float32)
+    pq[2, 200, 3] = np.nan
+    kv = rng.standard_normal((tokens, 2, hkv, d)).astype(np.float16)
+    kv[96:120] = kv[96]
+    vals, offs, rec = gpu_build(hip, pq, kv.view(np.uint16).ravel(), tokens, hq, hkv, window, topk, d=d,
+                                block=block)
+    evals, eoffs, erec = O.local_causal_representatives_restated(pq, kv.view(np.uint16).ravel(), tokens, hq, hkv,
+                                                                 d, block, window, topk)
+    assert np.isnan(erec).any()
+    assert np.array_equal(np.isnan(rec), np.isnan(erec))
+    finite = ~np.isnan(erec)
+    assert np.array_equal(rec[finite].view(np.uint32), erec[finite].view(np.uint32))
+    assert np.array_equal(offs, eoffs.astype(np.int64))
+    assert np.array_equal(vals.view(np.uint32), evals.view(np.uint32))
 
 
 @pytest.mark.parametrize("window", [32, 64])

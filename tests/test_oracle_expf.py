@@ -95,6 +95,25 @@ def test_restated_builder_equals_reference_builder(ref_lib, seed, tokens, hq, hk
     assert np.array_equal(vals.view(np.uint32).ravel(), np.asarray(rvals, np.float32).view(np.uint32).ravel())
 
 
+@pytest.mark.parametrize("d,block,window,topk,hq,hkv,tokens", [
+    (128, 32, 1100, 8, 2, 1, 1280), (128, 32, 5000, 4, 2, 2, 512), (64, 16, 48, 5, 8, 4, 160),
+    (36, 8, 20, 3, 4, 2, 96), (256, 64, 100, 10, 4, 1, 256), (128, 100, 64, 7, 2, 1, 300), (8, 1, 3, 1, 2, 2, 40)])
+def test_restated_builder_equals_reference_general_shapes(ref_lib, d, block, window, topk, hq, hkv, tokens):
+    """The shapes the general GPU kernels take (any head_dim, block size and
+    window, selection.cpp:12-23): offsets and representative bits equal the
+    reference's own builder, run from oracle/_ref."""
+    rng = np.random.default_rng(d * 131 + block * 7 + window)
+    pq = rng.standard_normal(hq * tokens * d).astype(np.float32)
+    kv = rng.standard_normal(tokens * 2 * hkv * d).astype(np.float16).view(np.uint16)
+    vals, offs, received = ref_lib.local_causal_representatives_restated(pq, kv, tokens, hq, hkv, d, block, window,
+                                                                         topk)
+    rvals, roffs = ref_lib.local_causal_representatives(pq, kv, tokens, hq, hkv, d, block, window, topk, use_ref=True)
+    assert np.array_equal(offs.astype(np.int64).ravel(), np.asarray(roffs).astype(np.int64).ravel())
+    assert np.array_equal(vals.view(np.uint32).ravel(), np.asarray(rvals, np.float32).view(np.uint32).ravel())
+    # every query spreads a mass of one over its window
+    assert abs(float(received.astype(np.float64).sum()) - hq * tokens) < 1e-3 * hq * tokens
+
+
 def test_restated_builder_c21_offset_hash(oracle_lib):
     """The published C2.1 golden: offset FNV hash 7873450381430813043
     (docs/cpp-versions/C2.1-infllm-selection-uring.md:40-42)."""
