@@ -200,11 +200,20 @@ __global__ __launch_bounds__(kRowThreads) void score_rows_kernel(const Params p)
   }
   __syncthreads();
   const float heads_f = static_cast<float>(p.heads_per_sel);
+  // dot / heads for a power-of-two head count (every shape here): the
+  // product with the exact reciprocal rounds the same exact value once, as
+  // the division does, so the bits are the division's
+  const bool pow2 = (p.heads_per_sel & (p.heads_per_sel - 1)) == 0;
+  const float inv = 1.0f / heads_f;
   float* row = p.scores + (static_cast<int64_t>(b) * p.select_groups + sg) * p.rep_stride;
   for (int t = tid; t < kBlocks; t += kRowThreads) {
     if (first + t >= n) break;
     float score = 0.0f;
-    for (int h = 0; h < p.heads_per_sel; ++h) score = score + dots[h][t] / heads_f;
+    if (pow2) {
+      for (int h = 0; h < p.heads_per_sel; ++h) score = score + dots[h][t] * inv;
+    } else {
+      for (int h = 0; h < p.heads_per_sel; ++h) score = score + dots[h][t] / heads_f;
+    }
     row[first + t] = score;
   }
 }

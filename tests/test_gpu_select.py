@@ -236,14 +236,49 @@ def test_selection_at_the_8192_block_limit(hip, split):
     assert (res[1].cpu().numpy() == 0).all()
 
 
-@pytest.mark.parametrize("lengths", [[32 * 4096, 32 * 4095 + 7], [32 * 64, 32 * 65 + 1, 32 * 1]])
+@pytest.mark.parametrize("lengths", [[32 * 4096, 32 * 4095 + 7], [32 * 64, 32 * 65 + 1, 32 * 1],
+                                     [32 * 128, 32 * 129 + 5, 32 * 256, 32 * 127]])
 def test_shared_selection_long_context_rows(hip, lengths):
     """The reference's shared mode at the long-context shape (32 query heads
     over 8 representative rows, 4096 blocks, budget 128 = 4 + 8 + 116) and
-    at lengths around one 64-block chunk: the split scoring spreads the rows
-    over waves; ids and score bits equal the oracle's."""
+    at lengths around one 64- and one 128-block chunk: the split scoring
+    spreads the rows over waves; ids (every form) and score bits equal the
+    oracle's."""
     case = make_case(135, len(lengths), 32, 8, lengths, planted=16)
-    check(hip, case, 1, 128, 4, 8, modes=("single", "split"))
+    check(hip, case, 1, 128, 4, 8)
+
+
+def test_shared_selection_chunked_at_the_8192_block_limit(hip):
+    """The shared mode (32 query heads, one list per sequence) in the
+    chunked form at 8192 blocks (the last chunk selects from keys in LDS,
+    past the register form's 4096), and a flagged 8193: ids equal the
+    oracle's, twice on one workspace."""
+    rng = np.random.default_rng(141)
+    n, hq, hkv, budget = 8192, 32, 8, 128
+    rep_stride = n + 4
+    kv = hip.PagedKV(1, hq, hkv, rep_stride, num_pages=4, rep_stride=rep_stride)
+    reps = rng.standard_normal((1, hkv, D, rep_stride)).astype(np.float32)
+    kv.reps.copy_(torch.from_numpy(reps))
+    kv.sealed.fill_(n)
+    kv.seq_len.fill_(n * 32)
+    q = rng.standard_normal((1, hq, D)).astype(np.float32)
+    st = status_tensor()
+    ws, _ = hip.score_select_chunked_workspace(kv, 1, budget, 4, 8)
+    esel, ecnt = O.paged_score_select(q, reps, np.array([n], np.int32), 1, hq, hkv, D, hkv, rep_stride, 1,
+                                      budget, 4, 8)
+    for call in range(2):
+        print(f"case: shared rows {n} blocks, call {call}", flush=True)
+        sel, cnt = hip.score_select_chunked(kv, to_dev(q), 1, budget, 4, 8, ws, status=st)
+        torch.cuda.synchronize()
+        assert int(st.item()) == 0
+        assert np.array_equal(cnt.cpu().numpy(), ecnt)
+        assert np.array_equal(sel.cpu().numpy(), esel)
+    kv.sealed.fill_(n + 1)
+    kv.seq_len.fill_((n + 1) * 32)
+    _, cnt = hip.score_select_chunked(kv, to_dev(q), 1, budget, 4, 8, ws, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    assert (cnt.cpu().numpy() == 0).all()
 
 
 @pytest.mark.parametrize("group", [4, 8])
