@@ -48,7 +48,18 @@ extern "C" {
  *               representatives, head_dim-major so that lanes reading
  *               consecutive blocks are coalesced.  rep_heads is kv_heads
  *               (one representative per KV head, shared by its query heads)
- *               or query_heads (one per query head). */
+ *               or query_heads (one per query head).
+ * head_dim: 128 everywhere; the reference's selection and attention take
+ * any head_dim, and so do sa_hip_append_seal(_f16), sa_hip_seal,
+ * sa_hip_score_select (given the scores buffer), sa_hip_score_select_split,
+ * sa_hip_sparse_decode_attention and sa_hip_decode_step(_f16): at any other
+ * multiple of 8 up to 512 they run general kernels (append + seal one
+ * workgroup per sequence; scoring one lane per block; attention over the
+ * page list; the decode step as those launches in sequence), with the same
+ * results (bit-exact selection and state, attention within fp32 rounding).
+ * The other entry points (chunked and split-phase attention, the chunked
+ * selection, select-attend, the online seal, the allocation-free step)
+ * refuse a head_dim other than 128 with SA_HIP_EINVAL. */
 typedef struct sa_paged_kv {
   uint16_t* pool;
   int32_t* block_table;
@@ -285,7 +296,9 @@ int sa_hip_select_attend(const sa_paged_kv* kv, const float* query,
 /* ---- R8/R9/R4 + R3 + R6 fused: one layer's whole decode step ------------- */
 
 /* Workspace of sa_hip_decode_step: `batch` int32 arrival counters (padded
- * to 256 bytes) followed by the attention's split records.  The caller
+ * to 256 bytes) followed by the attention's split records; at a head_dim
+ * other than 128 the records are padded to 256 bytes and followed by the
+ * selection's scores (batch x query_heads x rep_stride floats).  The caller
  * zeroes it ONCE before the first call; every call leaves the counters at
  * zero again.  Calls sharing a workspace must not run concurrently. */
 size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv,

@@ -40,11 +40,18 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_geometry(const sa_paged_kv* kv, const char* op) {
+// any_head_dim: the entry point also takes a head_dim other than 128 (any
+// multiple of 8 up to 512), which its general kernels serve.
+int check_geometry(const sa_paged_kv* kv, const char* op, bool any_head_dim = false) {
   if (!kv) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv", op);
-  if (kv->head_dim != sa::kHeadDim)
-    return fail(SA_HIP_EINVAL, "%s: head_dim %d unsupported (built for %d)", op, kv->head_dim,
-                sa::kHeadDim);
+  if (kv->head_dim != sa::kHeadDim) {
+    if (!any_head_dim)
+      return fail(SA_HIP_EINVAL, "%s: head_dim %d unsupported (this entry point is built for %d)", op,
+                  kv->head_dim, sa::kHeadDim);
+    if (kv->head_dim <= 0 || kv->head_dim % 8 != 0 || kv->head_dim > sa::kAnyMaxHeadDim)
+      return fail(SA_HIP_EINVAL, "%s: head_dim %d unsupported (128, or a multiple of 8 up to %d)", op,
+                  kv->head_dim, sa::kAnyMaxHeadDim);
+  }
   if (kv->kv_heads <= 0 || kv->query_heads <= 0 || kv->query_heads % kv->kv_heads != 0)
     return fail(SA_HIP_EINVAL, "%s: invalid GQA dimensions %d/%d", op, kv->query_heads, kv->kv_heads);
   const int group = kv->query_heads / kv->kv_heads;
@@ -214,10 +221,13 @@ static int attention_common(const sa_paged_kv* kv, const float* query, const int
   a.scale = scale;
   a.chunk_pages = chunk_pages;
   a.sched = sched;
+  a.head_dim = kv->head_dim;
   const size_t need =
       sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
   if (workspace_bytes < need || (need && !workspace))
     return fail(SA_HIP_EINVAL, "attention: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (sa::general_head_dim(a.head_dim))
+    return check_hip(sa::launch_paged_attention_any(a, as_stream(stream)), "attention launch");
   return check_hip(sa::launch_sparse_decode_attention(a, as_stream(stream)), "attention launch");
 }
 
@@ -225,7 +235,7 @@ int sa_hip_sparse_decode_attention(const sa_paged_kv* kv, const float* query, co
                                    const int32_t* counts, int32_t select_groups, int32_t sel_stride,
                                    float scale, float* out, void* workspace, size_t workspace_bytes,
                                    int32_t splits, int32_t* status, void* stream) {
-  if (int e = check_geometry(kv, "sparse_decode_attention")) return e;
+  if (int e = check_geometry(kv, "sparse_decode_attention", true)) return e;
   if (!query || !out || !selected || !counts)
     return fail(SA_HIP_EINVAL, "sparse_decode_attention: null query/out/selected/counts");
   if (!aligned16(query)) return fail(SA_HIP_EINVAL, "sparse_decode_attention: query must be 16-byte aligned");
@@ -416,7 +426,7 @@ static int online_check(const sa_paged_kv* kv, const sa_online_seal* seal, const
 static int select_launch(const sa_paged_kv* kv, const float* query, const sa_select_params* params,
                          int32_t* selected, int32_t* counts, float* scores, int32_t* status, const char* op,
                          sa::SelectLaunch* l) {
-  if (int e = check_geometry(kv, op)) return e;
+  if (int e = check_geometry(kv, op, true)) return e;
   if (int e = check_reps(kv, op)) return e;
   if (!params || !query || !selected || !counts)
     return fail(SA_HIP_EINVAL, "%s: null params/query/selected/counts", op);
@@ -427,6 +437,9 @@ static int select_launch(const sa_paged_kv* kv, const float* query, const sa_sel
   if (heads_per_sel > sa::kMaxSelectHeads)
     return fail(SA_HIP_EINVAL, "%s: %d query heads per selection group exceeds %d", op, heads_per_sel,
                 sa::kMaxSelectHeads);
+  if (sa::general_head_dim(kv->head_dim) && heads_per_sel * kv->head_dim > sa::kMaxAnySelectQuery)
+    return fail(SA_HIP_EINVAL, "%s: %d query heads x head_dim %d per selection group exceed %d floats", op,
+                heads_per_sel, kv->head_dim, sa::kMaxAnySelectQuery);
   if (s.budget_blocks <= 0 || s.init_blocks < 0 || s.local_blocks < 0 ||
       s.init_blocks + s.local_blocks > s.budget_blocks)
     return fail(SA_HIP_EINVAL, "%s: invalid representative selection dimensions "
@@ -452,6 +465,7 @@ static int select_launch(const sa_paged_kv* kv, const float* query, const sa_sel
   l->init_blocks = s.init_blocks;
   l->local_blocks = s.local_blocks;
   l->sel_stride = s.sel_stride;
+  l->head_dim = kv->head_dim;
   return SA_HIP_OK;
 }
 
@@ -459,6 +473,12 @@ int sa_hip_score_select(const sa_paged_kv* kv, const float* query, const sa_sele
                         int32_t* selected, int32_t* counts, float* scores, int32_t* status, void* stream) {
   sa::SelectLaunch l;
   if (int e = select_launch(kv, query, params, selected, counts, scores, status, "score_select", &l)) return e;
+  if (sa::general_head_dim(l.head_dim)) {
+    // the general scoring hands its scores to the selection launch
+    if (!scores)
+      return fail(SA_HIP_EINVAL, "score_select: head_dim %d needs the scores buffer", kv->head_dim);
+    return check_hip(sa::launch_score_select_split(l, as_stream(stream)), "score_select launch");
+  }
   return check_hip(sa::launch_score_select(l, as_stream(stream)), "score_select launch");
 }
 
@@ -481,6 +501,9 @@ int sa_hip_score_select_chunked(const sa_paged_kv* kv, const float* query, const
   sa::SelectLaunch l;
   if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, "score_select_chunked", &l))
     return e;
+  if (sa::general_head_dim(l.head_dim))
+    return fail(SA_HIP_EINVAL, "score_select_chunked: head_dim %d unsupported (128 only; sa_hip_score_select_split "
+                "takes any)", kv->head_dim);
   if (!sa::score_select_chunked_supported(l))
     return fail(SA_HIP_EINVAL, "score_select_chunked: representatives must be 16-byte aligned with rep_stride a "
                                "multiple of 4");
@@ -514,7 +537,7 @@ int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv, const sa_sele
 }
 
 int sa_hip_select_attend_fused(const sa_paged_kv* kv, const sa_select_params* params, int32_t splits) {
-  if (!kv || !params) return 0;
+  if (!kv || !params || kv->head_dim != sa::kHeadDim) return 0;
   return splits == 1 && sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups,
                                                     params->sel_stride, kv->reps, kv->rep_stride)
              ? 1
@@ -556,6 +579,9 @@ int sa_hip_select_attend(const sa_paged_kv* kv, const float* query, const sa_sel
                          int32_t splits, int32_t* status, void* stream) {
   sa::SelectLaunch l;
   if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, "select_attend", &l)) return e;
+  if (sa::general_head_dim(l.head_dim))
+    return fail(SA_HIP_EINVAL, "select_attend: head_dim %d unsupported (128 only; sa_hip_decode_step, or "
+                "sa_hip_score_select_split then sa_hip_sparse_decode_attention, take any)", kv->head_dim);
   if (!out) return fail(SA_HIP_EINVAL, "select_attend: null out");
   if (!aligned16(query)) return fail(SA_HIP_EINVAL, "select_attend: query must be 16-byte aligned");
   if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "select_attend: splits out of range");
@@ -573,8 +599,20 @@ int sa_hip_select_attend(const sa_paged_kv* kv, const float* query, const sa_sel
 // then the attention's split records when the step is not fused.
 static size_t arrive_bytes(int32_t batch) { return (static_cast<size_t>(batch) * 4 + 255) / 256 * 256; }
 
+// With a head_dim other than 128 the step runs its launches in sequence and
+// the selection's scores follow the records: [batch][query_heads][rep_stride]
+// floats (enough for any select_groups).
+static size_t split_records_bytes(const sa_paged_kv* kv, int32_t splits) {
+  return (sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits) + 255) /
+         256 * 256;
+}
+
 size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv, int32_t splits) {
   if (!kv || kv->batch <= 0) return 0;
+  if (sa::general_head_dim(kv->head_dim))
+    return arrive_bytes(kv->batch) + split_records_bytes(kv, splits) +
+           static_cast<size_t>(kv->batch) * kv->query_heads * (kv->rep_stride > 0 ? kv->rep_stride : 0) *
+               sizeof(float);
   return arrive_bytes(kv->batch) +
          sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
 }
@@ -601,6 +639,21 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
   if (!aligned16(ka) || !aligned16(va)) return fail(SA_HIP_EINVAL, "%s: k/v must be 16-byte aligned", op);
   if (seal)
     if (int e = online_check(kv, seal, query, local_tokens, op)) return e;
+  if (sa::general_head_dim(kv->head_dim)) {
+    // the general kernels in sequence: append + seal, scoring into the
+    // workspace's scores, selection, attention
+    if (seal) return fail(SA_HIP_EINVAL, "%s: the online seal is built for head_dim %d", op, sa::kHeadDim);
+    const size_t rb = split_records_bytes(kv, splits);
+    const size_t sb = static_cast<size_t>(kv->batch) * params->select_groups * kv->rep_stride * sizeof(float);
+    if (records_bytes < rb + sb)
+      return fail(SA_HIP_EINVAL, "%s: workspace too small for the records and scores", op);
+    l.scores = reinterpret_cast<float*>(static_cast<uint8_t*>(records) + rb);
+    if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op, query, nullptr)) return e;
+    if (int e = check_hip(sa::launch_score_select_split(l, as_stream(stream)), "decode_step: score_select launch"))
+      return e;
+    return attention_common(kv, query, selected, counts, params->select_groups, params->sel_stride, scale, out,
+                            records, rb, splits, status, stream, 0);
+  }
   if (!sa_hip_select_attend_fused(kv, params, splits)) {
     if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op, query, seal)) return e;
     if (int e = check_hip(sa::launch_score_select(l, as_stream(stream)), "decode_step: score_select launch"))
@@ -686,6 +739,8 @@ int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k, const floa
                                int32_t* counts, float* out, int32_t splits, int32_t* status, void* stream) {
   const char* op = "decode_step_noalloc";
   if (!kv || kv->batch <= 0) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv or empty batch", op);
+  if (kv->head_dim != sa::kHeadDim)
+    return fail(SA_HIP_EINVAL, "%s: head_dim %d unsupported (built for %d)", op, kv->head_dim, sa::kHeadDim);
   if (kv->batch > 65535) return fail(SA_HIP_EINVAL, "%s: batch %d out of range", op, kv->batch);
   if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "%s: splits out of range", op);
   // the fused launch needs only the counters; the unfused ones need records
@@ -769,7 +824,7 @@ int sa_hip_local_causal_representatives(const float* prompt_queries, const uint1
 static int lifecycle_common(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
                             const uint16_t* v16, int32_t local_tokens, int append, int32_t* status,
                             void* stream, const char* op, const float* query, const sa_online_seal* seal) {
-  if (int e = check_geometry(kv, op)) return e;
+  if (int e = check_geometry(kv, op, !seal)) return e;
   if (int e = check_reps(kv, op)) return e;
   if (local_tokens < 0) return fail(SA_HIP_EINVAL, "%s: local_tokens must be >= 0", op);
   if (append) {
@@ -797,6 +852,7 @@ static int lifecycle_common(const sa_paged_kv* kv, const float* k, const float* 
   l.rep_stride = kv->rep_stride;
   l.query_heads = kv->query_heads;
   l.kv_heads = kv->kv_heads;
+  l.head_dim = kv->head_dim;
   l.local_tokens = local_tokens;
   l.append = append;
   if (seal) {

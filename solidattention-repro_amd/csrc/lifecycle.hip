@@ -46,6 +46,7 @@ struct Params {
   int32_t group;
   int32_t local_tokens;
   int32_t append;
+  int32_t head_dim;       // D, or another multiple of 8 (append_seal_kernel<false> only)
   const float* query;     // online seal: this step's decode queries [batch][query_heads][D]
   online::Args online;
 };
@@ -116,17 +117,18 @@ __global__ __launch_bounds__(kThreads) void append_seal_kernel(const Params p) {
       ++added;
       continue;
     }
-    for (int o = tid; o < p.width; o += kThreads) {  // o = kv_head * D + d
+    const int hd = ONLINE ? D : p.head_dim;
+    for (int o = tid; o < p.width; o += kThreads) {  // o = kv_head * head_dim + d
       float sum = 0.0f;
 #pragma unroll 8
       for (int t = 0; t < kPageTokens; ++t) sum = sum + h2f(src[t * p.token_elems + o]);
       const float rep = sum / static_cast<float>(kPageTokens);
-      const int g = o / D;
-      const int d = o % D;
+      const int g = o / hd;
+      const int d = o % hd;
       // group == 1 for per-KV-head representatives; otherwise every query
       // head of the group receives the (identical) mean key.
       for (int j = 0; j < p.group; ++j)
-        p.reps[((static_cast<int64_t>(b) * p.rep_heads + g * p.group + j) * D + d) * p.rep_stride + s] =
+        p.reps[((static_cast<int64_t>(b) * p.rep_heads + g * p.group + j) * hd + d) * p.rep_stride + s] =
             rep;
     }
     ++s;
@@ -481,16 +483,22 @@ hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream) {
   p.k16 = l.k16;
   p.v16 = l.v16;
   p.num_pages = l.num_pages;
-  p.token_elems = 2 * l.kv_heads * D;
+  p.head_dim = general_head_dim(l.head_dim) ? l.head_dim : D;
+  p.token_elems = 2 * l.kv_heads * p.head_dim;
   p.page_elems = static_cast<int64_t>(kPageTokens) * p.token_elems;
-  p.width = l.kv_heads * D;
+  p.width = l.kv_heads * p.head_dim;
   p.table_stride = l.table_stride;
   p.rep_heads = l.rep_heads;
   p.rep_stride = l.rep_stride;
   p.group = l.rep_heads == l.kv_heads ? 1 : l.query_heads / l.kv_heads;
   p.local_tokens = l.local_tokens;
   p.append = l.append;
-  if (l.ring) {
+  if (p.head_dim != D) {
+    // another head_dim: one workgroup per sequence appends (when asked) and
+    // seals every block the tail rule releases (no ring: checked by the API)
+    if (l.ring) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(append_seal_kernel<false>, dim3(l.batch), dim3(kThreads), 0, stream, p);
+  } else if (l.ring) {
     p.query = l.query;
     p.online = online::Args{l.ring, l.ring_tokens, l.window, l.topk, l.query_heads, l.seal_scale};
     hipLaunchKernelGGL(append_seal_kernel<true>, dim3(l.batch), dim3(kThreads), 0, stream, p);

@@ -50,6 +50,8 @@ struct AttnLaunch {
   int32_t include_tail;
   int32_t chunk_pages;     // > 0 (mode 0): split by chunks of pages, `splits` chunks
   int32_t* sched;          // chunked: 2 x batch x kv_heads x splits int32 for the longest-first order, or null
+  int32_t head_dim;        // 0 or kHeadDim: the paged kernels; another multiple of 8 up to
+                           // kAnyMaxHeadDim: the general kernel (mode 0, no chunks)
 };
 
 hipError_t launch_sparse_decode_attention(const AttnLaunch& a, hipStream_t stream);
@@ -73,6 +75,7 @@ struct SelectLaunch {
   int32_t init_blocks;
   int32_t local_blocks;
   int32_t sel_stride;
+  int32_t head_dim;  // 0 or kHeadDim; another head_dim scores with the general kernel (split form only)
 };
 
 hipError_t launch_score_select(const SelectLaunch& s, hipStream_t stream);
@@ -228,6 +231,7 @@ struct LifecycleLaunch {
   int32_t rep_stride;
   int32_t query_heads;
   int32_t kv_heads;
+  int32_t head_dim; // 0 or kHeadDim; another head_dim appends and seals one workgroup per sequence
   int32_t local_tokens;
   int32_t append;   // 0: seal only
   // InfLLM online seal (ring non-null; rep_heads == query_heads): the
@@ -247,6 +251,13 @@ hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream);
 // Contiguous attention for head dimensions other than 128 (attention_any.hip):
 // multiples of 8 up to kAnyMaxHeadDim, 1/2/4/8 query heads per KV head.
 constexpr int kAnyMaxHeadDim = 512;
+// The paged path at a head_dim other than kHeadDim (any multiple of 8 up to
+// kAnyMaxHeadDim): attention over the selected blocks and the tail
+// (AttnLaunch mode 0, no chunks), with a merge of the splits in split order.
+hipError_t launch_paged_attention_any(const AttnLaunch& a, hipStream_t stream);
+inline bool general_head_dim(int32_t head_dim) { return head_dim != 0 && head_dim != kHeadDim; }
+// The general scoring keeps a selection group's query rows in LDS.
+constexpr int kMaxAnySelectQuery = 16384;  // heads_per_sel x head_dim floats (64 KiB)
 bool attention_any_supported(int32_t query_heads, int32_t kv_heads, int32_t head_dim);
 size_t attention_any_workspace_bytes(int64_t tokens, int32_t query_heads, int32_t kv_heads, int32_t head_dim);
 hipError_t launch_attention_any(const uint16_t* kv, const float* query, int64_t tokens, int32_t query_heads,

@@ -147,6 +147,45 @@ __global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params 
   }
 }
 
+// ---- scoring at a head_dim other than 128 -------------------------------------
+// One lane per block, 256 blocks of one list per workgroup, the group's query
+// rows in LDS: score = the sum over the group's query heads, in head order,
+// of (the sequential fp32 dot over head_dim) / heads: the reference's
+// select_shared_blocks arithmetic (selection.cpp:108-119) for any head_dim.
+// The lanes read consecutive blocks of each d-row of the d-major
+// representatives (coalesced).  The selection launch of the split form
+// follows.
+__global__ __launch_bounds__(kChunkBlocks) void score_any_kernel(const Params p, int head_dim) {
+  extern __shared__ __align__(16) float q_any[];  // [heads_per_sel][head_dim]
+  const int sg = blockIdx.x;
+  const int b = blockIdx.y;
+  const int first = blockIdx.z * kChunkBlocks;
+  const int n = p.sealed[b];
+  // invalid lengths are flagged by the selection kernel
+  if (n < 0 || n > p.rep_stride || n > kMaxSelectBlocks || first >= n) return;
+  const int hps = p.heads_per_sel;
+  const int h_first = sg * hps;
+  const float* q = p.query + (static_cast<int64_t>(b) * p.query_heads + h_first) * head_dim;
+  for (int e = threadIdx.x; e < hps * head_dim; e += kChunkBlocks) q_any[e] = q[e];
+  __syncthreads();
+  const int blk = first + static_cast<int>(threadIdx.x);
+  if (blk >= n) return;
+  const float heads_f = static_cast<float>(hps);
+  const int64_t stride = p.rep_stride;
+  float score = 0.0f;
+  for (int j = 0; j < hps; ++j) {
+    const int h = h_first + j;
+    const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
+    const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * head_dim * stride + blk;
+    const float* qh = q_any + j * head_dim;
+    float dot = 0.0f;
+#pragma unroll 8
+    for (int d = 0; d < head_dim; ++d) dot = dot + qh[d] * r[d * stride];
+    score = score + dot / heads_f;
+  }
+  p.scores[(static_cast<int64_t>(b) * p.select_groups + sg) * p.rep_stride + blk] = score;
+}
+
 // ---- split scoring of a group with several representative rows -----------
 // A selection group whose query heads read several representative rows (the
 // reference's shared mode: one block set over every query head, a row per KV
@@ -561,8 +600,11 @@ hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream) 
   const int chunks = (s.rep_stride + kChunkBlocks - 1) / kChunkBlocks;
   const dim3 grid(s.select_groups, s.batch, chunks);
   const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
-  // a group over four or more representative rows: a wave per row
-  if (p.heads_per_sel / gr >= kRowWaves / 2) {
+  if (general_head_dim(s.head_dim)) {
+    const size_t smem = static_cast<size_t>(p.heads_per_sel) * s.head_dim * sizeof(float);
+    hipLaunchKernelGGL(score_any_kernel, grid, dim3(kChunkBlocks), smem, stream, p, s.head_dim);
+  } else if (p.heads_per_sel / gr >= kRowWaves / 2) {
+    // a group over four or more representative rows: a wave per row
     switch (gr) {
       case 1: launch_rows<1>(p, s.batch, stream); break;
       case 2: launch_rows<2>(p, s.batch, stream); break;

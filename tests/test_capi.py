@@ -100,10 +100,17 @@ def test_invalid_arguments_fail_before_any_launch():
     import solidattention_amd as sa
     L = sa.lib()
     kv = sa.PagedKVStruct()
+    # the paged path takes 128 or another multiple of 8 up to 512; the
+    # chunked attention 128 only
+    for d in (100, 1024, 0):
+        kv.head_dim = d
+        rc = L.sa_hip_sparse_decode_attention(C.byref(kv), None, None, None, 1, 1, C.c_float(1.0), None, None, 0, 1,
+                                              None, None)
+        assert rc == -1 and b"head_dim %d" % d in L.sa_hip_last_error()
     kv.head_dim = 64
-    rc = L.sa_hip_sparse_decode_attention(C.byref(kv), None, None, None, 1, 1, C.c_float(1.0), None, None, 0, 1,
-                                          None, None)
-    assert rc == -1 and b"head_dim" in L.sa_hip_last_error()
+    rc = L.sa_hip_sparse_decode_attention_chunked(C.byref(kv), None, None, None, 1, 1, C.c_float(1.0), None, None,
+                                                  0, 2, 4, None, None)
+    assert rc == -1 and b"head_dim 64" in L.sa_hip_last_error()
     kv.head_dim, kv.query_heads, kv.kv_heads = 128, 12, 8
     rc = L.sa_hip_score_select(C.byref(kv), None, None, None, None, None, None, None)
     assert rc == -1 and b"GQA" in L.sa_hip_last_error()
