@@ -109,6 +109,7 @@ class PagedKvPool {
   std::size_t batch() const { return batch_; }
   std::size_t query_heads() const { return query_heads_; }
   std::size_t kv_heads() const { return kv_heads_; }
+  std::size_t head_dim() const { return head_dim_; }
   std::size_t table_stride() const { return table_stride_; }
   std::size_t rep_heads() const { return rep_heads_; }
   std::size_t rep_stride() const { return rep_stride_; }
@@ -180,7 +181,8 @@ class SparseDecoder {
         counts_(pool.batch() * params.select_groups),
         workspace_bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),
                                                           static_cast<int32_t>(pool.query_heads()),
-                                                          static_cast<int32_t>(pool.kv_heads()), 128, splits_)),
+                                                          static_cast<int32_t>(pool.kv_heads()),
+                                                          static_cast<int32_t>(pool.head_dim()), splits_)),
         workspace_((workspace_bytes_ + 3) / 4),
         step_splits_(fused_splits(pool, params, splits)),
         step_workspace_bytes_(step_bytes(pool, step_splits_)),
@@ -190,19 +192,24 @@ class SparseDecoder {
         // the partial records and the longest-list-first schedule
         chunk_workspace_bytes_(sa_hip_attention_chunked_workspace_bytes(static_cast<int32_t>(pool.batch()),
                                                                         static_cast<int32_t>(pool.query_heads()),
-                                                                        static_cast<int32_t>(pool.kv_heads()), 128,
+                                                                        static_cast<int32_t>(pool.kv_heads()),
+                                                                        static_cast<int32_t>(pool.head_dim()),
                                                                         max_chunks_)),
-        chunk_workspace_((chunk_workspace_bytes_ + 3) / 4) {}
+        chunk_workspace_((chunk_workspace_bytes_ + 3) / 4),
+        // at a head_dim other than 128 the scoring hands its scores to the
+        // selection through this buffer
+        scores_(pool.head_dim() == 128 ? 0 : pool.batch() * params.select_groups * pool.rep_stride()) {}
 
-  // Score every sealed block against the query [batch][query_heads][128]
+  // Score every sealed block against the query [batch][query_heads][head_dim]
   // (device) and select per group; ids stay on the device.
   void select(const PagedKvPool& pool, const float* query, hipStream_t stream = nullptr,
               float* scores = nullptr, int32_t* status = nullptr) {
     const sa_paged_kv kv = pool.view();
+    if (!scores && scores_.size()) scores = scores_.get();
     check(sa_hip_score_select(&kv, query, &params_, selected_.get(), counts_.get(), scores, status, stream),
           "score_select");
   }
-  // out [batch][query_heads][128] fp32 (device).
+  // out [batch][query_heads][head_dim] fp32 (device).
   void attend(const PagedKvPool& pool, const float* query, float scale, float* out,
               hipStream_t stream = nullptr, int32_t* status = nullptr) {
     const sa_paged_kv kv = pool.view();
@@ -236,7 +243,8 @@ class SparseDecoder {
   }
   // One layer's decode step: pool.append_seal(k, v, local_tokens) then
   // select_attend(); one launch when fused() is true.  k, v: fp32
-  // [batch][kv_heads][128] on the device.
+  // [batch][kv_heads][head_dim] on the device.  (select_attend() is built
+  // for head_dim 128; decode_step() takes any multiple of 8 up to 512.)
   void decode_step(const PagedKvPool& pool, const float* k, const float* v, int local_tokens, const float* query,
                    float scale, float* out, hipStream_t stream = nullptr, int32_t* status = nullptr) {
     const sa_paged_kv kv = pool.view();
@@ -275,6 +283,7 @@ class SparseDecoder {
   int max_chunks_;
   std::size_t chunk_workspace_bytes_;
   DeviceArray<float> chunk_workspace_;
+  DeviceArray<float> scores_;
 
   static int chunks_for(int sel_stride, int chunk_pages) {
     if (chunk_pages < 1) throw std::runtime_error("SparseDecoder: chunk_pages must be positive");
@@ -387,7 +396,8 @@ class SplitAttention {
       : total_(total_splits),
         bytes_(sa_hip_attention_workspace_bytes(static_cast<int32_t>(pool.batch()),
                                                 static_cast<int32_t>(pool.query_heads()),
-                                                static_cast<int32_t>(pool.kv_heads()), 128, total_splits)),
+                                                static_cast<int32_t>(pool.kv_heads()),
+                                                static_cast<int32_t>(pool.head_dim()), total_splits)),
         workspace_((bytes_ + 3) / 4) {
     if (total_splits < 2) throw std::runtime_error("SplitAttention: total_splits must be >= 2");
   }
@@ -400,7 +410,7 @@ class SplitAttention {
                                                  total_, status, stream),
           "sparse_decode_attention_partial");
   }
-  // out [batch][query_heads][128] fp32 (device).
+  // out [batch][query_heads][head_dim] fp32 (device).
   void merge(const PagedKvPool& pool, float* out, hipStream_t stream = nullptr) {
     const sa_paged_kv kv = pool.view();
     check(sa_hip_attention_merge(&kv, workspace_.get(), bytes_, total_, out, stream), "attention_merge");

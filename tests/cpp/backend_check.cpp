@@ -247,13 +247,15 @@ void check_lifecycle() {
 }
 
 // Decode steps through SparseDecoder::decode_step (one fused launch per
-// step at G=2): 4 sequences, 34 steps across seal boundaries, against the
+// step at G=2 and head_dim 128; the general kernels in sequence at another
+// head_dim): 4 sequences, 34 steps across seal boundaries, against the
 // oracle's append, seal, select and attention (qwen_chain_main.cpp:390-395,
-// kv_lifecycle_main.cpp:92-113, selection.cpp:96-147).
-void check_decode_step() {
-  const std::size_t batch = 4, hq = 16, hkv = 8, d = 128, stride = 24, pages = batch * stride;
+// kv_lifecycle_main.cpp:92-113, selection.cpp:96-147).  Record names carry
+// `tag`.
+void check_decode_step(std::size_t d = 128, const std::string& tag = "") {
+  const std::size_t batch = 4, hq = 16, hkv = 8, stride = 24, pages = batch * stride;
   const std::size_t budget = 8, steps = 34;
-  sa::hip::PagedKvPool pool(batch, hq, hkv, stride, pages);
+  sa::hip::PagedKvPool pool(batch, hq, hkv, stride, pages, 0, 0, d);
   const std::size_t page_elems = pool.page_elems();
   std::vector<std::uint16_t> host_pool(pages * page_elems);
   sao_synth_fill_half(31, 0, host_pool.size(), host_pool.data());
@@ -273,7 +275,8 @@ void check_decode_step() {
   pool.reps().upload(reps);
   sa::hip::SparseDecoder dec(pool, sa_select_params{static_cast<int32_t>(hkv), static_cast<int32_t>(budget), 1, 2,
                                                     static_cast<int32_t>(budget), 0, nullptr});
-  record("decode_step_fused", dec.fused(pool) ? "true" : "false", dec.fused(pool));
+  // fused at head_dim 128 only
+  record("decode_step_fused" + tag, dec.fused(pool) ? "true" : "false", dec.fused(pool) == (d == 128));
   sa::hip::DeviceArray<float> dk(batch * hkv * d), dv(batch * hkv * d), dq(batch * hq * d), dout(batch * hq * d);
   std::vector<float> k(batch * hkv * d), v(batch * hkv * d), q(batch * hq * d), out(batch * hq * d);
   std::vector<int32_t> sel(batch * hkv * budget), cnt(batch * hkv);
@@ -311,9 +314,22 @@ void check_decode_step() {
                         pool.generation().download() == gen && pool.pool().download() == host_pool;
   const auto greps = pool.reps().download();
   const bool reps_ok = std::memcmp(greps.data(), reps.data(), reps.size() * sizeof(float)) == 0;
-  record("decode_step_selected_ids_exact", ids_ok ? "true" : "false", ids_ok);
-  record("decode_step_state_bytes_exact", state_ok && reps_ok ? "true" : "false", state_ok && reps_ok);
-  record("decode_step_max_rel_error", num(max_err), max_err <= 2e-3);
+  record("decode_step_selected_ids_exact" + tag, ids_ok ? "true" : "false", ids_ok);
+  record("decode_step_state_bytes_exact" + tag, state_ok && reps_ok ? "true" : "false", state_ok && reps_ok);
+  record("decode_step_max_rel_error" + tag, num(max_err), max_err <= 2e-3);
+  if (d != 128) {
+    // select() + attend() over the last step's query (the general scoring
+    // hands its scores over through the decoder's own buffer)
+    dec.select(pool, dq.get());
+    dec.attend(pool, dq.get(), scale, dout.get());
+    const auto gout = dout.download();
+    double err = 0.0;
+    for (std::size_t i = 0; i < out.size(); ++i)
+      err = std::max(err, std::abs(static_cast<double>(out[i]) - gout[i]) /
+                              std::max(1.0, std::abs(static_cast<double>(out[i]))));
+    record("select_attend_max_rel_error" + tag, num(err), err <= 2e-3);
+    return;
+  }
 
   // the chunked schedule over the last step's selection: 3-page chunks of
   // lists of up to 9 pages, against the oracle's attention of that step
@@ -346,6 +362,8 @@ int main() {
     check_c2(*backend);
     check_lifecycle();
     check_decode_step();
+    check_decode_step(64, "_head_dim_64");
+    check_decode_step(256, "_head_dim_256");
     g_json << "\n}\n";
     std::cout << g_json.str();
     return g_ok ? 0 : 2;
