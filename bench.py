@@ -162,7 +162,7 @@ class Layer:
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU: the KV-cache hot path is measured at its "
+        print(json.dumps({"error": "the benchmark runs on one GPU: the KV-cache hot path is measured at its "
                                    "real per-GPU shape; --gpus must be 1"}))
         sys.exit(2)
     if args.workload == "correction":

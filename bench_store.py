@@ -18,7 +18,8 @@ shape (16 query / 8 KV heads, head_dim 128, 128 KiB pages), batch 64,
    the current copies; reported as GB/s of the read, the copy and the whole
    bridge.
 The reference's tier runs on io_uring and a local SSD; the figures here are
-the GPU box's file system, so they describe the bridge, not a drive.
+those of the host's file system (wherever the store file lies), so they
+describe the bridge, not a drive.
 """
 from __future__ import annotations
 

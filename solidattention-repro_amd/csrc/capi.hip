@@ -777,7 +777,7 @@ int sa_hip_local_causal_representatives(const float* prompt_queries, const uint1
                                         int32_t block_tokens, int32_t local_window, int32_t topk, float* values,
                                         int32_t* offsets, float* reps, int32_t rep_stride, float* received,
                                         void* workspace, size_t workspace_bytes, void* stream) {
-  // the reference's argument checks (selection.cpp:18-23), then this build's limits
+  // the reference's argument checks (selection.cpp:18-23), then the library's limits
   if (!prompt_queries || !kv || tokens <= 0 || kv_heads <= 0 || query_heads % kv_heads != 0 ||
       block_tokens <= 0 || tokens % block_tokens != 0 || local_window <= 0 || topk <= 0 || topk > block_tokens)
     return fail(SA_HIP_EINVAL, "local_causal_representatives: invalid local-causal representative dimensions");

@@ -134,7 +134,7 @@ def test_loads_next_to_torch_hip_runtime():
 
 def test_local_causal_argument_checks():
     """Invalid builder arguments are refused before any launch (the
-    reference's checks, selection.cpp:18-23, plus this build's limits:
+    reference's checks, selection.cpp:18-23, plus the library's limits:
     topk <= 16384, aligned buffers, a large enough workspace).  Any
     head_dim, block size and window pass the checks."""
     import solidattention_amd as sa
