@@ -127,10 +127,12 @@ __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_at
   constexpr bool kStaged = G == 4 || G == 8;
   constexpr int kStageBytes = kWavesPerGroup * kStageVecs * 16;
   constexpr int kPbufFloats = (G * 32 + G + 3) / 4 * 4;
-  constexpr int kSmemBytes = kStaged ? kStageBytes + kWavesPerGroup * kPbufFloats * 4
-                                     : static_cast<int>(sizeof(CombineSmem<G, kWavesPerGroup>));
+  constexpr int kSmemBytes = kStaged ? kStageBytes : static_cast<int>(sizeof(CombineSmem<G, kWavesPerGroup>));
   static_assert(!kStaged || sizeof(CombineSmem<G, kWavesPerGroup>) <= kStageBytes, "combine fits the stage");
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
+  // the probabilities' LDS buffer is its own variable, so that its stores do
+  // not wait for the staging loads in flight into smem
+  __shared__ __align__(16) float pbuf_s[kStaged ? kWavesPerGroup * kPbufFloats : 1];
 
   int start, end, step;
   bool owns_last;  // this workgroup's range holds the list's last position
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(waves_per_group<G>() * kWave) void sparse_decode_at
     const bool split_last = L.total > L.n_sel && L.len % kPageTokens != 0;
     const int walk_end = split_last ? min(end, L.total - 1) : end;
     st.reset();
-    float* pbuf = reinterpret_cast<float*>(smem + kStageBytes) + wave * kPbufFloats;
+    float* pbuf = pbuf_s + wave * kPbufFloats;
     st.attend_staged_mfma(p.v, b, L, start, walk_end, step, lg, lane, g,
                           reinterpret_cast<uint4*>(smem) + wave * kStageVecs, pbuf, q_group, p.qscale);
     if (split_last && owns_last) {

@@ -537,7 +537,6 @@ struct WaveState {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           *reinterpret_cast<float2*>(pbuf + (col * 4 + r) * kIters + 2 * kq) = make_float2(sv[r], sv[4 + r]);
-        if (kq == 0) pbuf[G * 32 + col] = corr;
       }
       // the wave's LDS operations complete in issue order: the reads below
       // see the writes above
@@ -551,11 +550,10 @@ struct WaveState {
         p[h][0] = a.x; p[h][1] = a.y; p[h][2] = a.z; p[h][3] = a.w;
         p[h][4] = c.x; p[h][5] = c.y; p[h][6] = c.z; p[h][7] = c.w;
       }
+      // head h's rescale factor is the one lane h (column h) computed
 #pragma unroll
-      for (int h = 0; h < G; h += 4) {
-        const float4 c = *reinterpret_cast<const float4*>(pbuf + G * 32 + h);
-        cr[h] = c.x; cr[h + 1] = c.y; cr[h + 2] = c.z; cr[h + 3] = c.w;
-      }
+      for (int h = 0; h < G; ++h)
+        cr[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), h));
       __builtin_amdgcn_wave_barrier();
       if (valid < kPageTokens) {
         // rows past the tail were not staged: their slot holds stale bytes

@@ -514,14 +514,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_staged(const Params p)
   const int wave = tid / kWave;
   const int lane = tid % kWave;
 
-  __shared__ __align__(16) unsigned char smem[kStageBytes + kWaves * kPbufFloats * 4];
+  // The probabilities' LDS buffer is its own variable: the compiler then
+  // knows the staging loads in flight (into smem) do not write it, and its
+  // stores need not wait for them (one variable for both made every page's
+  // P.V wait for the next page's staging loads to land).
+  __shared__ __align__(16) unsigned char smem[kStageBytes];
+  __shared__ __align__(16) float pbuf_s[kWaves * kPbufFloats];
   __shared__ __align__(16) float q_t[G * D];
   __shared__ uint32_t hist[256];
   __shared__ ClaimSmem cl;
   __shared__ int32_t late_ids[kStagedIds + kTailPages];  // the selected ids, then (in place) the late pages
   uint32_t* keys = reinterpret_cast<uint32_t*>(smem);
   uint4* stage = reinterpret_cast<uint4*>(smem) + wave * attn::kStageVecs;
-  float* pbuf = reinterpret_cast<float*>(smem + kStageBytes) + wave * kPbufFloats;
+  float* pbuf = pbuf_s + wave * kPbufFloats;
   const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
 
   const int64_t out_row = static_cast<int64_t>(b) * p.v.kv_heads + g;
