@@ -359,40 +359,22 @@ __global__ __launch_bounds__(kThreads) void score_select_chunked_kernel(const Pa
 }
 
 // The selection of the split form: one workgroup per list, the list's
-// scores held in registers (kRegsKeys contiguous blocks per thread, the
-// workgroup sized by the launch to the representative row, at most 1024
-// threads: 8192 blocks), radix_threshold_regs() and compact_ids_regs().  The
-// same ids as score_select_kernel.
+// scores held in registers, radix_threshold_regs() and compact_ids_regs();
+// the same ids as score_select_kernel.  The workgroup is sized by the launch
+// to the representative row at 4 blocks per thread, at most 1024 threads;
+// a list longer than 4 per thread (rows past 4096 blocks) takes 8 per
+// thread (8192 blocks).  More threads with fewer keys each measured faster:
+// the radix passes and the compaction cost each thread's keys in turn (8
+// lists of 4096 blocks: 5.9-6.0 us at 4 per thread, 6.6-6.7 at 8, 8.7 at
+// 16, 12.8 at 32).
 constexpr int kRegsThreads = 1024;
-constexpr int kRegsKeys = 8;
-static_assert(kRegsThreads * kRegsKeys >= kMaxSelectBlocks, "every selectable block in registers");
+constexpr int kRegsKeys = 4;
+static_assert(kRegsThreads * 2 * kRegsKeys >= kMaxSelectBlocks, "every selectable block in registers");
 
 template <int kThreads, int NC>
-__global__ __launch_bounds__(kThreads) void select_scores_regs_kernel(const Params p) {
-  const int sg = blockIdx.x;
-  const int b = blockIdx.y;
+__device__ inline int select_scores_regs(const Params& p, const float* row, int n, const Budget& bs,
+                                         int32_t* out_ids, RegsSelectSmem<kThreads, 16>& sm) {
   const int tid = threadIdx.x;
-  __shared__ __align__(16) RegsSelectSmem<kThreads, 16> sm;
-  const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
-  int32_t* out_ids = p.selected + out_row * p.sel_stride;
-  clear_regs_select(sm);
-  const int n = p.sealed[b];
-  if (n < 0 || n > p.rep_stride || n > static_cast<int>(blockDim.x) * NC) {
-    if (tid == 0) {
-      flag_status(p.status, kStatusCapacity);
-      p.counts[out_row] = 0;
-    }
-    return;
-  }
-  const Budget bs = budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
-  if (bs.bad) {
-    if (tid == 0) {
-      flag_status(p.status, kStatusBadBudget);
-      p.counts[out_row] = 0;
-    }
-    return;
-  }
-  const float* row = p.scores + out_row * p.rep_stride;
   const int base = NC * tid;
   uint32_t kr[NC];
   if (base + NC <= n && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
@@ -415,8 +397,39 @@ __global__ __launch_bounds__(kThreads) void select_scores_regs_kernel(const Para
   __syncthreads();  // histograms zeroed
   uint32_t threshold = 0xffffffffu, equal_take = 0;
   if (dynamic) radix_threshold_regs<kThreads, NC, 16>(kr, cand, bs.k, sm, threshold, equal_take);
-  const int count =
-      compact_ids_regs<kThreads, NC, 16>(kr, cand, n, bs, threshold, equal_take, out_ids, p.sel_stride, sm);
+  return compact_ids_regs<kThreads, NC, 16>(kr, cand, n, bs, threshold, equal_take, out_ids, p.sel_stride, sm);
+}
+
+template <int kThreads, int NC>
+__global__ __launch_bounds__(kThreads) void select_scores_regs_kernel(const Params p) {
+  const int sg = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  __shared__ __align__(16) RegsSelectSmem<kThreads, 16> sm;
+  const int64_t out_row = static_cast<int64_t>(b) * p.select_groups + sg;
+  int32_t* out_ids = p.selected + out_row * p.sel_stride;
+  clear_regs_select(sm);
+  const int n = p.sealed[b];
+  if (n < 0 || n > p.rep_stride || n > static_cast<int>(blockDim.x) * 2 * NC) {
+    if (tid == 0) {
+      flag_status(p.status, kStatusCapacity);
+      p.counts[out_row] = 0;
+    }
+    return;
+  }
+  const Budget bs = budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride);
+  if (bs.bad) {
+    if (tid == 0) {
+      flag_status(p.status, kStatusBadBudget);
+      p.counts[out_row] = 0;
+    }
+    return;
+  }
+  const float* row = p.scores + out_row * p.rep_stride;
+  // uniform per list: NC keys per thread when they cover it, else 2 NC
+  const int count = n <= static_cast<int>(blockDim.x) * NC
+                        ? select_scores_regs<kThreads, NC>(p, row, n, bs, out_ids, sm)
+                        : select_scores_regs<kThreads, 2 * NC>(p, row, n, bs, out_ids, sm);
   if (tid == 0) p.counts[out_row] = count;
 }
 
@@ -623,10 +636,12 @@ hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream) 
   }
   const hipError_t e0 = hipGetLastError();
   if (e0 != hipSuccess) return e0;
-  // enough whole waves for every block of the row (the blocks past 8192 are
-  // refused by the kernel)
+  // enough whole waves for every block of the row at kRegsKeys per thread,
+  // at most 16 (the kernel takes twice as many per thread beyond 4096 blocks
+  // and refuses the blocks past 8192)
   const int keys = s.rep_stride < kMaxSelectBlocks ? s.rep_stride : kMaxSelectBlocks;
-  const int waves = (keys + kRegsKeys * kWave - 1) / (kRegsKeys * kWave);
+  int waves = (keys + kRegsKeys * kWave - 1) / (kRegsKeys * kWave);
+  if (waves > kRegsThreads / kWave) waves = kRegsThreads / kWave;
   hipLaunchKernelGGL((select_scores_regs_kernel<kRegsThreads, kRegsKeys>), dim3(s.select_groups, s.batch),
                      dim3(waves * kWave), 0, stream, p);
   return hipGetLastError();
