@@ -73,13 +73,14 @@ def parse():
     ap.add_argument("--prefetch-blocks", type=int, default=128,
                     help="store workload: blocks per store -> pool prefetch batch")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "correction", "represent", "stress", "store", "layer"],
+                    choices=["decode", "correction", "represent", "stress", "store", "layer", "shared"],
                     help="decode: the headline decode step; correction: long-context miss correction "
                          "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage); "
                          "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4); "
                          "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers; "
                          "store: seal writeback behind decoding and store -> pool prefetch; "
-                         "layer: decode step with its q/k/v producer and o-proj consumer")
+                         "layer: decode step with its q/k/v producer and o-proj consumer; "
+                         "shared: one block set over all heads, 1 sequence x 2048 tokens, one launch vs split")
     ap.add_argument("--select", default="auto", choices=["auto", "single", "split", "chunked"],
                     help="separate selection launch: one workgroup per list, scoring split over 256-block "
                          "workgroups (two launches), lists in chunks of 1024-2048 blocks (one launch), or the default "
@@ -180,6 +181,10 @@ def main():
     if args.workload == "store":
         import bench_store
         bench_store.run(args)
+        return
+    if args.workload == "shared":
+        import bench_shared
+        bench_shared.run(args)
         return
     if args.workload == "layer":
         import bench_layer

@@ -271,10 +271,16 @@ int sa_hip_score_select_split_preferred(const sa_paged_kv* kv,
  * params->select_groups, params->sel_stride, scale, out, workspace,
  * workspace_bytes, splits, status): the same selected ids and counts (bit-
  * exact) and the same attention output (within fp32 rounding).  When
- * sa_hip_select_attend_fused() is 1 (select_groups == kv_heads, 1 or 2 query
- * heads per KV head, splits == 1) it runs as ONE launch, one workgroup per
+ * sa_hip_select_attend_fused() is 1 it runs as ONE launch, one workgroup per
  * (sequence, KV head) that scores, selects, keeps the ids on chip and
- * attends; otherwise as the two launches.  splits >= 1; workspace as for
+ * attends; otherwise as the two launches.  Fused: splits == 1 and either
+ * select_groups == kv_heads with 1, 2 or 4 query heads per KV head (4: also
+ * sel_stride <= 2048 and an even rep_stride with 8-byte aligned
+ * representatives), or the shared selection (select_groups 1) with 1 or 2
+ * query heads per KV head, representatives per KV head, rep_stride <= 256
+ * and batch x kv_heads x (kv_heads - 1) x rep_stride x 512 bytes <= 32 MiB
+ * (every workgroup of a sequence scores the whole shared set, so the
+ * representatives are read once per KV head).  splits >= 1; workspace as for
  * sa_hip_sparse_decode_attention.  Replaces the reference's per-layer
  * select -> pack -> attention sequence (selection_main.cpp:178-230;
  * pipeline_main.cpp:803-876) with selection on the GPU. */
@@ -282,7 +288,8 @@ int sa_hip_select_attend_fused(const sa_paged_kv* kv,
                                const sa_select_params* params, int32_t splits);
 /* The split count to pass to sa_hip_select_attend / sa_hip_decode_step: 1
  * (the fused launch) when the fused kernel applies and its workgroups fill
- * the device (batch x kv_heads >= 2 x CUs); otherwise
+ * the device (batch x kv_heads >= 2 x CUs), or for the shared selection's
+ * one launch whenever it applies; otherwise
  * sa_hip_attention_splits_for(batch, query_heads, kv_heads, budget_blocks + 2) for the
  * separate launches. */
 int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv,
@@ -296,9 +303,10 @@ int sa_hip_select_attend(const sa_paged_kv* kv, const float* query,
 /* ---- R8/R9/R4 + R3 + R6 fused: one layer's whole decode step ------------- */
 
 /* Workspace of sa_hip_decode_step: `batch` int32 arrival counters (padded
- * to 256 bytes) followed by the attention's split records; at a head_dim
- * other than 128 the records are padded to 256 bytes and followed by the
- * selection's scores (batch x query_heads x rep_stride floats).  The caller
+ * to 256 bytes) followed by the attention's split records (padded to 256
+ * bytes) and the split selection's scores (batch x query_heads x rep_stride
+ * floats; used when the step runs as separate launches with few lists, and
+ * at every head_dim other than 128).  The caller
  * zeroes it ONCE before the first call; every call leaves the counters at
  * zero again.  Calls sharing a workspace must not run concurrently. */
 size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv,
@@ -309,8 +317,11 @@ size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv,
  * the same page bytes, representatives, seq_len/sealed/generation, selected
  * ids (bit-exact) and attention output (within fp32 rounding).  When
  * sa_hip_select_attend_fused() is 1 it is ONE launch: each (sequence, KV
- * head) workgroup appends and seals its own head, then scores, selects and
- * attends; the last workgroup of a sequence to arrive writes its counters.
+ * head) workgroup appends and seals its own head (with the shared selection:
+ * seals every KV head's representative, identical values in every
+ * workgroup), then scores, selects and attends; the last workgroup of a
+ * sequence to arrive writes its counters.  The online seal (the _online
+ * variant) runs as one launch only with select_groups == kv_heads.
  * Otherwise it runs the three launches.  The _f16 variant takes raw FP16
  * K/V bits like sa_hip_append_seal_f16.  Replaces the reference's per-layer
  * decode sequence of append_fp16_kv (qwen_layer_main.cpp:270-281 via
@@ -390,9 +401,12 @@ int sa_hip_decode_step_online(const sa_paged_kv* kv, const float* k,
  * the process ends; its device address is looked up on the first call on a
  * device.  The arrival counters are cleared by a small kernel on `stream`
  * before every fused launch.  Limit: launches whose split records
- * (sa_hip_decode_step_workspace_bytes(kv, splits) minus the counters) exceed
- * SA_HIP_NOALLOC_SCRATCH_BYTES - SA_HIP_NOALLOC_COUNTER_BYTES are refused
- * with SA_HIP_EINVAL (the fused launch, splits == 1, needs no records).
+ * (sa_hip_attention_workspace_bytes(batch, query_heads, kv_heads, head_dim,
+ * splits)) exceed SA_HIP_NOALLOC_SCRATCH_BYTES - SA_HIP_NOALLOC_COUNTER_BYTES
+ * are refused with SA_HIP_EINVAL (the fused launch, splits == 1, needs no
+ * records); the split selection keeps its scores after the records only
+ * where the array holds them (else the one-workgroup-per-list selection:
+ * the same ids).
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (unordered streams, or host threads) race and give wrong results; order
  * them on one stream.  Results equal sa_hip_decode_step's.

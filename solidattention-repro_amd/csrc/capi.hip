@@ -533,13 +533,20 @@ int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv, const sa_sele
       static_cast<int64_t>(kv->batch) * kv->kv_heads >=
           sa::select_attend_per_cu(kv->query_heads, kv->kv_heads) * static_cast<int64_t>(sa::compute_units()))
     return 1;
+  // the shared selection's one launch (short lists, few sequences) against
+  // its three or four split launches
+  if (sa::select_attend_shared_supported(kv->batch, kv->query_heads, kv->kv_heads, kv->rep_heads,
+                                         params->select_groups, kv->rep_stride))
+    return 1;
   return sa_hip_attention_splits_for(kv->batch, kv->query_heads, kv->kv_heads, params->budget_blocks + 2);
 }
 
 int sa_hip_select_attend_fused(const sa_paged_kv* kv, const sa_select_params* params, int32_t splits) {
-  if (!kv || !params || kv->head_dim != sa::kHeadDim) return 0;
-  return splits == 1 && sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups,
-                                                    params->sel_stride, kv->reps, kv->rep_stride)
+  if (!kv || !params || kv->head_dim != sa::kHeadDim || splits != 1) return 0;
+  return sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups, params->sel_stride,
+                                     kv->reps, kv->rep_stride) ||
+                 sa::select_attend_shared_supported(kv->batch, kv->query_heads, kv->kv_heads, kv->rep_heads,
+                                                    params->select_groups, kv->rep_stride)
              ? 1
              : 0;
 }
@@ -570,6 +577,7 @@ static sa::SelectAttendLaunch fused_launch(const sa_paged_kv* kv, const sa::Sele
   f.init_blocks = l.init_blocks;
   f.local_blocks = l.local_blocks;
   f.sel_stride = l.sel_stride;
+  f.select_groups = l.select_groups;
   f.scale = scale;
   return f;
 }
@@ -599,22 +607,22 @@ int sa_hip_select_attend(const sa_paged_kv* kv, const float* query, const sa_sel
 // then the attention's split records when the step is not fused.
 static size_t arrive_bytes(int32_t batch) { return (static_cast<size_t>(batch) * 4 + 255) / 256 * 256; }
 
-// With a head_dim other than 128 the step runs its launches in sequence and
-// the selection's scores follow the records: [batch][query_heads][rep_stride]
-// floats (enough for any select_groups).
+// When the step runs as separate launches its split selection (the only
+// scoring at a head_dim other than 128; at 128 the shared selection's, for
+// few lists) keeps the scores after the records: [batch][query_heads]
+// [rep_stride] floats (enough for any select_groups).
 static size_t split_records_bytes(const sa_paged_kv* kv, int32_t splits) {
   return (sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits) + 255) /
          256 * 256;
 }
 
+static size_t split_scores_bytes(const sa_paged_kv* kv, int32_t select_groups) {
+  return static_cast<size_t>(kv->batch) * select_groups * (kv->rep_stride > 0 ? kv->rep_stride : 0) * sizeof(float);
+}
+
 size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv, int32_t splits) {
   if (!kv || kv->batch <= 0) return 0;
-  if (sa::general_head_dim(kv->head_dim))
-    return arrive_bytes(kv->batch) + split_records_bytes(kv, splits) +
-           static_cast<size_t>(kv->batch) * kv->query_heads * (kv->rep_stride > 0 ? kv->rep_stride : 0) *
-               sizeof(float);
-  return arrive_bytes(kv->batch) +
-         sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
+  return arrive_bytes(kv->batch) + split_records_bytes(kv, splits) + split_scores_bytes(kv, kv->query_heads);
 }
 
 // The decode step on explicit scratch: `arrive` holds kv->batch arrival
@@ -644,7 +652,7 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
     // workspace's scores, selection, attention
     if (seal) return fail(SA_HIP_EINVAL, "%s: the online seal is built for head_dim %d", op, sa::kHeadDim);
     const size_t rb = split_records_bytes(kv, splits);
-    const size_t sb = static_cast<size_t>(kv->batch) * params->select_groups * kv->rep_stride * sizeof(float);
+    const size_t sb = split_scores_bytes(kv, params->select_groups);
     if (records_bytes < rb + sb)
       return fail(SA_HIP_EINVAL, "%s: workspace too small for the records and scores", op);
     l.scores = reinterpret_cast<float*>(static_cast<uint8_t*>(records) + rb);
@@ -654,10 +662,23 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
     return attention_common(kv, query, selected, counts, params->select_groups, params->sel_stride, scale, out,
                             records, rb, splits, status, stream, 0);
   }
-  if (!sa_hip_select_attend_fused(kv, params, splits)) {
+  // (the online seal's one launch selects per KV group)
+  const bool fused =
+      sa_hip_select_attend_fused(kv, params, splits) && !(seal && params->select_groups != kv->kv_heads);
+  if (!fused) {
     if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op, query, seal)) return e;
-    if (int e = check_hip(sa::launch_score_select(l, as_stream(stream)), "decode_step: score_select launch"))
+    // few lists: the split selection (scoring spread over the device, the
+    // scores after the records) where the scratch holds the scores; the same
+    // ids as the one-workgroup-per-list selection
+    const size_t rb = split_records_bytes(kv, splits);
+    if (sa_hip_score_select_split_preferred(kv, params) &&
+        records_bytes >= rb + split_scores_bytes(kv, params->select_groups)) {
+      l.scores = reinterpret_cast<float*>(static_cast<uint8_t*>(records) + rb);
+      if (int e = check_hip(sa::launch_score_select_split(l, as_stream(stream)), "decode_step: score_select launch"))
+        return e;
+    } else if (int e = check_hip(sa::launch_score_select(l, as_stream(stream)), "decode_step: score_select launch")) {
       return e;
+    }
     return attention_common(kv, query, selected, counts, params->select_groups, params->sel_stride, scale, out,
                             records, records_bytes, splits, status, stream, 0);
   }
@@ -744,7 +765,9 @@ int sa_hip_decode_step_noalloc(const sa_paged_kv* kv, const float* k, const floa
   if (kv->batch > 65535) return fail(SA_HIP_EINVAL, "%s: batch %d out of range", op, kv->batch);
   if (splits < 1 || splits > 1024) return fail(SA_HIP_EINVAL, "%s: splits out of range", op);
   // the fused launch needs only the counters; the unfused ones need records
-  const size_t records = sa_hip_decode_step_workspace_bytes(kv, splits) - arrive_bytes(kv->batch);
+  // (and keep the split selection's scores after them where they fit)
+  const size_t records =
+      sa_hip_attention_workspace_bytes(kv->batch, kv->query_heads, kv->kv_heads, kv->head_dim, splits);
   if (records > kNoallocScratchBytes - kNoallocCounterBytes)
     return fail(SA_HIP_EINVAL, "%s: %zu bytes of split records exceed the %zu-byte static scratch (fewer splits "
                 "or a smaller batch, or sa_hip_decode_step with a workspace)", op, records,

@@ -13,6 +13,9 @@ constexpr int kPartPad = 4;        // floats before the accumulator in a partial
 constexpr int kMaxSelectBlocks = 8192;
 constexpr int kMaxSelectHeads = 32;
 constexpr int kMaxStagedSelected = 2048;  // selected ids per list the fused kernel at 4 heads per KV head holds
+// Longest shared list (one block set over every query head) the one-launch
+// decode step takes: each of its workgroups scores the whole shared set.
+constexpr int kMaxSharedFusedBlocks = 256;
 
 // Partial-result record of one (sequence, KV head, split, query head):
 // [0] running max (log2 domain), [1] denominator, [kPartPad, kPartPad + D)
@@ -132,8 +135,8 @@ hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream);
 int compute_units();
 
 // Fused (append + seal +) score + select + attend, one workgroup per
-// (sequence, KV head); select_groups is kv_heads.  Supported for 1 or 2
-// query heads per KV head.
+// (sequence, KV head); select_groups is kv_heads, or 1 (the shared selection,
+// select_attend_shared_supported()).
 struct SelectAttendLaunch {
   const uint16_t* pool;
   const int32_t* table;
@@ -158,6 +161,7 @@ struct SelectAttendLaunch {
   int32_t init_blocks;
   int32_t local_blocks;
   int32_t sel_stride;
+  int32_t select_groups;  // kv_heads (a block set per KV group), or 1 (shared)
   float scale;
   // decode step: append one token per sequence (fp32 k/v or FP16 k16/v16),
   // seal, then select + attend; arrive = [batch] zeroed arrival counters
@@ -182,6 +186,12 @@ struct SelectAttendLaunch {
 bool select_attend_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups, int32_t sel_stride,
                              const float* reps, int32_t rep_stride);
 int select_attend_per_cu(int32_t query_heads, int32_t kv_heads);
+// The one-launch form of the shared selection (select_groups 1 over several
+// KV heads): 1-2 query heads per KV head, representatives per KV head,
+// rep_stride <= kMaxSharedFusedBlocks, and the representatives read once per
+// KV head (every workgroup scores the whole set) within a small byte budget.
+bool select_attend_shared_supported(int32_t batch, int32_t query_heads, int32_t kv_heads, int32_t rep_heads,
+                                    int32_t select_groups, int32_t rep_stride);
 hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream);
 
 // InfLLM local-causal block representatives of a prefill (contiguous KV).

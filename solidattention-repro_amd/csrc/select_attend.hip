@@ -489,6 +489,197 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   if (APPEND && tid == 0) commit_sequence(p, b, len, n, commit);
 }
 
+// ---- shared selection: one block set per sequence over every query head -----
+// The reference's shared mode (select_shared_blocks over all heads,
+// selection.cpp:96-147, as its selection and pipeline drivers call it,
+// selection_main.cpp:178-181, pipeline_main.cpp:480-499) as one launch.
+// Every workgroup of a sequence (one per KV head) scores the whole shared set
+// itself, so that no workgroup waits on another: a wave per representative
+// row computes its query heads' dots (each the sequential fp32 sum over d),
+// the dots meet in LDS, and one lane per block adds dot / heads in head
+// order: the arithmetic of the split scoring (score_rows_kernel), so the
+// scores are bit-identical.  Every workgroup then selects the same ids; the
+// workgroup of KV head 0 writes them.  Each workgroup reads the sequence's
+// representatives once per KV head, so the launch takes short lists only
+// (shared_fused_supported()).
+//
+// A step that seals a block computes every KV head's representative of it in
+// every workgroup and writes them all (the values are identical: the same
+// sums of the same FP16 keys in token order; the new token's key comes from
+// the step's input, as its own workgroup stores it to the page in this
+// launch), so the scoring reads only representatives written by its own
+// workgroup or by earlier launches.
+template <bool F16>
+__device__ inline bool append_seal_shared(const Params& p, int b, int g, int64_t& len, int& n, int& added) {
+  const int tid = threadIdx.x;
+  const int64_t page = table_page(p.v, b, len / kPageTokens);
+  if (page < 0) {
+    if (tid == 0) flag_status(p.v.status, kStatusCapacity);
+    return false;
+  }
+  if (tid < kWave) store_token_quad(p, page, len, g, tid, token_quad<F16>(p, b, g, tid));
+  const int64_t pos = len;  // the new token
+  len += 1;
+  const int kv = p.v.kv_heads;
+  while (len >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens) {
+    const int64_t sp = n < p.rep_stride ? table_page(p.v, b, n) : -1;
+    if (sp < 0) {
+      if (tid == 0) flag_status(p.v.status, kStatusCapacity);
+      break;
+    }
+    const int64_t first = static_cast<int64_t>(n) * kPageTokens;
+    for (int e = tid; e < kv * D; e += kThreads) {
+      const int h = e / D;
+      const int d = e % D;
+      const int64_t in = (static_cast<int64_t>(b) * kv + h) * D + d;
+      const uint16_t fresh = F16 ? p.k16[in] : f2h_rne(p.k[in]);
+      const uint16_t* src = p.v.pool + sp * p.v.page_elems + h * D + d;
+      float sum = 0.0f;
+#pragma unroll 8
+      for (int t = 0; t < kPageTokens; ++t) sum = sum + h2f(first + t == pos ? fresh : src[t * p.v.token_elems]);
+      p.reps[((static_cast<int64_t>(b) * p.rep_heads + h) * D + d) * p.rep_stride + n] =
+          sum / static_cast<float>(kPageTokens);
+    }
+    ++n;
+    ++added;
+  }
+  return true;
+}
+
+// G = query heads per KV head (1 or 2; representatives per KV head, G heads
+// per representative row); APPEND: decode step; F16: raw FP16 K/V input.
+template <int G, bool APPEND, bool F16>
+__global__ __launch_bounds__(kThreads) void decode_kernel_shared(const Params p) {
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+
+  __shared__ __align__(16) float q_t[kMaxSelectHeads * D];
+  __shared__ float dots[kMaxSelectHeads][kWave + 1];
+  // block keys, then the selected ids, then the late pages; the register
+  // selection reads n rounded up to a multiple of 256 keys
+  __shared__ uint32_t keys[kMaxSharedFusedBlocks + kTailPages];
+  __shared__ uint32_t hist[256];
+  __shared__ attn::CombineSmem<G, kWaves> cs;
+  __shared__ ClaimSmem cl;
+  static_assert(kMaxSharedFusedBlocks % 256 == 0, "whole register selections");
+
+  const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
+  int64_t len = p.seq_len[b];
+  int n = p.sealed[b];
+
+  SeqCommit commit{};
+  if (APPEND) {
+    commit.gen = p.generation ? p.generation[b] : 0;
+    commit.appended = append_seal_shared<F16>(p, b, g, len, n, commit.added);
+    if (tid == 0) commit.arrived = atomicAdd(&p.arrive[b], 1);
+  }
+
+  attn::WaveState<G> st;
+  const attn::LaneGeom lg = attn::lane_geom(p.v, g, lane);
+
+  // ---- score the shared set (every query head); forced pages looked up -------
+  const bool n_ok = n >= 0 && n <= p.rep_stride && n <= kMaxSharedFusedBlocks;
+  const sel::Budget bs =
+      n_ok ? sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride)
+           : sel::Budget{0, 0, 0, false, true};
+  const Forced fb = forced_blocks(bs, n);
+  const int32_t early = wave == kWaves - 1 ? early_page(p, b, n, fb, lane) : -1;
+  if (n_ok && !bs.take_all) {  // (a budget that takes every block needs no scores)
+    sel::ScoreArgs a{};
+    a.query = p.query;
+    a.reps = p.reps;
+    a.b = b;
+    a.h_first = 0;
+    a.heads_per_sel = p.query_heads;
+    a.query_heads = p.query_heads;
+    a.group = G;
+    a.rep_heads = p.rep_heads;
+    a.rep_stride = p.rep_stride;
+    sel::load_query_t<kThreads>(a, q_t);
+    __syncthreads();  // the query, and the representatives this workgroup sealed
+    const int hps = p.query_heads;
+    const float heads_f = static_cast<float>(hps);
+    // dot / heads for a power-of-two head count: the product with the exact
+    // reciprocal rounds the same exact value once, as the division does
+    const bool pow2 = (hps & (hps - 1)) == 0;
+    const float inv = 1.0f / heads_f;
+    for (int c0 = 0; c0 < n; c0 += kWave) {
+      const int blk = c0 + lane;
+      if (blk < n) {
+        for (int h0 = wave * G; h0 < hps; h0 += kWaves * G) {
+          float dot[G][1];
+          sel::row_dots<G, 1, 32>(a, q_t, blk, h0, dot);
+#pragma unroll
+          for (int j = 0; j < G; ++j) dots[h0 + j][lane] = dot[j][0];
+        }
+      }
+      __syncthreads();
+      if (tid < kWave && c0 + tid < n) {
+        float score = 0.0f;
+        if (pow2) {
+          for (int h = 0; h < hps; ++h) score = score + dots[h][tid] * inv;
+        } else {
+          for (int h = 0; h < hps; ++h) score = score + dots[h][tid] / heads_f;
+        }
+        keys[c0 + tid] = sel::order_key(score);
+      }
+      __syncthreads();
+    }
+  }
+  if (wave == kWaves - 1) cl.early[lane] = early;
+  if (tid == 0) cl.late_ready = 0;
+  st.init(q_group, p.qscale, lg.col);
+  int wn = n;
+  int64_t wlen = len;
+  if (wn < 0 || wlen < static_cast<int64_t>(wn) * kPageTokens) {
+    if (tid == 0) flag_status(p.v.status, kStatusBadLength);
+    if (wn < 0) wn = 0;
+    wlen = static_cast<int64_t>(wn) * kPageTokens;
+  }
+  const int tail_pages = static_cast<int>((wlen - static_cast<int64_t>(wn) * kPageTokens + kPageTokens - 1) /
+                                          kPageTokens);
+  __syncthreads();  // keys, the early pages and the flag visible
+
+  // ---- select (wave 0; the workgroup of KV head 0 writes the ids) and walk ----
+  int32_t* late = reinterpret_cast<int32_t*>(keys);
+  if (wave == 0) {
+    int count = 0;
+    if (!n_ok || bs.bad) {
+      if (lane == 0) {
+        flag_status(p.v.status, n_ok ? kStatusBadBudget : kStatusCapacity);
+        if (g == 0) p.counts[b] = 0;
+      }
+    } else {
+      count = sel::select_ids_wave(keys, n, bs, hist, g == 0 ? p.selected + static_cast<int64_t>(b) * p.sel_stride
+                                                              : nullptr,
+                                   p.sel_stride, late);
+      if (lane == 0 && g == 0) p.counts[b] = count;
+    }
+    list_late(p, b, cl, late, kMaxSharedFusedBlocks + kTailPages, count, fb, wn, tail_pages, lane);
+  }
+  PlanPages src(cl, late, p.v, b, wave, fb.F, wn, wlen);
+  for (;;) {
+    const attn::PageRef pr = src.next(true);
+    if (pr.valid <= 0) break;
+    st.attend(p.v, pr, lg);
+  }
+
+  st.reduce_rows();
+  attn::publish_wave<G, kWaves>(st, cs, wave, lane, lg.row, lg.col);
+  __syncthreads();
+  for (int o = tid; o < G * D; o += kThreads) {
+    const int h = o / D;
+    const int d = o % D;
+    float mx, lw, aw;
+    attn::combine_element<G, kWaves>(cs, h, d, mx, lw, aw);
+    p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
+  }
+  if (APPEND && tid == 0) commit_sequence(p, b, len, n, commit);
+}
+
 
 // ---- 4 query heads per KV head: LDS-staged pages, q.K on the matrix cores --
 // One 8-wave workgroup per (sequence, KV head), one per CU (the eight 16 KiB
@@ -700,8 +891,38 @@ int select_attend_per_cu(int32_t query_heads, int32_t kv_heads) {
   return kv_heads > 0 && query_heads / kv_heads == 4 ? 1 : 2;
 }
 
+// Representative bytes the shared one-launch step may read beyond the split
+// scoring's single pass (each of a sequence's kv_heads workgroups reads all
+// of them): 32 MiB, a few microseconds of HBM.
+constexpr int64_t kSharedRepeatBytes = int64_t{32} << 20;
+
+bool select_attend_shared_supported(int32_t batch, int32_t query_heads, int32_t kv_heads, int32_t rep_heads,
+                                    int32_t select_groups, int32_t rep_stride) {
+  if (select_groups != 1 || kv_heads <= 1 || rep_heads != kv_heads || query_heads > kMaxSelectHeads) return false;
+  const int group = query_heads / kv_heads;
+  if (group != 1 && group != 2) return false;
+  if (rep_stride < 0 || rep_stride > kMaxSharedFusedBlocks) return false;
+  const int64_t repeat = static_cast<int64_t>(batch) * kv_heads * (kv_heads - 1) * rep_stride * D * sizeof(float);
+  return repeat <= kSharedRepeatBytes;
+}
+
+template <bool APPEND, bool F16>
+hipError_t launch_shared(const Params& p, int batch, hipStream_t stream) {
+  const dim3 grid(p.v.kv_heads, batch);
+  if (p.query_heads == p.v.kv_heads) {
+    hipLaunchKernelGGL((decode_kernel_shared<1, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((decode_kernel_shared<2, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream) {
-  if (!select_attend_supported(s.query_heads, s.kv_heads, s.kv_heads, s.sel_stride, s.reps, s.rep_stride))
+  const bool shared = s.select_groups != s.kv_heads;
+  if (shared ? !select_attend_shared_supported(s.batch, s.query_heads, s.kv_heads, s.rep_heads, s.select_groups,
+                                               s.rep_stride)
+             : !select_attend_supported(s.query_heads, s.kv_heads, s.select_groups, s.sel_stride, s.reps,
+                                        s.rep_stride))
     return hipErrorInvalidValue;
   if (s.append && !s.arrive) return hipErrorInvalidValue;
   Params p{};
@@ -737,6 +958,11 @@ hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream)
   p.sel_stride = s.sel_stride;
   p.local_tokens = s.local_tokens;
   p.qscale = s.scale * attn::kLog2e;
+  if (shared) {
+    if (s.ring) return hipErrorInvalidValue;
+    if (!s.append) return launch_shared<false, false>(p, s.batch, stream);
+    return s.k16 ? launch_shared<true, true>(p, s.batch, stream) : launch_shared<true, false>(p, s.batch, stream);
+  }
   if (s.ring) {
     if (!s.append || s.k16) return hipErrorInvalidValue;
     p.online = online::Args{s.ring, s.ring_tokens, s.window, s.topk, s.query_heads, s.seal_scale};

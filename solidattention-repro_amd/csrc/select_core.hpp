@@ -655,7 +655,7 @@ __device__ inline int compact_ids_wave(const uint32_t* keys, int n, const Budget
     const uint64_t m_take = __ballot(take);
     const int pos = written + __popcll(m_take & below);
     if (take && pos < sel_stride) {
-      out_ids[pos] = blk;
+      if (out_ids) out_ids[pos] = blk;
       lds_ids[pos] = blk;
     }
     taken_eq += __popcll(m_eq);
@@ -759,7 +759,7 @@ __device__ inline int select_ids_wave_regs(const uint32_t* keys, int n, const Bu
     const uint64_t m_take = __ballot(take);
     const int pos = written + __popcll(m_take & below);
     if (take && pos < sel_stride) {
-      out_ids[pos] = blk;
+      if (out_ids) out_ids[pos] = blk;
       lds_ids[pos] = blk;
     }
     taken_eq += __popcll(m_eq);
@@ -939,9 +939,9 @@ __device__ inline int select_from_keys(const uint32_t* keys, int n, const Budget
 
 // Single-wave selection of one list: forced blocks plus the k best
 // candidates (lowest id first among equal keys), ids ascending into out_ids
-// and lds_ids (which may alias keys).  Up to 1024 blocks the keys are held in
-// registers (keys must hold 1024 entries); longer lists take the LDS radix
-// select.  Returns the count.
+// (null: none) and lds_ids (which may alias keys).  Up to 1024 blocks the
+// keys are held in registers (keys must hold n rounded up to a multiple of
+// 256 entries); longer lists take the LDS radix select.  Returns the count.
 __device__ inline int select_ids_wave(const uint32_t* keys, int n, const Budget& bs, uint32_t* hist,
                                       int32_t* out_ids, int sel_stride, int32_t* lds_ids) {
   if (n <= 4 * kWave) return select_ids_wave_regs<4>(keys, n, bs, out_ids, sel_stride, lds_ids);
