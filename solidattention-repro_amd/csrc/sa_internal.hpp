@@ -187,7 +187,7 @@ bool select_attend_supported(int32_t query_heads, int32_t kv_heads, int32_t sele
                              const float* reps, int32_t rep_stride);
 int select_attend_per_cu(int32_t query_heads, int32_t kv_heads);
 // The one-launch form of the shared selection (select_groups 1 over several
-// KV heads): 1-2 query heads per KV head, representatives per KV head,
+// KV heads): 1, 2 or 4 query heads per KV head, representatives per KV head,
 // rep_stride <= kMaxSharedFusedBlocks, and the representatives read once per
 // KV head (every workgroup scores the whole set) within a small byte budget.
 bool select_attend_shared_supported(int32_t batch, int32_t query_heads, int32_t kv_heads, int32_t rep_heads,

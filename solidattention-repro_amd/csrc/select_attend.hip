@@ -546,8 +546,9 @@ __device__ inline bool append_seal_shared(const Params& p, int b, int g, int64_t
   return true;
 }
 
-// G = query heads per KV head (1 or 2; representatives per KV head, G heads
-// per representative row); APPEND: decode step; F16: raw FP16 K/V input.
+// G = query heads per KV head (1, 2 or 4; representatives per KV head, G
+// heads per representative row; the pages walked in registers); APPEND:
+// decode step; F16: raw FP16 K/V input.
 template <int G, bool APPEND, bool F16>
 __global__ __launch_bounds__(kThreads) void decode_kernel_shared(const Params p) {
   const int g = blockIdx.x;
@@ -900,7 +901,7 @@ bool select_attend_shared_supported(int32_t batch, int32_t query_heads, int32_t 
                                     int32_t select_groups, int32_t rep_stride) {
   if (select_groups != 1 || kv_heads <= 1 || rep_heads != kv_heads || query_heads > kMaxSelectHeads) return false;
   const int group = query_heads / kv_heads;
-  if (group != 1 && group != 2) return false;
+  if (group != 1 && group != 2 && group != 4) return false;
   if (rep_stride < 0 || rep_stride > kMaxSharedFusedBlocks) return false;
   const int64_t repeat = static_cast<int64_t>(batch) * kv_heads * (kv_heads - 1) * rep_stride * D * sizeof(float);
   return repeat <= kSharedRepeatBytes;
@@ -909,10 +910,13 @@ bool select_attend_shared_supported(int32_t batch, int32_t query_heads, int32_t 
 template <bool APPEND, bool F16>
 hipError_t launch_shared(const Params& p, int batch, hipStream_t stream) {
   const dim3 grid(p.v.kv_heads, batch);
-  if (p.query_heads == p.v.kv_heads) {
+  const int group = p.query_heads / p.v.kv_heads;
+  if (group == 1) {
     hipLaunchKernelGGL((decode_kernel_shared<1, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
-  } else {
+  } else if (group == 2) {
     hipLaunchKernelGGL((decode_kernel_shared<2, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((decode_kernel_shared<4, APPEND, F16>), grid, dim3(kThreads), 0, stream, p);
   }
   return hipGetLastError();
 }

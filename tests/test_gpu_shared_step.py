@@ -67,7 +67,8 @@ def check_ids(sel, cnt, esel, ecnt, tag):
         assert sel[b, 0, :c].tolist() == esel[b, 0, :c].tolist(), (tag, b)
 
 
-@pytest.mark.parametrize("hq,local_tokens,f16", [(16, 0, False), (16, 16, False), (8, 0, False), (16, 0, True)])
+@pytest.mark.parametrize("hq,local_tokens,f16", [(16, 0, False), (16, 16, False), (8, 0, False), (16, 0, True),
+                                                  (32, 0, False), (32, 16, True)])
 def test_shared_decode_steps_bit_exact(hip, hq, local_tokens, f16):
     """36 one-launch steps of three sequences (tails of 30, 0 and 25 tokens:
     every sequence crosses a seal), queries and tokens fresh each step."""
@@ -144,7 +145,7 @@ def test_c1_shape_shared_decode_steps_equal_split_launches(hip):
     assert int(case.sealed[0]) == 65
 
 
-@pytest.mark.parametrize("hq", [16, 8])
+@pytest.mark.parametrize("hq", [16, 8, 32])
 def test_shared_select_attend_budgets_and_ties(hip, hq):
     """select_attend (no append) with select_groups 1 in one launch: mixed
     lengths (empty, a single block, under and over the budget, 200 blocks),
@@ -169,15 +170,16 @@ def test_shared_select_attend_budgets_and_ties(hip, hq):
 
 
 def test_shared_one_launch_predicate(hip):
-    """The one-launch shared form takes 1-2 query heads per KV head, per-KV-head
-    representatives, rows of at most 256 blocks and a bounded repeat of the
-    representative reads; other shapes run the split launches."""
+    """The one-launch shared form takes 1, 2 or 4 query heads per KV head,
+    per-KV-head representatives, rows of at most 256 blocks and a bounded
+    repeat of the representative reads; other shapes run the split launches."""
     def fused(batch, hq, table_stride, rep_heads=None):
         case = make_case(930, batch, hq, 8, [32 * 4] * batch, table_stride=table_stride, rep_heads=rep_heads)
         return hip.select_attend_fused(device_kv(case), 1)
     assert fused(1, 16, 64)
     assert fused(2, 8, 250)
-    assert not fused(1, 32, 64)            # 4 query heads per KV head
+    assert fused(1, 32, 64)
+    assert not fused(1, 64, 64)            # 8 query heads per KV head
     assert not fused(1, 16, 300)           # rows past 256 blocks
     assert not fused(1, 16, 64, rep_heads=16)  # a representative per query head
     assert fused(16, 16, 64)
