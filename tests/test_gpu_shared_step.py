@@ -211,3 +211,28 @@ def test_shared_decode_steps_long_lists_split_selection(hip):
         assert_close_2e3(out.cpu().numpy(), expect)
     check_state(kv, case)
     assert int(case.sealed[0]) == 501
+
+
+def test_shared_flags_bad_budget_and_capacity(hip):
+    """The one-launch shared form flags a per-sequence budget below init +
+    local (that sequence selects nothing, the others select) and a sequence
+    with more sealed blocks than rep_stride (capacity: nothing selected, its
+    tail attended), like the separate selection."""
+    case = make_case(950, 2, 16, 8, [32 * 40 + 3, 32 * 30])
+    kv = device_kv(case)
+    assert hip.select_attend_fused(kv, 1)
+    q = to_dev(case.query)
+    st = status_tensor()
+    budgets = to_dev(np.array([20, 10], np.int32))  # 10 < init + local
+    sel, cnt, out = hip.select_attend(kv, q, 1, 20, 4, 8, SCALE, status=st, sel_stride=20, budgets=budgets)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_BAD_BUDGET
+    assert cnt.cpu().numpy()[:, 0].tolist() == [20, 0]
+    kv.sealed.copy_(to_dev(np.array([case.rep_stride + 1, 30], np.int32)))
+    kv.seq_len.copy_(to_dev(np.array([32 * (case.rep_stride + 1) + 3, 32 * 30], np.int32)))
+    st.zero_()
+    sel, cnt, out = hip.select_attend(kv, q, 1, 20, 4, 8, SCALE, status=st, sel_stride=20)
+    torch.cuda.synchronize()
+    assert int(st.item()) & hip.STATUS_CAPACITY
+    assert cnt.cpu().numpy()[:, 0].tolist() == [0, 20]
+    assert np.isfinite(out.cpu().numpy()).all()

@@ -77,6 +77,36 @@ def test_noalloc_equals_workspace_entry_two_calls(hip, hq, splits):
         assert int(kv_b.sealed.cpu().numpy()[0]) == (32 * 40 + 31 + 3) // 32 or call == 1
 
 
+@pytest.mark.parametrize("hq,splits", [(16, 1), (32, 1), (16, 2)])
+def test_noalloc_shared_selection_two_calls(hip, hq, splits):
+    """The shared selection (select_groups 1): in one launch (splits 1) and as
+    separate launches whose split selection keeps its scores in the scratch
+    (splits 2), two calls in a row, the second smaller, equal to the decode
+    step with a workspace."""
+    for call, (seed, lengths, stride) in enumerate(CALLS):
+        print(f"case: shared hq={hq} call={call} batch={len(lengths)} splits={splits}", flush=True)
+        case = make_case(seed + 50 + hq, len(lengths), hq, 8, lengths, table_stride=stride, planted=3)
+        kv_a, kv_b = device_kv(case), device_kv(case)
+        assert hip.select_attend_fused(kv_a, 1, splits) == (splits == 1)
+        ws, _ = hip.decode_step_workspace(kv_a, splits)
+        rng = np.random.default_rng(seed + 1)
+        st_a, st_b = status_tensor(), status_tensor()
+        for step in range(3):
+            k = to_dev((rng.standard_normal((case.batch, 8, D)) * 2).astype(np.float32))
+            v = to_dev((rng.standard_normal((case.batch, 8, D)) * 2).astype(np.float32))
+            q = to_dev(rng.standard_normal((case.batch, hq, D)).astype(np.float32))
+            a = hip.decode_step(kv_a, k, v, 0, q, 1, BUDGET, INIT, LOCAL, SCALE, ws, splits=splits, status=st_a)
+            sel = torch.full((case.batch, 1, BUDGET), -1, dtype=torch.int32, device="cuda")
+            cnt = torch.full((case.batch, 1), -1, dtype=torch.int32, device="cuda")
+            out = torch.full((case.batch, hq, D), float("nan"), dtype=torch.float32, device="cuda")
+            b = hip.decode_step_noalloc(kv_b, k, v, 0, q, 1, BUDGET, INIT, LOCAL, SCALE, sel, cnt, out, splits=splits,
+                                        status=st_b)
+            torch.cuda.synchronize()
+            assert int(st_a.item()) == 0 and int(st_b.item()) == 0
+            assert_same_step(a, b)
+        assert_same_state(kv_a, kv_b)
+
+
 def test_noalloc_refuses_records_beyond_scratch(hip):
     case = make_case(805, 2, 16, 8, [32 * 4 + 1, 32 * 3], table_stride=8)
     kv = device_kv(case)
