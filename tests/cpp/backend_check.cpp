@@ -250,9 +250,10 @@ void check_lifecycle() {
 // step at G=2 and head_dim 128; the general kernels in sequence at another
 // head_dim): 4 sequences, 34 steps across seal boundaries, against the
 // oracle's append, seal, select and attention (qwen_chain_main.cpp:390-395,
-// kv_lifecycle_main.cpp:92-113, selection.cpp:96-147).  Record names carry
-// `tag`.
-void check_decode_step(std::size_t d = 128, const std::string& tag = "") {
+// kv_lifecycle_main.cpp:92-113, selection.cpp:96-147).  groups: selection
+// groups (8: one block set per KV group; 1: the shared selection of the C2/P1
+// drivers, also one launch at head_dim 128).  Record names carry `tag`.
+void check_decode_step(std::size_t d = 128, const std::string& tag = "", std::size_t groups = 8) {
   const std::size_t batch = 4, hq = 16, hkv = 8, stride = 24, pages = batch * stride;
   const std::size_t budget = 8, steps = 34;
   sa::hip::PagedKvPool pool(batch, hq, hkv, stride, pages, 0, 0, d);
@@ -273,13 +274,13 @@ void check_decode_step(std::size_t d = 128, const std::string& tag = "") {
   pool.sealed().upload(sealed);
   pool.generation().upload(gen);
   pool.reps().upload(reps);
-  sa::hip::SparseDecoder dec(pool, sa_select_params{static_cast<int32_t>(hkv), static_cast<int32_t>(budget), 1, 2,
+  sa::hip::SparseDecoder dec(pool, sa_select_params{static_cast<int32_t>(groups), static_cast<int32_t>(budget), 1, 2,
                                                     static_cast<int32_t>(budget), 0, nullptr});
   // fused at head_dim 128 only
   record("decode_step_fused" + tag, dec.fused(pool) ? "true" : "false", dec.fused(pool) == (d == 128));
   sa::hip::DeviceArray<float> dk(batch * hkv * d), dv(batch * hkv * d), dq(batch * hq * d), dout(batch * hq * d);
   std::vector<float> k(batch * hkv * d), v(batch * hkv * d), q(batch * hq * d), out(batch * hq * d);
-  std::vector<int32_t> sel(batch * hkv * budget), cnt(batch * hkv);
+  std::vector<int32_t> sel(batch * groups * budget), cnt(batch * groups);
   const float scale = 1.0f / std::sqrt(static_cast<float>(d));
   bool ids_ok = true;
   double max_err = 0.0;
@@ -295,14 +296,15 @@ void check_decode_step(std::size_t d = 128, const std::string& tag = "") {
                      batch, hkv, d);
     sao_paged_seal(host_pool.data(), 32, table.data(), stride, seq_len.data(), sealed.data(), gen.data(),
                    reps.data(), hkv, rep_stride, batch, hq, hkv, d, 0);
-    sao_paged_score_select(q.data(), reps.data(), sealed.data(), batch, hq, hkv, d, hkv, rep_stride, hkv, budget, 1,
-                           2, sel.data(), cnt.data(), budget, nullptr);
+    sao_paged_score_select(q.data(), reps.data(), sealed.data(), batch, hq, hkv, d, hkv, rep_stride,
+                           static_cast<int>(groups), budget, 1, 2, sel.data(), cnt.data(), budget, nullptr);
     sao_paged_sparse_attention(host_pool.data(), 32, table.data(), stride, seq_len.data(), sealed.data(), sel.data(),
-                               cnt.data(), budget, hkv, q.data(), batch, hq, hkv, d, scale, out.data());
+                               cnt.data(), budget, static_cast<int>(groups), q.data(), batch, hq, hkv, d, scale,
+                               out.data());
     const auto gsel = dec.selected().download();
     const auto gcnt = dec.counts().download();
     const auto gout = dout.download();
-    for (std::size_t r = 0; r < batch * hkv; ++r) {
+    for (std::size_t r = 0; r < batch * groups; ++r) {
       ids_ok &= gcnt[r] == cnt[r];
       for (int i = 0; i < cnt[r] && ids_ok; ++i) ids_ok &= gsel[r * budget + i] == sel[r * budget + i];
     }
@@ -330,6 +332,7 @@ void check_decode_step(std::size_t d = 128, const std::string& tag = "") {
     record("select_attend_max_rel_error" + tag, num(err), err <= 2e-3);
     return;
   }
+  if (groups != hkv) return;
 
   // the chunked schedule over the last step's selection: 3-page chunks of
   // lists of up to 9 pages, against the oracle's attention of that step
@@ -364,6 +367,7 @@ int main() {
     check_decode_step();
     check_decode_step(64, "_head_dim_64");
     check_decode_step(256, "_head_dim_256");
+    check_decode_step(128, "_shared", 1);
     g_json << "\n}\n";
     std::cout << g_json.str();
     return g_ok ? 0 : 2;

@@ -39,6 +39,11 @@ def test_cpp_backend_check(hip):
         assert m[f"decode_step_max_rel_error_head_dim_{d}"] <= 2e-3
         assert m[f"select_attend_max_rel_error_head_dim_{d}"] <= 2e-3
     assert m["decode_step_fused"] is True
+    # the shared selection (one block set per sequence) as one launch through the C++ API
+    assert m["decode_step_fused_shared"] is True
+    assert m["decode_step_selected_ids_exact_shared"] is True
+    assert m["decode_step_state_bytes_exact_shared"] is True
+    assert m["decode_step_max_rel_error_shared"] <= 2e-3
 
 
 EXE_STORE = os.path.join(ROOT, "tests", "cpp", "store_check")
