@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
 // scores are bit-identical.  Every workgroup then selects the same ids; the
 // workgroup of KV head 0 writes them.  Each workgroup reads the sequence's
 // representatives once per KV head, so the launch takes short lists only
-// (shared_fused_supported()).
+// (select_attend_shared_supported()).
 //
 // A step that seals a block computes every KV head's representative of it in
 // every workgroup and writes them all (the values are identical: the same
