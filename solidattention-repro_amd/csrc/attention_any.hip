@@ -14,7 +14,8 @@
 //     pieces (eight in flight) against the query heads held in LDS;
 //   * online softmax per head over the tile (log2 domain, wave reductions);
 //   * P.V: lanes over d (two values of d per 4-byte load, 256 d per
-//     instruction), four tokens' loads in flight, the tile's probabilities
+//     instruction), 16 tokens' loads in flight (8 or 4 at 4 or 8 query heads
+//     per KV head), the tile's probabilities
 //     read back from LDS.
 // The waves' states combine in LDS; with several splits each workgroup
 // writes (max, denominator, accumulator) per head and a merge kernel adds
@@ -32,6 +33,14 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxD = kAnyMaxHeadDim;
 constexpr int kPairs = kMaxD / (2 * kWave);  // 4-byte V loads per lane per token
 constexpr int kTile = kWave;                // tokens per wave tile
+// P.V tokens whose V loads are in flight together: each lane's pieces are
+// 4 bytes, so with 4 tokens a wave kept ~0.5 KiB in flight at head_dim 64
+// and the walk was bound by load latency.  Fewer at 4 and 8 query heads per
+// KV head, whose accumulators take the registers.
+template <int G>
+constexpr int pv_tokens() {
+  return G <= 2 ? 16 : (G == 4 ? 8 : 4);
+}
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -134,10 +143,11 @@ __global__ __launch_bounds__(kThreads) void attention_any_kernel(const AnyParams
     __builtin_amdgcn_wave_barrier();  // the wave's LDS writes precede its reads below
     // P.V: lane holds d = 2 (lane + 64 j) + {0, 1}
     const int n = static_cast<int>(std::min<int64_t>(kTile, t_end - t0));
-    for (int i0 = 0; i0 < n; i0 += 4) {
-      uint32_t vw[4][kPairs];
+    constexpr int kPvTokens = pv_tokens<G>();
+    for (int i0 = 0; i0 < n; i0 += kPvTokens) {
+      uint32_t vw[kPvTokens][kPairs];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPvTokens; ++i) {
         const uint16_t* v = vbase + (t0 + i0 + i) * tok_elems;
 #pragma unroll
         for (int j = 0; j < kPairs; ++j) {
@@ -147,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void attention_any_kernel(const AnyParams
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPvTokens; ++i) {
         if (i0 + i >= n) break;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -381,10 +391,11 @@ __global__ __launch_bounds__(kThreads) void paged_any_kernel(const PagedAnyParam
     }
     __builtin_amdgcn_wave_barrier();  // the wave's LDS writes precede its reads below
     const int n = static_cast<int>(std::min<int64_t>(kTile, q_end - t0));
-    for (int i0 = 0; i0 < n; i0 += 4) {
-      uint32_t vw[4][kPairs];
+    constexpr int kPvTokens = pv_tokens<G>();
+    for (int i0 = 0; i0 < n; i0 += kPvTokens) {
+      uint32_t vw[kPvTokens][kPairs];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPvTokens; ++i) {
         const int64_t o = i0 + i < n ? off_s[wave][i0 + i] : -1;
 #pragma unroll
         for (int j = 0; j < kPairs; ++j) {
@@ -394,7 +405,7 @@ __global__ __launch_bounds__(kThreads) void paged_any_kernel(const PagedAnyParam
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPvTokens; ++i) {
         if (i0 + i >= n) break;
         if (off_s[wave][i0 + i] < 0) continue;  // uniform: a token that does not exist adds nothing
 #pragma unroll
@@ -456,6 +467,268 @@ __global__ __launch_bounds__(kThreads) void paged_any_kernel(const PagedAnyParam
   }
 }
 
+// ---- the paged form in token rows (head_dim up to 256) --------------------------
+// The lane layout of the head_dim-128 kernels (attn_core.hpp) at other head
+// dimensions: one KV head's K (or V) row of a token is read by LPR lanes,
+// 16 bytes (8 dimensions) each, LPR the power of two at or above head_dim / 8
+// and at least 8 (lanes past head_dim idle), so one load of a wave covers
+// 64 / LPR whole rows and a page is 32 LPR / 64 loads of K and as many of V,
+// all in flight together (a unit of at most 8 row groups; two units per page
+// at LPR 32).  A row's dot is summed across its lanes, the online softmax
+// runs per wave over the page's rows, and P.V accumulates each lane's 8
+// dimensions over its rows; the rows are added at the end.  Grid (kv_heads,
+// splits, batch); split s takes a contiguous range of the list's pages
+// (selected blocks, then the tail), its 4 waves every 4th unit; the waves
+// combine in LDS into the output or the split's record (the records and the
+// merge of paged_any_kernel).
+constexpr int kRowsWaves = 4;
+constexpr int kRowsThreads = kRowsWaves * kWave;
+
+// Sum over the LPR lanes of a token row (every lane of the row gets it).
+template <int LPR>
+__device__ inline float lane_row_sum(float v) {
+  if constexpr (LPR == 8) {
+    v += dpp_f<kDppQuadXor1>(v);
+    v += dpp_f<kDppQuadXor2>(v);
+    v += dpp_f<kDppRowHalfMirror>(v);  // the quads are uniform: exchanges the two quads of 8 lanes
+    return v;
+  } else if constexpr (LPR == 16) {
+    return row16_sum(v);
+  } else {
+    static_assert(LPR == 32, "8, 16 or 32 lanes per row");
+    v = row16_sum(v);
+    return v + shfl_xor_f(v, 16);
+  }
+}
+
+// Sum / max over the token rows of a wave (the lanes of one column).
+template <int LPR>
+__device__ inline float across_rows_sum(float v) {
+#pragma unroll
+  for (int o = LPR; o < kWave; o <<= 1) v += shfl_xor_f(v, o);
+  return v;
+}
+
+template <int LPR>
+__device__ inline float across_rows_max(float v) {
+#pragma unroll
+  for (int o = LPR; o < kWave; o <<= 1) v = fmaxf(v, shfl_xor_f(v, o));
+  return v;
+}
+
+// Tokens of page i of the list (selected blocks, then the tail) and its pool
+// page; 0 when the page does not exist or is invalid (flagged as by
+// paged_token()).
+__device__ inline int list_page(const PagedAnyParams& p, int b, const int32_t* sel, int n_sel, int sealed,
+                                int64_t len, int i, int64_t& page) {
+  int64_t logical;
+  int valid = kPageTokens;
+  if (i < n_sel) {
+    logical = sel[i];
+    if (logical < 0 || logical >= sealed) {
+      flag_status(p.status, kStatusBadBlock);
+      return 0;
+    }
+  } else {
+    logical = static_cast<int64_t>(sealed) + (i - n_sel);
+    const int64_t left = len - logical * kPageTokens;
+    if (left <= 0) return 0;
+    valid = left < kPageTokens ? static_cast<int>(left) : kPageTokens;
+  }
+  if (logical >= p.table_stride) {
+    flag_status(p.status, kStatusBadBlock);
+    return 0;
+  }
+  page = p.table[static_cast<int64_t>(b) * p.table_stride + logical];
+  if (page < 0 || page >= p.num_pages) {
+    flag_status(p.status, kStatusBadPage);
+    return 0;
+  }
+  return valid;
+}
+
+template <int G, int LPR>
+__global__ __launch_bounds__(kRowsThreads) void paged_rows_kernel(const PagedAnyParams p) {
+  constexpr int kR = kWave / LPR;                   // token rows per load
+  constexpr int kI = kPageTokens / kR;              // loads per page (K or V)
+  constexpr int kMaxUnit = G == 8 ? 4 : 8;          // row groups held in registers
+  constexpr int NIT = kI < kMaxUnit ? kI : kMaxUnit;  // row groups per unit
+  constexpr int kParts = kI / NIT;                  // units per page
+  __shared__ float w_ml[kRowsWaves][G][2];
+  __shared__ float w_acc[kRowsWaves][G][LPR * 8];
+  const int g = blockIdx.x;
+  const int s = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int D = p.head_dim;
+  const int row = lane / LPR;
+  const int col = lane % LPR;
+  const bool dims = col * 8 < D;  // this lane's 8 dimensions exist
+  const int sg = g / (p.kv_heads / p.select_groups);
+  const int64_t list = static_cast<int64_t>(b) * p.select_groups + sg;
+  const int32_t* sel = p.selected + list * p.sel_stride;
+  int n_sel = p.counts[list];
+  n_sel = n_sel < 0 ? 0 : (n_sel > p.sel_stride ? p.sel_stride : n_sel);
+  const int64_t len = p.seq_len[b];
+  const int sealed = p.sealed[b];
+  const int64_t tail_tokens = len - static_cast<int64_t>(sealed) * kPageTokens;
+  const int tail_pages = tail_tokens > 0 ? static_cast<int>((tail_tokens + kPageTokens - 1) / kPageTokens) : 0;
+  const int total = n_sel + tail_pages;
+  const int chunk = (total + p.splits - 1) / p.splits;
+  const int i_begin = s * chunk;
+  const int i_end = total < i_begin + chunk ? total : i_begin + chunk;
+
+  // this lane's 8 dimensions of each head's query, in the log2 domain
+  const float sl2 = p.scale * kLog2e;
+  const float* q = p.query + (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(g) * G) * D;
+  float qf[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+    if (dims) {
+      a = *reinterpret_cast<const float4*>(q + h * D + col * 8);
+      c = *reinterpret_cast<const float4*>(q + h * D + col * 8 + 4);
+    }
+    qf[h][0] = a.x * sl2;
+    qf[h][1] = a.y * sl2;
+    qf[h][2] = a.z * sl2;
+    qf[h][3] = a.w * sl2;
+    qf[h][4] = c.x * sl2;
+    qf[h][5] = c.y * sl2;
+    qf[h][6] = c.z * sl2;
+    qf[h][7] = c.w * sl2;
+  }
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = kNegInf;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
+  }
+  const int64_t tok_elems = 2LL * p.kv_heads * D;
+  const int64_t page_elems = kPageTokens * tok_elems;
+  const int64_t lane_off = static_cast<int64_t>(row) * tok_elems + static_cast<int64_t>(g) * D + col * 8;
+  const int64_t v_off = static_cast<int64_t>(p.kv_heads) * D;
+
+  for (int u = i_begin * kParts + wave; u < i_end * kParts; u += kRowsWaves) {
+    const int i = u / kParts;
+    const int part = u % kParts;
+    int64_t page = 0;
+    const int valid = list_page(p, b, sel, n_sel, sealed, len, i, page);
+    if (valid <= 0) continue;
+    const uint16_t* base = p.pool + page * page_elems + lane_off;
+    uint4 kr[NIT], vr[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int rg = part * NIT + it;  // row group of the page
+      if (dims && rg * kR + row < valid) {
+        kr[it] = load_stream16(base + static_cast<int64_t>(rg) * kR * tok_elems);
+        vr[it] = load_stream16(base + static_cast<int64_t>(rg) * kR * tok_elems + v_off);
+      } else {
+        kr[it] = make_uint4(0, 0, 0, 0);
+        vr[it] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    // logits of this lane's rows for every head
+    float sc[G][NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const uint32_t w[4] = {kr[it].x, kr[it].y, kr[it].z, kr[it].w};
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float kj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
+          a = __builtin_fmaf(qf[h][j], kj, a);
+        }
+        sc[h][it] = lane_row_sum<LPR>(a);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float pmax = kNegInf;
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        if ((part * NIT + it) * kR + row >= valid) sc[h][it] = kNegInf;
+        pmax = fmaxf(pmax, sc[h][it]);
+      }
+      pmax = across_rows_max<LPR>(pmax);
+      const float mn = fmaxf(m[h], pmax);
+      // mn == -inf only if nothing finite was seen: the state stays empty
+      const float corr = (m[h] == mn) ? 1.0f : __builtin_amdgcn_exp2f(m[h] - mn);
+      const float base_m = (mn == kNegInf) ? 0.0f : mn;
+      m[h] = mn;
+      float lsum = l[h] * corr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[h][j] *= corr;
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        sc[h][it] = __builtin_amdgcn_exp2f(sc[h][it] - base_m);
+        lsum += sc[h][it];
+      }
+      l[h] = lsum;
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float vj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc[h][j] = __builtin_fmaf(sc[h][it], vj, acc[h][j]);
+      }
+    }
+  }
+
+  // the wave's rows added, then the waves combined
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    l[h] = across_rows_sum<LPR>(l[h]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] = across_rows_sum<LPR>(acc[h][j]);
+    if (lane == 0) {
+      w_ml[wave][h][0] = m[h];
+      w_ml[wave][h][1] = l[h];
+    }
+    if (row == 0 && dims) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w_acc[wave][h][col * 8 + j] = acc[h][j];
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < G * D; e += kRowsThreads) {
+    const int h = e / D;
+    const int d = e % D;
+    float mx = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kRowsWaves; ++w) mx = fmaxf(mx, w_ml[w][h][0]);
+    float lw = 0.0f, aw = 0.0f;
+    if (mx != kNegInf) {
+#pragma unroll
+      for (int w = 0; w < kRowsWaves; ++w) {
+        const float f = __builtin_amdgcn_exp2f(w_ml[w][h][0] - mx);  // waves without tokens: 0
+        lw += w_ml[w][h][1] * f;
+        aw += w_acc[w][h][d] * f;
+      }
+    }
+    const int64_t hq = static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(g) * G + h;
+    if (p.splits == 1) {
+      p.out[hq * D + d] = lw > 0.0f ? aw / lw : 0.0f;
+    } else {
+      float* rec = p.part + (((static_cast<int64_t>(b) * p.kv_heads + g) * p.splits + s) * G + h) * part_stride(D);
+      if (d == 0) {
+        rec[0] = mx;
+        rec[1] = lw;
+      }
+      rec[kPartPad + d] = aw;
+    }
+  }
+}
+
 // out[b][hq][d] from the splits' records of (b, hq), added in split order.
 __global__ __launch_bounds__(kThreads) void paged_any_merge_kernel(const PagedAnyParams p) {
   const int hq = blockIdx.x;
@@ -481,6 +754,21 @@ __global__ __launch_bounds__(kThreads) void paged_any_merge_kernel(const PagedAn
     }
     p.out[(static_cast<int64_t>(b) * p.query_heads + hq) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
   }
+}
+
+// head_dim the row layout takes (32 lanes x 8 dimensions); larger ones run
+// paged_any_kernel.
+constexpr int kMaxRowsHeadDim = 256;
+
+template <int LPR>
+hipError_t launch_rows(const PagedAnyParams& p, int group, dim3 grid, hipStream_t stream) {
+  switch (group) {
+    case 1: hipLaunchKernelGGL((paged_rows_kernel<1, LPR>), grid, dim3(kRowsThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((paged_rows_kernel<2, LPR>), grid, dim3(kRowsThreads), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((paged_rows_kernel<4, LPR>), grid, dim3(kRowsThreads), 0, stream, p); break;
+    default: hipLaunchKernelGGL((paged_rows_kernel<8, LPR>), grid, dim3(kRowsThreads), 0, stream, p); break;
+  }
+  return hipGetLastError();
 }
 
 // Splits that give every compute unit about two workgroups, each with at
@@ -538,6 +826,18 @@ hipError_t launch_paged_attention_any(const AttnLaunch& a, hipStream_t stream) {
   p.scale = a.scale;
   const int group = a.query_heads / a.kv_heads;
   const dim3 grid(a.kv_heads, a.splits, a.batch);
+  if (a.head_dim <= kMaxRowsHeadDim) {
+    const int lpr = a.head_dim <= 64 ? 8 : (a.head_dim <= 128 ? 16 : 32);
+    hipError_t e = hipSuccess;
+    switch (lpr) {
+      case 8: e = launch_rows<8>(p, group, grid, stream); break;
+      case 16: e = launch_rows<16>(p, group, grid, stream); break;
+      default: e = launch_rows<32>(p, group, grid, stream); break;
+    }
+    if (e != hipSuccess || p.splits == 1) return e;
+    hipLaunchKernelGGL(paged_any_merge_kernel, dim3(a.query_heads, a.batch), dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
+  }
   switch (group) {
     case 1: hipLaunchKernelGGL(paged_any_kernel<1>, grid, dim3(kThreads), 0, stream, p); break;
     case 2: hipLaunchKernelGGL(paged_any_kernel<2>, grid, dim3(kThreads), 0, stream, p); break;

@@ -153,8 +153,13 @@ __global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params 
 // of (the sequential fp32 dot over head_dim) / heads: the reference's
 // select_shared_blocks arithmetic (selection.cpp:108-119) for any head_dim.
 // The lanes read consecutive blocks of each d-row of the d-major
-// representatives (coalesced).  The selection launch of the split form
-// follows.
+// representatives (coalesced).  GR query heads share a representative row
+// (the group, with a row per KV head): their dots run side by side over one
+// pass of the row, and 32 rows of loads are in flight per lane.  The
+// selection launch of the split form follows.
+constexpr int kAnyRowBatch = 32;
+
+template <int GR>
 __global__ __launch_bounds__(kChunkBlocks) void score_any_kernel(const Params p, int head_dim) {
   extern __shared__ __align__(16) float q_any[];  // [heads_per_sel][head_dim]
   const int sg = blockIdx.x;
@@ -173,15 +178,27 @@ __global__ __launch_bounds__(kChunkBlocks) void score_any_kernel(const Params p,
   const float heads_f = static_cast<float>(hps);
   const int64_t stride = p.rep_stride;
   float score = 0.0f;
-  for (int j = 0; j < hps; ++j) {
-    const int h = h_first + j;
+  for (int j0 = 0; j0 < hps; j0 += GR) {  // GR divides hps
+    const int h = h_first + j0;
     const int rh = p.rep_heads == p.query_heads ? h : h / p.group;
     const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + rh) * head_dim * stride + blk;
-    const float* qh = q_any + j * head_dim;
-    float dot = 0.0f;
-#pragma unroll 8
-    for (int d = 0; d < head_dim; ++d) dot = dot + qh[d] * r[d * stride];
-    score = score + dot / heads_f;
+    float dot[GR];
+#pragma unroll
+    for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
+    for (int d0 = 0; d0 < head_dim; d0 += kAnyRowBatch) {
+      float rv[kAnyRowBatch];
+#pragma unroll
+      for (int k = 0; k < kAnyRowBatch; ++k)
+        rv[k] = d0 + k < head_dim ? load_stream_f32(r + static_cast<int64_t>(d0 + k) * stride) : 0.0f;
+#pragma unroll
+      for (int k = 0; k < kAnyRowBatch; ++k) {
+        if (d0 + k >= head_dim) break;
+#pragma unroll
+        for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_any[(j0 + j) * head_dim + d0 + k] * rv[k];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
   }
   p.scores[(static_cast<int64_t>(b) * p.select_groups + sg) * p.rep_stride + blk] = score;
 }
@@ -615,7 +632,13 @@ hipError_t launch_score_select_split(const SelectLaunch& s, hipStream_t stream) 
   const int gr = s.rep_heads == s.query_heads ? 1 : p.group;
   if (general_head_dim(s.head_dim)) {
     const size_t smem = static_cast<size_t>(p.heads_per_sel) * s.head_dim * sizeof(float);
-    hipLaunchKernelGGL(score_any_kernel, grid, dim3(kChunkBlocks), smem, stream, p, s.head_dim);
+    switch (gr) {
+      case 1: hipLaunchKernelGGL(score_any_kernel<1>, grid, dim3(kChunkBlocks), smem, stream, p, s.head_dim); break;
+      case 2: hipLaunchKernelGGL(score_any_kernel<2>, grid, dim3(kChunkBlocks), smem, stream, p, s.head_dim); break;
+      case 4: hipLaunchKernelGGL(score_any_kernel<4>, grid, dim3(kChunkBlocks), smem, stream, p, s.head_dim); break;
+      case 8: hipLaunchKernelGGL(score_any_kernel<8>, grid, dim3(kChunkBlocks), smem, stream, p, s.head_dim); break;
+      default: return hipErrorInvalidValue;
+    }
   } else if (p.heads_per_sel / gr >= kRowWaves / 2) {
     // a group over four or more representative rows: a wave per row
     switch (gr) {
