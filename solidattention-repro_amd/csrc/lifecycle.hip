@@ -223,6 +223,63 @@ __global__ __launch_bounds__(kThreads) void seal_blocks_kernel(const Params p) {
   }
 }
 
+// The bulk seal at a head_dim other than 128: thread = (block j, 16-byte
+// piece q of head g's key row) with head_dim / 8 pieces and 256 / pieces
+// blocks per workgroup (the row tile in dynamic LDS: head_dim x (blocks + 1)
+// floats), the same sums in token order and the same capacity rule as
+// seal_blocks_kernel.
+__global__ __launch_bounds__(kThreads) void seal_blocks_any_kernel(const Params p, int blocks_per_wg) {
+  extern __shared__ float any_tile[];  // [head_dim][blocks_per_wg + 1]
+  const int g = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int hd = p.head_dim;
+  const int pieces = hd / 8;
+  const int64_t s0 = p.sealed[b];
+  const int64_t target = seal_target(p.seq_len[b], p.local_tokens, s0);
+  const int64_t first = s0 + static_cast<int64_t>(blockIdx.x) * blocks_per_wg;
+  if (first >= target) return;
+  __shared__ int32_t s_stop;
+  const int64_t end = target < first + blocks_per_wg ? target : first + blocks_per_wg;
+  if (tid == 0) s_stop = static_cast<int32_t>(end - first);
+  __syncthreads();
+  const int64_t bad = first_unsealable(p, b, s0, end, tid, kThreads);
+  if (bad < end) atomicMin(&s_stop, static_cast<int32_t>(bad > first ? bad - first : 0));
+  __syncthreads();
+  const int n = s_stop;
+  if (n <= 0) return;
+  const int tile_stride = blocks_per_wg + 1;
+  const int j = tid / pieces, q = tid % pieces;
+  if (j < n) {
+    const int64_t page = table_page(p, b, first + j);
+    const uint16_t* src = p.pool + page * p.page_elems + static_cast<int64_t>(g) * hd + q * 8;
+    uint4 w[kPageTokens];
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) w[t] = load_stream16(src + static_cast<int64_t>(t) * p.token_elems);
+    float sum[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum[i] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) {
+      const uint32_t h[4] = {w[t].x, w[t].y, w[t].z, w[t].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sum[2 * i] = sum[2 * i] + lo_h2f(h[i]);
+        sum[2 * i + 1] = sum[2 * i + 1] + hi_h2f(h[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) any_tile[(q * 8 + i) * tile_stride + j] = sum[i] / static_cast<float>(kPageTokens);
+  }
+  __syncthreads();
+  for (int e = tid; e < hd * blocks_per_wg; e += kThreads) {
+    const int d = e / blocks_per_wg, jj = e % blocks_per_wg;
+    if (jj >= n) continue;
+    const float rep = any_tile[d * tile_stride + jj];
+    for (int r = 0; r < p.group; ++r)
+      p.reps[((static_cast<int64_t>(b) * p.rep_heads + g * p.group + r) * hd + d) * p.rep_stride + first + jj] = rep;
+  }
+}
+
 // One wave per sequence: the counters after the bulk seal.
 __global__ __launch_bounds__(kWave) void seal_commit_kernel(const Params p) {
   const int b = blockIdx.x;
@@ -494,10 +551,21 @@ hipError_t launch_append_seal(const LifecycleLaunch& l, hipStream_t stream) {
   p.local_tokens = l.local_tokens;
   p.append = l.append;
   if (p.head_dim != D) {
-    // another head_dim: one workgroup per sequence appends (when asked) and
-    // seals every block the tail rule releases (no ring: checked by the API)
+    // another head_dim (no ring: checked by the API): a decode step's append
+    // and seal in one workgroup per sequence; the bulk seal spread over
+    // blocks and KV heads
     if (l.ring) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(append_seal_kernel<false>, dim3(l.batch), dim3(kThreads), 0, stream, p);
+    if (l.append) {
+      hipLaunchKernelGGL(append_seal_kernel<false>, dim3(l.batch), dim3(kThreads), 0, stream, p);
+    } else {
+      const int per_wg = kThreads / (p.head_dim / 8);  // head_dim <= 512: at least 4
+      const int64_t blocks = l.table_stride < l.rep_stride ? l.table_stride : l.rep_stride;
+      const dim3 grid(static_cast<unsigned>((blocks + per_wg - 1) / per_wg), l.kv_heads, l.batch);
+      const size_t smem = static_cast<size_t>(p.head_dim) * (per_wg + 1) * sizeof(float);
+      hipLaunchKernelGGL(seal_blocks_any_kernel, grid, dim3(kThreads), smem, stream, p, per_wg);
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+      hipLaunchKernelGGL(seal_commit_kernel, dim3(l.batch), dim3(kWave), 0, stream, p);
+    }
   } else if (l.ring) {
     p.query = l.query;
     p.online = online::Args{l.ring, l.ring_tokens, l.window, l.topk, l.query_heads, l.seal_scale};

@@ -94,10 +94,17 @@ def test_append_seal_general_head_dim(hip, d, hq, hkv, rep_heads, local):
         st.check_device(kv)
 
 
-def test_seal_only_general_head_dim(hip):
-    """sa_hip_seal (no append) on a prefill at head_dim 64: the per-sequence
-    seal runs to the tail rule's end, as the oracle's."""
-    st = State(31, 2, 8, 4, 64, [32 * 9 + 4, 32 * 3])
+@pytest.mark.parametrize("d,hq,hkv,rep_heads,lengths", [(64, 8, 4, None, [32 * 9 + 4, 32 * 3]),
+                                                       (96, 8, 4, 8, [32 * 70 + 4, 32 * 3, 32 * 41 + 31]),
+                                                       (256, 16, 8, None, [32 * 40 + 1, 32 * 17]),
+                                                       (512, 4, 2, None, [32 * 12 + 7]),
+                                                       (8, 4, 4, None, [32 * 33, 5])])
+def test_seal_only_general_head_dim(hip, d, hq, hkv, rep_heads, lengths):
+    """sa_hip_seal (no append) on a prefill (the bulk seal, spread over
+    blocks and KV heads): every block the tail rule releases is sealed, with
+    the oracle's representative bits and counters."""
+    print(f"case: bulk seal d={d} hq={hq} hkv={hkv} rep_heads={rep_heads} lengths={lengths}", flush=True)
+    st = State(31 + d, len(lengths), hq, hkv, d, lengths, rep_heads=rep_heads)
     kv = st.device(hip)
     kv.sealed.zero_()
     kv.generation.zero_()
