@@ -73,14 +73,15 @@ def parse():
     ap.add_argument("--prefetch-blocks", type=int, default=128,
                     help="store workload: blocks per store -> pool prefetch batch")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "correction", "represent", "stress", "store", "layer", "shared"],
+                    choices=["decode", "correction", "represent", "stress", "store", "layer", "shared", "head_dim"],
                     help="decode: the headline decode step; correction: long-context miss correction "
                          "(Qwen3-8B shape, B=8, 128K context, 128-block budget, ~75%% history coverage); "
                          "represent: InfLLM prefill representatives (16K-token prompt, window 32, top 4); "
                          "stress: B=128 mixed contexts 1K-64K, budgets 512/2048/full, +-60000 outliers; "
                          "store: seal writeback behind decoding and store -> pool prefetch; "
                          "layer: decode step with its q/k/v producer and o-proj consumer; "
-                         "shared: one block set over all heads, 1 sequence x 2048 tokens, one launch vs split")
+                         "shared: one block set over all heads, 1 sequence x 2048 tokens, one launch vs split; "
+                         "head_dim: the decode step and bulk seal at head_dim 64 / 128 / 256")
     ap.add_argument("--select", default="auto", choices=["auto", "single", "split", "chunked"],
                     help="separate selection launch: one workgroup per list, scoring split over 256-block "
                          "workgroups (two launches), lists in chunks of 1024-2048 blocks (one launch), or the default "
@@ -181,6 +182,10 @@ def main():
     if args.workload == "store":
         import bench_store
         bench_store.run(args)
+        return
+    if args.workload == "head_dim":
+        import bench_head_dim
+        bench_head_dim.run(args)
         return
     if args.workload == "shared":
         import bench_shared

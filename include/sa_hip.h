@@ -289,7 +289,9 @@ int sa_hip_select_attend_fused(const sa_paged_kv* kv,
 /* The split count to pass to sa_hip_select_attend / sa_hip_decode_step: 1
  * (the fused launch) when the fused kernel applies and its workgroups fill
  * the device (batch x kv_heads >= 2 x CUs), or for the shared selection's
- * one launch whenever it applies; otherwise
+ * one launch whenever it applies; at a head_dim other than 128, splits that
+ * give about four attention workgroups per CU with at least 4 pages per
+ * wave; otherwise
  * sa_hip_attention_splits_for(batch, query_heads, kv_heads, budget_blocks + 2) for the
  * separate launches. */
 int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv,
