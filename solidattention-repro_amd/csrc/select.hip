@@ -155,8 +155,8 @@ __global__ __launch_bounds__(kChunkBlocks) void score_chunk_kernel(const Params 
 // The lanes read consecutive blocks of each d-row of the d-major
 // representatives (coalesced).  GR query heads share a representative row
 // (the group, with a row per KV head): their dots run side by side over one
-// pass of the row, and 32 rows of loads are in flight per lane.  The
-// selection launch of the split form follows.
+// pass of the row, in batches of 32 rows, the next batch's loads in flight
+// while one is summed.  The selection launch of the split form follows.
 constexpr int kAnyRowBatch = 32;
 
 template <int GR>
@@ -185,17 +185,28 @@ __global__ __launch_bounds__(kChunkBlocks) void score_any_kernel(const Params p,
     float dot[GR];
 #pragma unroll
     for (int j = 0; j < GR; ++j) dot[j] = 0.0f;
-    for (int d0 = 0; d0 < head_dim; d0 += kAnyRowBatch) {
-      float rv[kAnyRowBatch];
+    // two batches of rows in flight: the next batch loads while this one is summed
+    auto load = [&](int d0, float (&rv)[kAnyRowBatch]) {
 #pragma unroll
       for (int k = 0; k < kAnyRowBatch; ++k)
         rv[k] = d0 + k < head_dim ? load_stream_f32(r + static_cast<int64_t>(d0 + k) * stride) : 0.0f;
+    };
+    auto sum = [&](int d0, const float (&rv)[kAnyRowBatch]) {
 #pragma unroll
       for (int k = 0; k < kAnyRowBatch; ++k) {
         if (d0 + k >= head_dim) break;
 #pragma unroll
         for (int j = 0; j < GR; ++j) dot[j] = dot[j] + q_any[(j0 + j) * head_dim + d0 + k] * rv[k];
       }
+    };
+    float ra[kAnyRowBatch], rb[kAnyRowBatch];
+    load(0, ra);
+    for (int d0 = 0; d0 < head_dim; d0 += 2 * kAnyRowBatch) {
+      const bool second = d0 + kAnyRowBatch < head_dim;
+      if (second) load(d0 + kAnyRowBatch, rb);
+      sum(d0, ra);
+      if (d0 + 2 * kAnyRowBatch < head_dim) load(d0 + 2 * kAnyRowBatch, ra);
+      if (second) sum(d0 + kAnyRowBatch, rb);
     }
 #pragma unroll
     for (int j = 0; j < GR; ++j) score = score + dot[j] / heads_f;
