@@ -403,7 +403,7 @@ def test_decode_steps_qwen3_06b_shape_two_heads(hip):
     seals on the way.  Ids and state bit-exact, attention within 2e-3 of the
     oracle on every step."""
     lengths = [32 * 512 + 20, 32 * 530 + 30, 32 * 600 + 9, 32 * 515 + 31]
-    print(f"case: G=2 cfg2 shape lengths={lengths}", flush=True)
+    print(f"case: G=2 Qwen3-0.6B heads, lists of 512+ blocks, lengths={lengths}", flush=True)
     case = make_case(771, 4, 16, 8, lengths, table_stride=620, planted=8)
     kv = device_kv(case)
     budget, init, local = 64, 4, 8
