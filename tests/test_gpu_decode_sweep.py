@@ -54,32 +54,47 @@ def config(seed):
                 table_stride=table_stride, rep_stride=rep_stride)
 
 
-def oracle_step(case, k, v, c):
+def oracle_step(case, k, v, c, groups=None):
+    """groups: selection groups (default: one per KV head; 1: the shared selection)."""
+    groups = groups or case.hkv
     O.paged_append(case.pool, PAGE, case.table, case.seq_len, k=k, v=v, batch=case.batch, hkv=case.hkv, d=D)
     O.paged_seal(case.pool, PAGE, case.table, case.seq_len, case.sealed, case.generation, case.reps,
                  case.rep_heads, case.rep_stride, case.batch, case.hq, case.hkv, D, c["local_tokens"])
     sel_stride = c["sel_stride"]
-    esel = np.full((case.batch, case.hkv, sel_stride), -1, np.int32)
-    ecnt = np.zeros((case.batch, case.hkv), np.int32)
+    esel = np.full((case.batch, groups, sel_stride), -1, np.int32)
+    ecnt = np.zeros((case.batch, groups), np.int32)
     for b in range(case.batch):
         bud = c["budget"] if c["budgets"] is None else int(c["budgets"][b])
         s_, n_ = O.paged_score_select(case.query[b:b + 1], case.reps[b:b + 1], case.sealed[b:b + 1], 1, case.hq,
-                                      case.hkv, D, case.rep_heads, case.rep_stride, case.hkv, bud, c["init"],
+                                      case.hkv, D, case.rep_heads, case.rep_stride, groups, bud, c["init"],
                                       c["local"], sel_stride=sel_stride)
         esel[b], ecnt[b] = s_[0], n_[0]
-    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, esel, ecnt, case.hkv,
+    expect = O.paged_sparse_attention(case.pool, PAGE, case.table, case.seq_len, case.sealed, esel, ecnt, groups,
                                       case.query, case.batch, case.hq, case.hkv, D, SCALE)
     return esel, ecnt, expect
 
 
 @pytest.mark.parametrize("seed", range(64))
 def test_decode_step_sweep(hip, seed):
-    c = config(9100 + seed)
-    print(f"case: sweep seed={seed} {c}", flush=True)
+    run_sweep(hip, seed, 9100, 9200, None)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_decode_step_shared_sweep(hip, seed):
+    """The same sweep with the shared selection (select_groups 1): one launch
+    where the lists are short enough (select_attend_shared_supported), the
+    separate launches otherwise; both against the oracle's shared selection."""
+    run_sweep(hip, seed, 9300, 9400, 1)
+
+
+def run_sweep(hip, seed, config_base, case_base, groups):
+    c = config(config_base + seed)
+    print(f"case: sweep seed={seed} groups={groups} {c}", flush=True)
     hq = c["hkv"] * c["group"]
-    case = make_case(9200 + seed, c["batch"], hq, c["hkv"], c["lengths"], table_stride=c["table_stride"],
+    case = make_case(case_base + seed, c["batch"], hq, c["hkv"], c["lengths"], table_stride=c["table_stride"],
                      rep_heads=c["rep_heads"], local_tokens=c["local_tokens"], rep_stride=c["rep_stride"],
                      planted=2)
+    groups = groups or c["hkv"]
     kv = device_kv(case)
     ws, _ = hip.decode_step_workspace(kv)
     st = status_tensor()
@@ -89,16 +104,16 @@ def test_decode_step_sweep(hip, seed):
         k = (rng.standard_normal((c["batch"], c["hkv"], D)) * 2).astype(np.float32)
         v = (rng.standard_normal((c["batch"], c["hkv"], D)) * 2).astype(np.float32)
         case.query[:] = rng.standard_normal(case.query.shape).astype(np.float32)
-        sel, cnt, out = hip.decode_step(kv, to_dev(k), to_dev(v), c["local_tokens"], to_dev(case.query), c["hkv"],
+        sel, cnt, out = hip.decode_step(kv, to_dev(k), to_dev(v), c["local_tokens"], to_dev(case.query), groups,
                                         c["budget"], c["init"], c["local"], SCALE, ws, status=st,
                                         sel_stride=c["sel_stride"], budgets=budgets)
-        esel, ecnt, expect = oracle_step(case, k, v, c)
+        esel, ecnt, expect = oracle_step(case, k, v, c, groups)
         torch.cuda.synchronize()
         assert int(st.item()) == 0, step
         got_sel, got_cnt = sel.cpu().numpy(), cnt.cpu().numpy()
         assert np.array_equal(got_cnt, ecnt), step
         for b in range(c["batch"]):
-            for g in range(c["hkv"]):
+            for g in range(groups):
                 n = int(ecnt[b, g])
                 assert got_sel[b, g, :n].tolist() == esel[b, g, :n].tolist(), (step, b, g)
         got = out.cpu().numpy()
@@ -109,4 +124,4 @@ def test_decode_step_sweep(hip, seed):
     assert np.array_equal(kv.generation.cpu().numpy(), case.generation)
     assert np.array_equal(pool_numpy(kv), case.pool)
     assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
-    assert int(ws.abs().sum().item()) == 0, "arrival counters must be left at zero"
+    assert int(ws[:kv.batch].abs().sum().item()) == 0, "arrival counters must be left at zero"

@@ -103,7 +103,7 @@ def test_shared_decode_steps_bit_exact(hip, hq, local_tokens, f16):
         assert_close_2e3(out.cpu().numpy(), expect)
         if step % 11 == 0 or step == 35:
             check_state(kv, case)
-    assert int(ws.abs().sum().item()) == 0, "arrival counters must be left at zero"
+    assert int(ws[:kv.batch].abs().sum().item()) == 0, "arrival counters must be left at zero"
 
 
 def test_c1_shape_shared_decode_steps_equal_split_launches(hip):
