@@ -280,7 +280,11 @@ int sa_hip_score_select_split_preferred(const sa_paged_kv* kv,
  * 4 query heads per KV head, representatives per KV head, rep_stride <= 256
  * and batch x kv_heads x (kv_heads - 1) x rep_stride x 512 bytes <= 32 MiB
  * (every workgroup of a sequence scores the whole shared set, so the
- * representatives are read once per KV head).  splits >= 1; workspace as for
+ * representatives are read once per KV head).  At a head_dim other than 128
+ * it answers for sa_hip_decode_step only (select_attend refuses that
+ * head_dim): one launch up to 256 with select_groups == kv_heads, 1, 2 or 4
+ * query heads per KV head and representatives per KV head.  splits >= 1;
+ * workspace as for
  * sa_hip_sparse_decode_attention.  Replaces the reference's per-layer
  * select -> pack -> attention sequence (selection_main.cpp:178-230;
  * pipeline_main.cpp:803-876) with selection on the GPU. */

@@ -22,6 +22,7 @@
 // the splits in split order (deterministic).
 #include <algorithm>
 
+#include "attn_rows.hpp"
 #include "sa_device.hpp"
 #include "sa_internal.hpp"
 
@@ -468,53 +469,14 @@ __global__ __launch_bounds__(kThreads) void paged_any_kernel(const PagedAnyParam
 }
 
 // ---- the paged form in token rows (head_dim up to 256) --------------------------
-// The lane layout of the head_dim-128 kernels (attn_core.hpp) at other head
-// dimensions: one KV head's K (or V) row of a token is read by LPR lanes,
-// 16 bytes (8 dimensions) each, LPR the power of two at or above head_dim / 8
-// and at least 8 (lanes past head_dim idle), so one load of a wave covers
-// 64 / LPR whole rows and a page is 32 LPR / 64 loads of K and as many of V,
-// all in flight together (a unit of at most 8 row groups; two units per page
-// at LPR 32).  A row's dot is summed across its lanes, the online softmax
-// runs per wave over the page's rows, and P.V accumulates each lane's 8
-// dimensions over its rows; the rows are added at the end.  Grid (kv_heads,
-// splits, batch); split s takes a contiguous range of the list's pages
-// (selected blocks, then the tail), its 4 waves every 4th unit; the waves
-// combine in LDS into the output or the split's record (the records and the
-// merge of paged_any_kernel).
+// The token-row walk of attn_rows.hpp over the list of (sequence b, KV head
+// g).  Grid (kv_heads, splits, batch); split s takes a contiguous range of
+// the list's pages (selected blocks, then the tail), its 4 waves every 4th
+// unit (a page, or half a page at 32 lanes per row); the waves combine in
+// LDS into the output or the split's record (the records and the merge of
+// paged_any_kernel).
 constexpr int kRowsWaves = 4;
 constexpr int kRowsThreads = kRowsWaves * kWave;
-
-// Sum over the LPR lanes of a token row (every lane of the row gets it).
-template <int LPR>
-__device__ inline float lane_row_sum(float v) {
-  if constexpr (LPR == 8) {
-    v += dpp_f<kDppQuadXor1>(v);
-    v += dpp_f<kDppQuadXor2>(v);
-    v += dpp_f<kDppRowHalfMirror>(v);  // the quads are uniform: exchanges the two quads of 8 lanes
-    return v;
-  } else if constexpr (LPR == 16) {
-    return row16_sum(v);
-  } else {
-    static_assert(LPR == 32, "8, 16 or 32 lanes per row");
-    v = row16_sum(v);
-    return v + shfl_xor_f(v, 16);
-  }
-}
-
-// Sum / max over the token rows of a wave (the lanes of one column).
-template <int LPR>
-__device__ inline float across_rows_sum(float v) {
-#pragma unroll
-  for (int o = LPR; o < kWave; o <<= 1) v += shfl_xor_f(v, o);
-  return v;
-}
-
-template <int LPR>
-__device__ inline float across_rows_max(float v) {
-#pragma unroll
-  for (int o = LPR; o < kWave; o <<= 1) v = fmaxf(v, shfl_xor_f(v, o));
-  return v;
-}
 
 // Tokens of page i of the list (selected blocks, then the tail) and its pool
 // page; 0 when the page does not exist or is invalid (flagged as by
@@ -549,11 +511,7 @@ __device__ inline int list_page(const PagedAnyParams& p, int b, const int32_t* s
 
 template <int G, int LPR>
 __global__ __launch_bounds__(kRowsThreads) void paged_rows_kernel(const PagedAnyParams p) {
-  constexpr int kR = kWave / LPR;                   // token rows per load
-  constexpr int kI = kPageTokens / kR;              // loads per page (K or V)
-  constexpr int kMaxUnit = G == 8 ? 4 : 8;          // row groups held in registers
-  constexpr int NIT = kI < kMaxUnit ? kI : kMaxUnit;  // row groups per unit
-  constexpr int kParts = kI / NIT;                  // units per page
+  using State = rows::RowsState<G, LPR>;
   __shared__ float w_ml[kRowsWaves][G][2];
   __shared__ float w_acc[kRowsWaves][G][LPR * 8];
   const int g = blockIdx.x;
@@ -563,9 +521,6 @@ __global__ __launch_bounds__(kRowsThreads) void paged_rows_kernel(const PagedAny
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int D = p.head_dim;
-  const int row = lane / LPR;
-  const int col = lane % LPR;
-  const bool dims = col * 8 < D;  // this lane's 8 dimensions exist
   const int sg = g / (p.kv_heads / p.select_groups);
   const int64_t list = static_cast<int64_t>(b) * p.select_groups + sg;
   const int32_t* sel = p.selected + list * p.sel_stride;
@@ -580,123 +535,33 @@ __global__ __launch_bounds__(kRowsThreads) void paged_rows_kernel(const PagedAny
   const int i_begin = s * chunk;
   const int i_end = total < i_begin + chunk ? total : i_begin + chunk;
 
-  // this lane's 8 dimensions of each head's query, in the log2 domain
-  const float sl2 = p.scale * kLog2e;
-  const float* q = p.query + (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(g) * G) * D;
-  float qf[G][8];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
-    if (dims) {
-      a = *reinterpret_cast<const float4*>(q + h * D + col * 8);
-      c = *reinterpret_cast<const float4*>(q + h * D + col * 8 + 4);
-    }
-    qf[h][0] = a.x * sl2;
-    qf[h][1] = a.y * sl2;
-    qf[h][2] = a.z * sl2;
-    qf[h][3] = a.w * sl2;
-    qf[h][4] = c.x * sl2;
-    qf[h][5] = c.y * sl2;
-    qf[h][6] = c.z * sl2;
-    qf[h][7] = c.w * sl2;
-  }
-  float m[G], l[G], acc[G][8];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m[h] = kNegInf;
-    l[h] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
-  }
+  State st;
+  st.init(p.query + (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(g) * G) * D, D,
+          p.scale * kLog2e, lane);
   const int64_t tok_elems = 2LL * p.kv_heads * D;
   const int64_t page_elems = kPageTokens * tok_elems;
-  const int64_t lane_off = static_cast<int64_t>(row) * tok_elems + static_cast<int64_t>(g) * D + col * 8;
+  const int64_t lane_off = st.lane_offset(tok_elems, g, D);
   const int64_t v_off = static_cast<int64_t>(p.kv_heads) * D;
-
-  for (int u = i_begin * kParts + wave; u < i_end * kParts; u += kRowsWaves) {
-    const int i = u / kParts;
-    const int part = u % kParts;
+  for (int u = i_begin * State::kParts + wave; u < i_end * State::kParts; u += kRowsWaves) {
+    const int i = u / State::kParts;
+    const int part = u % State::kParts;
     int64_t page = 0;
     const int valid = list_page(p, b, sel, n_sel, sealed, len, i, page);
-    if (valid <= 0) continue;
-    const uint16_t* base = p.pool + page * page_elems + lane_off;
-    uint4 kr[NIT], vr[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int rg = part * NIT + it;  // row group of the page
-      if (dims && rg * kR + row < valid) {
-        kr[it] = load_stream16(base + static_cast<int64_t>(rg) * kR * tok_elems);
-        vr[it] = load_stream16(base + static_cast<int64_t>(rg) * kR * tok_elems + v_off);
-      } else {
-        kr[it] = make_uint4(0, 0, 0, 0);
-        vr[it] = make_uint4(0, 0, 0, 0);
-      }
-    }
-    // logits of this lane's rows for every head
-    float sc[G][NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const uint32_t w[4] = {kr[it].x, kr[it].y, kr[it].z, kr[it].w};
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float a = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float kj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
-          a = __builtin_fmaf(qf[h][j], kj, a);
-        }
-        sc[h][it] = lane_row_sum<LPR>(a);
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float pmax = kNegInf;
-#pragma unroll
-      for (int it = 0; it < NIT; ++it) {
-        if ((part * NIT + it) * kR + row >= valid) sc[h][it] = kNegInf;
-        pmax = fmaxf(pmax, sc[h][it]);
-      }
-      pmax = across_rows_max<LPR>(pmax);
-      const float mn = fmaxf(m[h], pmax);
-      // mn == -inf only if nothing finite was seen: the state stays empty
-      const float corr = (m[h] == mn) ? 1.0f : __builtin_amdgcn_exp2f(m[h] - mn);
-      const float base_m = (mn == kNegInf) ? 0.0f : mn;
-      m[h] = mn;
-      float lsum = l[h] * corr;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[h][j] *= corr;
-#pragma unroll
-      for (int it = 0; it < NIT; ++it) {
-        sc[h][it] = __builtin_amdgcn_exp2f(sc[h][it] - base_m);
-        lsum += sc[h][it];
-      }
-      l[h] = lsum;
-    }
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float vj = (j & 1) ? hi_h2f(w[j >> 1]) : lo_h2f(w[j >> 1]);
-#pragma unroll
-        for (int h = 0; h < G; ++h) acc[h][j] = __builtin_fmaf(sc[h][it], vj, acc[h][j]);
-      }
-    }
+    if (valid <= part * State::NIT * State::kR) continue;  // no page, or no token in this unit
+    st.attend_unit(p.pool + page * page_elems + lane_off, tok_elems, v_off, valid, part);
   }
 
   // the wave's rows added, then the waves combined
+  st.finish();
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    l[h] = across_rows_sum<LPR>(l[h]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[h][j] = across_rows_sum<LPR>(acc[h][j]);
     if (lane == 0) {
-      w_ml[wave][h][0] = m[h];
-      w_ml[wave][h][1] = l[h];
+      w_ml[wave][h][0] = st.m[h];
+      w_ml[wave][h][1] = st.l[h];
     }
-    if (row == 0 && dims) {
+    if (st.row == 0 && st.dims) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) w_acc[wave][h][col * 8 + j] = acc[h][j];
+      for (int j = 0; j < 8; ++j) w_acc[wave][h][st.col * 8 + j] = st.acc[h][j];
     }
   }
   __syncthreads();
@@ -758,7 +623,7 @@ __global__ __launch_bounds__(kThreads) void paged_any_merge_kernel(const PagedAn
 
 // head_dim the row layout takes (32 lanes x 8 dimensions); larger ones run
 // paged_any_kernel.
-constexpr int kMaxRowsHeadDim = 256;
+constexpr int kMaxRowsHeadDim = rows::kMaxHeadDim;
 
 template <int LPR>
 hipError_t launch_rows(const PagedAnyParams& p, int group, dim3 grid, hipStream_t stream) {
@@ -827,7 +692,7 @@ hipError_t launch_paged_attention_any(const AttnLaunch& a, hipStream_t stream) {
   const int group = a.query_heads / a.kv_heads;
   const dim3 grid(a.kv_heads, a.splits, a.batch);
   if (a.head_dim <= kMaxRowsHeadDim) {
-    const int lpr = a.head_dim <= 64 ? 8 : (a.head_dim <= 128 ? 16 : 32);
+    const int lpr = rows::lanes_per_row(a.head_dim);
     hipError_t e = hipSuccess;
     switch (lpr) {
       case 8: e = launch_rows<8>(p, group, grid, stream); break;

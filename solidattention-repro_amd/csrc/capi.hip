@@ -527,10 +527,15 @@ int sa_hip_score_select_split_preferred(const sa_paged_kv* kv, const sa_select_p
 int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv, const sa_select_params* params) {
   if (!kv || !params) return 1;
   if (sa::general_head_dim(kv->head_dim)) {
+    const int64_t lists = static_cast<int64_t>(kv->batch) * kv->kv_heads;
+    // the one-launch step once its workgroups (two per CU) fill the device
+    if (sa::select_attend_rows_supported(kv->query_heads, kv->kv_heads, kv->rep_heads, params->select_groups,
+                                         kv->head_dim) &&
+        lists >= 2LL * sa::compute_units())
+      return 1;
     // the token-row attention (4-wave workgroups, several per CU): about four
     // workgroups per CU with at least 4 pages per wave (measured at B=64, 8
     // KV heads, head_dim 64: splits 2 81 us against 85 us for 1 and 88 us for 4)
-    const int64_t lists = static_cast<int64_t>(kv->batch) * kv->kv_heads;
     const int64_t pages = std::max<int32_t>(params->budget_blocks + 2, 1);
     int64_t splits = 1;
     while (lists * splits < 4LL * sa::compute_units() && (splits * 2) * 4 * 4 <= pages) splits *= 2;
@@ -552,7 +557,12 @@ int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv, const sa_sele
 }
 
 int sa_hip_select_attend_fused(const sa_paged_kv* kv, const sa_select_params* params, int32_t splits) {
-  if (!kv || !params || kv->head_dim != sa::kHeadDim || splits != 1) return 0;
+  if (!kv || !params || splits != 1) return 0;
+  if (sa::general_head_dim(kv->head_dim))  // the decode step only
+    return sa::select_attend_rows_supported(kv->query_heads, kv->kv_heads, kv->rep_heads, params->select_groups,
+                                            kv->head_dim)
+               ? 1
+               : 0;
   return sa::select_attend_supported(kv->query_heads, kv->kv_heads, params->select_groups, params->sel_stride,
                                      kv->reps, kv->rep_stride) ||
                  sa::select_attend_shared_supported(kv->batch, kv->query_heads, kv->kv_heads, kv->rep_heads,
@@ -588,6 +598,7 @@ static sa::SelectAttendLaunch fused_launch(const sa_paged_kv* kv, const sa::Sele
   f.local_blocks = l.local_blocks;
   f.sel_stride = l.sel_stride;
   f.select_groups = l.select_groups;
+  f.head_dim = kv->head_dim;
   f.scale = scale;
   return f;
 }
@@ -657,9 +668,10 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
   if (!aligned16(ka) || !aligned16(va)) return fail(SA_HIP_EINVAL, "%s: k/v must be 16-byte aligned", op);
   if (seal)
     if (int e = online_check(kv, seal, query, local_tokens, op)) return e;
-  if (sa::general_head_dim(kv->head_dim)) {
-    // the general kernels in sequence: append + seal, scoring into the
-    // workspace's scores, selection, attention
+  if (sa::general_head_dim(kv->head_dim) && (seal || !sa_hip_select_attend_fused(kv, params, splits))) {
+    // the general kernels in sequence (where the one-launch step does not
+    // apply): append + seal, scoring into the workspace's scores, selection,
+    // attention
     if (seal) return fail(SA_HIP_EINVAL, "%s: the online seal is built for head_dim %d", op, sa::kHeadDim);
     const size_t rb = split_records_bytes(kv, splits);
     const size_t sb = split_scores_bytes(kv, params->select_groups);

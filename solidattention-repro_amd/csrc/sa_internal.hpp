@@ -162,6 +162,7 @@ struct SelectAttendLaunch {
   int32_t local_blocks;
   int32_t sel_stride;
   int32_t select_groups;  // kv_heads (a block set per KV group), or 1 (shared)
+  int32_t head_dim;       // 0 or kHeadDim; another (decode step only): select_attend_rows_supported()
   float scale;
   // decode step: append one token per sequence (fp32 k/v or FP16 k16/v16),
   // seal, then select + attend; arrive = [batch] zeroed arrival counters
@@ -192,6 +193,11 @@ int select_attend_per_cu(int32_t query_heads, int32_t kv_heads);
 // KV head (every workgroup scores the whole set) within a small byte budget.
 bool select_attend_shared_supported(int32_t batch, int32_t query_heads, int32_t kv_heads, int32_t rep_heads,
                                     int32_t select_groups, int32_t rep_stride);
+// The one-launch decode step at a head_dim other than 128: a multiple of 8
+// up to 256, 1, 2 or 4 query heads per KV head, selection per KV group,
+// representatives per KV head.
+bool select_attend_rows_supported(int32_t query_heads, int32_t kv_heads, int32_t rep_heads, int32_t select_groups,
+                                  int32_t head_dim);
 hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream);
 
 // InfLLM local-causal block representatives of a prefill (contiguous KV).

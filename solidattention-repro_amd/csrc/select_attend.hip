@@ -30,6 +30,7 @@
 // This file is compiled with -ffp-contract=off (scoring and seal sums are
 // bit-exact); the attention writes its fused multiply-adds explicitly.
 #include "attn_core.hpp"
+#include "attn_rows.hpp"
 #include "online_seal.hpp"
 #include "select_core.hpp"
 
@@ -682,6 +683,211 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_shared(const Params p)
 }
 
 
+// ---- one launch at a head_dim other than 128 (up to 256) -----------------------
+// decode_kernel's step with the head_dim at run time (hd): append + seal of
+// KV head g (the new token as hd / 4 four-value pieces of K and of V; the
+// seal's mean key summed in token order by hd threads), the group's scoring
+// with one lane per block (the GR = G query heads sharing the KV head's
+// representative row summed side by side over one pass of it, the
+// reference's sequential dots, then dot / heads in head order: the
+// arithmetic of score_any_kernel, bit-identical scores), wave 0's selection
+// and the planned walk of the forced, selected and tail pages, each page
+// with the token-row walk of attn_rows.hpp (LPR lanes per token row).
+// Representatives per KV head only.
+constexpr int kRowsMaxG = 4;
+
+template <bool F16>
+__device__ inline bool append_seal_head_any(const Params& p, int b, int g, int hd, int64_t& len, int& n,
+                                            int& added) {
+  const int tid = threadIdx.x;
+  const int64_t page = table_page(p.v, b, len / kPageTokens);
+  if (page < 0) {
+    if (tid == 0) flag_status(p.v.status, kStatusCapacity);
+    return false;
+  }
+  const int pieces = hd / 4;  // four values each, of K then of V
+  for (int u = tid; u < 2 * pieces; u += kThreads) {
+    const int is_v = u / pieces;
+    const int e = (u % pieces) * 4;
+    const int64_t src = (static_cast<int64_t>(b) * p.v.kv_heads + g) * hd + e;
+    ushort4 h;
+    if constexpr (F16) {
+      h = *reinterpret_cast<const ushort4*>((is_v ? p.v16 : p.k16) + src);
+    } else {
+      const float4 f = *reinterpret_cast<const float4*>((is_v ? p.vv : p.k) + src);
+      h = make_ushort4(f2h_rne(f.x), f2h_rne(f.y), f2h_rne(f.z), f2h_rne(f.w));
+    }
+    uint16_t* dst = const_cast<uint16_t*>(p.v.pool) + page * p.v.page_elems +
+                    (len % kPageTokens) * p.v.token_elems + static_cast<int64_t>(is_v) * p.v.kv_heads * hd +
+                    static_cast<int64_t>(g) * hd + e;
+    *reinterpret_cast<ushort4*>(dst) = h;
+  }
+  len += 1;
+  // the new token visible to the seal below; without a seal nothing in this
+  // workgroup reads it
+  if (len >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens) __syncthreads();
+  while (len >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens) {
+    const int64_t sp = n < p.rep_stride ? table_page(p.v, b, n) : -1;
+    if (sp < 0) {
+      if (tid == 0) flag_status(p.v.status, kStatusCapacity);
+      break;
+    }
+    if (tid < hd) {
+      const uint16_t* src = p.v.pool + sp * p.v.page_elems + static_cast<int64_t>(g) * hd + tid;
+      float sum = 0.0f;
+#pragma unroll 8
+      for (int t = 0; t < kPageTokens; ++t) sum = sum + h2f(src[t * p.v.token_elems]);
+      p.reps[((static_cast<int64_t>(b) * p.rep_heads + g) * hd + tid) * p.rep_stride + n] =
+          sum / static_cast<float>(kPageTokens);
+    }
+    ++n;
+    ++added;
+  }
+  return true;
+}
+
+// Score of block blk for the group's G heads (one representative row),
+// q_s = the G query rows of hd floats in LDS.
+template <int G>
+__device__ inline float score_block_any(const Params& p, const float* q_s, int b, int g, int hd, int blk) {
+  constexpr int kBatch = 32;
+  const int64_t stride = p.rep_stride;
+  const float* r = p.reps + (static_cast<int64_t>(b) * p.rep_heads + g) * hd * stride + blk;
+  float dot[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) dot[j] = 0.0f;
+  for (int d0 = 0; d0 < hd; d0 += kBatch) {
+    float rv[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      rv[k] = d0 + k < hd ? load_stream_f32(r + static_cast<int64_t>(d0 + k) * stride) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (d0 + k >= hd) break;
+#pragma unroll
+      for (int j = 0; j < G; ++j) dot[j] = dot[j] + q_s[j * hd + d0 + k] * rv[k];
+    }
+  }
+  const float heads_f = static_cast<float>(G);
+  float score = 0.0f;
+#pragma unroll
+  for (int j = 0; j < G; ++j) score = score + dot[j] / heads_f;
+  return score;
+}
+
+template <int G, int LPR, bool F16>
+__global__ __launch_bounds__(kThreads) void decode_kernel_rows(const Params p, int hd) {
+  static_assert(G <= kRowsMaxG, "1, 2 or 4 query heads per KV head");
+  using State = rows::RowsState<G, LPR>;
+  const int g = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+
+  __shared__ __align__(16) float q_s[G * rows::kMaxHeadDim];
+  __shared__ uint32_t keys[kMaxSelectBlocks];  // block keys, then the selected ids, then the late pages
+  __shared__ uint32_t hist[256];
+  __shared__ ClaimSmem cl;
+  __shared__ float w_ml[kWaves][G][2];
+  __shared__ float w_acc[kWaves][G][LPR * 8];
+
+  const int64_t out_row = static_cast<int64_t>(b) * p.v.kv_heads + g;
+  const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * hd;
+  for (int e = tid; e < G * hd; e += kThreads) q_s[e] = q_group[e];
+  int64_t len = p.seq_len[b];
+  int n = p.sealed[b];
+
+  SeqCommit commit{};
+  commit.gen = p.generation ? p.generation[b] : 0;
+  commit.appended = append_seal_head_any<F16>(p, b, g, hd, len, n, commit.added);
+  if (tid == 0) commit.arrived = atomicAdd(&p.arrive[b], 1);
+
+  State st;
+  st.init(q_group, hd, p.qscale, lane);
+
+  // ---- score; the forced blocks' pages looked up meanwhile ----------------
+  const bool n_ok = n >= 0 && n <= p.rep_stride && n <= kMaxSelectBlocks;
+  const sel::Budget bs =
+      n_ok ? sel::budget_split(n, p.budget, p.budgets, b, p.init_blocks, p.local_blocks, p.sel_stride)
+           : sel::Budget{0, 0, 0, false, true};
+  const Forced fb = forced_blocks(bs, n);
+  const int32_t early = wave == kWaves - 1 ? early_page(p, b, n, fb, lane) : -1;
+  __syncthreads();  // the query rows, and the representatives this workgroup sealed
+  if (n_ok && !bs.take_all) {  // (a budget that takes every block needs no scores)
+    for (int blk = tid; blk < n; blk += kThreads) keys[blk] = sel::order_key(score_block_any<G>(p, q_s, b, g, hd, blk));
+  }
+  if (wave == kWaves - 1) cl.early[lane] = early;
+  if (tid == 0) cl.late_ready = 0;
+  int wn = n;
+  int64_t wlen = len;
+  if (wn < 0 || wlen < static_cast<int64_t>(wn) * kPageTokens) {
+    if (tid == 0) flag_status(p.v.status, kStatusBadLength);
+    if (wn < 0) wn = 0;
+    wlen = static_cast<int64_t>(wn) * kPageTokens;
+  }
+  const int tail_pages = static_cast<int>((wlen - static_cast<int64_t>(wn) * kPageTokens + kPageTokens - 1) /
+                                          kPageTokens);
+  __syncthreads();  // keys, the early pages and the flag visible
+
+  // ---- select (wave 0) and walk (every wave, planned positions) -------------
+  int32_t* late = reinterpret_cast<int32_t*>(keys);
+  if (wave == 0) {
+    int count = 0;
+    if (!n_ok || bs.bad) {
+      if (lane == 0) {
+        flag_status(p.v.status, n_ok ? kStatusBadBudget : kStatusCapacity);
+        p.counts[out_row] = 0;
+      }
+    } else {
+      count = sel::select_ids_wave(keys, n, bs, hist, p.selected + out_row * p.sel_stride, p.sel_stride, late);
+      if (lane == 0) p.counts[out_row] = count;
+    }
+    list_late(p, b, cl, late, kMaxSelectBlocks, count, fb, wn, tail_pages, lane);
+  }
+  const int64_t lane_off = st.lane_offset(p.v.token_elems, g, hd);
+  const int64_t v_off = static_cast<int64_t>(p.v.kv_heads) * hd;
+  PlanPages src(cl, late, p.v, b, wave, fb.F, wn, wlen);
+  for (;;) {
+    const attn::PageRef pr = src.next(true);
+    if (pr.valid <= 0) break;
+    st.attend_page(p.v.pool + pr.page * p.v.page_elems + lane_off, p.v.token_elems, v_off, pr.valid);
+  }
+
+  st.finish();
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    if (lane == 0) {
+      w_ml[wave][h][0] = st.m[h];
+      w_ml[wave][h][1] = st.l[h];
+    }
+    if (st.row == 0 && st.dims) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w_acc[wave][h][st.col * 8 + j] = st.acc[h][j];
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < G * hd; e += kThreads) {
+    const int h = e / hd;
+    const int d = e % hd;
+    float mx = rows::kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, w_ml[w][h][0]);
+    float lw = 0.0f, aw = 0.0f;
+    if (mx != rows::kNegInf) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float f = __builtin_amdgcn_exp2f(w_ml[w][h][0] - mx);  // waves without tokens: 0
+        lw += w_ml[w][h][1] * f;
+        aw += w_acc[w][h][d] * f;
+      }
+    }
+    p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * hd + d] = lw > 0.0f ? aw / lw : 0.0f;
+  }
+  if (tid == 0) commit_sequence(p, b, len, n, commit);
+}
+
+
 // ---- 4 query heads per KV head: LDS-staged pages, q.K on the matrix cores --
 // One 8-wave workgroup per (sequence, KV head), one per CU (the eight 16 KiB
 // page slots).  After append + seal, all 512 threads score two blocks per lane
@@ -921,7 +1127,76 @@ hipError_t launch_shared(const Params& p, int batch, hipStream_t stream) {
   return hipGetLastError();
 }
 
+bool select_attend_rows_supported(int32_t query_heads, int32_t kv_heads, int32_t rep_heads, int32_t select_groups,
+                                  int32_t head_dim) {
+  if (kv_heads <= 0 || select_groups != kv_heads || rep_heads != kv_heads) return false;
+  const int group = query_heads / kv_heads;
+  return (group == 1 || group == 2 || group == 4) && head_dim > 0 && head_dim % 8 == 0 &&
+         head_dim <= rows::kMaxHeadDim && head_dim != kHeadDim;
+}
+
+template <int LPR, bool F16>
+hipError_t launch_rows_step(const Params& p, int batch, int hd, hipStream_t stream) {
+  const dim3 grid(p.v.kv_heads, batch);
+  switch (p.query_heads / p.v.kv_heads) {
+    case 1: hipLaunchKernelGGL((decode_kernel_rows<1, LPR, F16>), grid, dim3(kThreads), 0, stream, p, hd); break;
+    case 2: hipLaunchKernelGGL((decode_kernel_rows<2, LPR, F16>), grid, dim3(kThreads), 0, stream, p, hd); break;
+    default: hipLaunchKernelGGL((decode_kernel_rows<4, LPR, F16>), grid, dim3(kThreads), 0, stream, p, hd); break;
+  }
+  return hipGetLastError();
+}
+
+template <bool F16>
+hipError_t launch_rows_lpr(const Params& p, int batch, int hd, hipStream_t stream) {
+  switch (rows::lanes_per_row(hd)) {
+    case 8: return launch_rows_step<8, F16>(p, batch, hd, stream);
+    case 16: return launch_rows_step<16, F16>(p, batch, hd, stream);
+    default: return launch_rows_step<32, F16>(p, batch, hd, stream);
+  }
+}
+
 hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream) {
+  const int hd = s.head_dim > 0 ? s.head_dim : kHeadDim;
+  if (hd != kHeadDim) {
+    // another head_dim: the decode step only, representatives per KV head
+    if (!s.append || !s.arrive || s.ring ||
+        !select_attend_rows_supported(s.query_heads, s.kv_heads, s.rep_heads, s.select_groups, hd))
+      return hipErrorInvalidValue;
+    Params p{};
+    p.v.pool = s.pool;
+    p.v.table = s.table;
+    p.v.status = s.status;
+    p.v.num_pages = s.num_pages;
+    p.v.contig_tokens = 0;
+    p.v.token_elems = 2 * s.kv_heads * hd;
+    p.v.page_elems = static_cast<int64_t>(kPageTokens) * p.v.token_elems;
+    p.v.table_stride = s.table_stride;
+    p.v.kv_heads = s.kv_heads;
+    p.seq_len = s.seq_len;
+    p.sealed = s.sealed;
+    p.generation = s.generation;
+    p.reps = s.reps;
+    p.query = s.query;
+    p.selected = s.selected;
+    p.counts = s.counts;
+    p.out = s.out;
+    p.k = s.k;
+    p.vv = s.v;
+    p.k16 = s.k16;
+    p.v16 = s.v16;
+    p.arrive = s.arrive;
+    p.query_heads = s.query_heads;
+    p.rep_heads = s.rep_heads;
+    p.rep_stride = s.rep_stride;
+    p.budget = s.budget;
+    p.budgets = s.budgets;
+    p.init_blocks = s.init_blocks;
+    p.local_blocks = s.local_blocks;
+    p.sel_stride = s.sel_stride;
+    p.local_tokens = s.local_tokens;
+    p.qscale = s.scale * attn::kLog2e;
+    return s.k16 ? launch_rows_lpr<true>(p, s.batch, hd, stream) : launch_rows_lpr<false>(p, s.batch, hd, stream);
+  }
   const bool shared = s.select_groups != s.kv_heads;
   if (shared ? !select_attend_shared_supported(s.batch, s.query_heads, s.kv_heads, s.rep_heads, s.select_groups,
                                                s.rep_stride)

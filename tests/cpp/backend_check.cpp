@@ -247,8 +247,8 @@ void check_lifecycle() {
 }
 
 // Decode steps through SparseDecoder::decode_step (one fused launch per
-// step at G=2 and head_dim 128; the general kernels in sequence at another
-// head_dim): 4 sequences, 34 steps across seal boundaries, against the
+// step at G=2: the tuned kernel at head_dim 128, the token-row kernel at 64
+// and 256): 4 sequences, 34 steps across seal boundaries, against the
 // oracle's append, seal, select and attention (qwen_chain_main.cpp:390-395,
 // kv_lifecycle_main.cpp:92-113, selection.cpp:96-147).  groups: selection
 // groups (8: one block set per KV group; 1: the shared selection of the C2/P1
@@ -276,8 +276,8 @@ void check_decode_step(std::size_t d = 128, const std::string& tag = "", std::si
   pool.reps().upload(reps);
   sa::hip::SparseDecoder dec(pool, sa_select_params{static_cast<int32_t>(groups), static_cast<int32_t>(budget), 1, 2,
                                                     static_cast<int32_t>(budget), 0, nullptr});
-  // fused at head_dim 128 only
-  record("decode_step_fused" + tag, dec.fused(pool) ? "true" : "false", dec.fused(pool) == (d == 128));
+  // one launch at every head_dim up to 256 (the token-row kernel away from 128)
+  record("decode_step_fused" + tag, dec.fused(pool) ? "true" : "false", dec.fused(pool) == (d <= 256));
   sa::hip::DeviceArray<float> dk(batch * hkv * d), dv(batch * hkv * d), dq(batch * hq * d), dout(batch * hq * d);
   std::vector<float> k(batch * hkv * d), v(batch * hkv * d), q(batch * hq * d), out(batch * hq * d);
   std::vector<int32_t> sel(batch * groups * budget), cnt(batch * groups);

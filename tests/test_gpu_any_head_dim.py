@@ -198,16 +198,20 @@ def test_attention_general_head_dim_bad_block_flagged(hip):
     assert_close_2e3(out.cpu().numpy()[1], expect.reshape(out.shape)[1])
 
 
-@pytest.mark.parametrize("d,hq,hkv,groups,splits,local", [(64, 16, 8, 8, 1, 0), (96, 8, 4, 1, 2, 4),
-                                                          (256, 16, 4, 4, 3, 0)])
-def test_decode_steps_general_head_dim(hip, d, hq, hkv, groups, splits, local):
-    """sa_hip_decode_step at another head_dim (its launches in sequence: append
-    + seal, scoring, selection, attention) over 36 steps that seal blocks:
+@pytest.mark.parametrize("d,hq,hkv,groups,splits,local,f16", [
+    (64, 16, 8, 8, 1, 0, False), (96, 8, 4, 1, 2, 4, False), (256, 16, 4, 4, 3, 0, False),
+    (96, 8, 4, 4, 1, 4, False), (256, 16, 4, 4, 1, 0, True), (8, 4, 4, 4, 1, 0, False),
+    (200, 8, 8, 8, 1, 3, False), (64, 32, 8, 8, 1, 0, True), (64, 16, 8, 8, 2, 0, False)])
+def test_decode_steps_general_head_dim(hip, d, hq, hkv, groups, splits, local, f16):
+    """sa_hip_decode_step at another head_dim over 36 steps that seal blocks:
+    one launch (decode_kernel_rows: selection per KV group, splits 1) or its
+    launches in sequence (append + seal, scoring, selection, attention);
     state bit-exact, ids equal, attention within 2e-3 of the oracle at every
-    step."""
-    print(f"case: decode steps d={d} hq={hq} hkv={hkv} groups={groups} splits={splits}", flush=True)
+    step, fp32 and FP16 token input."""
+    print(f"case: decode steps d={d} hq={hq} hkv={hkv} groups={groups} splits={splits} f16={f16}", flush=True)
     st = State(120 + d, 2, hq, hkv, d, [32 * 30 + 29, 32 * 8 + 2], local=local)
     kv = st.device(hip)
+    assert hip.select_attend_fused(kv, groups, splits) == (groups == hkv and splits == 1)
     budget, init, loc = 16, 1, 2
     scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
     ws, _ = hip.decode_step_workspace(kv, splits)
@@ -216,9 +220,18 @@ def test_decode_steps_general_head_dim(hip, d, hq, hkv, groups, splits, local):
         k = st.rng.standard_normal((st.batch, hkv, d)).astype(np.float32)
         v = st.rng.standard_normal((st.batch, hkv, d)).astype(np.float32)
         q = st.rng.standard_normal((st.batch, hq, d)).astype(np.float32)
-        sel, cnt, out = hip.decode_step(kv, to_dev(k), to_dev(v), local, to_dev(q), groups, budget, init, loc,
+        if f16:
+            k16, v16 = k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)
+            kd = to_dev(k16.view(np.int16)).view(torch.uint16)
+            vd = to_dev(v16.view(np.int16)).view(torch.uint16)
+        else:
+            kd, vd = to_dev(k), to_dev(v)
+        sel, cnt, out = hip.decode_step(kv, kd, vd, local, to_dev(q), groups, budget, init, loc,
                                         scale, ws, splits=splits, status=status)
-        O.paged_append(st.pool, PAGE, st.table, st.seq_len, k=k, v=v, batch=st.batch, hkv=hkv, d=d)
+        if f16:
+            O.paged_append(st.pool, PAGE, st.table, st.seq_len, k16=k16, v16=v16, batch=st.batch, hkv=hkv, d=d)
+        else:
+            O.paged_append(st.pool, PAGE, st.table, st.seq_len, k=k, v=v, batch=st.batch, hkv=hkv, d=d)
         O.paged_seal(st.pool, PAGE, st.table, st.seq_len, st.sealed, st.gen, st.reps, st.rep_heads, st.rep_stride,
                      st.batch, hq, hkv, d, local)
         esel, ecnt = O.paged_score_select(q, st.reps, st.sealed, st.batch, hq, hkv, d, st.rep_heads,

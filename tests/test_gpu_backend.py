@@ -32,8 +32,8 @@ def test_cpp_backend_check(hip):
     for d in (64, 256):  # any head_dim through make_hip_backend()
         assert m[f"c1_head_dim_{d}_attention_max_abs_error"] <= 2e-5
         assert m[f"c1_head_dim_{d}_consumed_abs_error"] <= 1e-4
-        # and through the paged C++ API (SparseDecoder over the general kernels)
-        assert m[f"decode_step_fused_head_dim_{d}"] is False
+        # and through the paged C++ API (SparseDecoder: one launch, the token-row kernel)
+        assert m[f"decode_step_fused_head_dim_{d}"] is True
         assert m[f"decode_step_selected_ids_exact_head_dim_{d}"] is True
         assert m[f"decode_step_state_bytes_exact_head_dim_{d}"] is True
         assert m[f"decode_step_max_rel_error_head_dim_{d}"] <= 2e-3
