@@ -54,9 +54,12 @@ extern "C" {
  * sa_hip_score_select (given the scores buffer), sa_hip_score_select_split,
  * sa_hip_sparse_decode_attention and sa_hip_decode_step(_f16): at any other
  * multiple of 8 up to 512 they run general kernels (append + seal one
- * workgroup per sequence; scoring one lane per block; attention over the
- * page list; the decode step as those launches in sequence), with the same
- * results (bit-exact selection and state, attention within fp32 rounding).
+ * workgroup per sequence, the bulk seal spread over blocks and KV heads;
+ * scoring one lane per block; attention over the page list in token rows up
+ * to 256; the decode step as one launch up to 256 with selection per KV
+ * group and representatives per KV head, else those launches in sequence),
+ * with the same results (bit-exact selection and state, attention within
+ * fp32 rounding).
  * The other entry points (chunked and split-phase attention, the chunked
  * selection, select-attend, the online seal, the allocation-free step)
  * refuse a head_dim other than 128 with SA_HIP_EINVAL. */
@@ -293,9 +296,10 @@ int sa_hip_select_attend_fused(const sa_paged_kv* kv,
 /* The split count to pass to sa_hip_select_attend / sa_hip_decode_step: 1
  * (the fused launch) when the fused kernel applies and its workgroups fill
  * the device (batch x kv_heads >= 2 x CUs), or for the shared selection's
- * one launch whenever it applies; at a head_dim other than 128, splits that
- * give about four attention workgroups per CU with at least 4 pages per
- * wave; otherwise
+ * one launch whenever it applies; at a head_dim other than 128, 1 where the
+ * one-launch step applies and fills the device, else splits that give about
+ * four attention workgroups per CU with at least 4 pages per wave;
+ * otherwise
  * sa_hip_attention_splits_for(batch, query_heads, kv_heads, budget_blocks + 2) for the
  * separate launches. */
 int32_t sa_hip_select_attend_default_splits(const sa_paged_kv* kv,
