@@ -280,7 +280,7 @@ int sa_hip_score_select_split_preferred(const sa_paged_kv* kv,
  * select_groups == kv_heads with 1, 2 or 4 query heads per KV head (4: also
  * sel_stride <= 2048 and an even rep_stride with 8-byte aligned
  * representatives), or the shared selection (select_groups 1) with 1, 2 or
- * 4 query heads per KV head, representatives per KV head, rep_stride <= 256
+ * 4 query heads per KV head, representatives per KV head, rep_stride <= 128
  * and batch x kv_heads x (kv_heads - 1) x rep_stride x 512 bytes <= 32 MiB
  * (every workgroup of a sequence scores the whole shared set, so the
  * representatives are read once per KV head).  At a head_dim other than 128

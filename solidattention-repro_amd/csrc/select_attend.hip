@@ -562,11 +562,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_shared(const Params p)
   __shared__ float dots[kMaxSelectHeads][kWave + 1];
   // block keys, then the selected ids, then the late pages; the register
   // selection reads n rounded up to a multiple of 256 keys
-  __shared__ uint32_t keys[kMaxSharedFusedBlocks + kTailPages];
+  constexpr int kKeys = (kMaxSharedFusedBlocks + 255) / 256 * 256 + kTailPages;
+  __shared__ uint32_t keys[kKeys];
   __shared__ uint32_t hist[256];
   __shared__ attn::CombineSmem<G, kWaves> cs;
   __shared__ ClaimSmem cl;
-  static_assert(kMaxSharedFusedBlocks % 256 == 0, "whole register selections");
 
   const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
   int64_t len = p.seq_len[b];
@@ -660,7 +660,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel_shared(const Params p)
                                    p.sel_stride, late);
       if (lane == 0 && g == 0) p.counts[b] = count;
     }
-    list_late(p, b, cl, late, kMaxSharedFusedBlocks + kTailPages, count, fb, wn, tail_pages, lane);
+    list_late(p, b, cl, late, kKeys, count, fb, wn, tail_pages, lane);
   }
   PlanPages src(cl, late, p.v, b, wave, fb.F, wn, wlen);
   for (;;) {

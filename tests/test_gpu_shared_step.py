@@ -148,12 +148,12 @@ def test_c1_shape_shared_decode_steps_equal_split_launches(hip):
 @pytest.mark.parametrize("hq", [16, 8, 32])
 def test_shared_select_attend_budgets_and_ties(hip, hq):
     """select_attend (no append) with select_groups 1 in one launch: mixed
-    lengths (empty, a single block, under and over the budget, 200 blocks),
+    lengths (empty, a single block, under and over the budget, 120 blocks),
     per-sequence budgets, and duplicated representatives (equal scores,
     lowest id first)."""
     print(f"case: shared select_attend hq={hq}", flush=True)
-    lengths = [0, 32, 32 * 5 + 7, 32 * 200 + 3, 32 * 40]
-    case = make_case(920 + hq, 5, hq, 8, lengths, table_stride=202, planted=3)
+    lengths = [0, 32, 32 * 5 + 7, 32 * 120 + 3, 32 * 40]
+    case = make_case(920 + hq, 5, hq, 8, lengths, table_stride=122, planted=3)
     for b in (3, 4):
         case.reps[b, :, :, 20:30] = case.reps[b, :, :, 10:11]  # ties with block 10
     kv = device_kv(case)
@@ -171,16 +171,16 @@ def test_shared_select_attend_budgets_and_ties(hip, hq):
 
 def test_shared_one_launch_predicate(hip):
     """The one-launch shared form takes 1, 2 or 4 query heads per KV head,
-    per-KV-head representatives, rows of at most 256 blocks and a bounded
+    per-KV-head representatives, rows of at most 128 blocks and a bounded
     repeat of the representative reads; other shapes run the split launches."""
     def fused(batch, hq, table_stride, rep_heads=None):
         case = make_case(930, batch, hq, 8, [32 * 4] * batch, table_stride=table_stride, rep_heads=rep_heads)
         return hip.select_attend_fused(device_kv(case), 1)
     assert fused(1, 16, 64)
-    assert fused(2, 8, 250)
+    assert fused(2, 8, 120)
     assert fused(1, 32, 64)
     assert not fused(1, 64, 64)            # 8 query heads per KV head
-    assert not fused(1, 16, 300)           # rows past 256 blocks
+    assert not fused(1, 16, 130)           # rows past 128 blocks
     assert not fused(1, 16, 64, rep_heads=16)  # a representative per query head
     assert fused(16, 16, 64)
     assert not fused(20, 16, 64)           # the repeated reads past the byte budget
