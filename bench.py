@@ -93,6 +93,9 @@ def parse():
                          "longest-first schedule)")
     ap.add_argument("--microbatches", type=int, default=1,
                     help="layer workload: the batch in this many parts, each a chain of layers on its own stream")
+    ap.add_argument("--separate-producer", action="store_true",
+                    help="layer workload: the q/k/v producer as its own call before the decode step (else the "
+                         "decode step runs the producer's epilogue: sa_hip_decode_step_qkv)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="PAGES",
                     help="also run one plain page copy of PAGES pages (HBM counter calibration)")
     return ap.parse_args()

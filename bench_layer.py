@@ -3,13 +3,16 @@
 
 Qwen3-0.6B attention shape (hidden 1024, 16 query / 8 KV heads, head_dim
 128), batch 64 sequences of 16384 tokens, budget 64 blocks (4 + 8 + 52),
-fp32 weights.  One layer step = three calls, five launches: the q/k/v
-producer (K-slice partial projections with the RMSNorm of the hidden rows
-folded in, then the slices' sum with head RMS norm and RoPE at each
-sequence's position) -> the one-launch decode step (append k/v, seal,
-score + select, attend) -> the o-projection (partials, then their sum with
-the residual add).  Every layer's output is the next layer's input; inputs and
-weights are resident in HBM.
+fp32 weights.  One layer step = two calls, four launches: the decode step
+fed by its q/k/v producer (sa_hip_decode_step_qkv: the K-slice partial
+projections with the RMSNorm of the hidden rows folded in, then the
+one-launch decode step whose workgroups first add their heads' slices and
+apply head RMS norm and RoPE at the sequence's position, then append k/v,
+seal, score + select and attend) -> the o-projection (partials, then their
+sum with the residual add).  With --separate-producer the producer is its own
+call (partials, then a reduce launch) before the decode step: three calls,
+five launches, the same bits.  Every layer's output is the next layer's
+input; inputs and weights are resident in HBM.
 
 Reported: µs per layer (HIP graph of one step over all layers), the
 components (event-bracketed eager launches), the projections' achieved HBM
@@ -78,6 +81,7 @@ def run(args):
     if batch % mb:
         raise SystemExit(f"--microbatches {mb} does not divide the batch of {batch}")
     part = batch // mb
+    fused_producer = not getattr(args, "separate_producer", False)
     parts = []
     for i in range(mb):
         a, b = i * part, (i + 1) * part
@@ -100,11 +104,21 @@ def run(args):
         if ev: ev[0].record(st)
         # RMSNorm + q/k/v + head RMS + RoPE; the new token's position is the
         # sequence's length before the append
-        sa.qkv_project(hs[l][r], w["wq"], w["wk"], w["wv"], w["qn"], w["kn"], kv.seq_len, hq, hkv, q=q[r], k=k[r],
-                       v=v[r], workspace=pt["qkv_ws"], input_norm=w["inorm"], input_eps=1e-6, stream=st)
-        if ev: ev[1].record(st)
-        sa.decode_step(kv, k[r], v[r], 0, q[r], hkv, budget, init, local, scale, pt["ws"], selected=ly.selected[r],
-                       counts=ly.counts[r], out=ly.out[r], splits=1, status=status, stream=st)
+        if fused_producer:
+            # the producer's partials, then the decode step running its
+            # epilogue (two launches)
+            sa.decode_step_qkv(kv, hs[l][r], w["wq"], w["wk"], w["wv"], w["qn"], w["kn"], kv.seq_len, q[r], k[r],
+                               v[r], pt["qkv_ws"], 0, hkv, budget, init, local, scale, pt["ws"],
+                               input_norm=w["inorm"], input_eps=1e-6, selected=ly.selected[r], counts=ly.counts[r],
+                               out=ly.out[r], splits=1, status=status, stream=st)
+            if ev: ev[1].record(st)
+        else:
+            sa.qkv_project(hs[l][r], w["wq"], w["wk"], w["wv"], w["qn"], w["kn"], kv.seq_len, hq, hkv, q=q[r],
+                           k=k[r], v=v[r], workspace=pt["qkv_ws"], input_norm=w["inorm"], input_eps=1e-6, stream=st)
+            if ev: ev[1].record(st)
+            sa.decode_step(kv, k[r], v[r], 0, q[r], hkv, budget, init, local, scale, pt["ws"],
+                           selected=ly.selected[r], counts=ly.counts[r], out=ly.out[r], splits=1, status=status,
+                           stream=st)
         if ev: ev[2].record(st)
         sa.linear(ly.out[r].reshape(part, hq * D), w["wo"], hs[l][r], out=hs[l + 1][r], workspace=pt["lin_ws"],
                   stream=st)
@@ -158,16 +172,20 @@ def run(args):
         "warmup": args.warmup, "higher_is_better": False, "dtype": "fp32 weights and math, fp16 KV",
         "data": f"synthetic: seeded weights and hidden rows, FP16 KV from the {bench.GENERATOR} generator, "
                 "planted blocks",
-        "config": {"workload": "RMSNorm + q/k/v projections + head RMS + RoPE (one launch) -> decode step -> "
-                               "o-proj + residual", "layers": layers, "batch": batch, "hidden": hidden, "query_heads": hq,
+        "config": {"workload": "RMSNorm + q/k/v projections + head RMS + RoPE -> decode step -> o-proj + residual",
+                   "producer": "partials launch, epilogue inside the decode step" if fused_producer
+                   else "partials launch + reduce launch, then the decode step",
+                   "layers": layers, "batch": batch, "hidden": hidden, "query_heads": hq,
                    "kv_heads": hkv, "head_dim": D, "context": ctx, "budget_blocks": budget,
                    "microbatches": mb, "streams": mb},
         "tokens_per_s": round(batch / (us_per_layer * layers * 1e-6), 1),
-        "components_us": {"qkv_project_rms": round(comp_us[0], 3), "decode_step": round(comp_us[1], 3),
-                          "o_proj": round(comp_us[2], 3),
+        "components_us": ({"decode_step_qkv": round(comp_us[0], 3)} if fused_producer else
+                          {"qkv_project_rms": round(comp_us[0], 3), "decode_step": round(comp_us[1], 3)}) |
+                         {"o_proj": round(comp_us[2], 3),
                           "timing": "events around each call of the first micro-batch in eager steps"},
-        "projections": {"qkv_bytes": qkv_bytes, "qkv_gbps": round(qkv_bytes / (comp_us[0] * 1e-6) / 1e9, 1),
-                        "o_bytes": o_bytes, "o_gbps": round(o_bytes / (comp_us[2] * 1e-6) / 1e9, 1)},
+        "projections": ({} if fused_producer else
+                        {"qkv_bytes": qkv_bytes, "qkv_gbps": round(qkv_bytes / (comp_us[0] * 1e-6) / 1e9, 1)}) |
+                       {"o_bytes": o_bytes, "o_gbps": round(o_bytes / (comp_us[2] * 1e-6) / 1e9, 1)},
         "parity": parity, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

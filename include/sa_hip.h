@@ -621,6 +621,48 @@ int sa_hip_qkv_project_rms(const float* hidden_rows, const float* input_norm, fl
                            int32_t kv_heads, float theta, float eps, float* q, float* k, float* v, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* The arguments of sa_hip_qkv_project_rms (input_norm NULL:
+ * sa_hip_qkv_project's) for a decode step's batch: rows = kv->batch,
+ * q_heads = kv->query_heads, kv_heads = kv->kv_heads. */
+typedef struct sa_qkv_producer {
+  const float* hidden_rows; /* [batch][hidden] */
+  const float* input_norm;  /* [hidden] or NULL */
+  float input_eps;
+  const float* wq;
+  const float* wk;
+  const float* wv;
+  const float* q_norm;
+  const float* k_norm;
+  const int32_t* positions; /* [batch] device int32 (may be kv->seq_len) */
+  int32_t hidden;
+  float theta;
+  float eps;
+  float* q; /* [batch][query_heads][128]: written */
+  float* k; /* [batch][kv_heads][128]: written */
+  float* v;
+  void* workspace; /* sa_hip_qkv_workspace_bytes(batch, hidden, query_heads, kv_heads) */
+  size_t workspace_bytes;
+} sa_qkv_producer;
+
+/* The decode step fed by its q/k/v producer: sa_hip_qkv_project_rms (or
+ * sa_hip_qkv_project) with producer's arguments, then
+ * sa_hip_decode_step(kv, producer->k, producer->v, local_tokens,
+ * producer->q, ...).  The same q/k/v bits, page bytes, representatives,
+ * counters and selected ids, and the same attention output bits.  Where the
+ * step's one launch applies (sa_hip_select_attend_fused() is 1) with 1 or 2
+ * query heads per KV head and select_groups == kv_heads, it is TWO launches:
+ * the producer's K-slice partials, then the step, whose workgroups run the
+ * producer's epilogue (slice sums, RMSNorm scale, head RMS norm, RoPE) for
+ * their own heads at entry; otherwise the two calls.  head_dim 128 only; the
+ * positions are read before the step advances seq_len, so they may be
+ * kv->seq_len.  Replaces the reference layer's rms -> Q/K/V projections ->
+ * head_norm -> apply_rope -> pack_kv -> sparse_attention sequence
+ * (qwen_chain_main.cpp:365-395) with the paged step. */
+int sa_hip_decode_step_qkv(const sa_paged_kv* kv, const sa_qkv_producer* producer, int32_t local_tokens,
+                           const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
+                           float* out, void* workspace, size_t workspace_bytes, int32_t splits, int32_t* status,
+                           void* stream);
+
 /* ---- synthetic data ------------------------------------------------------ */
 
 /* dst[i] = fp16_rne(normal(seed, first_index + i)), the generator of the

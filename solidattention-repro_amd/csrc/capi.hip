@@ -2,6 +2,7 @@
 // validation, error strings, launch dispatch.  Hot entry points allocate
 // nothing; scratch comes in through workspace arguments, or for
 // sa_hip_decode_step_noalloc from the static `scratch` array below.
+#include "qkv_epilogue.hpp"
 #include "sa_hip.h"
 #include "sa_internal.hpp"
 
@@ -655,7 +656,7 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
                            const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
                            float* out, int32_t* arrive, bool clear_arrive, void* records, size_t records_bytes,
                            int32_t splits, int32_t* status, void* stream, const char* op,
-                           const sa_online_seal* seal = nullptr) {
+                           const sa_online_seal* seal = nullptr, const sa::QkvLaunch* producer = nullptr) {
   sa::SelectLaunch l;
   if (int e = select_launch(kv, query, params, selected, counts, nullptr, status, op, &l)) return e;
   if (!out) return fail(SA_HIP_EINVAL, "%s: null out", op);
@@ -668,6 +669,9 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
   if (!aligned16(ka) || !aligned16(va)) return fail(SA_HIP_EINVAL, "%s: k/v must be 16-byte aligned", op);
   if (seal)
     if (int e = online_check(kv, seal, query, local_tokens, op)) return e;
+  if (producer && (seal || k16 || sa::general_head_dim(kv->head_dim)))
+    return fail(SA_HIP_EINVAL, "%s: the q/k/v producer feeds head_dim %d and fp32 tokens, without the online seal",
+                op, sa::kHeadDim);
   if (sa::general_head_dim(kv->head_dim) && (seal || !sa_hip_select_attend_fused(kv, params, splits))) {
     // the general kernels in sequence (where the one-launch step does not
     // apply): append + seal, scoring into the workspace's scores, selection,
@@ -687,6 +691,10 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
   // (the online seal's one launch selects per KV group)
   const bool fused =
       sa_hip_select_attend_fused(kv, params, splits) && !(seal && params->select_groups != kv->kv_heads);
+  if (producer && !(fused && sa::decode_step_qkv_supported(kv->query_heads, kv->kv_heads, params->select_groups,
+                                                           kv->head_dim)))
+    if (int e = check_hip(sa::launch_qkv_project(*producer, as_stream(stream)), "decode_step: q/k/v producer launch"))
+      return e;
   if (!fused) {
     if (int e = lifecycle_common(kv, k, v, k16, v16, local_tokens, 1, status, stream, op, query, seal)) return e;
     // few lists: the split selection (scoring spread over the device, the
@@ -724,6 +732,15 @@ static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v
                        arrive, kv->batch);
     if (int e = check_hip(hipGetLastError(), "decode_step: counter clear launch")) return e;
   }
+  if (producer && sa::decode_step_qkv_supported(kv->query_heads, kv->kv_heads, params->select_groups,
+                                                kv->head_dim)) {
+    // the producer's partial launch, then the step running its epilogue
+    sa::qkv::ReduceParams r;
+    if (int e = check_hip(sa::launch_qkv_partials(*producer, &r, as_stream(stream)),
+                          "decode_step: q/k/v partials launch"))
+      return e;
+    return check_hip(sa::launch_decode_step_qkv(f, r, as_stream(stream)), "decode_step launch");
+  }
   return check_hip(sa::launch_select_attend(f, as_stream(stream)), "decode_step launch");
 }
 
@@ -731,7 +748,7 @@ static int decode_step_common(const sa_paged_kv* kv, const float* k, const float
                               const uint16_t* v16, int32_t local_tokens, const float* query,
                               const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
                               float* out, void* workspace, size_t workspace_bytes, int32_t splits, int32_t* status,
-                              void* stream, const char* op) {
+                              void* stream, const char* op, const sa::QkvLaunch* producer = nullptr) {
   if (!kv || kv->batch <= 0) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv or empty batch", op);
   const size_t need = sa_hip_decode_step_workspace_bytes(kv, splits);
   if (!workspace || workspace_bytes < need)
@@ -740,7 +757,7 @@ static int decode_step_common(const sa_paged_kv* kv, const float* k, const float
   const size_t ab = arrive_bytes(kv->batch);
   return decode_step_run(kv, k, v, k16, v16, local_tokens, query, params, scale, selected, counts, out,
                          static_cast<int32_t*>(workspace), false, static_cast<uint8_t*>(workspace) + ab,
-                         workspace_bytes - ab, splits, status, stream, op);
+                         workspace_bytes - ab, splits, status, stream, op, nullptr, producer);
 }
 
 int sa_hip_decode_step(const sa_paged_kv* kv, const float* k, const float* v, int32_t local_tokens,
@@ -1059,11 +1076,11 @@ size_t sa_hip_qkv_workspace_bytes(int32_t rows, int32_t hidden, int32_t q_heads,
   return sa::split_part_bytes(rows, hidden, out, true);
 }
 
-static int qkv_common(const float* x, const float* gain, float in_eps, const float* wq, const float* wk,
-                      const float* wv, const float* q_norm, const float* k_norm, const int32_t* positions,
-                      int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads, float theta, float eps,
-                      float* q, float* k, float* v, void* workspace, size_t workspace_bytes, void* stream,
-                      const char* op) {
+static int qkv_prepare(const float* x, const float* gain, float in_eps, const float* wq, const float* wk,
+                       const float* wv, const float* q_norm, const float* k_norm, const int32_t* positions,
+                       int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads, float theta, float eps,
+                       float* q, float* k, float* v, void* workspace, size_t workspace_bytes,
+                       sa::QkvLaunch* out, const char* op) {
   if (q_heads <= 0 || kv_heads <= 0 || q_heads > 256 || kv_heads > 256)
     return fail(SA_HIP_EINVAL, "%s: bad head counts %d/%d", op, q_heads, kv_heads);
   if (int e = linear_shape_ok(rows, hidden, (q_heads + 2 * kv_heads) * sa::kHeadDim, op)) return e;
@@ -1078,7 +1095,8 @@ static int qkv_common(const float* x, const float* gain, float in_eps, const flo
   if (workspace_bytes < sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads))
     return fail(SA_HIP_EINVAL, "%s: workspace of %zu bytes < %zu", op, workspace_bytes,
                 sa_hip_qkv_workspace_bytes(rows, hidden, q_heads, kv_heads));
-  sa::QkvLaunch l{};
+  sa::QkvLaunch& l = *out;
+  l = sa::QkvLaunch{};
   l.x = x;
   l.gain = gain;
   l.in_eps = in_eps;
@@ -1100,6 +1118,18 @@ static int qkv_common(const float* x, const float* gain, float in_eps, const flo
   // theta^(-2i/128), correctly rounded (the reference's powf is within 2 ulp)
   for (int i = 0; i < 64; ++i)
     l.inv_freq[i] = static_cast<float>(std::pow(static_cast<double>(theta), -2.0 * i / sa::kHeadDim));
+  return 0;
+}
+
+static int qkv_common(const float* x, const float* gain, float in_eps, const float* wq, const float* wk,
+                      const float* wv, const float* q_norm, const float* k_norm, const int32_t* positions,
+                      int32_t rows, int32_t hidden, int32_t q_heads, int32_t kv_heads, float theta, float eps,
+                      float* q, float* k, float* v, void* workspace, size_t workspace_bytes, void* stream,
+                      const char* op) {
+  sa::QkvLaunch l;
+  if (int e = qkv_prepare(x, gain, in_eps, wq, wk, wv, q_norm, k_norm, positions, rows, hidden, q_heads, kv_heads,
+                          theta, eps, q, k, v, workspace, workspace_bytes, &l, op))
+    return e;
   return check_hip(sa::launch_qkv_project(l, as_stream(stream)), op);
 }
 
@@ -1119,6 +1149,23 @@ int sa_hip_qkv_project_rms(const float* hidden_rows, const float* input_norm, fl
   if (!input_norm) return fail(SA_HIP_EINVAL, "qkv_project_rms: null input_norm");
   return qkv_common(hidden_rows, input_norm, input_eps, wq, wk, wv, q_norm, k_norm, positions, rows, hidden, q_heads,
                     kv_heads, theta, eps, q, k, v, workspace, workspace_bytes, stream, "qkv_project_rms");
+}
+
+int sa_hip_decode_step_qkv(const sa_paged_kv* kv, const sa_qkv_producer* producer, int32_t local_tokens,
+                           const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
+                           float* out, void* workspace, size_t workspace_bytes, int32_t splits, int32_t* status,
+                           void* stream) {
+  const char* op = "decode_step_qkv";
+  if (!kv || kv->batch <= 0) return fail(SA_HIP_EINVAL, "%s: null sa_paged_kv or empty batch", op);
+  if (!producer) return fail(SA_HIP_EINVAL, "%s: null producer", op);
+  const sa_qkv_producer& pr = *producer;
+  sa::QkvLaunch l;
+  if (int e = qkv_prepare(pr.hidden_rows, pr.input_norm, pr.input_eps, pr.wq, pr.wk, pr.wv, pr.q_norm, pr.k_norm,
+                          pr.positions, kv->batch, pr.hidden, kv->query_heads, kv->kv_heads, pr.theta, pr.eps, pr.q,
+                          pr.k, pr.v, pr.workspace, pr.workspace_bytes, &l, op))
+    return e;
+  return decode_step_common(kv, pr.k, pr.v, nullptr, nullptr, local_tokens, pr.q, params, scale, selected, counts,
+                            out, workspace, workspace_bytes, splits, status, stream, op, &l);
 }
 
 int sa_hip_pages_to_host_async(const uint16_t* pool, int64_t page_bytes, int64_t num_pages, const int32_t* pages,

@@ -23,6 +23,7 @@
 //     head RMS norm + RoPE for q/k heads (qkv).
 #include <algorithm>
 
+#include "qkv_epilogue.hpp"
 #include "sa_device.hpp"
 #include "sa_internal.hpp"
 
@@ -257,31 +258,8 @@ __global__ __launch_bounds__(kThreads) void proj_split_kernel(const SplitParams 
   }
 }
 
-struct QkvReduceParams {
-  const float* part;       // [slices][rows_pad][out]
-  const float* ss;         // [slices][rows_pad] or null (no input RMSNorm)
-  int32_t slices;
-  int32_t rows;
-  int32_t rows_pad;
-  int32_t in;
-  int32_t out;
-  float in_eps;
-  const float* q_norm;
-  const float* k_norm;
-  const int32_t* positions;
-  float* q;
-  float* k;
-  float* v;
-  int32_t q_heads;
-  int32_t kv_heads;
-  float eps;
-  alignas(16) float inv_freq[64];  // 16-byte aligned: a lane reads its 4 frequencies in one load
-};
+using QkvReduceParams = qkv::ReduceParams;
 
-// Workgroup (head, 8-row block): the slices of the head's 128 columns added
-// in slice order, times the row's input RMSNorm scale; q and k heads then
-// take the head RMS norm and RoPE (NeoX pairs d, d + 64).  Thread t: row
-// t / 32, d = 4 (t % 32) .. + 3; d and d + 64 sit 16 threads apart.
 // The K-slice partials at offset off of each slice (slice_stride floats
 // apart), added in slice order from zero; each batch of 8 slices' loads is
 // issued before its adds.
@@ -302,76 +280,17 @@ __device__ inline f32x4_t sum_slices4(const float* part, int slices, int64_t sli
   return v;
 }
 
-// sum_slices4 together with the same slices' scalars (sum of squares) at
-// soff of each sslice_stride-float slice, both batches in flight at once.
-__device__ inline f32x4_t sum_slices4_ss(const float* part, int slices, int64_t slice_stride, int64_t off,
-                                         const float* ss, int64_t ss_stride, int64_t soff, float& tot) {
-  constexpr int kBatch = 8;
-  f32x4_t v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  tot = 0.0f;
-  for (int z0 = 0; z0 < slices; z0 += kBatch) {
-    f32x4_t s[kBatch];
-    float q[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int z = z0 + i < slices ? z0 + i : slices - 1;
-      s[i] = *reinterpret_cast<const f32x4_t*>(part + z * slice_stride + off);
-      q[i] = ss[z * ss_stride + soff];
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      if (z0 + i < slices) {
-        v += s[i];
-        tot += q[i];
-      }
-    }
-  }
-  return v;
-}
-
+// Workgroup (head, 8-row block): the slices of the head's 128 columns added
+// in slice order, times the row's input RMSNorm scale; q and k heads then
+// take the head RMS norm and RoPE (qkv::head_value).  Thread t: row t / 32,
+// d = 4 (t % 32) .. + 3; d and d + 64 sit 16 threads apart.
 __device__ inline void qkv_reduce_rows(const QkvReduceParams& p, int hh, int rb) {
   const int tid = threadIdx.x;
-  const int j = tid % 32;
   const int row = rb * 8 + tid / 32;
   const int rr = row < p.rows ? row : p.rows - 1;  // rows past the batch compute row rows-1, not stored
-  const int64_t col = static_cast<int64_t>(hh) * kHeadDim + 4 * j;
-  const bool is_v = hh >= p.q_heads + p.kv_heads;
-  const bool is_q = hh < p.q_heads;
-  // every load of the row issued up front: the position, the head norm
-  // weights, the RoPE frequencies of d and d + 64 (the same 4), the slices
-  const float pos = static_cast<float>(p.positions[rr]);
-  const f32x4_t n4 = *reinterpret_cast<const f32x4_t*>((is_q ? p.q_norm : p.k_norm) + 4 * j);
-  const f32x4_t fr = *reinterpret_cast<const f32x4_t*>(p.inv_freq + 4 * (j % 16));
-  // (without an input RMSNorm the sums of squares are read from the
-  // partials instead, unconditionally, and not used)
-  float tot;
-  f32x4_t v = sum_slices4_ss(p.part, p.slices, static_cast<int64_t>(p.rows_pad) * p.out,
-                             static_cast<int64_t>(rr) * p.out + col, p.ss ? p.ss : p.part, p.rows_pad, rr, tot);
-  if (p.ss) v *= 1.0f / __builtin_sqrtf(tot / static_cast<float>(p.in) + p.in_eps);
-  // q and k heads: head RMS norm, then RoPE (v heads take v as it is; the
-  // head is uniform over the workgroup, so the selects below cost nothing
-  // but keep the loads above ahead of the slice sums)
-  float sq = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
-  const float inv = 1.0f / __builtin_sqrtf(sq / static_cast<float>(kHeadDim) + p.eps);
-  f32x4_t x, y, o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) x[e] = v[e] * inv * n4[e];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) y[e] = __shfl_xor(x[e], 16, kWave);  // the pair partner, d +- 64
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float sn, cs;
-    sincosf(pos * fr[e], &sn, &cs);
-    o[e] = j < 16 ? x[e] * cs - y[e] * sn : x[e] * cs + y[e] * sn;
-  }
-  if (row < p.rows) {
-    float* dst = is_v ? p.v + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads - p.kv_heads)) * kHeadDim
-                 : is_q ? p.q + (static_cast<int64_t>(row) * p.q_heads + hh) * kHeadDim
-                        : p.k + (static_cast<int64_t>(row) * p.kv_heads + (hh - p.q_heads)) * kHeadDim;
-    *reinterpret_cast<f32x4_t*>(dst + 4 * j) = is_v ? v : o;
-  }
+  const int j = tid % 32;
+  const qkv::f32x4_t o = qkv::head_value(p, hh, rr, j);
+  if (row < p.rows) *reinterpret_cast<qkv::f32x4_t*>(qkv::head_dst(p, hh, row) + 4 * j) = o;
 }
 
 __global__ __launch_bounds__(kThreads) void qkv_reduce_kernel(const QkvReduceParams p) {
@@ -458,7 +377,7 @@ hipError_t launch_linear(const LinearLaunch& l, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream) {
+hipError_t launch_qkv_partials(const QkvLaunch& q, qkv::ReduceParams* r, hipStream_t stream) {
   const int qw = q.q_heads * kHeadDim, kw = q.kv_heads * kHeadDim;
   const int out = qw + 2 * kw;
   const SplitShape sh = split_shape(q.rows, q.hidden, out);
@@ -480,25 +399,32 @@ hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream) {
   p.out = out;
   hipError_t e = launch_split(p, sh, rb, stream);
   if (e != hipSuccess) return e;
-  QkvReduceParams r{};
-  r.part = p.part;
-  r.ss = q.gain ? p.ss : nullptr;
-  r.slices = sh.slices;
-  r.rows = q.rows;
-  r.rows_pad = p.rows_pad;
-  r.in = q.hidden;
-  r.out = out;
-  r.in_eps = q.in_eps;
-  r.q_norm = q.q_norm;
-  r.k_norm = q.k_norm;
-  r.positions = q.positions;
-  r.q = q.q;
-  r.k = q.k;
-  r.v = q.v;
-  r.q_heads = q.q_heads;
-  r.kv_heads = q.kv_heads;
-  r.eps = q.eps;
-  for (int i = 0; i < 64; ++i) r.inv_freq[i] = q.inv_freq[i];
+  *r = qkv::ReduceParams{};
+  r->part = p.part;
+  r->ss = q.gain ? p.ss : nullptr;
+  r->slices = sh.slices;
+  r->rows = q.rows;
+  r->rows_pad = p.rows_pad;
+  r->in = q.hidden;
+  r->out = out;
+  r->in_eps = q.in_eps;
+  r->q_norm = q.q_norm;
+  r->k_norm = q.k_norm;
+  r->positions = q.positions;
+  r->q = q.q;
+  r->k = q.k;
+  r->v = q.v;
+  r->q_heads = q.q_heads;
+  r->kv_heads = q.kv_heads;
+  r->eps = q.eps;
+  for (int i = 0; i < 64; ++i) r->inv_freq[i] = q.inv_freq[i];
+  return hipSuccess;
+}
+
+hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream) {
+  QkvReduceParams r;
+  hipError_t e = launch_qkv_partials(q, &r, stream);
+  if (e != hipSuccess) return e;
   const dim3 grid(q.q_heads + 2 * q.kv_heads, std::min((q.rows + 7) / 8, 65535));
   hipLaunchKernelGGL(qkv_reduce_kernel, grid, dim3(kThreads), 0, stream, r);
   return hipGetLastError();

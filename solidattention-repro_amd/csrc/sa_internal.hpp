@@ -133,6 +133,12 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* out, int rows,
                            hipStream_t stream);
 hipError_t launch_linear(const LinearLaunch& l, hipStream_t stream);
 hipError_t launch_qkv_project(const QkvLaunch& q, hipStream_t stream);
+// The q/k/v projection's partial launch only; *r receives the parameters of
+// its epilogue (qkv_epilogue.hpp), which the caller runs.
+namespace qkv {
+struct ReduceParams;
+}
+hipError_t launch_qkv_partials(const QkvLaunch& q, qkv::ReduceParams* r, hipStream_t stream);
 
 // Compute units of the current device (cached per device; 256 if unknown).
 int compute_units();
@@ -202,6 +208,13 @@ bool select_attend_shared_supported(int32_t batch, int32_t query_heads, int32_t 
 bool select_attend_rows_supported(int32_t query_heads, int32_t kv_heads, int32_t rep_heads, int32_t select_groups,
                                   int32_t head_dim);
 hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream);
+// The decode step (append, with k, v and query the producer's outputs) fed
+// by the q/k/v projection's partials: the producer's epilogue runs inside the
+// one-launch step.  head_dim 128, selection per KV group, 1 or 2 query heads
+// per KV head, fp32 token, no online seal; r from launch_qkv_partials() with
+// rows == batch and r.q == s.query.
+bool decode_step_qkv_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups, int32_t head_dim);
+hipError_t launch_decode_step_qkv(const SelectAttendLaunch& s, const qkv::ReduceParams& r, hipStream_t stream);
 
 // InfLLM local-causal block representatives of a prefill (contiguous KV).
 struct RepresentativeLaunch {

@@ -29,9 +29,12 @@
 //
 // This file is compiled with -ffp-contract=off (scoring and seal sums are
 // bit-exact); the attention writes its fused multiply-adds explicitly.
+#include <type_traits>
+
 #include "attn_core.hpp"
 #include "attn_rows.hpp"
 #include "online_seal.hpp"
+#include "qkv_epilogue.hpp"
 #include "select_core.hpp"
 
 namespace sa {
@@ -108,16 +111,22 @@ __device__ inline bool append_seals(const Params& p, int64_t len, int n) {
   return len + 1 >= static_cast<int64_t>(n + 1) * kPageTokens + p.local_tokens;
 }
 
-template <int G, bool F16, bool ONLINE = false>
+// TOK_W1: the token is not read from p.k/p.vv but given, in token_quad()'s
+// layout, by the lanes of wave 1 (tok).
+template <int G, bool F16, bool ONLINE = false, bool TOK_W1 = false>
 __device__ inline bool append_seal_head(const Params& p, int b, int g, int64_t& len, int& n, int& added,
-                                        float* seal_smem = nullptr) {
+                                        float* seal_smem = nullptr, ushort4 tok = {}) {
   const int tid = threadIdx.x;
   const int64_t page = table_page(p.v, b, len / kPageTokens);
   if (page < 0) {
     if (tid == 0) flag_status(p.v.status, kStatusCapacity);
     return false;
   }
-  if (tid < kWave) store_token_quad(p, page, len, g, tid, token_quad<F16>(p, b, g, tid));
+  if (TOK_W1) {
+    if (tid >= kWave && tid < 2 * kWave) store_token_quad(p, page, len, g, tid - kWave, tok);
+  } else if (tid < kWave) {
+    store_token_quad(p, page, len, g, tid, token_quad<F16>(p, b, g, tid));
+  }
   if (ONLINE) online::store_queries(p.online, p.query, b, g * G, G, len, tid, kThreads);
   len += 1;
   // the new token (and its queries) visible to the seal below; without a
@@ -367,8 +376,19 @@ struct PlanPages {
 // G = query heads per KV head; GR = query heads sharing one representative
 // row (G for per-KV-head representatives, 1 for per-query-head ones);
 // APPEND: decode step (append + seal first); F16: raw FP16 K/V input.
-template <int G, int GR, bool APPEND, bool F16, bool ONLINE = false>
-__global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
+// No q/k/v producer: the step's query and token are inputs.
+struct NoProducer {};
+
+// Prod = qkv::ReduceParams: the step takes the q/k/v projection's K-slice
+// partials instead of q, k and v, and runs their epilogue (qkv_epilogue.hpp)
+// for its own heads at entry: wave 0 the group's query heads (32 lanes each),
+// wave 1 KV head g's k (lanes 0..31) and v (lanes 32..63), the layout in which
+// wave 1 appends the token.  q, k and v are also written out, the values the
+// producer's reduce launch would write.
+template <int G, int GR, bool APPEND, bool F16, bool ONLINE, class Prod>
+__device__ inline void decode_body(const Params& p, const Prod& qp) {
+  constexpr bool kProd = !std::is_same<Prod, NoProducer>::value;
+  static_assert(!kProd || (G <= 2 && APPEND && !F16 && !ONLINE), "the producer epilogue: 1-2 heads, fp32 token");
   const int g = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
@@ -384,9 +404,29 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   const int64_t out_row = static_cast<int64_t>(b) * p.v.kv_heads + g;
   // the group's query rows, loaded at entry (their latency overlaps the append)
   const float* q_group = p.query + (static_cast<int64_t>(b) * p.query_heads + g * G) * D;
-  const float q_entry = tid < G * D ? q_group[tid] : 0.0f;
+  float q_entry = 0.0f;
+  if constexpr (!kProd) q_entry = tid < G * D ? q_group[tid] : 0.0f;
   int64_t len = p.seq_len[b];
   int n = p.sealed[b];
+
+  ushort4 tok{};
+  if constexpr (kProd) {
+    if (wave < 2) {
+      const int half = lane / 32;
+      const int j = lane % 32;
+      // (with one query head, wave 0's upper half repeats it and stores nothing)
+      const int hh = wave == 0 ? g * G + (half < G ? half : 0) : qp.q_heads + half * qp.kv_heads + g;
+      const qkv::f32x4_t val = qkv::head_value(qp, hh, b, j);
+      if (wave == 1 || half < G) *reinterpret_cast<qkv::f32x4_t*>(qkv::head_dst(qp, hh, b) + 4 * j) = val;
+      if (wave == 0 && half < G) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q_s[half * D + 4 * j + e] = val[e];
+      }
+      if (wave == 1) tok = make_ushort4(f2h_rne(val[0]), f2h_rne(val[1]), f2h_rne(val[2]), f2h_rne(val[3]));
+    }
+    // (no barrier: waves 2 and 3 go on to their prefetch; q_s is read after
+    // the scoring's barrier, or the one before st.init)
+  }
 
   // ---- 0. start the representative stream: the first batch of this thread's
   // first block, for blocks sealed before this step (a seal below only adds
@@ -415,8 +455,8 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   SeqCommit commit{};
   if (APPEND) {
     commit.gen = p.generation ? p.generation[b] : 0;
-    commit.appended =
-        append_seal_head<G, F16, ONLINE>(p, b, g, len, n, commit.added, reinterpret_cast<float*>(keys));
+    commit.appended = append_seal_head<G, F16, ONLINE, kProd>(p, b, g, len, n, commit.added,
+                                                              reinterpret_cast<float*>(keys), tok);
     if (tid == 0) commit.arrived = atomicAdd(&p.arrive[b], 1);
   }
 
@@ -431,7 +471,7 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   const Forced fb = forced_blocks(bs, n);
   const int32_t early = wave == kWaves - 1 ? early_page(p, b, n, fb, lane) : -1;
   if (n_ok && !bs.take_all) {  // (a budget that takes every block needs no scores)
-    if (tid < G * D) q_s[tid] = q_entry;
+    if (!kProd && tid < G * D) q_s[tid] = q_entry;
     __syncthreads();
     if (kPrefetch) {
       sel::score_blocks<GR, kThreads>(a, q_s, n, keys, nullptr, pre, have_pre);
@@ -441,7 +481,8 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
   }
   if (wave == kWaves - 1) cl.early[lane] = early;
   if (tid == 0) cl.late_ready = 0;
-  st.init(q_group, p.qscale, lg.col);
+  if (kProd && !(n_ok && !bs.take_all)) __syncthreads();  // q_s complete (no scoring barrier)
+  st.init(kProd ? q_s : q_group, p.qscale, lg.col);
   // the walk's view of the sequence (a length below the sealed blocks is
   // flagged and walked as no tail)
   int wn = n;
@@ -488,6 +529,17 @@ __global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
     p.out[(static_cast<int64_t>(b) * p.query_heads + g * G + h) * D + d] = lw > 0.0f ? aw / lw : 0.0f;
   }
   if (APPEND && tid == 0) commit_sequence(p, b, len, n, commit);
+}
+
+template <int G, int GR, bool APPEND, bool F16, bool ONLINE = false>
+__global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
+  decode_body<G, GR, APPEND, F16, ONLINE>(p, NoProducer{});
+}
+
+// The decode step fed by the q/k/v projection's partials (fp32 token).
+template <int G, int GR>
+__global__ __launch_bounds__(kThreads, 4) void decode_kernel_qkv(const Params p, const qkv::ReduceParams qp) {
+  decode_body<G, GR, true, false, false>(p, qp);
 }
 
 // ---- shared selection: one block set per sequence over every query head -----
@@ -1155,62 +1207,16 @@ hipError_t launch_rows_lpr(const Params& p, int batch, int hd, hipStream_t strea
   }
 }
 
-hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream) {
-  const int hd = s.head_dim > 0 ? s.head_dim : kHeadDim;
-  if (hd != kHeadDim) {
-    // another head_dim: the decode step only, representatives per KV head
-    if (!s.append || !s.arrive || s.ring ||
-        !select_attend_rows_supported(s.query_heads, s.kv_heads, s.rep_heads, s.select_groups, hd))
-      return hipErrorInvalidValue;
-    Params p{};
-    p.v.pool = s.pool;
-    p.v.table = s.table;
-    p.v.status = s.status;
-    p.v.num_pages = s.num_pages;
-    p.v.contig_tokens = 0;
-    p.v.token_elems = 2 * s.kv_heads * hd;
-    p.v.page_elems = static_cast<int64_t>(kPageTokens) * p.v.token_elems;
-    p.v.table_stride = s.table_stride;
-    p.v.kv_heads = s.kv_heads;
-    p.seq_len = s.seq_len;
-    p.sealed = s.sealed;
-    p.generation = s.generation;
-    p.reps = s.reps;
-    p.query = s.query;
-    p.selected = s.selected;
-    p.counts = s.counts;
-    p.out = s.out;
-    p.k = s.k;
-    p.vv = s.v;
-    p.k16 = s.k16;
-    p.v16 = s.v16;
-    p.arrive = s.arrive;
-    p.query_heads = s.query_heads;
-    p.rep_heads = s.rep_heads;
-    p.rep_stride = s.rep_stride;
-    p.budget = s.budget;
-    p.budgets = s.budgets;
-    p.init_blocks = s.init_blocks;
-    p.local_blocks = s.local_blocks;
-    p.sel_stride = s.sel_stride;
-    p.local_tokens = s.local_tokens;
-    p.qscale = s.scale * attn::kLog2e;
-    return s.k16 ? launch_rows_lpr<true>(p, s.batch, hd, stream) : launch_rows_lpr<false>(p, s.batch, hd, stream);
-  }
-  const bool shared = s.select_groups != s.kv_heads;
-  if (shared ? !select_attend_shared_supported(s.batch, s.query_heads, s.kv_heads, s.rep_heads, s.select_groups,
-                                               s.rep_stride)
-             : !select_attend_supported(s.query_heads, s.kv_heads, s.select_groups, s.sel_stride, s.reps,
-                                        s.rep_stride))
-    return hipErrorInvalidValue;
-  if (s.append && !s.arrive) return hipErrorInvalidValue;
+namespace {
+
+Params step_params(const SelectAttendLaunch& s, int hd) {
   Params p{};
   p.v.pool = s.pool;
   p.v.table = s.table;
   p.v.status = s.status;
   p.v.num_pages = s.num_pages;
   p.v.contig_tokens = 0;
-  p.v.token_elems = 2 * s.kv_heads * D;
+  p.v.token_elems = 2 * s.kv_heads * hd;
   p.v.page_elems = static_cast<int64_t>(kPageTokens) * p.v.token_elems;
   p.v.table_stride = s.table_stride;
   p.v.kv_heads = s.kv_heads;
@@ -1237,6 +1243,29 @@ hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream)
   p.sel_stride = s.sel_stride;
   p.local_tokens = s.local_tokens;
   p.qscale = s.scale * attn::kLog2e;
+  return p;
+}
+
+}  // namespace
+
+hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream) {
+  const int hd = s.head_dim > 0 ? s.head_dim : kHeadDim;
+  if (hd != kHeadDim) {
+    // another head_dim: the decode step only, representatives per KV head
+    if (!s.append || !s.arrive || s.ring ||
+        !select_attend_rows_supported(s.query_heads, s.kv_heads, s.rep_heads, s.select_groups, hd))
+      return hipErrorInvalidValue;
+    const Params p = step_params(s, hd);
+    return s.k16 ? launch_rows_lpr<true>(p, s.batch, hd, stream) : launch_rows_lpr<false>(p, s.batch, hd, stream);
+  }
+  const bool shared = s.select_groups != s.kv_heads;
+  if (shared ? !select_attend_shared_supported(s.batch, s.query_heads, s.kv_heads, s.rep_heads, s.select_groups,
+                                               s.rep_stride)
+             : !select_attend_supported(s.query_heads, s.kv_heads, s.select_groups, s.sel_stride, s.reps,
+                                        s.rep_stride))
+    return hipErrorInvalidValue;
+  if (s.append && !s.arrive) return hipErrorInvalidValue;
+  Params p = step_params(s, D);
   if (shared) {
     if (s.ring) return hipErrorInvalidValue;
     if (!s.append) return launch_shared<false, false>(p, s.batch, stream);
@@ -1249,6 +1278,30 @@ hipError_t launch_select_attend(const SelectAttendLaunch& s, hipStream_t stream)
   }
   if (!s.append) return launch_mode<false, false>(p, s.batch, stream);
   return s.k16 ? launch_mode<true, true>(p, s.batch, stream) : launch_mode<true, false>(p, s.batch, stream);
+}
+
+bool decode_step_qkv_supported(int32_t query_heads, int32_t kv_heads, int32_t select_groups, int32_t head_dim) {
+  if (kv_heads <= 0 || select_groups != kv_heads || (head_dim != 0 && head_dim != kHeadDim)) return false;
+  const int group = query_heads / kv_heads;
+  return group == 1 || group == 2;
+}
+
+hipError_t launch_decode_step_qkv(const SelectAttendLaunch& s, const qkv::ReduceParams& r, hipStream_t stream) {
+  if (!s.append || !s.arrive || s.ring || s.k16 || !s.k || !s.v || r.rows != s.batch ||
+      r.q_heads != s.query_heads || r.kv_heads != s.kv_heads || r.q != s.query ||
+      !decode_step_qkv_supported(s.query_heads, s.kv_heads, s.select_groups, s.head_dim))
+    return hipErrorInvalidValue;
+  const Params p = step_params(s, D);
+  const dim3 grid(s.kv_heads, s.batch);
+  const int group = s.query_heads / s.kv_heads;
+  if (group == 1) {
+    hipLaunchKernelGGL((decode_kernel_qkv<1, 1>), grid, dim3(kThreads), 0, stream, p, r);
+  } else if (s.rep_heads == s.query_heads) {
+    hipLaunchKernelGGL((decode_kernel_qkv<2, 1>), grid, dim3(kThreads), 0, stream, p, r);
+  } else {
+    hipLaunchKernelGGL((decode_kernel_qkv<2, 2>), grid, dim3(kThreads), 0, stream, p, r);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace sa

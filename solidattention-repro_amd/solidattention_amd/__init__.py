@@ -52,6 +52,15 @@ class OnlineSealStruct(C.Structure):
                 ("topk", C.c_int32), ("reserved", C.c_int32)]
 
 
+class QkvProducerStruct(C.Structure):
+    """Mirror of sa_qkv_producer (include/sa_hip.h)."""
+    _fields_ = [("hidden_rows", C.c_void_p), ("input_norm", C.c_void_p), ("input_eps", C.c_float),
+                ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p), ("positions", C.c_void_p), ("hidden", C.c_int32), ("theta", C.c_float),
+                ("eps", C.c_float), ("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p),
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+
+
 # name -> (restype, argtypes)
 _P, _I32, _I64, _SZ, _F = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t, C.c_float
 _KV = C.POINTER(PagedKVStruct)
@@ -112,6 +121,8 @@ EXPORTS = {
                                             C.POINTER(SelectParamsStruct), _F, _P, _P, _P, _P, _SZ, _I32, _P, _P]),
     "sa_hip_decode_step_noalloc": (C.c_int, [_KV, _P, _P, _I32, _P, C.POINTER(SelectParamsStruct), _F, _P, _P, _P,
                                              _I32, _P, _P]),
+    "sa_hip_decode_step_qkv": (C.c_int, [_KV, C.POINTER(QkvProducerStruct), _I32, C.POINTER(SelectParamsStruct), _F,
+                                         _P, _P, _P, _P, _SZ, _I32, _P, _P]),
     "sa_hip_append_seal": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_append_seal_f16": (C.c_int, [_KV, _P, _P, _I32, _P, _P]),
     "sa_hip_seal": (C.c_int, [_KV, _I32, _P, _P]),
@@ -526,6 +537,38 @@ def decode_step(kv: PagedKV, k, v, local_tokens, query, select_groups, budget, i
     check(fn(C.byref(s), _ptr(k), _ptr(v), local_tokens, _ptr(query), C.byref(params), C.c_float(scale),
              _ptr(selected), _ptr(counts), _ptr(out), _ptr(workspace), nbytes, splits, _ptr(status),
              _stream(stream)), "decode_step")
+    return selected, counts, out
+
+
+def decode_step_qkv(kv: PagedKV, x, wq, wk, wv, q_norm, k_norm, positions, q, k, v, qkv_workspace, local_tokens,
+                    select_groups, budget, init, local, scale, workspace, input_norm=None, input_eps=1e-6, theta=1e6,
+                    eps=1e-6, selected=None, counts=None, out=None, splits=1, status=None, sel_stride=None,
+                    stream=None, budgets=None):
+    """qkv_project (x [batch][hidden] -> q, k, v) followed by decode_step(kv,
+    k, v, local_tokens, q, ...): two launches where the one-launch step takes
+    the producer's epilogue (1-2 query heads per KV head), else the two calls.
+    q, k, v are written as qkv_project writes them.  Returns (selected,
+    counts, out)."""
+    import torch
+    sel_stride = sel_stride or budget
+    dev = x.device
+    if selected is None:
+        selected = torch.full((kv.batch, select_groups, sel_stride), -1, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.zeros((kv.batch, select_groups), dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.empty((kv.batch, kv.query_heads, kv.head_dim), dtype=torch.float32, device=dev)
+    params = SelectParamsStruct(select_groups, budget, init, local, sel_stride, 0,
+                                None if budgets is None else budgets.data_ptr())
+    pr = QkvProducerStruct(x.data_ptr(), None if input_norm is None else input_norm.data_ptr(), input_eps,
+                           wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(),
+                           positions.data_ptr(), x.shape[1], theta, eps, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                           qkv_workspace.data_ptr(), qkv_workspace.numel() * qkv_workspace.element_size())
+    s = kv.struct()
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().sa_hip_decode_step_qkv(C.byref(s), C.byref(pr), local_tokens, C.byref(params), C.c_float(scale),
+                                       _ptr(selected), _ptr(counts), _ptr(out), _ptr(workspace), nbytes, splits,
+                                       _ptr(status), _stream(stream)), "decode_step_qkv")
     return selected, counts, out
 
 

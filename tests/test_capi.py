@@ -239,3 +239,37 @@ def test_noalloc_decode_step_refuses_records_beyond_scratch():
     kv.batch = 0
     assert L.sa_hip_decode_step_noalloc(C.byref(kv), f, f, 0, f, C.byref(params), C.c_float(0.1), f, f, f, 1, None,
                                         None) == -1
+
+
+def test_decode_step_qkv_argument_checks():
+    """The producer-fed decode step refuses a null producer, the producer's
+    own bad arguments and a head_dim other than 128 before any launch."""
+    import solidattention_amd as sa
+    L = sa.lib()
+    fake = 4096
+    f = C.c_void_p(fake)
+    kv = sa.PagedKVStruct(fake, fake, fake, fake, fake, fake, 1000, 4, 64, 8, 64, 16, 8, 128, 0)
+    params = sa.SelectParamsStruct(8, 8, 1, 2, 8, 0, None)
+    ws = L.sa_hip_decode_step_workspace_bytes(C.byref(kv), 1)
+    qn = L.sa_hip_qkv_workspace_bytes(4, 1024, 16, 8)
+    pr = sa.QkvProducerStruct(fake, fake, 1e-6, fake, fake, fake, fake, fake, fake, 1024, 1e6, 1e-6, fake, fake, fake,
+                              fake, qn)
+
+    def call(producer, kvs=kv, nbytes=ws):
+        return L.sa_hip_decode_step_qkv(C.byref(kvs), producer, 0, C.byref(params), C.c_float(0.1), f, f, f, f,
+                                        nbytes, 1, None, None)
+
+    assert call(None) == -1 and b"null producer" in L.sa_hip_last_error()
+    pr.theta = 1.0
+    assert call(C.byref(pr)) == -1 and b"theta" in L.sa_hip_last_error()
+    pr.theta = 1e6
+    pr.workspace_bytes = qn - 4
+    assert call(C.byref(pr)) == -1 and b"workspace" in L.sa_hip_last_error()
+    pr.workspace_bytes = qn
+    pr.hidden = 1000
+    assert call(C.byref(pr)) == -1
+    pr.hidden = 1024
+    assert call(C.byref(pr), nbytes=ws - 4) == -1 and b"workspace" in L.sa_hip_last_error()
+    kv64 = sa.PagedKVStruct(fake, fake, fake, fake, fake, fake, 1000, 4, 64, 8, 64, 16, 8, 64, 0)
+    assert call(C.byref(pr), kvs=kv64, nbytes=L.sa_hip_decode_step_workspace_bytes(C.byref(kv64), 1)) == -1
+    assert b"head_dim 128" in L.sa_hip_last_error()
