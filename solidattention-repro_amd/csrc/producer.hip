@@ -9,8 +9,9 @@
 // Projections: y[r][o] = sum_i x[r][i] w[o][i].  At decode the rows are few
 // (the batch) and the weights are the traffic.  Two launches:
 //   * proj_split_kernel<C, KS>: a workgroup of 4 waves takes 64 rows x C
-//     columns (64 or 32) over one K slice of KS = 256 (one workgroup per
-//     compute unit at 1024 -> 4096 and 2048 -> 1024).  It issues all its
+//     columns (64 or 32) over one K slice of KS = 256 or 128 (two
+//     workgroups per compute unit at 1024 -> 4096, one at 2048 -> 1024;
+//     split_shape()).  It issues all its
 //     loads at once in 32-k units, stores each
 //     unit to its LDS region as it arrives and runs that unit's
 //     v_mfma_f32_16x16x4f32 steps (wave t: rows 16 t .. + 15) while later
@@ -314,17 +315,26 @@ __global__ __launch_bounds__(kWave) void linear_reduce_kernel(const float* part,
 
 }  // namespace
 
-// Tile of a split projection: always in / 256 K slices of 256 k (no upper
-// bound: the reduce adds any number of slices in slice order), with 64
-// columns per workgroup when the slices number at most 8 and the 64-column
-// grid still gives every compute unit a workgroup (1024 -> 4096: 256
-// workgroups, 4 slices), else 32 columns (2048 -> 1024: 256 workgroups, 8
+// Tile of a split projection: K slices of 256 k (no upper bound: the reduce
+// adds any number of slices in slice order), with 64 columns per workgroup
+// when the slices number at most 8 and the 64-column grid still gives every
+// compute unit a workgroup, else 32 columns (2048 -> 1024: 256 workgroups, 8
 // slices; 4096 -> 4096, the Qwen3-8B o-projection: 2048 workgroups, 16
-// slices).  The workspace holds slices x rows x out partial sums.
+// slices).  A 64-column tile of at most 4 slices takes 128 k instead (twice
+// the slices): its 66 KB of LDS lets two workgroups share a compute unit, one
+// staging while the other runs its matrix steps (1024 -> 4096: 512
+// workgroups, 8 slices; 10.0 against 10.9 us for 4 slices of 256 k, the
+// epilogue's loads of the extra slices issued together).  The workspace holds
+// slices x rows x out partial sums.
 SplitShape split_shape(int64_t rows, int64_t in, int64_t out) {
   const int64_t rb = (rows + kRowsPerWg - 1) / kRowsPerWg;
-  SplitShape sh{64, static_cast<int32_t>(in / 256)};
-  if (sh.slices > kWideTileMaxSlices || (out / 64) * sh.slices * rb < compute_units()) sh.cols = 32;
+  SplitShape sh{64, static_cast<int32_t>(in / 256), 256};
+  if (sh.slices > kWideTileMaxSlices || (out / 64) * sh.slices * rb < compute_units()) {
+    sh.cols = 32;
+  } else if (2 * sh.slices <= kWideTileMaxSlices) {
+    sh.slices *= 2;
+    sh.ks = 128;
+  }
   return sh;
 }
 
@@ -339,7 +349,10 @@ namespace {
 
 hipError_t launch_split(const SplitParams& p, const SplitShape& sh, int rb, hipStream_t stream) {
   const dim3 grid(sh.slices, p.out / sh.cols, rb);
-  if (sh.cols == 64) {
+  if (sh.cols == 64 && sh.ks == 128) {
+    if (p.gain) hipLaunchKernelGGL((proj_split_kernel<64, 128, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((proj_split_kernel<64, 128, false>), grid, dim3(kThreads), 0, stream, p);
+  } else if (sh.cols == 64) {
     if (p.gain) hipLaunchKernelGGL((proj_split_kernel<64, 256, true>), grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL((proj_split_kernel<64, 256, false>), grid, dim3(kThreads), 0, stream, p);
   } else {

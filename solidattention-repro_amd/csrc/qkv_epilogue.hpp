@@ -73,7 +73,7 @@ __device__ inline f32x4_t sum_slices4_ss(const float* part, int slices, int64_t 
 // of the row is issued first; the RoPE angles' sines and cosines, which need
 // only the position, are computed while the slices are in flight.
 __device__ inline f32x4_t head_value(const ReduceParams& p, int hh, int rr, int j) {
-  constexpr int kBatch = 4;  // the first batch (a 1024-wide hidden has 4 slices); the rest 8 at a time
+  constexpr int kBatch = 8;  // the first batch (a 1024-wide hidden has 8 slices of 128 k); the rest 8 at a time
   const int64_t col = static_cast<int64_t>(hh) * kHeadDim + 4 * j;
   const bool is_v = hh >= p.q_heads + p.kv_heads;
   const bool is_q = hh < p.q_heads;

@@ -126,6 +126,7 @@ struct QkvLaunch {
 struct SplitShape {
   int32_t cols;
   int32_t slices;
+  int32_t ks;  // k per slice: 256, or 128 for two 64-column workgroups per compute unit
 };
 SplitShape split_shape(int64_t rows, int64_t in, int64_t out);
 size_t split_part_bytes(int64_t rows, int64_t in, int64_t out, bool with_ss);

@@ -209,7 +209,9 @@ def test_producer_argument_checks():
     assert L.sa_hip_linear(f, f, None, f, 4, 1024, 2048, None, need, None) == -1
     assert L.sa_hip_linear(f, f, None, f, 0, 1024, 2048, f, need, None) == -1
     qn = L.sa_hip_qkv_workspace_bytes(4, 1024, 16, 8)
-    assert qn == 4 * 64 * 4096 * 4 + 4 * 64 * 4  # 4 slices of partial tiles + sums of squares
+    # 8 slices of 128 k (two 64-column workgroups per compute unit) of partial
+    # tiles + sums of squares
+    assert qn == 8 * 64 * 4096 * 4 + 8 * 64 * 4
     args = [f, f, f, f, f, f, f, 4, 1024, 16, 8]
     assert L.sa_hip_qkv_project(*args, C.c_float(1.0), C.c_float(1e-6), f, f, f, f, qn, None) == -1
     assert b"theta" in L.sa_hip_last_error()
