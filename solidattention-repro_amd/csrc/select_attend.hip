@@ -531,8 +531,10 @@ __device__ inline void decode_body(const Params& p, const Prod& qp) {
   if (APPEND && tid == 0) commit_sequence(p, b, len, n, commit);
 }
 
+// (the online seal's builder state takes more registers: 2 resident
+// workgroups per compute unit, the fused grid's usual count, without spills)
 template <int G, int GR, bool APPEND, bool F16, bool ONLINE = false>
-__global__ __launch_bounds__(kThreads, 4) void decode_kernel(const Params p) {
+__global__ __launch_bounds__(kThreads, ONLINE ? 2 : 4) void decode_kernel(const Params p) {
   decode_body<G, GR, APPEND, F16, ONLINE>(p, NoProducer{});
 }
 
