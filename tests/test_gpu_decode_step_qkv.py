@@ -38,18 +38,20 @@ def state(kv):
     return [t.clone() for t in (kv.pool, kv.reps, kv.seq_len, kv.sealed, kv.generation)]
 
 
-@pytest.mark.parametrize("hq,hkv,rep_heads,splits,rms", [
-    (16, 8, None, 1, True),     # two launches: 2 query heads per KV head, representatives per KV head
-    (16, 8, 16, 1, True),       # two launches: 2 query heads, representatives per query head
-    (8, 8, None, 1, False),     # two launches: 1 query head per KV head, no input RMSNorm
-    (32, 8, None, 1, True),     # 4 query heads per KV head: the two calls
-    (16, 8, None, 2, True),     # split attention: the two calls
+@pytest.mark.parametrize("hq,hkv,rep_heads,splits,rms,batch", [
+    (16, 8, None, 1, True, 4),     # two launches: 2 query heads per KV head, representatives per KV head
+    (16, 8, 16, 1, True, 4),       # two launches: 2 query heads, representatives per query head
+    (8, 8, None, 1, False, 4),     # two launches: 1 query head per KV head, no input RMSNorm
+    (32, 8, None, 1, True, 4),     # 4 query heads per KV head: the two calls
+    (16, 8, None, 2, True, 4),     # split attention: the two calls
+    (16, 8, None, 1, True, 70),    # two launches over two 64-row tiles of the projection
 ])
-def test_decode_step_qkv_equals_two_calls(hip, hq, hkv, rep_heads, splits, rms):
-    print(f"case: decode_step_qkv hq={hq} hkv={hkv} rep_heads={rep_heads} splits={splits} rms={rms}", flush=True)
-    rng = np.random.default_rng(hq * 10 + hkv + (rep_heads or 0) + splits)
-    batch, hidden = 4, 1024
-    lengths = [32 * 40 + 25, 32 * 17 + 5, 32 * 25 + 30, 32 * 9]
+def test_decode_step_qkv_equals_two_calls(hip, hq, hkv, rep_heads, splits, rms, batch):
+    print(f"case: decode_step_qkv hq={hq} hkv={hkv} rep_heads={rep_heads} splits={splits} rms={rms} batch={batch}",
+          flush=True)
+    rng = np.random.default_rng(hq * 10 + hkv + (rep_heads or 0) + splits + batch)
+    hidden = 1024
+    lengths = ([32 * 40 + 25, 32 * 17 + 5, 32 * 25 + 30, 32 * 9] * 18)[:batch]
     case = make_case(300 + hq + splits, batch, hq, hkv, lengths, rep_heads=rep_heads, planted=2)
     kva, kvb = device_kv(case), device_kv(case)
     W = make_weights(rng, hidden, hq, hkv)
