@@ -69,14 +69,16 @@ def test_seal_after_prefill_per_query_head_reps(hip):
     assert np.array_equal(kv.reps.cpu().numpy().view(np.uint32), case.reps.view(np.uint32))
 
 
-@pytest.mark.parametrize("rep_heads,local_tokens", [(8, 0), (8, 32), (16, 0)])
-def test_bulk_seal_from_partial_state(hip, rep_heads, local_tokens):
+@pytest.mark.parametrize("rep_heads,local_tokens,hq,hkv", [(8, 0, 16, 8), (8, 32, 16, 8), (16, 0, 16, 8),
+                                                          (2, 0, 4, 2), (12, 32, 12, 6)])
+def test_bulk_seal_from_partial_state(hip, rep_heads, local_tokens, hq, hkv):
     """The bulk seal (one workgroup per 16 blocks and KV head) from sealed
     counts part-way through the range, over chunk boundaries (0, 1, 15, 16,
-    17, 33, 100 blocks to seal): representatives, sealed and generation
-    bit-exact against the oracle's tail rule."""
+    17, 33, 100 blocks to seal), at 8, 2 and 6 KV heads: representatives,
+    sealed and generation bit-exact against the oracle's tail rule."""
+    print(f"case: bulk seal rep_heads={rep_heads} local={local_tokens} hq={hq} hkv={hkv}", flush=True)
     lengths = [32 * 100 + 7, 32 * 17, 32 * 16 + 31, 31, 32 * 33, 32 * 61 + 1, 32 * 2]
-    case = make_case(214 + local_tokens + rep_heads, len(lengths), 16, 8, lengths, rep_heads=rep_heads,
+    case = make_case(214 + local_tokens + rep_heads, len(lengths), hq, hkv, lengths, rep_heads=rep_heads,
                      local_tokens=local_tokens)
     start = np.array([0, 0, 1, 0, 3, 44, 1], np.int32)
     start = np.minimum(start, case.sealed)
@@ -92,7 +94,7 @@ def test_bulk_seal_from_partial_state(hip, rep_heads, local_tokens):
     gen = start * 3
     reps = reps0.copy()
     O.paged_seal(case.pool, PAGE, case.table, case.seq_len, sealed, gen, reps, rep_heads, case.rep_stride,
-                 case.batch, 16, 8, D, local_tokens)
+                 case.batch, hq, hkv, D, local_tokens)
     torch.cuda.synchronize()
     assert int(st.item()) == 0
     assert np.array_equal(kv.sealed.cpu().numpy(), sealed)
