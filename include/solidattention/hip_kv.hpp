@@ -16,6 +16,10 @@
 //                              decode step (qwen_chain_main.cpp:390-395 with
 //                              selection on the GPU), one launch where the
 //                              fused kernel applies
+//   SparseDecoder::decode_step_qkv  the same fed by the q/k/v projections,
+//                              head RMS norm and RoPE (qwen_chain_main.cpp:
+//                              365-395): two launches where the one-launch
+//                              step takes the producer's epilogue
 //   MissCorrector              CudaPipeline::correct_and_wait without the
 //                              host barrier (pipeline_main.cpp:305-331)
 //   SplitAttention             attention of the resident blocks while the
@@ -251,6 +255,17 @@ class SparseDecoder {
     check(sa_hip_decode_step(&kv, k, v, local_tokens, query, &params_, scale, selected_.get(), counts_.get(), out,
                              step_workspace_.get(), step_workspace_bytes_, step_splits_, status, stream),
           "decode_step");
+  }
+  // decode_step() fed by its q/k/v producer (sa_hip_decode_step_qkv): the
+  // projection of producer.hidden_rows into producer.q/k/v, then the step on
+  // them; two launches where the one launch applies with 1 or 2 query heads
+  // per KV head.  head_dim 128.
+  void decode_step_qkv(const PagedKvPool& pool, const sa_qkv_producer& producer, int local_tokens, float scale,
+                       float* out, hipStream_t stream = nullptr, int32_t* status = nullptr) {
+    const sa_paged_kv kv = pool.view();
+    check(sa_hip_decode_step_qkv(&kv, &producer, local_tokens, &params_, scale, selected_.get(), counts_.get(), out,
+                                 step_workspace_.get(), step_workspace_bytes_, step_splits_, status, stream),
+          "decode_step_qkv");
   }
   bool fused(const PagedKvPool& pool) const {
     const sa_paged_kv kv = pool.view();

@@ -349,6 +349,74 @@ void check_decode_step(std::size_t d = 128, const std::string& tag = "", std::si
   record("attend_chunked_max_rel_error", num(chunk_err), chunk_err <= 2e-3);
 }
 
+// SparseDecoder::decode_step_qkv (the q/k/v projection's partials feeding
+// the one-launch step, which runs the reduce's epilogue for its own heads)
+// against the two calls it replaces, sa_hip_qkv_project_rms then
+// SparseDecoder::decode_step, on two copies of the same pool over 34 steps
+// across seals: q/k/v, ids, outputs and state equal bit for bit.
+void check_decode_step_qkv() {
+  const std::size_t batch = 4, hq = 16, hkv = 8, d = 128, stride = 24, pages = batch * stride, hidden = 1024;
+  const std::size_t budget = 8, steps = 34;
+  std::vector<std::uint16_t> host_pool(pages * 32 * 2 * hkv * d);
+  sao_synth_fill_half(41, 0, host_pool.size(), host_pool.data());
+  std::vector<int32_t> table(batch * stride);
+  for (std::size_t i = 0; i < table.size(); ++i) table[i] = static_cast<int32_t>((i * 29 + 5) % pages);
+  std::vector<int32_t> seq_len = {32 * 9 + 30, 32 * 12, 32 * 5 + 7, 32 * 16 + 1};
+  sa::hip::PagedKvPool pa(batch, hq, hkv, stride, pages), pb(batch, hq, hkv, stride, pages);
+  for (auto* pool : {&pa, &pb}) {
+    pool->pool().upload(host_pool);
+    pool->block_table().upload(table);
+    pool->seq_len().upload(seq_len);
+    pool->seal(0);
+  }
+  const sa_select_params params{static_cast<int32_t>(hkv), static_cast<int32_t>(budget), 1, 2,
+                                static_cast<int32_t>(budget), 0, nullptr};
+  sa::hip::SparseDecoder da(pa, params), db(pb, params);
+  auto weights = [](std::size_t n, std::uint64_t seed, float scale, float offset) {
+    std::vector<float> w(n);
+    sao_synth_fill_float(seed, 0, n, w.data());
+    for (auto& x : w) x = offset + scale * x;
+    sa::hip::DeviceArray<float> dw(n);
+    dw.upload(w);
+    return dw;
+  };
+  const float ws = 1.0f / std::sqrt(static_cast<float>(hidden));
+  auto wq = weights(hq * d * hidden, 51, ws, 0.0f), wk = weights(hkv * d * hidden, 52, ws, 0.0f),
+       wv = weights(hkv * d * hidden, 53, ws, 0.0f), qn = weights(d, 54, 0.1f, 1.0f), kn = weights(d, 55, 0.1f, 1.0f),
+       in_norm = weights(hidden, 56, 0.1f, 1.0f);
+  const std::size_t qkv_bytes = sa_hip_qkv_workspace_bytes(static_cast<int32_t>(batch), static_cast<int32_t>(hidden),
+                                                           static_cast<int32_t>(hq), static_cast<int32_t>(hkv));
+  sa::hip::DeviceArray<float> qkv_ws((qkv_bytes + 3) / 4), x(batch * hidden);
+  sa::hip::DeviceArray<float> qa(batch * hq * d), ka(batch * hkv * d), va(batch * hkv * d), oa(batch * hq * d);
+  sa::hip::DeviceArray<float> qb(batch * hq * d), kb(batch * hkv * d), vb(batch * hkv * d), ob(batch * hq * d);
+  std::vector<float> hx(batch * hidden);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(d));
+  bool same = true;
+  for (std::size_t step = 0; step < steps; ++step) {
+    sao_synth_fill_float(4000 + step, 0, hx.size(), hx.data());
+    x.upload(hx);
+    int rc = sa_hip_qkv_project_rms(x.get(), in_norm.get(), 1e-6f, wq.get(), wk.get(), wv.get(), qn.get(), kn.get(),
+                                    pa.seq_len().get(), static_cast<int32_t>(batch), static_cast<int32_t>(hidden),
+                                    static_cast<int32_t>(hq), static_cast<int32_t>(hkv), 1e6f, 1e-6f, qa.get(),
+                                    ka.get(), va.get(), qkv_ws.get(), qkv_bytes, nullptr);
+    if (rc != 0) throw std::runtime_error(std::string("qkv_project_rms: ") + sa_hip_last_error());
+    da.decode_step(pa, ka.get(), va.get(), 0, qa.get(), scale, oa.get());
+    const sa_qkv_producer pr{x.get(), in_norm.get(), 1e-6f, wq.get(), wk.get(), wv.get(), qn.get(), kn.get(),
+                             pb.seq_len().get(), static_cast<int32_t>(hidden), 1e6f, 1e-6f, qb.get(), kb.get(),
+                             vb.get(), qkv_ws.get(), qkv_bytes};
+    db.decode_step_qkv(pb, pr, 0, scale, ob.get());
+    same &= qa.download() == qb.download() && ka.download() == kb.download() && va.download() == vb.download();
+    same &= da.selected().download() == db.selected().download() && da.counts().download() == db.counts().download();
+    const auto ga = oa.download(), gb = ob.download();
+    same &= std::memcmp(ga.data(), gb.data(), ga.size() * sizeof(float)) == 0;
+  }
+  const auto ra = pa.reps().download(), rb = pb.reps().download();
+  same &= pa.pool().download() == pb.pool().download() && pa.seq_len().download() == pb.seq_len().download() &&
+          pa.sealed().download() == pb.sealed().download() &&
+          std::memcmp(ra.data(), rb.data(), ra.size() * sizeof(float)) == 0;
+  record("decode_step_qkv_equals_two_calls", same ? "true" : "false", same);
+}
+
 }  // namespace
 
 int main() {
@@ -368,6 +436,7 @@ int main() {
     check_decode_step(64, "_head_dim_64");
     check_decode_step(256, "_head_dim_256");
     check_decode_step(128, "_shared", 1);
+    check_decode_step_qkv();
     g_json << "\n}\n";
     std::cout << g_json.str();
     return g_ok ? 0 : 2;

@@ -44,6 +44,8 @@ def test_cpp_backend_check(hip):
     assert m["decode_step_selected_ids_exact_shared"] is True
     assert m["decode_step_state_bytes_exact_shared"] is True
     assert m["decode_step_max_rel_error_shared"] <= 2e-3
+    # the producer-fed step through the C++ API, equal to the two calls bit for bit
+    assert m["decode_step_qkv_equals_two_calls"] is True
 
 
 EXE_STORE = os.path.join(ROOT, "tests", "cpp", "store_check")
