@@ -6,10 +6,10 @@ init 4 + local 8 + 52) at head_dim 64, 128 and 256: 128 runs the tuned
 one-launch step, the others the general kernels in sequence (append + seal,
 scoring, selection, token-row attention).  Each head_dim builds its own pool
 (synthetic FP16 keys and values in a randomly permuted page table), seals
-it, then times `steps` decode steps eagerly (HIP events around the timed
-steps; every step appends one token).  Reported per head_dim: µs per step
-and the algorithmic bytes rate (representatives + selected pages), the bulk
-seal's time, and the status word.
+it, then times `steps` decode steps eagerly and `steps` more as one HIP graph
+(HIP events around the timed steps; every step appends one token).  Reported per head_dim: µs per step (graphs; eager beside it) and the
+algorithmic bytes rate (representatives + selected pages), the bulk seal's
+time, and the status word.
 """
 from __future__ import annotations
 
@@ -35,7 +35,7 @@ def run(args):
     torch.cuda.set_device(0)
     results = {}
     for d in (64, 128, 256):
-        ts = (ctx + steps + warmup + PAGE - 1) // PAGE + 2
+        ts = (ctx + 3 * steps + warmup + PAGE - 1) // PAGE + 2
         kv = sa.PagedKV(batch, hq, hkv, ts, num_pages=batch * ts, head_dim=d)
         g = torch.Generator(device="cpu")
         g.manual_seed(args.seed + d)
@@ -44,7 +44,7 @@ def run(args):
         kv.seq_len.fill_(ctx)
         q = torch.empty((batch, hq, d), dtype=torch.float32, device="cuda")
         sa.fill_synthetic_f32(q.view(-1), args.seed + d + 1, 0)
-        k = torch.empty((steps + warmup, batch, hkv, d), dtype=torch.float32, device="cuda")
+        k = torch.empty((2 * steps + warmup, batch, hkv, d), dtype=torch.float32, device="cuda")
         v = torch.empty_like(k)
         sa.fill_synthetic_f32(k.view(-1), args.seed + d + 2, 0)
         sa.fill_synthetic_f32(v.view(-1), args.seed + d + 3, 0)
@@ -70,16 +70,31 @@ def run(args):
         for s in range(warmup):
             step(s)
         torch.cuda.synchronize()
+        # eager steps, then the same number of steps as one HIP graph (every
+        # step appends its own token; the graph is replayed once to warm up)
         e0.record()
         for s in range(warmup, warmup + steps):
             step(s)
         e1.record()
         torch.cuda.synchronize()
+        eager_us = 1000.0 * e0.elapsed_time(e1) / steps
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for s in range(warmup + steps, warmup + 2 * steps):
+                step(s)
+        gr.replay()  # warm replay
+        torch.cuda.synchronize()
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
         us = 1000.0 * e0.elapsed_time(e1) / steps
+        del gr
         blocks = ctx // PAGE
         alg = batch * hkv * (blocks * d * 4 + budget * PAGE * 2 * d * 2)
         results[str(d)] = {
             "us_per_step": round(us, 2),
+            "eager_us_per_step": round(eager_us, 2),
             "algorithmic_gbps": round(alg / us / 1e3, 1),
             "fused_one_launch": bool(sa.select_attend_fused(kv, hkv, splits, sel_stride=budget)),
             "bulk_seal_us": round(seal_us, 1),
@@ -100,7 +115,8 @@ def run(args):
         "data": f"synthetic ({bench.GENERATOR}), randomly permuted page tables",
         "config": {"workload": "decode step at head_dim 64 / 128 / 256", "batch": batch, "heads": f"{hq}/{hkv}",
                    "context": ctx, "budget": f"{init} + {local} + {budget - init - local}",
-                   "timing": "eager, HIP events around the timed steps"},
+                   "timing": "one HIP graph of the timed steps, events around its replay (eager_us_per_step: "
+                             "the same number of eager steps)"},
         "by_head_dim": results,
     }
     print(json.dumps(line), flush=True)
