@@ -156,3 +156,52 @@ def test_decode_step_qkv_graph_replays(hip):
         assert torch.equal(oa.view(torch.int32), out.view(torch.int32)), step
     for a, b in zip(state(kva), state(kvb)):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_decode_step_qkv_sweep(hip, seed):
+    """Seeded configurations of the producer-fed step against the two calls,
+    bit for bit: batch 1-6, 1 or 2 query heads per KV head, budgets 3-20
+    blocks with init 0-2 and local 0-3, local_tokens 0, 5 or 32, with and
+    without the input RMSNorm, 6 steps each."""
+    rng = np.random.default_rng(900 + seed)
+    hkv = int(rng.choice([2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2]))
+    batch = int(rng.integers(1, 7))
+    local_tokens = int(rng.choice([0, 5, 32]))
+    lengths = [int(rng.integers(40, 32 * 50)) for _ in range(batch)]
+    budget = int(rng.integers(3, 21))
+    init = int(rng.integers(0, 3))
+    loc = int(rng.integers(0, 4))
+    rms = bool(rng.integers(0, 2))
+    print(f"case: decode_step_qkv sweep seed={seed} hq={hq} hkv={hkv} batch={batch} local_tokens={local_tokens} "
+          f"budget={budget} init={init} local={loc} rms={rms}", flush=True)
+    case = make_case(950 + seed, batch, hq, hkv, lengths, local_tokens=local_tokens)
+    kva, kvb = device_kv(case), device_kv(case)
+    hidden = 1024
+    W = make_weights(rng, hidden, hq, hkv)
+    inorm = W["inorm"] if rms else None
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+    wsa, _ = hip.decode_step_workspace(kva, 1)
+    wsb, _ = hip.decode_step_workspace(kvb, 1)
+    qws = torch.empty(hip.lib().sa_hip_qkv_workspace_bytes(batch, hidden, hq, hkv) // 4, dtype=torch.float32,
+                      device="cuda")
+    qa, qb = (torch.empty((batch, hq, 128), dtype=torch.float32, device="cuda") for _ in range(2))
+    ka, kb, va, vb = (torch.empty((batch, hkv, 128), dtype=torch.float32, device="cuda") for _ in range(4))
+    sta, stb = status_tensor(), status_tensor()
+    for step in range(6):
+        x = to_dev(rng.standard_normal((batch, hidden)).astype(np.float32))
+        hip.qkv_project(x, W["wq"], W["wk"], W["wv"], W["qn"], W["kn"], kva.seq_len, hq, hkv, q=qa, k=ka, v=va,
+                        workspace=qws, input_norm=inorm)
+        sa_, ca, oa = hip.decode_step(kva, ka, va, local_tokens, qa, hkv, budget, init, loc, scale, wsa, status=sta)
+        sb, cb, ob = hip.decode_step_qkv(kvb, x, W["wq"], W["wk"], W["wv"], W["qn"], W["kn"], kvb.seq_len, qb, kb, vb,
+                                         qws, local_tokens, hkv, budget, init, loc, scale, wsb, input_norm=inorm,
+                                         status=stb)
+        torch.cuda.synchronize()
+        assert int(sta.item()) == int(stb.item()), step
+        for a, b, what in ((qa, qb, "q"), (ka, kb, "k"), (va, vb, "v"), (sa_, sb, "ids"), (ca, cb, "counts"),
+                           (oa, ob, "out")):
+            assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a,
+                               b.view(torch.int32) if b.dtype == torch.float32 else b), (step, what)
+    for a, b in zip(state(kva), state(kvb)):
+        assert torch.equal(a, b)
