@@ -651,6 +651,10 @@ size_t sa_hip_decode_step_workspace_bytes(const sa_paged_kv* kv, int32_t splits)
 // counters, zero on entry to the fused launch, which leaves them at zero
 // (clear_arrive: zeroed here first, whatever they hold); `records` the
 // attention's split records of the unfused launches (records_bytes of them).
+// With a producer (validated by the caller; k, v and query are its q/k/v
+// outputs), its partial launch precedes the one-launch step that runs its
+// epilogue (decode_step_qkv_supported()), else its whole projection runs
+// before the step's launches.
 static int decode_step_run(const sa_paged_kv* kv, const float* k, const float* v, const uint16_t* k16,
                            const uint16_t* v16, int32_t local_tokens, const float* query,
                            const sa_select_params* params, float scale, int32_t* selected, int32_t* counts,
